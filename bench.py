@@ -1,0 +1,205 @@
+"""Benchmark of the MI355X CKKS hot path (one JSON line on stdout).
+
+Headline (BASELINE.json metric, config 2): batched forward negacyclic NTT at
+N = 2^16 over a batch of 2 polys x 35 limbs (35 x 50-bit primes; the 60-bit
+special prime is in the table but not transformed).  One step = one forward
+NTT of one batch, inputs resident in HBM.  value = limbs transformed per second.
+
+To keep the measurement an HBM measurement, the timed steps cycle through
+several distinct batches whose total size exceeds the 256 MiB Infinity Cache,
+so no step finds its batch cached from the previous one.
+
+Also reported (same line): inverse NTT limbs/s, and HMult + relinearize +
+rescale latency for config 3 (|Q| = 24, alpha = 4, dnum = 6) and for the
+metric's "L=35" variant (|Q| = 35, alpha = 1).
+
+cpu_baseline: the CPU oracle's forward NTT (oracle/ckks_oracle.c, a C
+restatement of the reference algorithm) on the same workload, single thread,
+timed on this host for a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "phantom-fhe_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+N = 1 << 16
+LIMBS = 35
+POLYS = 2
+HBM_PEAK_GBS = 8000.0
+LIMB_BYTES = N * 8
+# algorithmic bytes of one forward NTT of the batch: each residue read once and written once
+NTT_BYTES = POLYS * LIMBS * N * 16
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def uniform(torch, shape, mods, dev, gen):
+    """uint64 residues uniform in [0, q_l) on the device; limb axis is -2."""
+    *pre, L, n = shape
+    out = torch.empty(tuple(shape), dtype=torch.int64, device=dev)
+    for l in range(L):
+        out[..., l, :] = torch.randint(0, int(mods[l]), tuple(pre) + (n,), dtype=torch.int64, device=dev,
+                                       generator=gen)
+    return out.view(torch.uint64)
+
+
+def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
+    stream = torch.cuda.current_stream()
+    fn = ctx.ntt_inverse if inverse else ctx.ntt_forward
+    for i in range(warmup):
+        fn(batches[i % len(batches)], POLYS, LIMBS, 0, stream.cuda_stream)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fn(batches[i % len(batches)], POLYS, LIMBS, 0, stream.cuda_stream)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [a.elapsed_time(b) for a, b in ev]
+    return wall, sum(per) / len(per)
+
+
+def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
+    """multiply_and_relin + rescale on fresh chain-index-1 ciphertexts; returns ms per op."""
+    bits = [60] + [50] * (nq - 1) + [60] * alpha
+    mods = P.create_coeff_modulus(N, bits)
+    ctx = P.NativeContext(N, mods, alpha)
+    dnum = nq // alpha
+    a = uniform(torch, (2, nq, N), mods, dev, gen)
+    b = uniform(torch, (2, nq, N), mods, dev, gen)
+    key = torch.empty((dnum, 2, nq + alpha, N), dtype=torch.uint64, device=dev)
+    for d in range(dnum):
+        key[d] = uniform(torch, (2, nq + alpha, N), mods, dev, gen)
+    out = torch.empty((2, nq, N), dtype=torch.uint64, device=dev)
+    res = torch.empty((2, nq - 1, N), dtype=torch.uint64, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(warmup):
+        ctx.multiply_and_relin(1, a, b, key, out, s)
+        ctx.rescale(1, out, res, s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ctx.multiply_and_relin(1, a, b, key, out, s)
+        ctx.rescale(1, out, res, s)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    compulsory = (2 * 2 * nq + dnum * 2 * (nq + alpha) + 2 * (nq - 1)) * LIMB_BYTES
+    del key, a, b, out, res
+    ctx.close()
+    return {"ms": round(ms, 4), "compulsory_bytes": compulsory,
+            "hbm_roofline_frac": round(compulsory / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+            "chain": f"{{60, 50 x {nq - 1}, 60 x {alpha}}}", "dnum": dnum}
+
+
+def cpu_baseline(mods, seconds):
+    """Oracle forward NTT, one thread, repeated over the config-2 batch for ~`seconds`."""
+    import numpy as np
+
+    import py_oracle as O
+
+    orc = O.Oracle(N, mods, 1)
+    rng = np.random.default_rng(0)
+    x = np.stack([rng.integers(0, q, size=(POLYS, N), dtype=np.uint64) for q in mods[:LIMBS]], axis=1)
+    limbs, t0 = 0, time.perf_counter()
+    while True:
+        orc.ntt_fwd(x, threads=1)
+        limbs += POLYS * LIMBS
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(limbs / el, 2), "unit": "limbs/s", "cores": 1, "kind": "port",
+            "sample": f"{limbs // (POLYS * LIMBS)} forward NTTs of the 2x35-limb N=2^16 batch "
+                      f"({limbs} limbs, {el:.1f} s) by oracle/ckks_oracle.c (radix-2, Shoup), 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-hmult", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
+              "the path's sharding is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import pfa_native as P
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    mods = P.create_coeff_modulus(N, [50] * LIMBS + [60])
+    ctx = P.NativeContext(N, mods, 1)
+    n_batches = 10  # 10 x 35 MiB > 256 MiB Infinity Cache
+    batches = [uniform(torch, (POLYS, LIMBS, N), mods, dev, gen) for _ in range(n_batches)]
+    log(f"bench: config 2 forward NTT, {args.steps} steps, {args.warmup} warmup, {n_batches} rotating batches")
+    wall, ev_ms = time_ntt(torch, ctx, batches, args.steps, args.warmup)
+    log(f"bench: forward done, {ev_ms * 1e3:.1f} us/launch")
+    _, ev_inv_ms = time_ntt(torch, ctx, batches, args.steps, args.warmup, inverse=True)
+    log(f"bench: inverse done, {ev_inv_ms * 1e3:.1f} us/launch")
+    limbs = POLYS * LIMBS
+    value = limbs * args.steps / wall
+    achieved = NTT_BYTES / (ev_ms * 1e-3) / 1e9
+    del batches
+    torch.cuda.empty_cache()
+
+    hm = {}
+    if not args.no_hmult:
+        hm["config3_Q24_alpha4"] = time_hmult(torch, P, dev, gen, 24, 4, max(10, args.steps // 4), 5)
+        log(f"bench: hmult config3 {hm['config3_Q24_alpha4']['ms']} ms")
+        torch.cuda.empty_cache()
+        hm["L35_Q35_alpha1"] = time_hmult(torch, P, dev, gen, 35, 1, max(5, args.steps // 10), 3)
+        log(f"bench: hmult L=35 {hm['L35_Q35_alpha1']['ms']} ms")
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(mods, args.cpu_seconds)
+        log(f"bench: cpu baseline {cpu['value']} limbs/s")
+
+    line = {
+        "metric": "NTT limbs/s at N=2^16; HMult+relin+rescale ms (L=35); % HBM roofline",
+        "value": round(value, 1),
+        "unit": "limbs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic: uint64 residues uniform in [0, q_l) from a seeded torch generator",
+        "config": {"workload": "config 2: batched forward NTT, N=2^16, 2 polys x 35 limbs (50-bit primes)",
+                   "N": N, "polys": POLYS, "limbs": LIMBS, "rotating_batches": n_batches},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "forward NTT (ntt_fwd_cols + ntt_fwd_rows), 16 B/residue algorithmic"},
+        "cpu_baseline": cpu,
+        "ntt_inverse_limbs_per_s": round(limbs / (ev_inv_ms * 1e-3), 1),
+        "ntt_forward_us": round(ev_ms * 1e3, 2),
+        "ntt_inverse_us": round(ev_inv_ms * 1e3, 2),
+        "hmult_relin_rescale": hm,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,170 @@
+/*
+ * phantom_amd.h -- C ABI of the MI355X (gfx950) CKKS evaluation core.
+ *
+ * Drop-in boundary for the data-parallel hot path of gold9598/phantom-fhe:
+ * batched negacyclic RNS NTT/INTT, ModUp/ModDown fast base conversion, the
+ * hybrid key-switching inner product, the Galois automorphism and rescale.
+ * Each entry point names the reference interface it replaces (file:line in
+ * the reference tree).
+ *
+ * Conventions
+ *   - All residue buffers are DEVICE pointers to uint64 residues, limb-major:
+ *       limb = N residues of one prime, poly = [L][N], ciphertext = [size][L][N]
+ *     (the reference's layout, include/ciphertext.h:7-308).
+ *   - Keys are contiguous [dnum][2][|QP|][N] in NTT form, row 0 =
+ *     -(a s + e) + [P]_q s' on digit d's own alpha limbs, row 1 = a
+ *     (src/secretkey.cu:354-398).  The reference keeps the same rows behind an
+ *     array of per-digit pointers.
+ *   - chain_index follows the reference's context chain (src/context.cu:121-168):
+ *     0 = key level (all |QP| primes), chain c >= 1 holds |Ql| = |Q| - c + 1
+ *     data primes.
+ *   - stream: a hipStream_t; NULL means hipStreamPerThread, the counterpart of
+ *     the reference's cudaStreamPerThread (src/evaluate.cu:1079).  Calls are
+ *     asynchronous on that stream.
+ *   - Every function returns PFA_OK or an error code; pfa_last_error() gives
+ *     the calling thread's message.  Codes map to the reference's exception
+ *     classes: INVALID_ARGUMENT = std::invalid_argument (ValueError in
+ *     Python), LOGIC = std::logic_error, RUNTIME = std::runtime_error
+ *     (PHANTOM_CHECK_CUDA, include/cuda_wrapper.cuh:19-43).
+ *   - Temporaries are stream-ordered allocations (hipMallocAsync), as the
+ *     reference's cuda_auto_ptr (include/cuda_wrapper.cuh:185-189).
+ */
+#ifndef PHANTOM_AMD_H
+#define PHANTOM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PFA_OK 0
+#define PFA_ERR_INVALID_ARGUMENT 1
+#define PFA_ERR_LOGIC 2
+#define PFA_ERR_RUNTIME 3
+
+typedef struct pfa_context pfa_context;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *pfa_last_error(void);
+
+/* ABI version of this library. */
+int pfa_abi_version(void);
+
+/* ------------------------------------------------------------------ setup */
+
+/* CoeffModulus::Create (src/host/modulus.cu:80-111; python binding
+ * create_coeff_modulus, python/src/binding.cu:56).  out[count]. */
+int pfa_create_coeff_modulus(uint64_t poly_degree, const int *bit_sizes, size_t count, uint64_t *out);
+
+/* PhantomContext::PhantomContext (src/context.cu:121-183): builds the chain,
+ * the NTT tables of all |QP| primes (minimal primitive 2N-th root, bit-reversed
+ * powers, N^-1 folded, src/host/ntt.cu:11-56) and the per-level RNS constants
+ * (src/rns.cu:11-195) on `device`.  moduli = the |Q| data primes followed by
+ * the special_size special primes, as EncryptionParameters::coeff_modulus. */
+int pfa_context_create(uint64_t poly_degree, const uint64_t *moduli, size_t size_QP, size_t special_size,
+                       int device, pfa_context **out);
+void pfa_context_destroy(pfa_context *ctx);
+
+/* Copies the minimal primitive 2N-th root of every prime (|QP| values). */
+int pfa_context_roots(const pfa_context *ctx, uint64_t *out);
+
+/* ------------------------------------------------------------------ NTT */
+
+/* nwt_2d_radix8_forward_inplace[_batched] (include/ntt.cuh:173, :184;
+ * src/ntt/fntt_2d.cu:665-784): in-place forward NTT of M polys x L limbs,
+ * limb l of each poly using table row start + l. */
+int pfa_ntt_forward(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L, size_t start, void *stream);
+
+/* nwt_2d_radix8_backward_inplace (include/ntt.cuh:216; src/ntt/intt_2d.cu:769-813),
+ * batched over M polys like the forward. */
+int pfa_ntt_inverse(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L, size_t start, void *stream);
+
+/* --------------------------------------------------- RNS / key switching */
+
+/* DRNSTool::modup (include/rns.cuh:156; src/rns_bconv.cu:530-628):
+ * c2 [|Ql|][N] (NTT form) -> t_mod_up [beta][|Ql|+alpha][N]. */
+int pfa_modup(const pfa_context *ctx, size_t chain_index, const uint64_t *c2, uint64_t *t_mod_up, void *stream);
+
+/* key_switch_inner_prod (include/evaluate.cuh:41-43; kernel
+ * src/eval_key_switch.cu:175-230): cx [2][|Ql|+alpha][N]. */
+int pfa_ks_inner_prod(const pfa_context *ctx, size_t chain_index, const uint64_t *t_mod_up, const uint64_t *key,
+                      size_t key_dnum, uint64_t *cx, void *stream);
+
+/* DRNSTool::moddown_from_NTT (include/rns.cuh; src/rns_bconv.cu:776-828):
+ * cx_k [|Ql|+alpha][N] -> out [|Ql|][N] = (cx - NTT(BConv_P->Ql(INTT(cx_P)))) * P^-1.
+ * cx_k is not modified. */
+int pfa_moddown(const pfa_context *ctx, size_t chain_index, const uint64_t *cx_k, uint64_t *out, void *stream);
+
+/* keyswitch_inplace (include/evaluate.cuh:45-48; src/eval_key_switch.cu:294-381):
+ * ct[0..1] ([2][|Ql|][N]) += ModDown(<ModUp(c2), key>). */
+int pfa_keyswitch(const pfa_context *ctx, size_t chain_index, uint64_t *ct, const uint64_t *c2, const uint64_t *key,
+                  size_t key_dnum, void *stream);
+
+/* ------------------------------------------------------------ evaluator */
+
+/* bgv_ckks_multiply's tensor (src/evaluate.cu:345-397 -> tensor_prod_2x2_rns_poly,
+ * src/polymath.cu:463-498): a, b [2][|Ql|][N] -> out [3][|Ql|][N]. */
+int pfa_tensor(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b, uint64_t *out,
+               void *stream);
+
+/* multiply_and_relin_inplace (src/evaluate.cu:1061-1104): out [2][|Ql|][N]. */
+int pfa_multiply_and_relin(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
+                           const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream);
+
+/* relinearize_inplace (src/evaluate.cu:1342-1374): ct3 [3][|Ql|][N] -> out [2][|Ql|][N]. */
+int pfa_relinearize(const pfa_context *ctx, size_t chain_index, const uint64_t *ct3, const uint64_t *rlk,
+                    size_t key_dnum, uint64_t *out, void *stream);
+
+/* rescale_to_next -> divide_and_round_q_last_ntt (src/evaluate.cu:1582-1602,
+ * src/rns.cu:1128-1184): in [size][|Ql|][N] -> out [size][|Ql|-1][N] (floor). */
+int pfa_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *in, size_t size, uint64_t *out,
+                void *stream);
+
+/* get_elt_from_step (include/galois.cuh:16-49): 5^step mod 2N, step 0 -> 2N-1. */
+int pfa_galois_elt_from_step(int step, uint64_t poly_degree, uint32_t *elt);
+
+/* PhantomGaloisTool::apply_galois_ntt (include/galois.cuh:157; src/galois.cu:11-18,
+ * :86-102): dst[l][i] = src[l][pi(i)] for L limbs; src != dst. */
+int pfa_apply_galois_ntt(const pfa_context *ctx, uint32_t elt, const uint64_t *src, uint64_t *dst, size_t L,
+                         void *stream);
+
+/* apply_galois_with_ksk (src/evaluate.cu:1607-1656) on a size-2 ciphertext, in place. */
+int pfa_apply_galois(const pfa_context *ctx, size_t chain_index, uint64_t *ct, uint32_t elt, const uint64_t *key,
+                     size_t key_dnum, void *stream);
+
+/* hoist_rotations (src/evaluate.cu:1929-2082): one ModUp of c1 shared by n
+ * rotations; keys = host array of n device key pointers; out [n][2][|Ql|][N]. */
+int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts,
+                        size_t n, const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream);
+
+/* -------------------------------------------- key material and elementwise */
+
+/* generate_one_kswitch_key (src/secretkey.cu:354-398, with
+ * multiply_temp_mod_and_add_rns_poly, src/polymath.cu:318-336): all NTT form,
+ * new_key, s [|QP|][N]; a, e [dnum][|QP|][N] -> key [dnum][2][|QP|][N]. */
+int pfa_kswitch_key(const pfa_context *ctx, const uint64_t *new_key, const uint64_t *s, const uint64_t *a,
+                    const uint64_t *e, uint64_t *key, void *stream);
+
+/* Elementwise ops over L limbs using primes start..start+L-1
+ * (add_rns_poly / sub_rns_poly / multiply_rns_poly / negate_rns_poly,
+ * src/polymath.cu).  out may alias an input. */
+int pfa_poly_add(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream);
+int pfa_poly_sub(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream);
+int pfa_poly_mul(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream);
+int pfa_poly_negate(const pfa_context *ctx, const uint64_t *a, uint64_t *out, size_t L, size_t start, void *stream);
+
+/* Reduces signed 64-bit coefficients (one poly, N values) into L limbs using
+ * primes start..start+L-1: out[l][i] = in[i] mod q_(start+l) (sampler output
+ * decomposition, src/prng.cu / src/secretkey.cu:236-299). */
+int pfa_poly_from_signed(const pfa_context *ctx, const int64_t *in, uint64_t *out, size_t L, size_t start,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PHANTOM_AMD_H */

@@ -1,0 +1,344 @@
+// Context construction: moduli, NTT tables and per-level RNS constants.
+//
+// Host precompute restated from the mathematics of the reference's
+// src/host/{modulus,numth,ntt,rns}.cu and src/rns.cu:11-195; all tables are
+// uploaded once to HBM and are read-only afterwards.
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
+#include "internal.h"
+
+namespace pfa {
+
+// ---------------------------------------------------------------- errors
+static thread_local std::string g_last_error;
+
+void set_last_error(const std::string &msg) { g_last_error = msg; }
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) fail(PFA_ERR_RUNTIME, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int handle_exception() {
+    try {
+        throw;
+    } catch (const Error &e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::invalid_argument &e) {
+        set_last_error(e.what());
+        return PFA_ERR_INVALID_ARGUMENT;
+    } catch (const std::logic_error &e) {
+        set_last_error(e.what());
+        return PFA_ERR_LOGIC;
+    } catch (const std::exception &e) {
+        set_last_error(e.what());
+        return PFA_ERR_RUNTIME;
+    } catch (...) {
+        set_last_error("unknown error");
+        return PFA_ERR_RUNTIME;
+    }
+}
+
+// ---------------------------------------------------------------- host math
+uint64_t powmod(uint64_t a, uint64_t e, uint64_t q) {
+    uint64_t r = 1 % q;
+    a %= q;
+    for (; e; e >>= 1) {
+        if (e & 1) r = mulmod(r, a, q);
+        a = mulmod(a, a, q);
+    }
+    return r;
+}
+
+uint64_t invmod(uint64_t a, uint64_t q) {
+    a %= q;
+    if (a == 0) fail(PFA_ERR_INVALID_ARGUMENT, "value not invertible");
+    return powmod(a, q - 2, q);
+}
+
+// Deterministic Miller-Rabin: the first twelve primes as bases decide every
+// n < 3.3e24 (the reference decides the same question with 40 random rounds,
+// src/host/numth.cu:129-205).
+bool is_prime(uint64_t n) {
+    static const uint64_t bases[] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+    if (n < 2) return false;
+    for (uint64_t p : bases) {
+        if (n % p == 0) return n == p;
+    }
+    uint64_t d = n - 1;
+    int s = 0;
+    while (!(d & 1)) {
+        d >>= 1;
+        ++s;
+    }
+    for (uint64_t a : bases) {
+        uint64_t x = powmod(a, d, n);
+        if (x == 1 || x == n - 1) continue;
+        bool composite = true;
+        for (int i = 1; i < s && composite; ++i) {
+            x = mulmod(x, x, n);
+            if (x == n - 1) composite = false;
+        }
+        if (composite) return false;
+    }
+    return true;
+}
+
+// Smallest primitive degree-th root of unity mod q (try_minimal_primitive_root,
+// src/host/numth.cu:309-331).  The primitive roots are the odd powers of any
+// one of them; a first one comes from x^((q-1)/degree) for the smallest x whose
+// power has order exactly degree.
+uint64_t minimal_root(uint64_t degree, uint64_t q) {
+    if ((q - 1) % degree) fail(PFA_ERR_INVALID_ARGUMENT, "prime is not congruent to 1 mod 2N");
+    const uint64_t cof = (q - 1) / degree;
+    uint64_t g = 0;
+    for (uint64_t x = 2; x < q && !g; ++x) {
+        uint64_t c = powmod(x, cof, q);
+        if (powmod(c, degree / 2, q) == q - 1) g = c;
+    }
+    if (!g) fail(PFA_ERR_INVALID_ARGUMENT, "no primitive root");
+    const uint64_t g2 = mulmod(g, g, q);
+    uint64_t best = g;
+    for (uint64_t k = 1, cur = g; k < degree; k += 2, cur = mulmod(cur, g2, q)) best = std::min(best, cur);
+    return best;
+}
+
+ulonglong2 ntt_pair(uint64_t w, uint64_t q) {
+    if (q < (1ULL << 50)) {
+        double wd = (double)w, wq = (double)w / (double)q;
+        uint64_t a, b;
+        std::memcpy(&a, &wd, 8);
+        std::memcpy(&b, &wq, 8);
+        return ulonglong2{a, b};
+    }
+    return shoup_pair(w, q);
+}
+
+static uint32_t bitrev(uint32_t x, int bits) {
+    uint32_t r = 0;
+    for (int i = 0; i < bits; ++i) r |= ((x >> i) & 1u) << (bits - 1 - i);
+    return r;
+}
+
+// ---------------------------------------------------------------- primes
+// CoeffModulus::Create (src/host/modulus.cu:80-111): for each bit size b the
+// candidates are 2^b - 2N + 1, 2^b - 4N + 1, ... (q = 1 mod 2N, q > 2^(b-1));
+// the k requests of size b receive the k largest such primes, smallest first.
+static void create_coeff_modulus(uint64_t N, const int *bits, size_t count, uint64_t *out) {
+    require(N >= 2 && (N & (N - 1)) == 0, "poly_modulus_degree must be a power of two");
+    for (size_t i = 0; i < count; ++i) require(bits[i] >= 2 && bits[i] <= 60, "bit size must be in [2, 60]");
+    std::vector<int> sizes(bits, bits + count);
+    std::sort(sizes.begin(), sizes.end());
+    sizes.erase(std::unique(sizes.begin(), sizes.end()), sizes.end());
+    for (int b : sizes) {
+        size_t want = std::count(bits, bits + count, b);
+        std::vector<uint64_t> found;
+        const uint64_t step = 2 * N, lower = 1ULL << (b - 1);
+        uint64_t v = (1ULL << b) - step + 1;
+        while (found.size() < want) {
+            if (v <= lower) fail(PFA_ERR_LOGIC, "failed to find enough qualifying primes");
+            if (is_prime(v)) found.push_back(v);
+            v -= step;
+        }
+        std::reverse(found.begin(), found.end());  // smallest first
+        size_t k = 0;
+        for (size_t i = 0; i < count; ++i)
+            if (bits[i] == b) out[i] = found[k++];
+    }
+}
+
+// ---------------------------------------------------------------- context
+template <class T>
+T *Ctx::upload(const std::vector<T> &v) {
+    void *p = nullptr;
+    PFA_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(T)));
+    allocations.push_back(p);
+    if (!v.empty()) PFA_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+    return (T *)p;
+}
+
+static uint64_t prod_mod(const uint64_t *m, size_t n, size_t skip, uint64_t p) {
+    uint64_t r = 1 % p;
+    for (size_t k = 0; k < n; ++k)
+        if (k != skip) r = mulmod(r, m[k] % p, p);
+    return r;
+}
+
+// Argument checks of PhantomContext construction, done before any device call.
+static void validate(uint64_t N, const uint64_t *moduli, size_t QP, size_t P) {
+    require(N >= 1024 && N <= (1u << 17) && (N & (N - 1)) == 0, "poly_modulus_degree must be 2^10 .. 2^17");
+    require(QP >= 2 && P >= 1 && P < QP, "need at least one data prime and one special prime");
+    for (size_t i = 0; i < QP; ++i) {
+        uint64_t q = moduli[i];
+        require(q < (1ULL << 61) && q % (2 * N) == 1 && is_prime(q), "moduli must be primes = 1 mod 2N below 2^61");
+        for (size_t j = 0; j < i; ++j) require(moduli[j] != q, "moduli must be distinct");
+    }
+}
+
+static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t P) {
+    c.N = (uint32_t)N;
+    c.logN = 0;
+    while ((1u << c.logN) < c.N) ++c.logN;
+    c.QP = (uint32_t)QP;
+    c.P = (uint32_t)P;
+    c.Q = (uint32_t)(QP - P);
+    c.moduli.assign(moduli, moduli + QP);
+
+    // NTT tables (src/host/ntt.cu:11-56): tw[brv(i)] = psi^i, itw[brv(i)] = psi^-i,
+    // itw[1] *= N^-1.
+    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP);
+    c.roots.resize(QP);
+    for (size_t r = 0; r < QP; ++r) {
+        const uint64_t q = moduli[r];
+        const uint64_t psi = minimal_root(2 * N, q), ipsi = invmod(psi, q);
+        c.roots[r] = psi;
+        const uint64_t ni = invmod(N % q, q);
+        std::vector<uint64_t> f(N), b(N);
+        uint64_t p = 1, ip = 1;
+        for (uint32_t i = 0; i < N; ++i) {
+            uint32_t k = bitrev(i, (int)c.logN);
+            f[k] = p;
+            b[k] = ip;
+            p = mulmod(p, psi, q);
+            ip = mulmod(ip, ipsi, q);
+        }
+        b[1] = mulmod(b[1], ni, q);
+        for (uint32_t i = 0; i < N; ++i) {
+            tw[r * N + i] = ntt_pair(f[i], q);
+            itw[r * N + i] = ntt_pair(b[i], q);
+        }
+        ninv[r] = ntt_pair(ni, q);
+        u128 rt = (~(u128)0) / q;  // floor((2^128 - 1) / q) == floor(2^128 / q) for non powers of two
+        ratio[r] = ulonglong2{(uint64_t)rt, (uint64_t)(rt >> 64)};
+    }
+    c.mod = c.upload(c.moduli);
+    c.ratio = c.upload(ratio);
+    c.tw = c.upload(tw);
+    c.itw = c.upload(itw);
+    c.ninv = c.upload(ninv);
+
+    const uint64_t *Qm = moduli, *Pm = moduli + c.Q;
+    const uint32_t alpha = c.P;
+
+    // ModDown constants (src/rns.cu:107-138, src/rns.cu:193-194)
+    {
+        std::vector<ulonglong2> sc(alpha), pinv(c.Q), pq(QP);
+        std::vector<uint64_t> mat((size_t)alpha * c.Q);
+        for (uint32_t j = 0; j < alpha; ++j) {
+            const uint64_t p = Pm[j];
+            sc[j] = ntt_pair(invmod(prod_mod(Pm, alpha, j, p), p), p);
+            for (uint32_t i = 0; i < c.Q; ++i) mat[(size_t)j * c.Q + i] = prod_mod(Pm, alpha, j, Qm[i]);
+        }
+        for (uint32_t i = 0; i < c.Q; ++i) {
+            const uint64_t q = Qm[i];
+            const uint64_t pm = prod_mod(Pm, alpha, alpha, q);
+            pinv[i] = shoup_pair(invmod(pm, q), q);
+            pq[i] = shoup_pair(pm, q);
+        }
+        for (uint32_t j = 0; j < alpha; ++j) pq[c.Q + j] = ulonglong2{0, 0};
+        c.moddown_scale = c.upload(sc);
+        c.moddown_mat = c.upload(mat);
+        c.pinv = c.upload(pinv);
+        c.pmodq = c.upload(pq);
+    }
+
+    // Per-level constants (src/rns.cu:66-95, :141-190)
+    c.levels.resize(c.Q + 1);
+    for (uint32_t chain = 1; chain <= c.Q; ++chain) {
+        Level &lv = c.levels[chain];
+        const uint32_t Ql = c.size_Ql(chain), QlP = Ql + alpha;
+        lv.Ql = Ql;
+        lv.beta = (Ql + alpha - 1) / alpha;
+        std::vector<ulonglong2> sc(Ql);
+        std::vector<uint64_t> mat((size_t)lv.beta * alpha * QlP, 0);
+        for (uint32_t b = 0; b < lv.beta; ++b) {
+            const uint32_t st = b * alpha, sz = std::min(alpha, Ql - st);
+            for (uint32_t i = 0; i < sz; ++i) {
+                const uint64_t q = Qm[st + i];
+                sc[st + i] = ntt_pair(invmod(prod_mod(Qm + st, sz, i, q), q), q);
+                for (uint32_t r = 0; r < QlP; ++r) {
+                    const uint64_t p = moduli[c.qlp_row(Ql, r)];
+                    mat[((size_t)b * alpha + i) * QlP + r] = prod_mod(Qm + st, sz, i, p);
+                }
+            }
+        }
+        lv.modup_scale = c.upload(sc);
+        lv.modup_mat = c.upload(mat);
+        std::vector<ulonglong2> rs(Ql > 1 ? Ql - 1 : 0);
+        if (Ql > 1) {
+            const uint64_t ql = Qm[Ql - 1];
+            for (uint32_t j = 0; j + 1 < Ql; ++j) rs[j] = shoup_pair(invmod(ql % Qm[j], Qm[j]), Qm[j]);
+        }
+        lv.rescale_inv = c.upload(rs);
+    }
+}
+
+static void destroy(Ctx *c) {
+    if (!c) return;
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(c->device);
+    for (void *p : c->allocations) (void)hipFree(p);
+    (void)hipSetDevice(prev);
+    delete c;
+}
+
+Ctx *ctx_of(const pfa_context *c) {
+    if (!c) fail(PFA_ERR_INVALID_ARGUMENT, "null context");
+    return (Ctx *)c;
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" {
+
+const char *pfa_last_error(void) { return g_last_error.c_str(); }
+
+int pfa_abi_version(void) { return 1; }
+
+int pfa_create_coeff_modulus(uint64_t poly_degree, const int *bit_sizes, size_t count, uint64_t *out) {
+    return guarded([&] {
+        require(bit_sizes && out, "null argument");
+        create_coeff_modulus(poly_degree, bit_sizes, count, out);
+    });
+}
+
+int pfa_context_create(uint64_t poly_degree, const uint64_t *moduli, size_t size_QP, size_t special_size,
+                       int device, pfa_context **out) {
+    Ctx *c = nullptr;
+    int rc = guarded([&] {
+        require(moduli && out, "null argument");
+        validate(poly_degree, moduli, size_QP, special_size);
+        c = new Ctx();
+        c->device = device;
+        int prev = 0;
+        PFA_HIP(hipGetDevice(&prev));
+        PFA_HIP(hipSetDevice(device));
+        try {
+            build(*c, poly_degree, moduli, size_QP, special_size);
+        } catch (...) {
+            (void)hipSetDevice(prev);
+            throw;
+        }
+        PFA_HIP(hipSetDevice(prev));
+        *out = (pfa_context *)c;
+    });
+    if (rc != PFA_OK) destroy(c);
+    return rc;
+}
+
+void pfa_context_destroy(pfa_context *ctx) { destroy((Ctx *)ctx); }
+
+int pfa_context_roots(const pfa_context *ctx, uint64_t *out) {
+    return guarded([&] {
+        const Ctx *c = ctx_of(ctx);
+        require(out != nullptr, "null argument");
+        std::copy(c->roots.begin(), c->roots.end(), out);
+    });
+}
+
+}  // extern "C"

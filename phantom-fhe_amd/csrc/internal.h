@@ -1,0 +1,124 @@
+// Internal host-side declarations shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "phantom_amd.h"
+
+namespace pfa {
+
+// ---------------------------------------------------------------- errors
+// Exceptions carry the C-ABI status they map to; every extern "C" entry point
+// catches them, records the message for pfa_last_error() and returns the code.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] inline void fail(int code, const std::string &msg) { throw Error(code, msg); }
+
+inline void require(bool ok, const std::string &msg) {
+    if (!ok) fail(PFA_ERR_INVALID_ARGUMENT, msg);
+}
+
+void hip_check(hipError_t e, const char *what);
+#define PFA_HIP(x) ::pfa::hip_check((x), #x)
+
+void set_last_error(const std::string &msg);
+int handle_exception();
+
+template <class F>
+int guarded(F &&f) {
+    try {
+        f();
+        return PFA_OK;
+    } catch (...) {
+        return handle_exception();
+    }
+}
+
+inline hipStream_t as_stream(void *s) { return s ? (hipStream_t)s : hipStreamPerThread; }
+
+// ---------------------------------------------------------------- host math
+typedef unsigned __int128 u128;
+inline uint64_t mulmod(uint64_t a, uint64_t b, uint64_t q) { return (uint64_t)((u128)a * b % q); }
+uint64_t powmod(uint64_t a, uint64_t e, uint64_t q);
+uint64_t invmod(uint64_t a, uint64_t q);  // q prime
+inline uint64_t shoup_of(uint64_t w, uint64_t q) { return (uint64_t)(((u128)w << 64) / q); }
+bool is_prime(uint64_t n);
+uint64_t minimal_root(uint64_t degree, uint64_t q);
+// Pair encoding of a constant w mod q for the NTT arithmetic policy of q
+// (integer Shoup pair, or (double w, fl(w/q)) for q < 2^50).
+ulonglong2 ntt_pair(uint64_t w, uint64_t q);
+// Integer Shoup pair (w, floor(w 2^64/q)) for the elementwise kernels.
+inline ulonglong2 shoup_pair(uint64_t w, uint64_t q) { return ulonglong2{w, shoup_of(w, q)}; }
+
+// ---------------------------------------------------------------- context
+// Constants of one chain level (chain index c >= 1, |Ql| = |Q| - c + 1),
+// restating DRNSTool's per-level precompute (src/rns.cu:11-195).
+struct Level {
+    uint32_t Ql = 0, beta = 0;
+    // ModUp: [(Q_part / q_i)^-1]_{q_i} per limb i < Ql, NTT-policy pairs
+    ulonglong2 *modup_scale = nullptr;
+    // ModUp: base-conversion matrix of digit b, [beta][alpha][QlP]:
+    //   mat[b][i][r] = [Q_part_b / q_(b alpha + i)]_{p_r}   (p_r = prime of QlP row r)
+    uint64_t *modup_mat = nullptr;
+    // rescale: [q_last^-1]_{q_j} Shoup pairs, j < Ql - 1
+    ulonglong2 *rescale_inv = nullptr;
+};
+
+struct Ctx {
+    int device = 0;
+    uint32_t N = 0, logN = 0;
+    uint32_t QP = 0, P = 0, Q = 0;
+    std::vector<uint64_t> moduli;  // Q primes then P primes
+    std::vector<uint64_t> roots;   // minimal primitive 2N-th roots
+    // device, all primes (rows of the QP table)
+    uint64_t *mod = nullptr;        // [QP]
+    ulonglong2 *ratio = nullptr;    // [QP] floor(2^128 / q) as (lo, hi)
+    ulonglong2 *tw = nullptr;       // [QP][N]
+    ulonglong2 *itw = nullptr;      // [QP][N]
+    ulonglong2 *ninv = nullptr;     // [QP] NTT-policy pairs of N^-1
+    // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
+    // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
+    ulonglong2 *moddown_scale = nullptr;
+    uint64_t *moddown_mat = nullptr;
+    ulonglong2 *pinv = nullptr;
+    // key construction: [P]_{q_i} Shoup pairs over all QP rows (0 on P rows)
+    ulonglong2 *pmodq = nullptr;
+    std::vector<Level> levels;  // index = chain index (0 unused)
+    std::vector<void *> allocations;
+
+    uint32_t size_Ql(uint32_t chain) const { return Q - (chain - 1); }
+    const Level &level(uint32_t chain) const {
+        require(chain >= 1 && chain <= Q, "chain index out of range");
+        return levels[chain];
+    }
+    // physical table row of position r of the QlP basis (Ql primes, then P primes)
+    uint32_t qlp_row(uint32_t Ql, uint32_t r) const { return r < Ql ? r : Q + (r - Ql); }
+    template <class T>
+    T *upload(const std::vector<T> &v);
+};
+
+Ctx *ctx_of(const pfa_context *c);
+
+// ---------------------------------------------------------------- launchers
+// NTT over M polys x L limbs; see NttBatch in ntt_kernels.h for the fields.
+struct NttLaunch {
+    const uint64_t *src;
+    uint64_t *dst;
+    uint64_t sstride, dstride;  // poly strides (elements); 0 -> L * N
+    uint32_t M, L;
+    uint32_t start = 0, split = 0xffffffffu, split_base = 0;
+    uint32_t ex_lo = 0, ex_step = 0, ex_len = 0, ex_cap = 0;
+    const ulonglong2 *scale = nullptr;
+};
+void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s);
+void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s);
+
+}  // namespace pfa

@@ -1,0 +1,184 @@
+// Device modular arithmetic for the CKKS hot path on gfx950.
+//
+// Two arithmetic policies share every NTT kernel; the policy is chosen per
+// limb from the limb's prime (uniform per workgroup, no divergence):
+//
+//   ArithF64 -- primes q < 2^50.  Residues live in registers as exact integers
+//               held in doubles.  A modular product costs six full-rate FP64
+//               VALU ops (two-product split + rounded quotient), against ~20
+//               32-bit integer ops for 64-bit Shoup on this ISA.
+//   ArithInt -- any prime q < 2^62.  Harvey-style lazy Shoup butterflies on
+//               uint64 ([0, 4q) between stages).
+//
+// Both policies are exact: every butterfly output is congruent mod q to the
+// textbook value, and outputs are brought to the canonical range [0, q)
+// before they leave a kernel.  Results are therefore bit-identical to the
+// reference's (src/ntt/ntt_1d.cu:17-292, include/butterfly.cuh), whose
+// kernels also emit canonical residues.
+//
+// Exactness bounds of ArithF64 (q < 2^50, twiddle w in [0, q), wq = fl(w/q)):
+//   mul(y, w) with |y| <= B q, B <= 8:
+//     qt = rint(fl(y*wq))          |qt - y w / q| <= 1 + B/16
+//     h = fl(y*w), l = fma(y,w,-h)  y w = h + l exactly, |l| <= 2^50
+//     r1 = fma(-qt, q, h)           exact: |h - qt q| < 2^52 is an integer
+//     r  = r1 + l                   exact, r == y w - qt q, |r| <= (1 + B/16) q
+//   A CT butterfly maps bound B to B + 1 + B/16: four stages from B = 1 reach
+//   5.66 < 8, so each four-stage round starts from a reduced value
+//   (reduce(): |x| <= 1 q after x - rint(x/q) q).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pfa {
+
+constexpr uint64_t kF64PrimeBound = 1ULL << 50;
+
+__device__ __forceinline__ uint64_t mulhi64(uint64_t a, uint64_t b) { return __umul64hi(a, b); }
+
+__device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
+
+// y * w mod q in [0, 2q) for any y < 2^64, w < q < 2^63, ws = floor(w 2^64 / q).
+__device__ __forceinline__ uint64_t shoup_lazy(uint64_t y, uint64_t w, uint64_t ws, uint64_t q) {
+    return y * w - mulhi64(y, ws) * q;
+}
+
+__device__ __forceinline__ uint64_t shoup(uint64_t y, uint64_t w, uint64_t ws, uint64_t q) {
+    return csub(shoup_lazy(y, w, ws, q), q);
+}
+
+__device__ __forceinline__ uint64_t add_mod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
+
+__device__ __forceinline__ uint64_t sub_mod(uint64_t a, uint64_t b, uint64_t q) { return a >= b ? a - b : a + q - b; }
+
+// 128-bit accumulator for sums of products.
+struct U128 {
+    uint64_t lo, hi;
+};
+
+__device__ __forceinline__ void mac(U128 &acc, uint64_t a, uint64_t b) {
+    uint64_t lo = a * b, hi = mulhi64(a, b);
+    acc.lo += lo;
+    acc.hi += hi + (acc.lo < lo ? 1 : 0);
+}
+
+// x mod q for any 128-bit x, with ratio = floor(2^128 / q) = (r1 : r0).
+// The quotient estimate drops only the low word of x0*r0 and the truncation of
+// ratio, so it is at most 2 below floor(x/q); two conditional subtractions
+// finish (requires 3q < 2^64).
+__device__ __forceinline__ uint64_t barrett128(U128 x, uint64_t q, uint64_t r0, uint64_t r1) {
+    uint64_t c = mulhi64(x.lo, r0);
+    uint64_t a_lo = x.lo * r1, a_hi = mulhi64(x.lo, r1);
+    uint64_t s = a_lo + c;
+    uint64_t t = a_hi + (s < c ? 1 : 0);
+    uint64_t b_lo = x.hi * r0, b_hi = mulhi64(x.hi, r0);
+    uint64_t s2 = s + b_lo;
+    uint64_t u = b_hi + (s2 < b_lo ? 1 : 0) + t;
+    uint64_t est = x.hi * r1 + u;
+    uint64_t r = x.lo - est * q;
+    r = csub(r, q);
+    return csub(r, q);
+}
+
+// ----------------------------------------------------------------------------
+// NTT arithmetic policies.  Twiddle table entries are 16-byte pairs whose
+// meaning depends on the prime's policy:
+//   ArithInt: (w, floor(w 2^64 / q))
+//   ArithF64: (bits of double(w), bits of fl(w / q))
+// ----------------------------------------------------------------------------
+
+struct ArithInt {
+    using T = uint64_t;
+    uint64_t q, q2;
+
+    __device__ __forceinline__ explicit ArithInt(uint64_t q_) : q(q_), q2(2 * q_) {}
+
+    __device__ __forceinline__ T load(uint64_t v) const { return v; }
+    // canonical residue from [0, 4q)
+    __device__ __forceinline__ uint64_t store(T v) const { return csub(csub(v, q2), q); }
+    // intermediate (between the two passes of one transform): keep lazy form
+    __device__ __forceinline__ uint64_t store_mid(T v) const { return v; }
+    __device__ __forceinline__ T load_mid(uint64_t v) const { return v; }
+    __device__ __forceinline__ void reduce(T &) const {}
+
+    // Cooley-Tukey: (x, y) -> (x + w y, x - w y); inputs and outputs in [0, 4q)
+    __device__ __forceinline__ void ct(T &x, T &y, ulonglong2 w) const {
+        uint64_t a = csub(x, q2);
+        uint64_t t = shoup_lazy(y, w.x, w.y, q);
+        x = a + t;
+        y = a - t + q2;
+    }
+    // Gentleman-Sande: (x, y) -> (x + y, (x - y) w); inputs and outputs in [0, 2q)
+    __device__ __forceinline__ void gs(T &x, T &y, ulonglong2 w) const {
+        uint64_t s = csub(x + y, q2);
+        uint64_t d = x - y + q2;
+        x = s;
+        y = shoup_lazy(d, w.x, w.y, q);
+    }
+    // last inverse stage: (x, y) -> ((x + y) n, (x - y) w) with n = N^-1 (a pair)
+    __device__ __forceinline__ void gs_last(T &x, T &y, ulonglong2 w, ulonglong2 n) const {
+        uint64_t s = x + y;
+        uint64_t d = x - y + q2;
+        x = shoup_lazy(s, n.x, n.y, q);
+        y = shoup_lazy(d, w.x, w.y, q);
+    }
+    __device__ __forceinline__ void mul(T &x, ulonglong2 c) const { x = shoup_lazy(x, c.x, c.y, q); }
+};
+
+struct ArithF64 {
+    using T = double;
+    double q, qinv;
+
+    __device__ __forceinline__ explicit ArithF64(uint64_t q_) : q((double)q_), qinv(1.0 / (double)q_) {}
+
+    static __device__ __forceinline__ double as_f(uint64_t b) { return __longlong_as_double((long long)b); }
+    static __device__ __forceinline__ uint64_t as_u(double d) { return (uint64_t)__double_as_longlong(d); }
+
+    __device__ __forceinline__ T load(uint64_t v) const {
+        // exact for v < 2^53
+        return __fma_rn((double)(uint32_t)(v >> 32), 4294967296.0, (double)(uint32_t)v);
+    }
+    __device__ __forceinline__ uint64_t store(T v) const {
+        double k = floor(v * qinv);
+        double r = __fma_rn(-k, q, v);
+        r = r < 0.0 ? r + q : r;
+        r = r >= q ? r - q : r;
+        uint32_t hi = (uint32_t)(r * (1.0 / 4294967296.0));
+        uint32_t lo = (uint32_t)__fma_rn(-(double)hi, 4294967296.0, r);
+        return ((uint64_t)hi << 32) | lo;
+    }
+    __device__ __forceinline__ uint64_t store_mid(T v) const {
+        reduce(v);
+        return as_u(v);
+    }
+    __device__ __forceinline__ T load_mid(uint64_t v) const { return as_f(v); }
+    __device__ __forceinline__ void reduce(T &x) const { x = __fma_rn(-rint(x * qinv), q, x); }
+
+    __device__ __forceinline__ T mulw(T y, double w, double wq) const {
+        double qt = rint(y * wq);
+        double h = y * w;
+        double l = __fma_rn(y, w, -h);
+        return __fma_rn(-qt, q, h) + l;
+    }
+    __device__ __forceinline__ void ct(T &x, T &y, ulonglong2 w) const {
+        double t = mulw(y, as_f(w.x), as_f(w.y));
+        y = x - t;
+        x = x + t;
+    }
+    __device__ __forceinline__ void gs(T &x, T &y, ulonglong2 w) const {
+        double s = x + y;
+        double d = x - y;
+        reduce(s);
+        x = s;
+        y = mulw(d, as_f(w.x), as_f(w.y));
+    }
+    __device__ __forceinline__ void gs_last(T &x, T &y, ulonglong2 w, ulonglong2 n) const {
+        double s = x + y;
+        double d = x - y;
+        x = mulw(s, as_f(n.x), as_f(n.y));
+        y = mulw(d, as_f(w.x), as_f(w.y));
+    }
+    __device__ __forceinline__ void mul(T &x, ulonglong2 c) const { x = mulw(x, as_f(c.x), as_f(c.y)); }
+};
+
+}  // namespace pfa

@@ -1,0 +1,123 @@
+// NTT launchers and the raw-limb NTT entry points of the C ABI.
+#include "internal.h"
+#include "ntt_kernels.h"
+
+namespace pfa {
+
+namespace {
+
+NttBatch make_batch(const Ctx &c, const NttLaunch &a) {
+    NttBatch b;
+    b.src = a.src;
+    b.dst = a.dst;
+    b.sstride = a.sstride ? a.sstride : (uint64_t)a.L * c.N;
+    b.dstride = a.dstride ? a.dstride : (uint64_t)a.L * c.N;
+    b.M = a.M;
+    b.L = a.L;
+    b.map = LimbMap{a.start, a.split, a.split_base};
+    b.ex_lo = a.ex_lo;
+    b.ex_step = a.ex_step;
+    b.ex_len = a.ex_len;
+    b.ex_cap = a.ex_cap;
+    b.scale = a.scale;
+    return b;
+}
+
+NttTables tables(const Ctx &c) { return NttTables{c.mod, c.tw, c.itw, c.ninv}; }
+
+template <int S1, int S2>
+void fwd(const NttBatch &b, const NttTables &t, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    const uint32_t ml = b.M * b.L;
+    hipLaunchKernelGGL((ntt_fwd_cols<S1, S2>), dim3(ml * G::COL_TILES), dim3(G::COL_THREADS), 0, s, b, t);
+    NttBatch b2 = b;
+    b2.src = b.dst;
+    b2.sstride = b.dstride;
+    hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(ml * G::ROW_TILES), dim3(G::ROW_THREADS), 0, s, b2, t);
+}
+
+template <int S1, int S2>
+void inv(const NttBatch &b, const NttTables &t, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    const uint32_t ml = b.M * b.L;
+    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(ml * G::ROW_TILES), dim3(G::ROW_THREADS), 0, s, b, t);
+    NttBatch b2 = b;
+    b2.src = b.dst;
+    b2.sstride = b.dstride;
+    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(ml * G::COL_TILES), dim3(G::COL_THREADS), 0, s, b2, t);
+}
+
+void check_launch(const Ctx &c, const NttLaunch &a) {
+    require(a.src && a.dst, "null data pointer");
+    require(a.M >= 1 && a.L >= 1, "empty batch");
+    if (a.M > 1) {
+        require(a.sstride == 0 || a.sstride >= (uint64_t)a.L * c.N, "poly stride smaller than one poly");
+        require(a.dstride == 0 || a.dstride >= (uint64_t)a.L * c.N, "poly stride smaller than one poly");
+    }
+    require((uint64_t)a.M * a.L * (c.N / 16) < (1ULL << 31), "batch too large for one launch");
+    // every limb must map to a table row inside the context
+    const uint32_t last = a.L - 1;
+    const uint32_t rlast = last < a.split ? a.start + last : a.split_base + (last - a.split);
+    const uint32_t rfirst = 0 < a.split ? a.start : a.split_base;
+    require(rfirst < c.QP && rlast < c.QP, "limb range exceeds the context's primes");
+    if (a.split < a.L) require(a.start + a.split <= c.QP, "limb range exceeds the context's primes");
+}
+
+}  // namespace
+
+#define PFA_NTT_DISPATCH(FN)                                                 \
+    switch (c.logN) {                                                        \
+    case 10: FN<5, 5>(b, t, s); break;                                       \
+    case 11: FN<5, 6>(b, t, s); break;                                       \
+    case 12: FN<6, 6>(b, t, s); break;                                       \
+    case 13: FN<6, 7>(b, t, s); break;                                       \
+    case 14: FN<7, 7>(b, t, s); break;                                       \
+    case 15: FN<7, 8>(b, t, s); break;                                       \
+    case 16: FN<8, 8>(b, t, s); break;                                       \
+    case 17: FN<8, 9>(b, t, s); break;                                       \
+    default: fail(PFA_ERR_INVALID_ARGUMENT, "unsupported poly_modulus_degree"); \
+    }
+
+void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+    check_launch(c, a);
+    const NttBatch b = make_batch(c, a);
+    const NttTables t = tables(c);
+    PFA_NTT_DISPATCH(fwd);
+    PFA_HIP(hipGetLastError());
+}
+
+void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+    check_launch(c, a);
+    const NttBatch b = make_batch(c, a);
+    const NttTables t = tables(c);
+    PFA_NTT_DISPATCH(inv);
+    PFA_HIP(hipGetLastError());
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" {
+
+int pfa_ntt_forward(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L, size_t start, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(start + L <= c.QP, "limb range exceeds the context's primes");
+        NttLaunch a{inout, inout, 0, 0, (uint32_t)M, (uint32_t)L};
+        a.start = (uint32_t)start;
+        ntt_forward(c, a, as_stream(stream));
+    });
+}
+
+int pfa_ntt_inverse(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L, size_t start, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(start + L <= c.QP, "limb range exceeds the context's primes");
+        NttLaunch a{inout, inout, 0, 0, (uint32_t)M, (uint32_t)L};
+        a.start = (uint32_t)start;
+        ntt_inverse(c, a, as_stream(stream));
+    });
+}
+
+}  // extern "C"

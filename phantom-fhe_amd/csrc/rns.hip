@@ -1,0 +1,576 @@
+// RNS / key-switching / evaluator kernels and their C-ABI entry points:
+// ModUp, the key-switch inner product, ModDown, key switching, tensor,
+// relinearization, rescale, the Galois automorphism, hoisted rotations, key
+// construction and the elementwise poly ops.
+//
+// Every kernel emits canonical residues; each formula is the reference's
+// (file:line given per kernel), so outputs are bit-identical to it.
+#include <algorithm>
+
+#include "internal.h"
+#include "modarith.h"
+
+namespace pfa {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kMaxAlpha = 16;  // special primes per digit supported by the BConv kernels
+
+__device__ __forceinline__ uint64_t mulmod_b(uint64_t a, uint64_t b, uint64_t q, ulonglong2 r) {
+    U128 p{a * b, mulhi64(a, b)};
+    return barrett128(p, q, r.x, r.y);
+}
+
+__device__ __forceinline__ uint32_t brv(uint32_t x, uint32_t bits) { return __builtin_bitreverse32(x) >> (32 - bits); }
+
+// Galois permutation of NTT slots (include/galois.cuh:98-113):
+//   pi(i) = brv(((elt * brv(N + i, logN + 1)) >> 1) mod N, logN),
+// with brv(N + i, logN + 1) = 2 brv(i, logN) + 1.
+__device__ __forceinline__ uint32_t galois_perm(uint32_t elt, uint32_t i, uint32_t logN) {
+    const uint64_t rev = 2ull * brv(i, logN) + 1;
+    const uint32_t raw = (uint32_t)((elt * rev) >> 1) & ((1u << logN) - 1);
+    return brv(raw, logN);
+}
+
+// ------------------------------------------------------------ elementwise
+enum BinOp { kAdd, kSub, kMul, kNeg };
+
+__global__ void __launch_bounds__(kThreads)
+k_poly_binop(int op, const uint64_t *a, const uint64_t *b, uint64_t *out, const uint64_t *mod,
+             const ulonglong2 *ratio, uint32_t start, uint32_t N) {
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[start + l];
+    const size_t i = (size_t)l * N + n;
+    const uint64_t x = a[i];
+    uint64_t r;
+    switch (op) {
+    case kAdd: r = add_mod(x, b[i], q); break;
+    case kSub: r = sub_mod(x, b[i], q); break;
+    case kMul: r = mulmod_b(x, b[i], q, ratio[start + l]); break;
+    default: r = x ? q - x : 0; break;
+    }
+    out[i] = r;
+}
+
+__global__ void __launch_bounds__(kThreads)
+k_from_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t start, uint32_t N) {
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[start + l];
+    const int64_t v = in[n];
+    uint64_t r;
+    if (v >= 0) {
+        r = (uint64_t)v % q;
+    } else {
+        r = (uint64_t)(-(v + 1)) % q;  // |v| - 1, avoids overflow at INT64_MIN
+        r = q - 1 - r;                 // q - (|v| mod q), in [0, q)
+    }
+    out[(size_t)l * N + n] = r;
+}
+
+// tensor_prod_2x2_rns_poly (src/polymath.cu:463-498):
+//   d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1  (mod q_l)
+__global__ void __launch_bounds__(kThreads)
+k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint64_t *d2, const uint64_t *mod,
+         const ulonglong2 *ratio, uint32_t Ql, uint32_t N) {
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[l];
+    const ulonglong2 r = ratio[l];
+    const size_t i = (size_t)l * N + n, LN = (size_t)Ql * N;
+    const uint64_t a0 = a[i], a1 = a[LN + i], b0 = b[i], b1 = b[LN + i];
+    U128 m{0, 0};
+    mac(m, a0, b1);
+    mac(m, a1, b0);
+    d0[i] = mulmod_b(a0, b0, q, r);
+    d1[i] = barrett128(m, q, r.x, r.y);
+    d2[i] = mulmod_b(a1, b1, q, r);
+}
+
+// ModUp base conversion per digit (src/rns_bconv.cu:455-485, :522-528, :530-628):
+// slab b, position r of the QlP basis:
+//   own limbs (r in digit b): copy of c2 (NTT form)
+//   others: y = sum_{i in digit b} t_i [Q_b / q_i]_{p_r}  mod p_r (uncorrected)
+// where t = INTT(c2) * [(Q_b / q_i)^-1]_{q_i} (coefficient form, canonical).
+__global__ void __launch_bounds__(kThreads)
+k_modup_bconv(const uint64_t *t, const uint64_t *c2, uint64_t *out, const uint64_t *mat, const uint64_t *mod,
+              const ulonglong2 *ratio, uint32_t Ql, uint32_t alpha, uint32_t Q, uint32_t N) {
+    const uint32_t b = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t QlP = Ql + alpha, st = b * alpha, sz = min(alpha, Ql - st);
+    uint64_t tv[kMaxAlpha];
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxAlpha; i++)
+        if (i < sz) tv[i] = t[(size_t)(st + i) * N + n];
+    uint64_t *slab = out + (size_t)b * QlP * N;
+    const uint64_t *m = mat + (size_t)b * alpha * QlP;
+    for (uint32_t r = 0; r < QlP; r++) {
+        const size_t o = (size_t)r * N + n;
+        if (r >= st && r < st + sz) {
+            slab[o] = c2[o];
+            continue;
+        }
+        const uint32_t row = r < Ql ? r : Q + (r - Ql);
+        U128 acc{0, 0};
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxAlpha; i++)
+            if (i < sz) mac(acc, tv[i], m[(size_t)i * QlP + r]);
+        slab[o] = barrett128(acc, mod[row], ratio[row].x, ratio[row].y);
+    }
+}
+
+// key_switch_inner_prod_c2_and_evk (src/eval_key_switch.cu:175-230):
+//   cx[k][r] = sum_{b < beta} t[b][r] * key[b][k][row(r)]  mod q_row(r)
+// accumulated in 128 bits and reduced once.  With elt != 0 the slabs are read
+// through the Galois permutation (hoisted rotations, src/evaluate.cu:2039-2049).
+__global__ void __launch_bounds__(kThreads)
+k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t *mod, const ulonglong2 *ratio,
+           uint32_t Ql, uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N, uint32_t elt,
+           uint32_t logN) {
+    const uint32_t r = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t row = r < Ql ? r : Q + (r - Ql);
+    const uint32_t sn = elt ? galois_perm(elt, n, logN) : n;
+    U128 a0{0, 0}, a1{0, 0};
+    for (uint32_t b = 0; b < beta; b++) {
+        const uint64_t x = t[((size_t)b * QlP + r) * N + sn];
+        const uint64_t *kb = key + (size_t)b * 2 * QP * N + (size_t)row * N + n;
+        mac(a0, x, kb[0]);
+        mac(a1, x, kb[(size_t)QP * N]);
+    }
+    const uint64_t q = mod[row];
+    const ulonglong2 rt = ratio[row];
+    cx[(size_t)r * N + n] = barrett128(a0, q, rt.x, rt.y);
+    cx[((size_t)QlP + r) * N + n] = barrett128(a1, q, rt.x, rt.y);
+}
+
+// ModDown base conversion P -> Ql (bConv_BEHZ, src/rns_bconv.cu:212-229):
+//   d[m][i] = sum_j xP[m][j] [P / p_j]_{q_i}  mod q_i,  xP already scaled by [(P/p_j)^-1]_{p_j}
+__global__ void __launch_bounds__(kThreads)
+k_moddown_bconv(const uint64_t *xP, uint64_t *d, const uint64_t *mat, const uint64_t *mod, const ulonglong2 *ratio,
+                uint32_t Ql, uint32_t alpha, uint32_t Q, uint32_t N) {
+    const uint32_t m = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    uint64_t xv[kMaxAlpha];
+#pragma unroll
+    for (uint32_t j = 0; j < kMaxAlpha; j++)
+        if (j < alpha) xv[j] = xP[((size_t)m * alpha + j) * N + n];
+    uint64_t *dm = d + (size_t)m * Ql * N;
+    for (uint32_t i = 0; i < Ql; i++) {
+        U128 acc{0, 0};
+#pragma unroll
+        for (uint32_t j = 0; j < kMaxAlpha; j++)
+            if (j < alpha) mac(acc, xv[j], mat[(size_t)j * Q + i]);
+        dm[(size_t)i * N + n] = barrett128(acc, mod[i], ratio[i].x, ratio[i].y);
+    }
+}
+
+struct Bases {
+    const uint64_t *p[2];
+};
+
+// FuseModDownEpilogue (include/ntt_radix8_tmpl.cuh:216-233) plus add_to_ct_kernel
+// (src/rns_bconv.cu:763-769): out[m][i] = base[m][i] + (cx[m][i] - d[m][i]) P^-1 mod q_i
+__global__ void __launch_bounds__(kThreads)
+k_moddown_final(const uint64_t *cx, const uint64_t *d, uint64_t *out, Bases base, const uint64_t *mod,
+                const ulonglong2 *pinv, uint32_t Ql, uint32_t QlP, uint32_t N) {
+    const uint32_t i = blockIdx.y, m = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[i];
+    const ulonglong2 pi = pinv[i];
+    const size_t o = ((size_t)m * Ql + i) * N + n;
+    uint64_t v = shoup(sub_mod(cx[((size_t)m * QlP + i) * N + n], d[o], q), pi.x, pi.y, q);
+    const uint64_t *bp = base.p[m];
+    if (bp) v = add_mod(v, bp[(size_t)i * N + n], q);
+    out[o] = v;
+}
+
+// divide_and_round_reduce_q_last_kernel (src/rns.cu:1128-1139): t[s][j] = c_last[s] mod q_j
+__global__ void __launch_bounds__(kThreads)
+k_rescale_reduce(const uint64_t *last, uint64_t *t, const uint64_t *mod, const ulonglong2 *ratio, uint32_t L1,
+                 uint32_t N) {
+    const uint32_t j = blockIdx.y, s = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    U128 v{last[(size_t)s * N + n], 0};
+    t[((size_t)s * L1 + j) * N + n] = barrett128(v, mod[j], ratio[j].x, ratio[j].y);
+}
+
+// divide_and_round_ntt_inv_scalar_kernel (src/rns.cu:1141-1158):
+//   out[s][j] = (c[s][j] - t[s][j]) q_last^-1 mod q_j   (floor division, no rounding term)
+__global__ void __launch_bounds__(kThreads)
+k_rescale_final(const uint64_t *in, const uint64_t *t, uint64_t *out, const uint64_t *mod, const ulonglong2 *inv,
+                uint32_t L, uint32_t N) {
+    const uint32_t j = blockIdx.y, s = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[j];
+    const size_t o = ((size_t)s * (L - 1) + j) * N + n;
+    out[o] = shoup(sub_mod(in[((size_t)s * L + j) * N + n], t[o], q), inv[j].x, inv[j].y, q);
+}
+
+// apply_galois_ntt_permutation (src/galois.cu:11-18): dst[l][i] = src[l][pi(i)]
+__global__ void __launch_bounds__(kThreads)
+k_galois(const uint64_t *src, uint64_t *dst, uint32_t elt, uint32_t N, uint32_t logN) {
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    dst[(size_t)l * N + n] = src[(size_t)l * N + galois_perm(elt, n, logN)];
+}
+
+// generate_one_kswitch_key (src/secretkey.cu:354-398) with
+// multiply_temp_mod_and_add_rns_poly (src/polymath.cu:318-336):
+//   key[d][0][j] = -(a_d s + e_d)_j + [P]_{q_j} new_key_j * [j in digit d],  key[d][1][j] = a_d
+__global__ void __launch_bounds__(kThreads)
+k_kswitch_key(const uint64_t *new_key, const uint64_t *s, const uint64_t *a, const uint64_t *e, uint64_t *key,
+              const uint64_t *mod, const ulonglong2 *ratio, const ulonglong2 *pmodq, uint32_t QP, uint32_t alpha,
+              uint32_t N) {
+    const uint32_t j = blockIdx.y, d = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t q = mod[j];
+    const size_t ij = (size_t)j * N + n, idj = ((size_t)d * QP + j) * N + n;
+    const uint64_t av = a[idj];
+    U128 acc{0, 0};
+    mac(acc, av, s[ij]);
+    const uint64_t ev = e[idj];
+    acc.lo += ev;
+    acc.hi += acc.lo < ev ? 1 : 0;
+    const uint64_t red = barrett128(acc, q, ratio[j].x, ratio[j].y);
+    uint64_t v = red ? q - red : 0;
+    if (j >= d * alpha && j < (d + 1) * alpha) v = add_mod(v, shoup(new_key[ij], pmodq[j].x, pmodq[j].y, q), q);
+    key[((size_t)d * 2 * QP + j) * N + n] = v;
+    key[(((size_t)d * 2 + 1) * QP + j) * N + n] = av;
+}
+
+// ------------------------------------------------------------ host helpers
+// Stream-ordered temporary (the counterpart of cuda_auto_ptr).
+struct Tmp {
+    uint64_t *p = nullptr;
+    hipStream_t s;
+    Tmp(size_t elems, hipStream_t st) : s(st) {
+        PFA_HIP(hipMallocAsync((void **)&p, std::max<size_t>(elems, 1) * sizeof(uint64_t), s));
+    }
+    ~Tmp() {
+        if (p) (void)hipFreeAsync(p, s);
+    }
+    Tmp(const Tmp &) = delete;
+    Tmp &operator=(const Tmp &) = delete;
+};
+
+inline dim3 grid(const Ctx &c, uint32_t y, uint32_t z = 1) { return dim3(c.N / kThreads, y, z); }
+
+void check_chain(const Ctx &c, size_t chain) {
+    require(chain >= 1 && chain <= c.Q, "chain index out of range (key level 0 is not a data level)");
+}
+
+void check_alpha(const Ctx &c) { require(c.P <= kMaxAlpha, "at most 16 special primes are supported"); }
+
+}  // namespace
+
+// ------------------------------------------------------------ operations
+// Each takes device pointers and enqueues work on stream s.
+
+void op_modup(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, hipStream_t s) {
+    check_chain(c, chain);
+    check_alpha(c);
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    Tmp t((size_t)Ql * c.N, s);
+    NttLaunch inv{c2, t.p, 0, 0, 1, Ql};
+    inv.scale = lv.modup_scale;
+    ntt_inverse(c, inv, s);
+    hipLaunchKernelGGL(k_modup_bconv, grid(c, lv.beta), dim3(kThreads), 0, s, t.p, c2, out, lv.modup_mat, c.mod,
+                       c.ratio, Ql, alpha, c.Q, c.N);
+    PFA_HIP(hipGetLastError());
+    // NTT every slab except its own digit's limbs (ntt_modup.cu:670-717)
+    NttLaunch fw{out, out, (uint64_t)QlP * c.N, (uint64_t)QlP * c.N, lv.beta, QlP};
+    fw.start = 0;
+    fw.split = Ql;
+    fw.split_base = c.Q;
+    fw.ex_lo = 0;
+    fw.ex_step = alpha;
+    fw.ex_len = alpha;
+    fw.ex_cap = Ql;
+    ntt_forward(c, fw, s);
+}
+
+void op_inner(const Ctx &c, uint32_t chain, const uint64_t *t, const uint64_t *key, size_t dnum, uint64_t *cx,
+              uint32_t elt, hipStream_t s) {
+    check_chain(c, chain);
+    const Level &lv = c.level(chain);
+    require(key != nullptr, "null key");
+    require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
+    const uint32_t QlP = lv.Ql + c.P;
+    hipLaunchKernelGGL(k_ks_inner, grid(c, QlP), dim3(kThreads), 0, s, t, key, cx, c.mod, c.ratio, lv.Ql, QlP, c.Q,
+                       c.QP, lv.beta, c.N, elt, c.logN);
+    PFA_HIP(hipGetLastError());
+}
+
+// cx [M][QlP][N] -> out [M][Ql][N] (+ base[m] when given), M <= 2
+void op_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out, Bases base,
+                hipStream_t s) {
+    check_chain(c, chain);
+    check_alpha(c);
+    const uint32_t Ql = c.size_Ql(chain), alpha = c.P, QlP = Ql + alpha;
+    Tmp xP((size_t)M * alpha * c.N, s);
+    NttLaunch inv{cx + (size_t)Ql * c.N, xP.p, (uint64_t)QlP * c.N, (uint64_t)alpha * c.N, M, alpha};
+    inv.start = c.Q;
+    inv.scale = c.moddown_scale;
+    ntt_inverse(c, inv, s);
+    Tmp d((size_t)M * Ql * c.N, s);
+    hipLaunchKernelGGL(k_moddown_bconv, grid(c, M), dim3(kThreads), 0, s, xP.p, d.p, c.moddown_mat, c.mod, c.ratio,
+                       Ql, alpha, c.Q, c.N);
+    PFA_HIP(hipGetLastError());
+    NttLaunch fw{d.p, d.p, 0, 0, M, Ql};
+    ntt_forward(c, fw, s);
+    hipLaunchKernelGGL(k_moddown_final, grid(c, Ql, M), dim3(kThreads), 0, s, cx, d.p, out, base, c.mod, c.pinv,
+                       Ql, QlP, c.N);
+    PFA_HIP(hipGetLastError());
+}
+
+// out[k] = base_k + KS(c2)_k for k = 0, 1 (out [2][Ql][N]; bases may alias out or be null)
+void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum, uint64_t *out,
+                  Bases base, hipStream_t s) {
+    check_chain(c, chain);
+    const Level &lv = c.level(chain);
+    const uint32_t QlP = lv.Ql + c.P;
+    require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
+    Tmp mu((size_t)lv.beta * QlP * c.N, s);
+    op_modup(c, chain, c2, mu.p, s);
+    Tmp cx((size_t)2 * QlP * c.N, s);
+    op_inner(c, chain, mu.p, key, dnum, cx.p, 0, s);
+    op_moddown(c, chain, cx.p, 2, out, base, s);
+}
+
+void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1,
+               uint64_t *d2, hipStream_t s) {
+    check_chain(c, chain);
+    const uint32_t Ql = c.size_Ql(chain);
+    hipLaunchKernelGGL(k_tensor, grid(c, Ql), dim3(kThreads), 0, s, a, b, d0, d1, d2, c.mod, c.ratio, Ql, c.N);
+    PFA_HIP(hipGetLastError());
+}
+
+void op_galois(const Ctx &c, uint32_t elt, const uint64_t *src, uint64_t *dst, uint32_t L, hipStream_t s) {
+    require((elt & 1) && elt < 2 * c.N, "Galois element must be odd and below 2N");
+    require(src != dst, "apply_galois_ntt cannot run in place");
+    hipLaunchKernelGGL(k_galois, grid(c, L), dim3(kThreads), 0, s, src, dst, elt, c.N, c.logN);
+    PFA_HIP(hipGetLastError());
+}
+
+void op_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s) {
+    check_chain(c, chain);
+    const Level &lv = c.level(chain);
+    const uint32_t L = lv.Ql;
+    require(L >= 2, "cannot rescale at the last level");
+    require(size >= 1 && size <= 65535, "bad ciphertext size");
+    Tmp last((size_t)size * c.N, s);
+    NttLaunch inv{in + (size_t)(L - 1) * c.N, last.p, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
+    inv.start = L - 1;
+    ntt_inverse(c, inv, s);
+    Tmp t((size_t)size * (L - 1) * c.N, s);
+    hipLaunchKernelGGL(k_rescale_reduce, grid(c, L - 1, size), dim3(kThreads), 0, s, last.p, t.p, c.mod, c.ratio,
+                       L - 1, c.N);
+    PFA_HIP(hipGetLastError());
+    NttLaunch fw{t.p, t.p, 0, 0, size, L - 1};
+    ntt_forward(c, fw, s);
+    hipLaunchKernelGGL(k_rescale_final, grid(c, L - 1, size), dim3(kThreads), 0, s, in, t.p, out, c.mod,
+                       lv.rescale_inv, L, c.N);
+    PFA_HIP(hipGetLastError());
+}
+
+}  // namespace pfa
+
+using namespace pfa;
+
+extern "C" {
+
+int pfa_modup(const pfa_context *ctx, size_t chain_index, const uint64_t *c2, uint64_t *t_mod_up, void *stream) {
+    return guarded([&] {
+        require(c2 && t_mod_up, "null argument");
+        op_modup(*ctx_of(ctx), (uint32_t)chain_index, c2, t_mod_up, as_stream(stream));
+    });
+}
+
+int pfa_ks_inner_prod(const pfa_context *ctx, size_t chain_index, const uint64_t *t_mod_up, const uint64_t *key,
+                      size_t key_dnum, uint64_t *cx, void *stream) {
+    return guarded([&] {
+        require(t_mod_up && cx, "null argument");
+        op_inner(*ctx_of(ctx), (uint32_t)chain_index, t_mod_up, key, key_dnum, cx, 0, as_stream(stream));
+    });
+}
+
+int pfa_moddown(const pfa_context *ctx, size_t chain_index, const uint64_t *cx_k, uint64_t *out, void *stream) {
+    return guarded([&] {
+        require(cx_k && out, "null argument");
+        op_moddown(*ctx_of(ctx), (uint32_t)chain_index, cx_k, 1, out, Bases{{nullptr, nullptr}}, as_stream(stream));
+    });
+}
+
+int pfa_keyswitch(const pfa_context *ctx, size_t chain_index, uint64_t *ct, const uint64_t *c2, const uint64_t *key,
+                  size_t key_dnum, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && c2, "null argument");
+        check_chain(c, chain_index);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        op_keyswitch(c, (uint32_t)chain_index, c2, key, key_dnum, ct, Bases{{ct, ct + LN}}, as_stream(stream));
+    });
+}
+
+int pfa_tensor(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b, uint64_t *out,
+               void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && b && out, "null argument");
+        check_chain(c, chain_index);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, out + 2 * LN, as_stream(stream));
+    });
+}
+
+int pfa_multiply_and_relin(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
+                           const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && b && out && rlk, "null argument");
+        check_chain(c, chain_index);
+        const hipStream_t s = as_stream(stream);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        Tmp c2(LN, s);
+        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2.p, s);
+        op_keyswitch(c, (uint32_t)chain_index, c2.p, rlk, key_dnum, out, Bases{{out, out + LN}}, s);
+    });
+}
+
+int pfa_relinearize(const pfa_context *ctx, size_t chain_index, const uint64_t *ct3, const uint64_t *rlk,
+                    size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct3 && out && rlk, "null argument");
+        check_chain(c, chain_index);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        op_keyswitch(c, (uint32_t)chain_index, ct3 + 2 * LN, rlk, key_dnum, out, Bases{{ct3, ct3 + LN}},
+                     as_stream(stream));
+    });
+}
+
+int pfa_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *in, size_t size, uint64_t *out,
+                void *stream) {
+    return guarded([&] {
+        require(in && out && in != out, "rescale needs distinct input and output buffers");
+        op_rescale(*ctx_of(ctx), (uint32_t)chain_index, in, (uint32_t)size, out, as_stream(stream));
+    });
+}
+
+int pfa_galois_elt_from_step(int step, uint64_t poly_degree, uint32_t *elt) {
+    return guarded([&] {
+        require(elt != nullptr, "null argument");
+        require(poly_degree >= 2 && (poly_degree & (poly_degree - 1)) == 0 && poly_degree <= (1u << 30),
+                "poly_modulus_degree must be a power of two");
+        // get_elt_from_step (include/galois.cuh:16-49)
+        const uint64_t n = poly_degree, m = 2 * n;
+        if (step == 0) {
+            *elt = (uint32_t)(m - 1);
+            return;
+        }
+        const uint64_t pos = step < 0 ? (uint64_t)(-(int64_t)step) : (uint64_t)step;
+        require(pos < n / 2, "step count too large");
+        uint64_t k = step < 0 ? n / 2 - pos : pos;
+        uint64_t g = 1;
+        while (k--) g = (g * 5) & (m - 1);
+        *elt = (uint32_t)g;
+    });
+}
+
+int pfa_apply_galois_ntt(const pfa_context *ctx, uint32_t elt, const uint64_t *src, uint64_t *dst, size_t L,
+                         void *stream) {
+    return guarded([&] {
+        require(src && dst && L >= 1, "null argument");
+        op_galois(*ctx_of(ctx), elt, src, dst, (uint32_t)L, as_stream(stream));
+    });
+}
+
+int pfa_apply_galois(const pfa_context *ctx, size_t chain_index, uint64_t *ct, uint32_t elt, const uint64_t *key,
+                     size_t key_dnum, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && key, "null argument");
+        check_chain(c, chain_index);
+        const hipStream_t s = as_stream(stream);
+        const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
+        const size_t LN = (size_t)Ql * c.N;
+        Tmp t(2 * LN, s);
+        op_galois(c, elt, ct, t.p, Ql, s);
+        op_galois(c, elt, ct + LN, t.p + LN, Ql, s);
+        // c0' = sigma(c0) + KS0(sigma(c1)), c1' = KS1(sigma(c1))  (src/evaluate.cu:1607-1656)
+        op_keyswitch(c, (uint32_t)chain_index, t.p + LN, key, key_dnum, ct, Bases{{t.p, nullptr}}, s);
+    });
+}
+
+int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts,
+                        size_t n, const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && out && (n == 0 || (elts && keys)), "null argument");
+        check_chain(c, chain_index);
+        if (n == 0) return;
+        const hipStream_t s = as_stream(stream);
+        const uint32_t chain = (uint32_t)chain_index;
+        const Level &lv = c.level(chain);
+        const uint32_t Ql = lv.Ql, QlP = Ql + c.P;
+        const size_t LN = (size_t)Ql * c.N;
+        for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
+        Tmp mu((size_t)lv.beta * QlP * c.N, s);
+        op_modup(c, chain, ct + LN, mu.p, s);
+        Tmp cx((size_t)2 * QlP * c.N, s);
+        for (size_t e = 0; e < n; ++e) {
+            uint64_t *o = out + e * 2 * LN;
+            op_galois(c, elts[e], ct, o, Ql, s);
+            op_inner(c, chain, mu.p, keys[e], key_dnum, cx.p, elts[e], s);
+            op_moddown(c, chain, cx.p, 2, o, Bases{{o, nullptr}}, s);
+        }
+    });
+}
+
+int pfa_kswitch_key(const pfa_context *ctx, const uint64_t *new_key, const uint64_t *s_key, const uint64_t *a,
+                    const uint64_t *e, uint64_t *key, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(new_key && s_key && a && e && key, "null argument");
+        const uint32_t dnum = c.Q / c.P;
+        require(dnum >= 1, "need at least one key digit");
+        hipLaunchKernelGGL(k_kswitch_key, grid(c, c.QP, dnum), dim3(kThreads), 0, as_stream(stream), new_key, s_key,
+                           a, e, key, c.mod, c.ratio, c.pmodq, c.QP, c.P, c.N);
+        PFA_HIP(hipGetLastError());
+    });
+}
+
+static int binop(const pfa_context *ctx, int op, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L,
+                 size_t start, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && out && (op == kNeg || b), "null argument");
+        require(L >= 1 && start + L <= c.QP, "limb range exceeds the context's primes");
+        hipLaunchKernelGGL(k_poly_binop, grid(c, (uint32_t)L), dim3(kThreads), 0, as_stream(stream), op, a,
+                           op == kNeg ? a : b, out, c.mod, c.ratio, (uint32_t)start, c.N);
+        PFA_HIP(hipGetLastError());
+    });
+}
+
+int pfa_poly_add(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream) {
+    return binop(ctx, kAdd, a, b, out, L, start, stream);
+}
+int pfa_poly_sub(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream) {
+    return binop(ctx, kSub, a, b, out, L, start, stream);
+}
+int pfa_poly_mul(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
+                 void *stream) {
+    return binop(ctx, kMul, a, b, out, L, start, stream);
+}
+int pfa_poly_negate(const pfa_context *ctx, const uint64_t *a, uint64_t *out, size_t L, size_t start, void *stream) {
+    return binop(ctx, kNeg, a, nullptr, out, L, start, stream);
+}
+
+int pfa_poly_from_signed(const pfa_context *ctx, const int64_t *in, uint64_t *out, size_t L, size_t start,
+                         void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(in && out, "null argument");
+        require(L >= 1 && start + L <= c.QP, "limb range exceeds the context's primes");
+        hipLaunchKernelGGL(k_from_signed, grid(c, (uint32_t)L), dim3(kThreads), 0, as_stream(stream), in, out, c.mod,
+                           (uint32_t)start, c.N);
+        PFA_HIP(hipGetLastError());
+    });
+}
+
+}  // extern "C"

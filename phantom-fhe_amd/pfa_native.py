@@ -1,0 +1,245 @@
+"""ctypes binding of libphantom_amd.so (the C ABI declared in include/phantom_amd.h).
+
+This is the only way Python reaches the HIP kernels.  It fails loudly when the
+library is missing: there is no CPU fallback anywhere in the product.
+
+Device buffers are torch tensors of dtype torch.uint64 on a ROCm device; only
+their data pointers cross the boundary.  Streams default to torch's current
+stream on the tensor's device.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libphantom_amd.so")
+
+PFA_OK = 0
+PFA_ERR_INVALID_ARGUMENT = 1
+PFA_ERR_LOGIC = 2
+PFA_ERR_RUNTIME = 3
+
+_vp, _sz, _u64, _u32, _i32 = C.c_void_p, C.c_size_t, C.c_uint64, C.c_uint32, C.c_int
+_u64p = C.POINTER(C.c_uint64)
+
+# name -> (restype, argtypes); mirrors include/phantom_amd.h one to one
+SIGNATURES = {
+    "pfa_last_error": (C.c_char_p, []),
+    "pfa_abi_version": (_i32, []),
+    "pfa_create_coeff_modulus": (_i32, [_u64, C.POINTER(C.c_int), _sz, _u64p]),
+    "pfa_context_create": (_i32, [_u64, _u64p, _sz, _sz, _i32, C.POINTER(_vp)]),
+    "pfa_context_destroy": (None, [_vp]),
+    "pfa_context_roots": (_i32, [_vp, _u64p]),
+    "pfa_ntt_forward": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp]),
+    "pfa_ntt_inverse": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp]),
+    "pfa_modup": (_i32, [_vp, _sz, _vp, _vp, _vp]),
+    "pfa_ks_inner_prod": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_moddown": (_i32, [_vp, _sz, _vp, _vp, _vp]),
+    "pfa_keyswitch": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp]),
+    "pfa_tensor": (_i32, [_vp, _sz, _vp, _vp, _vp, _vp]),
+    "pfa_multiply_and_relin": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_relinearize": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_rescale": (_i32, [_vp, _sz, _vp, _sz, _vp, _vp]),
+    "pfa_galois_elt_from_step": (_i32, [_i32, _u64, C.POINTER(C.c_uint32)]),
+    "pfa_apply_galois_ntt": (_i32, [_vp, _u32, _vp, _vp, _sz, _vp]),
+    "pfa_apply_galois": (_i32, [_vp, _sz, _vp, _u32, _vp, _sz, _vp]),
+    "pfa_hoist_rotations": (_i32, [_vp, _sz, _vp, C.POINTER(C.c_uint32), _sz, C.POINTER(_vp), _sz, _vp, _vp]),
+    "pfa_kswitch_key": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pfa_poly_add": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_poly_sub": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_poly_mul": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_poly_negate": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_poly_from_signed": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
+}
+
+
+class PhantomError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """Load libphantom_amd.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"libphantom_amd.so not found at {LIB_PATH}: build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    """Raise the Python counterpart of the reference's exception class."""
+    if rc == PFA_OK:
+        return
+    msg = lib().pfa_last_error().decode(errors="replace")
+    if rc == PFA_ERR_INVALID_ARGUMENT:
+        raise ValueError(msg)  # std::invalid_argument under pybind11
+    raise PhantomError(msg)    # std::logic_error / std::runtime_error -> RuntimeError
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+def ptr(t) -> int:
+    """Device pointer of a contiguous torch uint64 tensor (None -> NULL)."""
+    if t is None:
+        return None
+    import torch
+
+    if t.device.type != "cuda":
+        raise ValueError("expected a device tensor")
+    if t.dtype != torch.uint64:
+        raise ValueError(f"expected torch.uint64, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def stream_of(t=None):
+    import torch
+
+    dev = t.device if t is not None else torch.device("cuda", torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def create_coeff_modulus(poly_degree: int, bit_sizes) -> list[int]:
+    bits = (C.c_int * len(bit_sizes))(*bit_sizes)
+    out = (C.c_uint64 * len(bit_sizes))()
+    call("pfa_create_coeff_modulus", poly_degree, bits, len(bit_sizes), out)
+    return [int(x) for x in out]
+
+
+def galois_elt_from_step(step: int, poly_degree: int) -> int:
+    e = C.c_uint32(0)
+    call("pfa_galois_elt_from_step", step, poly_degree, C.byref(e))
+    return int(e.value)
+
+
+class NativeContext:
+    """Owns a pfa_context: the chain, NTT tables and RNS constants on one device."""
+
+    def __init__(self, poly_degree: int, moduli, special_size: int, device: int = 0):
+        self.N = int(poly_degree)
+        self.moduli = [int(m) for m in moduli]
+        self.size_QP = len(self.moduli)
+        self.size_P = int(special_size)
+        self.size_Q = self.size_QP - self.size_P
+        self.device = device
+        arr = (C.c_uint64 * self.size_QP)(*self.moduli)
+        h = C.c_void_p()
+        call("pfa_context_create", self.N, arr, self.size_QP, self.size_P, device, C.byref(h))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().pfa_context_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def roots(self) -> list[int]:
+        out = (C.c_uint64 * self.size_QP)()
+        call("pfa_context_roots", self._h, out)
+        return [int(x) for x in out]
+
+    def size_Ql(self, chain_index: int) -> int:
+        return self.size_Q - (chain_index - 1)
+
+    def beta(self, chain_index: int) -> int:
+        return -(-self.size_Ql(chain_index) // self.size_P)
+
+    @property
+    def dnum(self) -> int:
+        return self.size_Q // self.size_P
+
+    # ---- raw entry points (device tensors in, device tensors out) ----
+    def ntt_forward(self, data, M: int, L: int, start: int = 0, stream=None):
+        call("pfa_ntt_forward", self._h, ptr(data), M, L, start, stream or stream_of(data))
+
+    def ntt_inverse(self, data, M: int, L: int, start: int = 0, stream=None):
+        call("pfa_ntt_inverse", self._h, ptr(data), M, L, start, stream or stream_of(data))
+
+    def modup(self, chain_index, c2, out, stream=None):
+        call("pfa_modup", self._h, chain_index, ptr(c2), ptr(out), stream or stream_of(c2))
+
+    def ks_inner_prod(self, chain_index, t_mod_up, key, cx, stream=None):
+        call("pfa_ks_inner_prod", self._h, chain_index, ptr(t_mod_up), ptr(key), key.shape[0], ptr(cx),
+             stream or stream_of(key))
+
+    def moddown(self, chain_index, cx_k, out, stream=None):
+        call("pfa_moddown", self._h, chain_index, ptr(cx_k), ptr(out), stream or stream_of(cx_k))
+
+    def keyswitch(self, chain_index, ct, c2, key, stream=None):
+        call("pfa_keyswitch", self._h, chain_index, ptr(ct), ptr(c2), ptr(key), key.shape[0],
+             stream or stream_of(ct))
+
+    def tensor(self, chain_index, a, b, out, stream=None):
+        call("pfa_tensor", self._h, chain_index, ptr(a), ptr(b), ptr(out), stream or stream_of(a))
+
+    def multiply_and_relin(self, chain_index, a, b, rlk, out, stream=None):
+        call("pfa_multiply_and_relin", self._h, chain_index, ptr(a), ptr(b), ptr(rlk), rlk.shape[0], ptr(out),
+             stream or stream_of(a))
+
+    def relinearize(self, chain_index, ct3, rlk, out, stream=None):
+        call("pfa_relinearize", self._h, chain_index, ptr(ct3), ptr(rlk), rlk.shape[0], ptr(out),
+             stream or stream_of(ct3))
+
+    def rescale(self, chain_index, ct, out, stream=None):
+        call("pfa_rescale", self._h, chain_index, ptr(ct), ct.shape[0], ptr(out), stream or stream_of(ct))
+
+    def apply_galois_ntt(self, elt, src, dst, L, stream=None):
+        call("pfa_apply_galois_ntt", self._h, elt, ptr(src), ptr(dst), L, stream or stream_of(src))
+
+    def apply_galois(self, chain_index, ct, elt, key, stream=None):
+        call("pfa_apply_galois", self._h, chain_index, ptr(ct), elt, ptr(key), key.shape[0],
+             stream or stream_of(ct))
+
+    def hoist_rotations(self, chain_index, ct, elts, keys, out, stream=None):
+        n = len(elts)
+        e = (C.c_uint32 * n)(*elts)
+        kp = (C.c_void_p * n)(*[ptr(k) for k in keys])
+        call("pfa_hoist_rotations", self._h, chain_index, ptr(ct), e, n, kp, keys[0].shape[0], ptr(out),
+             stream or stream_of(ct))
+
+    def kswitch_key(self, new_key, s, a, e, out, stream=None):
+        call("pfa_kswitch_key", self._h, ptr(new_key), ptr(s), ptr(a), ptr(e), ptr(out), stream or stream_of(s))
+
+    def poly_add(self, a, b, out, L, start=0, stream=None):
+        call("pfa_poly_add", self._h, ptr(a), ptr(b), ptr(out), L, start, stream or stream_of(a))
+
+    def poly_sub(self, a, b, out, L, start=0, stream=None):
+        call("pfa_poly_sub", self._h, ptr(a), ptr(b), ptr(out), L, start, stream or stream_of(a))
+
+    def poly_mul(self, a, b, out, L, start=0, stream=None):
+        call("pfa_poly_mul", self._h, ptr(a), ptr(b), ptr(out), L, start, stream or stream_of(a))
+
+    def poly_negate(self, a, out, L, start=0, stream=None):
+        call("pfa_poly_negate", self._h, ptr(a), ptr(out), L, start, stream or stream_of(a))
+
+    def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
+        import torch
+
+        if coeffs_i64.dtype != torch.int64 or coeffs_i64.device.type != "cuda":
+            raise ValueError("expected an int64 device tensor")
+        call("pfa_poly_from_signed", self._h, coeffs_i64.data_ptr(), ptr(out), L, start,
+             stream or stream_of(out))

@@ -1,0 +1,279 @@
+"""GPU parity of the key-switching path and the evaluator entry points against
+the CPU oracle, bit-exact on every RNS residue:
+
+  tensor (src/polymath.cu:463-498), ModUp (src/rns_bconv.cu:530-628), the
+  inner product (src/eval_key_switch.cu:175-230), ModDown
+  (src/rns_bconv.cu:776-828), keyswitch_inplace (src/eval_key_switch.cu:294-381),
+  multiply_and_relin (src/evaluate.cu:1061-1104), rescale
+  (src/rns.cu:1128-1184), the Galois permutation and rotation
+  (src/galois.cu, src/evaluate.cu:1607-1656), hoisted rotations
+  (src/evaluate.cu:1929-2082) and key construction (src/secretkey.cu:354-398).
+
+Shapes cover alpha = 1 (the single-special-prime BConv), a short last digit
+(|Ql| not a multiple of alpha), lower levels (chain index > 1) and the BASELINE
+config-3 shape (N = 2^16, |Q| = 24, alpha = 4, dnum = 6).
+"""
+import numpy as np
+import pytest
+
+import py_oracle as O
+from gpu_util import empty, first_mismatch, to_dev, to_host, uniform_limbs
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (logN, nq, alpha, chain)
+    (12, 6, 2, 1),
+    (12, 8, 3, 4),   # short last digit (|Ql| = 5, alpha = 3), lower level
+    (12, 5, 1, 2),   # alpha = 1
+    (12, 6, 3, 2),   # lower level, short last digit
+    (13, 8, 4, 1),
+    (16, 6, 2, 3),
+]
+# ModUp / ModDown need no key, so they also take the top level of a chain whose
+# |Q| is not a multiple of alpha (beta = 4 > dnum = 3: keys cannot serve it).
+KEYLESS_SHAPES = SHAPES + [(12, 7, 2, 1)]
+
+
+def chain_bits(nq, alpha):
+    return [60] + [50] * (nq - 1) + [60] * alpha
+
+
+class Setup:
+    def __init__(self, logN, nq, alpha, seed=0):
+        import pfa_native as P
+
+        self.N = 1 << logN
+        self.mods = O.create_coeff_modulus(self.N, chain_bits(nq, alpha))
+        self.nq, self.alpha = nq, alpha
+        self.ctx = P.NativeContext(self.N, self.mods, alpha)
+        self.orc = O.Oracle(self.N, self.mods, alpha)
+        self.rng = np.random.default_rng(seed)
+        self.QP = len(self.mods)
+
+    def qlp_mods(self, chain):
+        Ql = self.orc.size_Ql(chain)
+        return self.mods[:Ql] + self.mods[self.nq:]
+
+    def ct(self, chain, size=2):
+        Ql = self.orc.size_Ql(chain)
+        return uniform_limbs(self.rng, (size, Ql, self.N), self.mods[:Ql])
+
+    def key(self):
+        """A well-formed key switching key [dnum][2][QP][N] from uniform a and small e (via the oracle)."""
+        o, N = self.orc, self.N
+        s = np.zeros(N, dtype=np.int64)
+        idx = self.rng.choice(N, size=min(64, N), replace=False)
+        s[idx] = self.rng.choice([-1, 1], size=len(idx))
+        S = o.ntt_fwd(np.stack([(s % q).astype(np.uint64) for q in self.mods]), threads=8)
+        new = uniform_limbs(self.rng, (self.QP, N), self.mods)
+        a = uniform_limbs(self.rng, (o.dnum, self.QP, N), self.mods)
+        e = uniform_limbs(self.rng, (o.dnum, self.QP, N), self.mods)
+        return o.kswitch_key(new, S, a, e)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", KEYLESS_SHAPES)
+def test_modup(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=1)
+    Ql = st.orc.size_Ql(chain)
+    c2 = uniform_limbs(st.rng, (Ql, st.N), st.mods)
+    out = empty((st.orc.beta(chain), Ql + alpha, st.N), dev)
+    st.ctx.modup(chain, to_dev(c2, dev), out)
+    got, want = to_host(out), st.orc.modup(chain, c2, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", SHAPES)
+def test_inner_product(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=2)
+    Ql = st.orc.size_Ql(chain)
+    beta = st.orc.beta(chain)
+    t = uniform_limbs(st.rng, (beta, Ql + alpha, st.N), st.qlp_mods(chain))
+    key = uniform_limbs(st.rng, (st.orc.dnum, 2, st.QP, st.N), st.mods)
+    cx = empty((2, Ql + alpha, st.N), dev)
+    st.ctx.ks_inner_prod(chain, to_dev(t, dev), to_dev(key, dev), cx)
+    got, want = to_host(cx), st.orc.ks_inner_prod(chain, t, key)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", KEYLESS_SHAPES)
+def test_moddown(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=3)
+    Ql = st.orc.size_Ql(chain)
+    cx = uniform_limbs(st.rng, (Ql + alpha, st.N), st.qlp_mods(chain))
+    out = empty((Ql, st.N), dev)
+    st.ctx.moddown(chain, to_dev(cx, dev), out)
+    got, want = to_host(out), st.orc.moddown(chain, cx, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", SHAPES)
+def test_keyswitch(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=4)
+    Ql = st.orc.size_Ql(chain)
+    ct = st.ct(chain)
+    c2 = uniform_limbs(st.rng, (Ql, st.N), st.mods)
+    key = st.key()
+    d = to_dev(ct, dev)
+    st.ctx.keyswitch(chain, d, to_dev(c2, dev), to_dev(key, dev))
+    got, want = to_host(d), st.orc.keyswitch(chain, ct, c2, key, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", SHAPES[:3])
+def test_tensor_and_relinearize(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=5)
+    Ql = st.orc.size_Ql(chain)
+    a, b = st.ct(chain), st.ct(chain)
+    out3 = empty((3, Ql, st.N), dev)
+    st.ctx.tensor(chain, to_dev(a, dev), to_dev(b, dev), out3)
+    want3 = st.orc.tensor(a, b)
+    assert np.array_equal(to_host(out3), want3)
+    key = st.key()
+    out = empty((2, Ql, st.N), dev)
+    st.ctx.relinearize(chain, out3, to_dev(key, dev), out)
+    want = st.orc.keyswitch(chain, want3[:2], want3[2], key, threads=8)
+    assert np.array_equal(to_host(out), want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", SHAPES)
+def test_multiply_and_relin(dev, logN, nq, alpha, chain):
+    st = Setup(logN, nq, alpha, seed=6)
+    Ql = st.orc.size_Ql(chain)
+    a, b = st.ct(chain), st.ct(chain)
+    key = st.key()
+    out = empty((2, Ql, st.N), dev)
+    st.ctx.multiply_and_relin(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    got, want = to_host(out), st.orc.multiply_and_relin(chain, a, b, key, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_multiply_and_relin_config3(dev):
+    """BASELINE config 3 shape: N = 2^16, chain {60, 50 x 23, 60 x 4}: |Q| = 24,
+    alpha = 4, dnum = beta = 6, fresh ciphertexts at chain index 1."""
+    st = Setup(16, 24, 4, seed=7)
+    a, b = st.ct(1), st.ct(1)
+    key = st.key()
+    out = empty((2, 24, st.N), dev)
+    st.ctx.multiply_and_relin(1, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    got, want = to_host(out), st.orc.multiply_and_relin(1, a, b, key, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("chain,size", [(1, 2), (2, 3), (4, 2)])
+def test_rescale(dev, chain, size):
+    st = Setup(16, 5, 1, seed=8)
+    ct = st.ct(chain, size)
+    Ql = st.orc.size_Ql(chain)
+    out = empty((size, Ql - 1, st.N), dev)
+    st.ctx.rescale(chain, to_dev(ct, dev), out)
+    got, want = to_host(out), st.orc.rescale(chain, ct, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_rescale_last_level_rejected(dev):
+    st = Setup(12, 3, 1)
+    ct = st.ct(3)
+    with pytest.raises(ValueError):
+        st.ctx.rescale(3, to_dev(ct, dev), empty((2, 1, st.N), dev))
+
+
+@pytest.mark.parametrize("step", [1, -1, 5, 0, 1000])
+def test_galois_ntt(dev, step):
+    import pfa_native as P
+
+    st = Setup(16, 4, 1, seed=9)
+    elt = P.galois_elt_from_step(step, st.N)
+    assert elt == O.elt_from_step(step, st.N)
+    x = uniform_limbs(st.rng, (3, st.N), st.mods)
+    out = empty((3, st.N), dev)
+    st.ctx.apply_galois_ntt(elt, to_dev(x, dev), out, 3)
+    assert np.array_equal(to_host(out), st.orc.apply_galois_ntt(x, elt))
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", SHAPES[:4])
+def test_apply_galois(dev, logN, nq, alpha, chain):
+    import pfa_native as P
+
+    st = Setup(logN, nq, alpha, seed=10)
+    ct = st.ct(chain)
+    key = st.key()
+    elt = P.galois_elt_from_step(3, st.N)
+    d = to_dev(ct, dev)
+    st.ctx.apply_galois(chain, d, elt, to_dev(key, dev))
+    got, want = to_host(d), st.orc.apply_galois(chain, ct, elt, key, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 6, 2, 1), (12, 5, 1, 2), (16, 6, 3, 1)])
+def test_hoist_rotations(dev, logN, nq, alpha, chain):
+    import pfa_native as P
+
+    st = Setup(logN, nq, alpha, seed=11)
+    ct = st.ct(chain)
+    steps = [1, 2, -3, 7]
+    elts = [P.galois_elt_from_step(s, st.N) for s in steps]
+    keys = [st.key() for _ in steps]
+    Ql = st.orc.size_Ql(chain)
+    out = empty((len(steps), 2, Ql, st.N), dev)
+    st.ctx.hoist_rotations(chain, to_dev(ct, dev), elts, [to_dev(k, dev) for k in keys], out)
+    got, want = to_host(out), st.orc.hoist_rotations(chain, ct, elts, keys, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha", [(12, 6, 2), (12, 5, 1), (13, 8, 4)])
+def test_kswitch_key(dev, logN, nq, alpha):
+    st = Setup(logN, nq, alpha, seed=12)
+    o = st.orc
+    new = uniform_limbs(st.rng, (st.QP, st.N), st.mods)
+    s = uniform_limbs(st.rng, (st.QP, st.N), st.mods)
+    a = uniform_limbs(st.rng, (o.dnum, st.QP, st.N), st.mods)
+    e = uniform_limbs(st.rng, (o.dnum, st.QP, st.N), st.mods)
+    out = empty((o.dnum, 2, st.QP, st.N), dev)
+    st.ctx.kswitch_key(to_dev(new, dev), to_dev(s, dev), to_dev(a, dev), to_dev(e, dev), out)
+    assert np.array_equal(to_host(out), o.kswitch_key(new, s, a, e))
+
+
+def test_poly_elementwise(dev):
+    import torch
+
+    st = Setup(12, 4, 2, seed=13)
+    L = st.QP
+    a = uniform_limbs(st.rng, (L, st.N), st.mods)
+    b = uniform_limbs(st.rng, (L, st.N), st.mods)
+    da, db, out = to_dev(a, dev), to_dev(b, dev), empty((L, st.N), dev)
+    qs = np.array(st.mods, dtype=object)[:, None]
+    A, B = a.astype(object), b.astype(object)
+    st.ctx.poly_add(da, db, out, L)
+    assert np.array_equal(to_host(out).astype(object), (A + B) % qs)
+    st.ctx.poly_sub(da, db, out, L)
+    assert np.array_equal(to_host(out).astype(object), (A - B) % qs)
+    st.ctx.poly_mul(da, db, out, L)
+    assert np.array_equal(to_host(out).astype(object), (A * B) % qs)
+    st.ctx.poly_negate(da, out, L)
+    assert np.array_equal(to_host(out).astype(object), (-A) % qs)
+    v = st.rng.integers(-(2 ** 62), 2 ** 62, size=st.N, dtype=np.int64)
+    v[:4] = [0, -1, np.iinfo(np.int64).min, np.iinfo(np.int64).max]
+    st.ctx.poly_from_signed(torch.from_numpy(v).to(dev), out, L)
+    want = np.array([[int(x) % q for x in v] for q in st.mods], dtype=object)
+    assert np.array_equal(to_host(out).astype(object), want)
+
+
+def test_key_too_short_rejected(dev):
+    st = Setup(12, 6, 2)
+    ct = st.ct(1)
+    key = uniform_limbs(st.rng, (2, 2, st.QP, st.N), st.mods)  # dnum 2 < beta 3
+    with pytest.raises(ValueError):
+        st.ctx.keyswitch(1, to_dev(ct, dev), to_dev(ct[1], dev), to_dev(key, dev))
+
+
+def test_top_level_of_uneven_chain_rejected(dev):
+    """|Q| = 7, alpha = 2: keys have dnum = 3 digits (src/secretkey.cu:366) but the top
+    level needs beta = 4; the reference would read past its key array, here it is an error
+    (and the oracle refuses it too)."""
+    st = Setup(12, 7, 2)
+    ct = st.ct(1)
+    key = st.key()
+    with pytest.raises(ValueError):
+        st.ctx.keyswitch(1, to_dev(ct, dev), to_dev(ct[1], dev), to_dev(key, dev))
+    with pytest.raises(ValueError):
+        st.orc.keyswitch(1, ct, ct[1], key)
