@@ -52,21 +52,23 @@ def uniform(torch, shape, mods, dev, gen):
 
 
 def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
+    """Returns (wall seconds for `steps` transforms, average ms per transform from
+    HIP events recorded on the launch stream around the whole timed region)."""
     stream = torch.cuda.current_stream()
+    h = stream.cuda_stream
     fn = ctx.ntt_inverse if inverse else ctx.ntt_forward
     for i in range(warmup):
-        fn(batches[i % len(batches)], POLYS, LIMBS, 0, stream.cuda_stream)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        fn(batches[i % len(batches)], POLYS, LIMBS, 0, h)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record(stream)
     for i in range(steps):
-        ev[i][0].record(stream)
-        fn(batches[i % len(batches)], POLYS, LIMBS, 0, stream.cuda_stream)
-        ev[i][1].record(stream)
+        fn(batches[i % len(batches)], POLYS, LIMBS, 0, h)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [a.elapsed_time(b) for a, b in ev]
-    return wall, sum(per) / len(per)
+    return wall, e0.elapsed_time(e1) / steps
 
 
 def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
@@ -103,6 +105,18 @@ def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
             "chain": f"{{60, 50 x {nq - 1}, 60 x {alpha}}}", "dnum": dnum}
 
 
+def measured_traffic():
+    """HBM bytes per forward NTT from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE of both kernels, scaled by the plain-copy factor);
+    None if that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "ntt_fwd_N65536_2x35_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_forward_ntt")
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(mods, seconds):
     """Oracle forward NTT, one thread, repeated over the config-2 batch for ~`seconds`."""
     import numpy as np
@@ -132,6 +146,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-hmult", action="store_true")
+    ap.add_argument("--mode", choices=["full", "ntt", "copy"], default="full",
+                    help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
+                         "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -149,6 +166,13 @@ def main():
     ctx = P.NativeContext(N, mods, 1)
     n_batches = 10  # 10 x 35 MiB > 256 MiB Infinity Cache
     batches = [uniform(torch, (POLYS, LIMBS, N), mods, dev, gen) for _ in range(n_batches)]
+    if args.mode == "copy":
+        dst = torch.empty_like(batches[0])
+        for i in range(args.steps):
+            dst.copy_(batches[i % n_batches])
+        torch.cuda.synchronize()
+        log(f"bench: {args.steps} copies of {POLYS * LIMBS * LIMB_BYTES} bytes done")
+        return
     log(f"bench: config 2 forward NTT, {args.steps} steps, {args.warmup} warmup, {n_batches} rotating batches")
     wall, ev_ms = time_ntt(torch, ctx, batches, args.steps, args.warmup)
     log(f"bench: forward done, {ev_ms * 1e3:.1f} us/launch")
@@ -159,6 +183,9 @@ def main():
     achieved = NTT_BYTES / (ev_ms * 1e-3) / 1e9
     del batches
     torch.cuda.empty_cache()
+    if args.mode == "ntt":
+        log(f"bench: ntt mode done, forward {value:.1f} limbs/s")
+        return
 
     hm = {}
     if not args.no_hmult:
@@ -190,7 +217,7 @@ def main():
         "config": {"workload": "config 2: batched forward NTT, N=2^16, 2 polys x 35 limbs (50-bit primes)",
                    "N": N, "polys": POLYS, "limbs": LIMBS, "rotating_batches": n_batches},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "forward NTT (ntt_fwd_cols + ntt_fwd_rows), 16 B/residue algorithmic"},
         "cpu_baseline": cpu,
         "ntt_inverse_limbs_per_s": round(limbs / (ev_inv_ms * 1e-3), 1),

@@ -4,6 +4,7 @@
 // src/host/{modulus,numth,ntt,rns}.cu and src/rns.cu:11-195; all tables are
 // uploaded once to HBM and are read-only afterwards.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -188,7 +189,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
 
     // NTT tables (src/host/ntt.cu:11-56): tw[brv(i)] = psi^i, itw[brv(i)] = psi^-i,
     // itw[1] *= N^-1.
-    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP);
+    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP), sfw(QP * 16), sinv(QP * 16);
     c.roots.resize(QP);
     for (size_t r = 0; r < QP; ++r) {
         const uint64_t q = moduli[r];
@@ -204,6 +205,10 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             p = mulmod(p, psi, q);
             ip = mulmod(ip, ipsi, q);
         }
+        for (uint32_t i = 0; i < 16; ++i) {
+            sfw[r * 16 + i] = ntt_pair(f[i], q);
+            sinv[r * 16 + i] = ntt_pair(b[i], q);  // before the N^-1 fold below
+        }
         b[1] = mulmod(b[1], ni, q);
         for (uint32_t i = 0; i < N; ++i) {
             tw[r * N + i] = ntt_pair(f[i], q);
@@ -218,6 +223,10 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     c.tw = c.upload(tw);
     c.itw = c.upload(itw);
     c.ninv = c.upload(ninv);
+    c.small_fw = c.upload(sfw);
+    c.small_inv = c.upload(sinv);
+    PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
+    if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
 
     const uint64_t *Qm = moduli, *Pm = moduli + c.Q;
     const uint32_t alpha = c.P;

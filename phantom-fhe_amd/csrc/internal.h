@@ -84,6 +84,10 @@ struct Ctx {
     ulonglong2 *tw = nullptr;       // [QP][N]
     ulonglong2 *itw = nullptr;      // [QP][N]
     ulonglong2 *ninv = nullptr;     // [QP] NTT-policy pairs of N^-1
+    ulonglong2 *small_fw = nullptr;  // [QP][16] psi^brv(i)
+    ulonglong2 *small_inv = nullptr; // [QP][16] psi^-brv(i), no N^-1 fold
+    int n_cu = 256;                  // compute units of the device
+    int ntt_wpc = 3;                 // resident NTT workgroups per CU the grid is sized for
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
     // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
     ulonglong2 *moddown_scale = nullptr;

@@ -89,6 +89,7 @@ __device__ __forceinline__ uint64_t barrett128(U128 x, uint64_t q, uint64_t r0, 
 
 struct ArithInt {
     using T = uint64_t;
+    static constexpr bool kF64 = false;
     uint64_t q, q2;
 
     __device__ __forceinline__ explicit ArithInt(uint64_t q_) : q(q_), q2(2 * q_) {}
@@ -127,6 +128,7 @@ struct ArithInt {
 
 struct ArithF64 {
     using T = double;
+    static constexpr bool kF64 = true;
     double q, qinv;
 
     __device__ __forceinline__ explicit ArithF64(uint64_t q_) : q((double)q_), qinv(1.0 / (double)q_) {}
@@ -179,6 +181,18 @@ struct ArithF64 {
         y = mulw(d, as_f(w.x), as_f(w.y));
     }
     __device__ __forceinline__ void mul(T &x, ulonglong2 c) const { x = mulw(x, as_f(c.x), as_f(c.y)); }
+
+    // Twiddle pair of base * s for a table pair `base` and a small-table pair s:
+    // w = base w * s w with |w| <= (1 + 1/16) q, and wq = w / q to within half
+    // an ulp (one FMA correction step), which keeps the butterfly bound above
+    // (growth B -> B + 1 + B/8 per stage, four stages from B = 1 reach 6.4 < 8).
+    __device__ __forceinline__ ulonglong2 twmul(ulonglong2 base, ulonglong2 s) const {
+        const double w = mulw(as_f(base.x), as_f(s.x), as_f(s.y));
+        double wq = w * qinv;
+        const double e = __fma_rn(-wq, q, w);
+        wq = __fma_rn(e, qinv, wq);
+        return ulonglong2{as_u(w), as_u(wq)};
+    }
 };
 
 }  // namespace pfa

@@ -23,28 +23,38 @@ NttBatch make_batch(const Ctx &c, const NttLaunch &a) {
     return b;
 }
 
-NttTables tables(const Ctx &c) { return NttTables{c.mod, c.tw, c.itw, c.ninv}; }
+NttTables tables(const Ctx &c) { return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv}; }
 
-template <int S1, int S2>
-void fwd(const NttBatch &b, const NttTables &t, hipStream_t s) {
-    using G = Geo<S1, S2>;
-    const uint32_t ml = b.M * b.L;
-    hipLaunchKernelGGL((ntt_fwd_cols<S1, S2>), dim3(ml * G::COL_TILES), dim3(G::COL_THREADS), 0, s, b, t);
-    NttBatch b2 = b;
-    b2.src = b.dst;
-    b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(ml * G::ROW_TILES), dim3(G::ROW_THREADS), 0, s, b2, t);
+// persistent grid: at most n_cu * ntt_wpc workgroups, each walking its tiles
+uint32_t grid_for(const Ctx &c, uint32_t tiles) {
+    const uint32_t cap = (uint32_t)c.n_cu * (uint32_t)c.ntt_wpc;
+    return tiles < cap ? tiles : cap;
 }
 
 template <int S1, int S2>
-void inv(const NttBatch &b, const NttTables &t, hipStream_t s) {
+void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
     const uint32_t ml = b.M * b.L;
-    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(ml * G::ROW_TILES), dim3(G::ROW_THREADS), 0, s, b, t);
+    hipLaunchKernelGGL((ntt_fwd_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES)), dim3(G::COL_THREADS), 0, s, b,
+                       t);
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(ml * G::COL_TILES), dim3(G::COL_THREADS), 0, s, b2, t);
+    hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES)), dim3(G::ROW_THREADS), 0, s, b2,
+                       t);
+}
+
+template <int S1, int S2>
+void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    const uint32_t ml = b.M * b.L;
+    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES)), dim3(G::ROW_THREADS), 0, s, b,
+                       t);
+    NttBatch b2 = b;
+    b2.src = b.dst;
+    b2.sstride = b.dstride;
+    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES)), dim3(G::COL_THREADS), 0, s, b2,
+                       t);
 }
 
 void check_launch(const Ctx &c, const NttLaunch &a) {
@@ -67,14 +77,14 @@ void check_launch(const Ctx &c, const NttLaunch &a) {
 
 #define PFA_NTT_DISPATCH(FN)                                                 \
     switch (c.logN) {                                                        \
-    case 10: FN<5, 5>(b, t, s); break;                                       \
-    case 11: FN<5, 6>(b, t, s); break;                                       \
-    case 12: FN<6, 6>(b, t, s); break;                                       \
-    case 13: FN<6, 7>(b, t, s); break;                                       \
-    case 14: FN<7, 7>(b, t, s); break;                                       \
-    case 15: FN<7, 8>(b, t, s); break;                                       \
-    case 16: FN<8, 8>(b, t, s); break;                                       \
-    case 17: FN<8, 9>(b, t, s); break;                                       \
+    case 10: FN<5, 5>(c, b, t, s); break;                                       \
+    case 11: FN<5, 6>(c, b, t, s); break;                                       \
+    case 12: FN<6, 6>(c, b, t, s); break;                                       \
+    case 13: FN<6, 7>(c, b, t, s); break;                                       \
+    case 14: FN<7, 7>(c, b, t, s); break;                                       \
+    case 15: FN<7, 8>(c, b, t, s); break;                                       \
+    case 16: FN<8, 8>(c, b, t, s); break;                                       \
+    case 17: FN<8, 9>(c, b, t, s); break;                                       \
     default: fail(PFA_ERR_INVALID_ARGUMENT, "unsupported poly_modulus_degree"); \
     }
 
