@@ -189,7 +189,10 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
 
     // NTT tables (src/host/ntt.cu:11-56): tw[brv(i)] = psi^i, itw[brv(i)] = psi^-i,
     // itw[1] *= N^-1.
-    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP), sfw(QP * 16), sinv(QP * 16);
+    // rows-pass geometry of the NTT kernels: N = N1 * N2 with S1 = min(8, logN / 2)
+    const uint32_t S1 = c.logN / 2 > 8 ? 8 : c.logN / 2, S2 = c.logN - S1, N1 = 1u << S1;
+    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP), sfw(QP * 256), sinv(QP * 256),
+        rbf((size_t)QP * S2 * N1), rbi((size_t)QP * S2 * N1);
     c.roots.resize(QP);
     for (size_t r = 0; r < QP; ++r) {
         const uint64_t q = moduli[r];
@@ -205,10 +208,16 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             p = mulmod(p, psi, q);
             ip = mulmod(ip, ipsi, q);
         }
-        for (uint32_t i = 0; i < 16; ++i) {
-            sfw[r * 16 + i] = ntt_pair(f[i], q);
-            sinv[r * 16 + i] = ntt_pair(b[i], q);  // before the N^-1 fold below
+        for (uint32_t i = 0; i < 256 && i < N; ++i) {
+            sfw[r * 256 + i] = ntt_pair(f[i], q);
+            sinv[r * 256 + i] = ntt_pair(b[i], q);  // before the N^-1 fold below
         }
+        for (uint32_t g = 0; g < S2; ++g)
+            for (uint32_t k1 = 0; k1 < N1; ++k1) {
+                const uint32_t idx = (N1 + k1) << g;  // >= 2: never the folded entry
+                rbf[((size_t)r * S2 + g) * N1 + k1] = ntt_pair(f[idx], q);
+                rbi[((size_t)r * S2 + g) * N1 + k1] = ntt_pair(b[idx], q);
+            }
         b[1] = mulmod(b[1], ni, q);
         for (uint32_t i = 0; i < N; ++i) {
             tw[r * N + i] = ntt_pair(f[i], q);
@@ -225,8 +234,21 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     c.ninv = c.upload(ninv);
     c.small_fw = c.upload(sfw);
     c.small_inv = c.upload(sinv);
+    c.rb_fw = c.upload(rbf);
+    c.rb_inv = c.upload(rbi);
     PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
+    // The fused NTT (experimental, off unless PFA_NTT_FUSED=1) relies on the
+    // full-chip mode of MI355X: 8 XCDs, each workgroup able to name its XCD.
+    {
+        hipDeviceProp_t prop;
+        PFA_HIP(hipGetDeviceProperties(&prop, c.device));
+        const bool can_fuse = c.N == 65536 && c.n_cu == 256 && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+        const char *f = std::getenv("PFA_NTT_FUSED");
+        c.ntt_fused = can_fuse && f && std::atoi(f) != 0;
+        if (const char *w = std::getenv("PFA_FUSED_WPC")) c.fused_wpc = std::max(1, std::atoi(w));
+        if (const char *w = std::getenv("PFA_FUSED_LAG")) c.fused_lag = std::max(1, std::atoi(w));
+    }
 
     const uint64_t *Qm = moduli, *Pm = moduli + c.Q;
     const uint32_t alpha = c.P;

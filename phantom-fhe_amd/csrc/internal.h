@@ -84,10 +84,15 @@ struct Ctx {
     ulonglong2 *tw = nullptr;       // [QP][N]
     ulonglong2 *itw = nullptr;      // [QP][N]
     ulonglong2 *ninv = nullptr;     // [QP] NTT-policy pairs of N^-1
-    ulonglong2 *small_fw = nullptr;  // [QP][16] psi^brv(i)
-    ulonglong2 *small_inv = nullptr; // [QP][16] psi^-brv(i), no N^-1 fold
+    ulonglong2 *small_fw = nullptr;  // [QP][256] psi^brv(j)
+    ulonglong2 *small_inv = nullptr; // [QP][256] psi^-brv(j), no N^-1 fold
+    ulonglong2 *rb_fw = nullptr;     // [QP][S2][N1] rows-pass stage bases tw[(N1 + k1) << g]
+    ulonglong2 *rb_inv = nullptr;    // [QP][S2][N1] itw[(N1 + k1) << g]
     int n_cu = 256;                  // compute units of the device
     int ntt_wpc = 3;                 // resident NTT workgroups per CU the grid is sized for
+    bool ntt_fused = false;          // single-launch NTT with L2-resident intermediate (see ntt_kernels.h)
+    int fused_wpc = 2;               // workgroups per CU of the fused NTT
+    int fused_lag = 2;               // jobs between a job's first and second pass in an XCD queue
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
     // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
     ulonglong2 *moddown_scale = nullptr;

@@ -23,7 +23,9 @@ NttBatch make_batch(const Ctx &c, const NttLaunch &a) {
     return b;
 }
 
-NttTables tables(const Ctx &c) { return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv}; }
+NttTables tables(const Ctx &c) {
+    return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv, c.rb_fw, c.rb_inv};
+}
 
 // persistent grid: at most n_cu * ntt_wpc workgroups, each walking its tiles
 uint32_t grid_for(const Ctx &c, uint32_t tiles) {
@@ -75,6 +77,27 @@ void check_launch(const Ctx &c, const NttLaunch &a) {
 
 }  // namespace
 
+// Fused single-launch transform (N = 2^16 only; see ntt_kernels.h).
+template <bool FWD>
+void fused(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+    const uint32_t jobs = b.M * b.L;
+    const uint32_t words = kXcds + jobs + 1;
+    uint32_t *ctl = nullptr;
+    uint64_t *scratch = nullptr;
+    PFA_HIP(hipMallocAsync((void **)&ctl, words * sizeof(uint32_t), s));
+    PFA_HIP(hipMallocAsync((void **)&scratch, (size_t)jobs * c.N * sizeof(uint64_t), s));
+    hipLaunchKernelGGL(k_zero_u32, dim3((words + 255) / 256), dim3(256), 0, s, ctl, words);
+    FusedCtl f{ctl, ctl + kXcds, ctl + kXcds + jobs, scratch};
+    const dim3 grid((uint32_t)c.n_cu * (uint32_t)c.fused_wpc);
+    if (FWD)
+        hipLaunchKernelGGL((ntt_fwd_fused<8, 8>), grid, dim3(256), 0, s, b, t, f, (uint32_t)c.fused_lag);
+    else
+        hipLaunchKernelGGL((ntt_inv_fused<8, 8>), grid, dim3(256), 0, s, b, t, f, (uint32_t)c.fused_lag);
+    PFA_HIP(hipGetLastError());
+    PFA_HIP(hipFreeAsync(scratch, s));
+    PFA_HIP(hipFreeAsync(ctl, s));
+}
+
 #define PFA_NTT_DISPATCH(FN)                                                 \
     switch (c.logN) {                                                        \
     case 10: FN<5, 5>(c, b, t, s); break;                                       \
@@ -92,6 +115,10 @@ void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
+    if (c.ntt_fused) {
+        fused<true>(c, b, t, s);
+        return;
+    }
     PFA_NTT_DISPATCH(fwd);
     PFA_HIP(hipGetLastError());
 }
@@ -100,6 +127,10 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
+    if (c.ntt_fused) {
+        fused<false>(c, b, t, s);
+        return;
+    }
     PFA_NTT_DISPATCH(inv);
     PFA_HIP(hipGetLastError());
 }

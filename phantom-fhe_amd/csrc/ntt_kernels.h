@@ -60,15 +60,21 @@ struct NttTables {
     const ulonglong2 *tw;        // [QP][N] forward pairs
     const ulonglong2 *itw;       // [QP][N] inverse pairs (itw[1] carries N^-1)
     const ulonglong2 *ninv;      // [QP] N^-1 pairs
-    const ulonglong2 *small_fw;  // [QP][16] psi^brv(i), i < 16
-    const ulonglong2 *small_inv; // [QP][16] psi^-brv(i), i < 16 (no N^-1 fold)
+    const ulonglong2 *small_fw;  // [QP][kSmall] psi^brv(j), j < kSmall
+    const ulonglong2 *small_inv; // [QP][kSmall] psi^-brv(j), j < kSmall (no N^-1 fold)
+    const ulonglong2 *rb_fw;     // [QP][S2][N1] tw[(N1 + k1) << g]: rows-pass stage bases
+    const ulonglong2 *rb_inv;    // [QP][S2][N1] itw[(N1 + k1) << g]
 };
 
+constexpr int kSmall = 256;
+
 // Twiddles whose index bits are disjoint factor: with brv additive on disjoint
-// bits, tw[A + i] = psi^brv(A) psi^brv(i) = tw[A] * small[i] when the low bits
-// of A that i occupies are zero.  The rows pass loads one table entry per stage
-// and derives the others from a 16-entry table with one modular product each
-// (FP64 policy), cutting its twiddle reads ~4x.
+// bits, tw[A + j] = psi^brv(A) psi^brv(j) = tw[A] * small[j] when the low bits
+// of A that j occupies are zero.  In the rows pass every stage-g twiddle of row
+// k1 is tw[((N1 + k1) << g) + j] with j < 2^g, so it is rb[g][k1] * small[j]:
+// one entry of a compact per-row table (contiguous across the rows of a tile)
+// times one of a 256-entry table, one modular product each (FP64 policy).  This
+// replaces the full-size table, whose strided reads cost a cache line per use.
 
 template <int S>
 struct Sub {
@@ -148,19 +154,26 @@ __device__ __forceinline__ void inv_round_b(typename A::T (&x)[Sub<S>::E], const
     }
 }
 
-// Rows-pass rounds with derived twiddles (FP64 policy only).
-// forward, stages g = 0 .. LE-1 on u = F + T e: index (base << g) + i, i = e >> (LE - g)
-template <int S>
+// Rows-pass rounds with derived twiddles (FP64 policy only).  rb points at this
+// prime's [S][N1] base table, small at its kSmall table; k1 is the row.
+template <int S, int N1>
+__device__ __forceinline__ ulonglong2 rows_tw(const ArithF64 &ar, const ulonglong2 *rb, const ulonglong2 *small,
+                                              uint32_t k1, int g, uint32_t j) {
+    const ulonglong2 B = rb[g * N1 + k1];
+    return j == 0 ? B : ar.twmul(B, small[j]);
+}
+
+// forward, stages g = 0 .. LE-1 on u = F + T e: j = e >> (LE - g)
+template <int S, int N1>
 __device__ __forceinline__ void fwd_round_a_derived(double (&x)[Sub<S>::E], const ArithF64 &ar,
-                                                    const ulonglong2 *tw, const ulonglong2 *small, uint32_t base) {
+                                                    const ulonglong2 *rb, const ulonglong2 *small, uint32_t k1) {
     constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
 #pragma unroll
     for (int g = 0; g < LE; g++) {
         const int d = E >> (g + 1);
-        const ulonglong2 B = tw[base << g];
         ulonglong2 w[1 << (LE - 1)];
 #pragma unroll
-        for (int i = 0; i < (1 << g); i++) w[i] = i == 0 ? B : ar.twmul(B, small[i]);
+        for (int i = 0; i < (1 << g); i++) w[i] = rows_tw<S, N1>(ar, rb, small, k1, g, i);
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if (e & d) continue;
@@ -169,19 +182,19 @@ __device__ __forceinline__ void fwd_round_a_derived(double (&x)[Sub<S>::E], cons
     }
 }
 
-// forward, stages g = LE .. S-1 on u = F' E + e: index (base << g) + (F' << (LE - S + g)) + i, i = e >> (S - g)
-template <int S>
+// forward, stages g = LE .. S-1 on u = F' E + e: j = (F' << (LE - S + g)) + (e >> (S - g))
+template <int S, int N1>
 __device__ __forceinline__ void fwd_round_b_derived(double (&x)[Sub<S>::E], const ArithF64 &ar,
-                                                    const ulonglong2 *tw, const ulonglong2 *small, uint32_t base,
+                                                    const ulonglong2 *rb, const ulonglong2 *small, uint32_t k1,
                                                     uint32_t F) {
     constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
 #pragma unroll
     for (int g = LE; g < S; g++) {
         const int d = 1 << (S - 1 - g);
-        const ulonglong2 B = tw[(base << g) + (F << (LE - S + g))];
+        const uint32_t jb = F << (LE - S + g);
         ulonglong2 w[1 << (LE - 1)];
 #pragma unroll
-        for (int i = 0; i < (1 << (g + LE - S)); i++) w[i] = i == 0 ? B : ar.twmul(B, small[i]);
+        for (int i = 0; i < (1 << (g + LE - S)); i++) w[i] = rows_tw<S, N1>(ar, rb, small, k1, g, jb + i);
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if (e & d) continue;
@@ -191,18 +204,18 @@ __device__ __forceinline__ void fwd_round_b_derived(double (&x)[Sub<S>::E], cons
 }
 
 // inverse, stages g = S-1 .. LE on u = F' E + e
-template <int S>
+template <int S, int N1>
 __device__ __forceinline__ void inv_round_a_derived(double (&x)[Sub<S>::E], const ArithF64 &ar,
-                                                    const ulonglong2 *itw, const ulonglong2 *small, uint32_t base,
+                                                    const ulonglong2 *rb, const ulonglong2 *small, uint32_t k1,
                                                     uint32_t F) {
     constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
 #pragma unroll
     for (int g = S - 1; g >= LE; g--) {
         const int d = 1 << (S - 1 - g);
-        const ulonglong2 B = itw[(base << g) + (F << (LE - S + g))];
+        const uint32_t jb = F << (LE - S + g);
         ulonglong2 w[1 << (LE - 1)];
 #pragma unroll
-        for (int i = 0; i < (1 << (g + LE - S)); i++) w[i] = i == 0 ? B : ar.twmul(B, small[i]);
+        for (int i = 0; i < (1 << (g + LE - S)); i++) w[i] = rows_tw<S, N1>(ar, rb, small, k1, g, jb + i);
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if (e & d) continue;
@@ -212,17 +225,16 @@ __device__ __forceinline__ void inv_round_a_derived(double (&x)[Sub<S>::E], cons
 }
 
 // inverse, stages g = LE-1 .. 0 on u = F + T e (rows pass: never the last stage)
-template <int S>
+template <int S, int N1>
 __device__ __forceinline__ void inv_round_b_derived(double (&x)[Sub<S>::E], const ArithF64 &ar,
-                                                    const ulonglong2 *itw, const ulonglong2 *small, uint32_t base) {
+                                                    const ulonglong2 *rb, const ulonglong2 *small, uint32_t k1) {
     constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
 #pragma unroll
     for (int g = LE - 1; g >= 0; g--) {
         const int d = E >> (g + 1);
-        const ulonglong2 B = itw[base << g];
         ulonglong2 w[1 << (LE - 1)];
 #pragma unroll
-        for (int i = 0; i < (1 << g); i++) w[i] = i == 0 ? B : ar.twmul(B, small[i]);
+        for (int i = 0; i < (1 << g); i++) w[i] = rows_tw<S, N1>(ar, rb, small, k1, g, i);
 #pragma unroll
         for (int e = 0; e < E; e++) {
             if (e & d) continue;
@@ -256,7 +268,7 @@ struct Geo {
     static constexpr int ROW_PITCH = N2 + N2 / 16;
     static_assert(S1 <= 8, "column tile must fit in 64 KiB of LDS");
     static_assert(N2 >= kCols, "need at least 16 columns");
-    static_assert(Sub<S2>::LE <= 5 && Sub<S1>::LE <= 5, "small twiddle table holds 16 entries");
+    static_assert((1 << (S2 - 1)) <= kSmall, "small twiddle table too short for the rows pass");
     static constexpr int ROW_LDS = ROWS * ROW_PITCH;
 };
 
@@ -301,13 +313,13 @@ __device__ __forceinline__ const uint64_t *cols_src(const NttBatch &b, const Til
 template <class A, int S1, int S2>
 __device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds) {
+                                              typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     using T = typename A::T;
     const A ar(q);
     const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
-    uint64_t *dst = b.dst + r.m * b.dstride + (size_t)r.l * G::N + r.tile * kCols;
+    uint64_t *dst = olimb + r.tile * kCols;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     T x[SB::E];
 #pragma unroll
@@ -352,9 +364,9 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         if (q < kF64PrimeBound)
-            fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds);
+            fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
         else
-            fwd_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds));
+            fwd_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -366,7 +378,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
 template <class A, int S1, int S2>
 __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds) {
+                                              typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -374,13 +386,13 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
     const uint32_t k1 = r.tile * G::ROWS + rr;
-    uint64_t *rowp = b.dst + r.m * b.dstride + (size_t)r.l * G::N + (size_t)k1 * G::N2;
+    uint64_t *rowp = olimb + (size_t)k1 * G::N2;
     T *lr = lds + rr * G::ROW_PITCH;
     T x[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(raw[e]);
     if constexpr (A::kF64)
-        fwd_round_a_derived<S2>(x, ar, tw, t.small_fw + (size_t)prow * 16, G::N1 + k1);
+        fwd_round_a_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1);
     else
         fwd_round_a<A, S2>(x, ar, tw, G::N1 + k1);
 #pragma unroll
@@ -392,7 +404,7 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
     if constexpr (A::kF64)
-        fwd_round_b_derived<S2>(x, ar, tw, t.small_fw + (size_t)prow * 16, G::N1 + k1, F);
+        fwd_round_b_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1, F);
     else
         fwd_round_b<A, S2>(x, ar, tw, G::N1 + k1, F);
     // transpose back through LDS so the stores are coalesced
@@ -438,9 +450,9 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         if (q < kF64PrimeBound)
-            fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds);
+            fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
         else
-            fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds));
+            fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -453,7 +465,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
 template <class A, int S1, int S2>
 __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds) {
+                                              typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -461,7 +473,7 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
     const uint32_t k1 = r.tile * G::ROWS + rr;
-    uint64_t *drow = b.dst + r.m * b.dstride + (size_t)r.l * G::N + (size_t)k1 * G::N2;
+    uint64_t *drow = olimb + (size_t)k1 * G::N2;
     T *lr = lds + rr * G::ROW_PITCH;
     T x[SB::E];
 #pragma unroll
@@ -470,7 +482,7 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
     if constexpr (A::kF64)
-        inv_round_a_derived<S2>(x, ar, itw, t.small_inv + (size_t)prow * 16, G::N1 + k1, F);
+        inv_round_a_derived<S2, G::N1>(x, ar, t.rb_inv + (size_t)prow * S2 * G::N1, t.small_inv + (size_t)prow * kSmall, k1, F);
     else
         inv_round_a<A, S2>(x, ar, itw, G::N1 + k1, F);
     __syncthreads();
@@ -480,7 +492,7 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F + SB::T * e)];
     if constexpr (A::kF64)
-        inv_round_b_derived<S2>(x, ar, itw, t.small_inv + (size_t)prow * 16, G::N1 + k1);
+        inv_round_b_derived<S2, G::N1>(x, ar, t.rb_inv + (size_t)prow * S2 * G::N1, t.small_inv + (size_t)prow * kSmall, k1);
     else
         inv_round_b<A, S2, false>(x, ar, itw, G::N1 + k1, ulonglong2{0, 0});
 #pragma unroll
@@ -513,9 +525,9 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         if (q < kF64PrimeBound)
-            inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds);
+            inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
         else
-            inv_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds));
+            inv_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -527,13 +539,13 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
 template <class A, int S1, int S2>
 __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds) {
+                                              typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     using T = typename A::T;
     const A ar(q);
     const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
-    uint64_t *data = b.dst + r.m * b.dstride + (size_t)r.l * G::N + r.tile * kCols;
+    uint64_t *data = olimb + r.tile * kCols;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     T x[SB::E];
 #pragma unroll
@@ -580,14 +592,214 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBa
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         if (q < kF64PrimeBound)
-            inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds);
+            inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
         else
-            inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds));
+            inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
         __syncthreads();
     }
+}
+
+}  // namespace pfa
+
+namespace pfa {
+
+// ================================================================ fused
+// One launch runs both passes of every limb, with the intermediate kept in
+// the L2 of one XCD:
+//   * every workgroup reads its XCD id from the hardware register and takes
+//     work only from that XCD's queue; limb-job j belongs to XCD j mod 8;
+//   * a job is P1 tiles (first pass) then P2 tiles (second pass); the queue of
+//     an XCD is ordered P1(0), P1(1), P2(0), P1(2), P2(1), ..., P2(n-1), so a P2
+//     tile only ever waits for P1 tiles already taken by running workgroups
+//     (no deadlock, whatever the residency), and waits are rare;
+//   * P1 tiles store the intermediate into a per-job scratch limb (written
+//     through to the XCD's L2), wait for the stores' acknowledgement, then bump
+//     the job's counter (device-scope atomic); P2 tiles poll the counter and
+//     read the scratch with plain loads from the shared L2.  No CU has
+//     read a scratch line before within the launch (one limb per job), so no
+//     L1 holds a stale copy, and the lines come from the shared L2.
+// HBM sees the input read once, the output written once, plus the write-back
+// of the dead scratch lines.  Every wait is bounded; on expiry a flag is raised
+// and the kernel still terminates.
+struct FusedCtl {
+    uint32_t *queue;    // [8] per-XCD item counters, zero at launch
+    uint32_t *done;     // [jobs] finished P1 tiles per job, zero at launch
+    uint32_t *flags;    // [1] bit 0: a wait expired
+    uint64_t *scratch;  // [jobs][N] intermediate, written by P1, read by P2
+};
+
+constexpr uint32_t kXcds = 8;
+constexpr uint32_t kSpinLimit = 1u << 18;
+
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & (kXcds - 1);
+}
+
+struct FusedItem {
+    uint32_t phase, k, tile;
+};
+
+// Queue order of one XCD with lag D (nx jobs, B tiles per phase of a job):
+//   P1(0) .. P1(D-1), then P1(D), P2(0), P1(D+1), P2(1), ..., then the last P2s.
+// P2(k) is taken about 2 D B items after P1(k) started, when its tiles are done.
+__device__ __forceinline__ FusedItem fused_item(uint32_t it, uint32_t nx, uint32_t B, uint32_t D) {
+    const uint32_t s = it / B, tile = it % B;
+    const uint32_t d = nx < D ? nx : D;
+    if (s < d) return FusedItem{1, s, tile};
+    const uint32_t u = s - d, np = nx > D ? nx - D : 0;
+    if (u < 2 * np) return (u & 1) ? FusedItem{2, u / 2, tile} : FusedItem{1, u / 2 + D, tile};
+    return FusedItem{2, np + (u - 2 * np), tile};
+}
+
+// Queue and counters use device-scope atomics: on gfx950 workgroup-scope
+// atomics are not coherent between CUs, so they cannot coordinate workgroups.
+__device__ __forceinline__ uint32_t fused_take(uint32_t *queue, uint32_t xcc, uint32_t *s_slot) {
+    if (threadIdx.x == 0)
+        *s_slot = __hip_atomic_fetch_add(queue + xcc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const uint32_t it = *s_slot;
+    __syncthreads();
+    return it;
+}
+
+// P1 side: all of this workgroup's stores are acknowledged by L2, then count the tile.
+__device__ __forceinline__ void fused_publish(uint32_t *done) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// P2 side: wait until all `need` P1 tiles of the job are published.
+__device__ __forceinline__ void fused_wait(uint32_t *done, uint32_t need, uint32_t *flags) {
+    if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+            __builtin_amdgcn_s_sleep(8);
+            if (++spins > kSpinLimit) {
+                __hip_atomic_fetch_or(flags, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int S1, int S2>
+struct FusedGeo {
+    using G = Geo<S1, S2>;
+    static constexpr bool OK = G::COL_THREADS == 256 && G::ROW_THREADS == 256 && G::COL_LDS == G::ROW_LDS &&
+                               G::COL_TILES == G::ROW_TILES;
+    static constexpr int THREADS = 256;
+    static constexpr int LDS = G::COL_LDS;
+};
+
+template <int S1, int S2>
+__global__ void __launch_bounds__(256) ntt_fwd_fused(NttBatch b, NttTables t, FusedCtl ctl, uint32_t lag) {
+    using G = Geo<S1, S2>;
+    using S1B = Sub<S1>;
+    using S2B = Sub<S2>;
+    static_assert(FusedGeo<S1, S2>::OK, "fused NTT needs matching 256-thread passes");
+    __shared__ double lds[FusedGeo<S1, S2>::LDS];
+    __shared__ uint32_t s_slot;
+    const uint32_t xcc = xcc_id();
+    const uint32_t jobs = b.M * b.L;
+    const uint32_t nx = jobs > xcc ? (jobs - xcc + kXcds - 1) / kXcds : 0;
+    const uint32_t n1 = G::COL_TILES, n2 = G::ROW_TILES, total = nx * (n1 + n2);
+    for (;;) {
+        const uint32_t it = fused_take(ctl.queue, xcc, &s_slot);
+        if (it >= total) break;
+        const FusedItem f = fused_item(it, nx, n1, lag);
+        const uint32_t job = xcc + kXcds * f.k;
+        const TileRef r{job % b.M, job / b.M, f.tile};
+        const bool skip = b.excluded(r.m, r.l);
+        const uint32_t prow = b.map.row(r.l);
+        const uint64_t q = t.mod[prow];
+        if (f.phase == 1) {
+            if (!skip) {
+                const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+                const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
+                uint64_t raw[S1B::E];
+#pragma unroll
+                for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F + S1B::T * e) * G::N2 + c];
+                if (q < kF64PrimeBound)
+                    fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
+                else
+                    fwd_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), ctl.scratch + (size_t)job * G::N);
+            }
+            fused_publish(ctl.done + job);
+        } else if (!skip) {
+            fused_wait(ctl.done + job, n1, ctl.flags);
+            const uint32_t F = threadIdx.x % S2B::T, rr = threadIdx.x / S2B::T;
+            const uint64_t *srow = ctl.scratch + (size_t)job * G::N + (size_t)(r.tile * G::ROWS + rr) * G::N2;
+            uint64_t raw[S2B::E];
+#pragma unroll
+            for (int e = 0; e < S2B::E; e++) raw[e] = srow[F + S2B::T * e];
+            if (q < kF64PrimeBound)
+                fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            else
+                fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+        }
+        __syncthreads();
+    }
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__(256) ntt_inv_fused(NttBatch b, NttTables t, FusedCtl ctl, uint32_t lag) {
+    using G = Geo<S1, S2>;
+    using S1B = Sub<S1>;
+    using S2B = Sub<S2>;
+    static_assert(FusedGeo<S1, S2>::OK, "fused NTT needs matching 256-thread passes");
+    __shared__ double lds[FusedGeo<S1, S2>::LDS];
+    __shared__ uint32_t s_slot;
+    const uint32_t xcc = xcc_id();
+    const uint32_t jobs = b.M * b.L;
+    const uint32_t nx = jobs > xcc ? (jobs - xcc + kXcds - 1) / kXcds : 0;
+    const uint32_t n1 = G::ROW_TILES, n2 = G::COL_TILES, total = nx * (n1 + n2);
+    for (;;) {
+        const uint32_t it = fused_take(ctl.queue, xcc, &s_slot);
+        if (it >= total) break;
+        const FusedItem f = fused_item(it, nx, n1, lag);
+        const uint32_t job = xcc + kXcds * f.k;
+        const TileRef r{job % b.M, job / b.M, f.tile};
+        const bool skip = b.excluded(r.m, r.l);
+        const uint32_t prow = b.map.row(r.l);
+        const uint64_t q = t.mod[prow];
+        if (f.phase == 1) {
+            if (!skip) {
+                const uint32_t F = threadIdx.x % S2B::T;
+                const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
+                uint64_t raw[S2B::E];
+#pragma unroll
+                for (int e = 0; e < S2B::E; e++) raw[e] = s[F + S2B::T * e];
+                if (q < kF64PrimeBound)
+                    inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
+                else
+                    inv_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), ctl.scratch + (size_t)job * G::N);
+            }
+            fused_publish(ctl.done + job);
+        } else if (!skip) {
+            fused_wait(ctl.done + job, n1, ctl.flags);
+            const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+            const uint64_t *scol = ctl.scratch + (size_t)job * G::N + r.tile * kCols;
+            uint64_t raw[S1B::E];
+#pragma unroll
+            for (int e = 0; e < S1B::E; e++) raw[e] = scol[(size_t)(F * S1B::E + e) * G::N2 + c];
+            if (q < kF64PrimeBound)
+                inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            else
+                inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void k_zero_u32(uint32_t *p, uint32_t n) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
 }  // namespace pfa
