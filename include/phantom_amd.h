@@ -139,6 +139,12 @@ int pfa_apply_galois(const pfa_context *ctx, size_t chain_index, uint64_t *ct, u
 int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts,
                         size_t n, const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream);
 
+/* hoisting_inplace (src/evaluate.cu:1732-1927): the sum of the n rotations
+ * of ct, sharing one ModUp of c1; the inner products of all rotations are
+ * accumulated before one ModDown.  out [2][|Ql|][N]. */
+int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts, size_t n,
+                 const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream);
+
 /* -------------------------------------------- key material and elementwise */
 
 /* generate_one_kswitch_key (src/secretkey.cu:354-398, with
@@ -163,6 +169,22 @@ int pfa_poly_negate(const pfa_context *ctx, const uint64_t *a, uint64_t *out, si
  * decomposition, src/prng.cu / src/secretkey.cu:236-299). */
 int pfa_poly_from_signed(const pfa_context *ctx, const int64_t *in, uint64_t *out, size_t L, size_t start,
                          void *stream);
+
+/* ------------------------------------------------------------ CKKS encoder */
+
+/* PhantomCKKSEncoder::encode (src/ckks.cu:71-137; special FFT src/fft.cu):
+ * n_values <= N/2 complex slot values (device, interleaved re/im doubles;
+ * missing slots are zero) times `scale`, rounded, into a plaintext of L limbs
+ * (primes 0..L-1) in NTT form.  INVALID_ARGUMENT if a coefficient reaches
+ * 2^62 ("encoded values are too large").  Synchronizes the stream. */
+int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_values, double scale, uint64_t *out,
+                    size_t L, void *stream);
+
+/* PhantomCKKSEncoder::decode (src/ckks.cu:139-190): plaintext of L limbs in
+ * NTT form -> N/2 complex slot values (device, interleaved re/im) divided by
+ * `scale`.  Coefficients are composed from the first two limbs. */
+int pfa_ckks_decode(const pfa_context *ctx, const uint64_t *in, size_t L, double scale, double *values,
+                    void *stream);
 
 #ifdef __cplusplus
 }

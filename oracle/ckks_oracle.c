@@ -643,6 +643,50 @@ int orc_hoist_rotations(const orc_ctx *c, size_t chain_index, const uint64_t *ct
     return 0;
 }
 
+/* hoisting_inplace (src/evaluate.cu:1732-1927): sum of the rotations by elts;
+ * the inner products of all rotations are accumulated in the QlP basis and
+ * moved down once:  out0 = sum sigma_e(c0) + ModDown(acc0), out1 = ModDown(acc1). */
+int orc_hoisting(const orc_ctx *c, size_t chain_index, const uint64_t *ct, const uint32_t *elts, size_t n_elts,
+                 const uint64_t *const *keys, size_t key_dnum, uint64_t *out, int threads) {
+    size_t N = c->N, alpha = c->size_P, Ql = size_Ql(c, chain_index), QlP = Ql + alpha;
+    size_t beta = (Ql + alpha - 1) / alpha;
+    if (alpha == 0 || beta > key_dnum || n_elts == 0) return -1;
+    uint64_t *mu = (uint64_t *)malloc(beta * QlP * N * sizeof(uint64_t));
+    uint64_t *mur = (uint64_t *)malloc(beta * QlP * N * sizeof(uint64_t));
+    uint64_t *cx = (uint64_t *)malloc(2 * QlP * N * sizeof(uint64_t));
+    uint64_t *acc = (uint64_t *)calloc(2 * QlP * N, sizeof(uint64_t));
+    uint64_t *c0 = (uint64_t *)calloc(Ql * N, sizeof(uint64_t));
+    uint64_t *t0 = (uint64_t *)malloc(Ql * N * sizeof(uint64_t));
+    orc_modup(c, chain_index, ct + Ql * N, mu, threads);
+    for (size_t e = 0; e < n_elts; e++) {
+        orc_apply_galois_ntt(N, elts[e], ct, t0, Ql);
+        for (size_t i = 0; i < Ql; i++)
+            for (size_t k = 0; k < N; k++) c0[i * N + k] = add_mod(c0[i * N + k], t0[i * N + k], c->moduli[i]);
+        for (size_t b = 0; b < beta; b++)
+            orc_apply_galois_ntt(N, elts[e], mu + b * QlP * N, mur + b * QlP * N, QlP);
+        orc_ks_inner_prod(c, chain_index, mur, keys[e], key_dnum, cx);
+        for (size_t h = 0; h < 2; h++)
+            for (size_t r = 0; r < QlP; r++) {
+                uint64_t q = c->moduli[qlp_row(c, Ql, r)];
+                for (size_t k = 0; k < N; k++) {
+                    size_t o = (h * QlP + r) * N + k;
+                    acc[o] = add_mod(acc[o], cx[o], q);
+                }
+            }
+    }
+    orc_moddown(c, chain_index, acc, out, threads);
+    for (size_t i = 0; i < Ql; i++)
+        for (size_t k = 0; k < N; k++) out[i * N + k] = add_mod(out[i * N + k], c0[i * N + k], c->moduli[i]);
+    orc_moddown(c, chain_index, acc + QlP * N, out + Ql * N, threads);
+    free(mu);
+    free(mur);
+    free(cx);
+    free(acc);
+    free(c0);
+    free(t0);
+    return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* key switching key (src/secretkey.cu:236-299, :354-398; polymath.cu:318-372) */
 /* ------------------------------------------------------------------------ */

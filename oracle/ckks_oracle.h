@@ -101,6 +101,10 @@ int orc_apply_galois(const orc_ctx *ctx, size_t chain_index, uint64_t *ct, uint3
 int orc_hoist_rotations(const orc_ctx *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts,
                         size_t n_elts, const uint64_t *const *keys, size_t key_dnum, uint64_t *out, int threads);
 
+/* hoisting_inplace (src/evaluate.cu:1732-1927): out [2][|Ql|][N] = sum of rotations */
+int orc_hoisting(const orc_ctx *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts, size_t n_elts,
+                 const uint64_t *const *keys, size_t key_dnum, uint64_t *out, int threads);
+
 /* ---- key construction (src/secretkey.cu:354-398, src/polymath.cu:318-372) ----
  * new_key, s: [|QP|][N] NTT form; a, e_ntt: [dnum][|QP|][N]; key_out: [dnum][2][|QP|][N] */
 void orc_kswitch_key(const orc_ctx *ctx, const uint64_t *new_key, const uint64_t *s, const uint64_t *a,

@@ -57,6 +57,7 @@ def _load():
         "orc_apply_galois_ntt": (None, [u64, C.c_uint32, _u64p, _u64p, sz]),
         "orc_apply_galois": (i32, [vp, sz, _u64p, C.c_uint32, _u64p, sz, i32]),
         "orc_hoist_rotations": (i32, [vp, sz, _u64p, _u32p, sz, C.POINTER(_u64p), sz, _u64p, i32]),
+        "orc_hoisting": (i32, [vp, sz, _u64p, _u32p, sz, C.POINTER(_u64p), sz, _u64p, i32]),
         "orc_kswitch_key": (None, [vp, _u64p, _u64p, _u64p, _u64p, _u64p]),
         "orc_mul_poly": (None, [vp, sz, sz, _u64p, _u64p, _u64p]),
     }
@@ -274,6 +275,19 @@ class Oracle:
                                        kp, keys[0].shape[0], _p(out), threads or threads_default())
         if rc != 0:
             raise ValueError("key has fewer digits than beta")
+        return out
+
+    def hoisting(self, chain_index: int, ct: np.ndarray, elts, keys, threads: int | None = None) -> np.ndarray:
+        ct = u64(ct)
+        keys = [u64(k) for k in keys]
+        Ql = self.size_Ql(chain_index)
+        out = np.zeros((2, Ql, self.N), dtype=np.uint64)
+        e = np.asarray(elts, dtype=np.uint32)
+        kp = (_u64p * len(keys))(*[_p(k) for k in keys])
+        rc = lib().orc_hoisting(self._ctx, chain_index, _p(ct), e.ctypes.data_as(_u32p), len(elts), kp,
+                                keys[0].shape[0], _p(out), threads or threads_default())
+        if rc != 0:
+            raise ValueError("key has fewer digits than beta, or no rotation")
         return out
 
     def kswitch_key(self, new_key, s, a, e_ntt) -> np.ndarray:

@@ -151,15 +151,6 @@ static void create_coeff_modulus(uint64_t N, const int *bits, size_t count, uint
 }
 
 // ---------------------------------------------------------------- context
-template <class T>
-T *Ctx::upload(const std::vector<T> &v) {
-    void *p = nullptr;
-    PFA_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(T)));
-    allocations.push_back(p);
-    if (!v.empty()) PFA_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
-    return (T *)p;
-}
-
 static uint64_t prod_mod(const uint64_t *m, size_t n, size_t skip, uint64_t p) {
     uint64_t r = 1 % p;
     for (size_t k = 0; k < n; ++k)
@@ -274,6 +265,8 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         c.pinv = c.upload(pinv);
         c.pmodq = c.upload(pq);
     }
+
+    encoder_init(c);
 
     // Per-level constants (src/rns.cu:66-95, :141-190)
     c.levels.resize(c.Q + 1);

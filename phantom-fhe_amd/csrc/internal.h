@@ -100,6 +100,7 @@ struct Ctx {
     ulonglong2 *pinv = nullptr;
     // key construction: [P]_{q_i} Shoup pairs over all QP rows (0 on P rows)
     ulonglong2 *pmodq = nullptr;
+    uint32_t *slot_perm = nullptr;   // [N/2] CKKS slot j -> DFT index (5^j mod 2N - 1) / 4
     std::vector<Level> levels;  // index = chain index (0 unused)
     std::vector<void *> allocations;
 
@@ -114,7 +115,17 @@ struct Ctx {
     T *upload(const std::vector<T> &v);
 };
 
+template <class T>
+T *Ctx::upload(const std::vector<T> &v) {
+    void *p = nullptr;
+    PFA_HIP(hipMalloc(&p, (v.empty() ? 1 : v.size()) * sizeof(T)));
+    allocations.push_back(p);
+    if (!v.empty()) PFA_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+    return (T *)p;
+}
+
 Ctx *ctx_of(const pfa_context *c);
+void encoder_init(Ctx &c);
 
 // ---------------------------------------------------------------- launchers
 // NTT over M polys x L limbs; see NttBatch in ntt_kernels.h for the fields.

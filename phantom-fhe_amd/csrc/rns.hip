@@ -121,10 +121,12 @@ k_modup_bconv(const uint64_t *t, const uint64_t *c2, uint64_t *out, const uint64
 //   cx[k][r] = sum_{b < beta} t[b][r] * key[b][k][row(r)]  mod q_row(r)
 // accumulated in 128 bits and reduced once.  With elt != 0 the slabs are read
 // through the Galois permutation (hoisted rotations, src/evaluate.cu:2039-2049).
+// With acc set the result is added to cx (hoisting accumulates the inner
+// products of all rotations before one ModDown, src/evaluate.cu:1836-1879).
 __global__ void __launch_bounds__(kThreads)
 k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t *mod, const ulonglong2 *ratio,
            uint32_t Ql, uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N, uint32_t elt,
-           uint32_t logN) {
+           uint32_t logN, uint32_t acc) {
     const uint32_t r = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t row = r < Ql ? r : Q + (r - Ql);
     const uint32_t sn = elt ? galois_perm(elt, n, logN) : n;
@@ -137,8 +139,14 @@ k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t 
     }
     const uint64_t q = mod[row];
     const ulonglong2 rt = ratio[row];
-    cx[(size_t)r * N + n] = barrett128(a0, q, rt.x, rt.y);
-    cx[((size_t)QlP + r) * N + n] = barrett128(a1, q, rt.x, rt.y);
+    uint64_t v0 = barrett128(a0, q, rt.x, rt.y), v1 = barrett128(a1, q, rt.x, rt.y);
+    uint64_t *o0 = cx + (size_t)r * N + n, *o1 = cx + ((size_t)QlP + r) * N + n;
+    if (acc) {
+        v0 = add_mod(v0, *o0, q);
+        v1 = add_mod(v1, *o1, q);
+    }
+    *o0 = v0;
+    *o1 = v1;
 }
 
 // ModDown base conversion P -> Ql (bConv_BEHZ, src/rns_bconv.cu:212-229):
@@ -283,14 +291,14 @@ void op_modup(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, h
 }
 
 void op_inner(const Ctx &c, uint32_t chain, const uint64_t *t, const uint64_t *key, size_t dnum, uint64_t *cx,
-              uint32_t elt, hipStream_t s) {
+              uint32_t elt, hipStream_t s, bool acc = false) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
     const uint32_t QlP = lv.Ql + c.P;
     hipLaunchKernelGGL(k_ks_inner, grid(c, QlP), dim3(kThreads), 0, s, t, key, cx, c.mod, c.ratio, lv.Ql, QlP, c.Q,
-                       c.QP, lv.beta, c.N, elt, c.logN);
+                       c.QP, lv.beta, c.N, elt, c.logN, acc ? 1u : 0u);
     PFA_HIP(hipGetLastError());
 }
 
@@ -517,6 +525,36 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
             op_inner(c, chain, mu.p, keys[e], key_dnum, cx.p, elts[e], s);
             op_moddown(c, chain, cx.p, 2, o, Bases{{o, nullptr}}, s);
         }
+    });
+}
+
+int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, const uint32_t *elts, size_t n,
+                 const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && out && n >= 1 && elts && keys, "null argument or no rotation steps");
+        check_chain(c, chain_index);
+        const hipStream_t s = as_stream(stream);
+        const uint32_t chain = (uint32_t)chain_index;
+        const Level &lv = c.level(chain);
+        const uint32_t Ql = lv.Ql, QlP = Ql + c.P;
+        const size_t LN = (size_t)Ql * c.N;
+        for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
+        Tmp mu((size_t)lv.beta * QlP * c.N, s);
+        op_modup(c, chain, ct + LN, mu.p, s);
+        Tmp cx((size_t)2 * QlP * c.N, s);
+        Tmp c0(2 * LN, s);  // accumulated sigma(c0), and one sigma(c0) term
+        for (size_t e = 0; e < n; ++e) {
+            op_galois(c, elts[e], ct, e == 0 ? c0.p : c0.p + LN, Ql, s);
+            if (e > 0) {
+                hipLaunchKernelGGL(k_poly_binop, grid(c, Ql), dim3(kThreads), 0, s, (int)kAdd, c0.p, c0.p + LN, c0.p,
+                                   c.mod, c.ratio, 0u, c.N);
+                PFA_HIP(hipGetLastError());
+            }
+            op_inner(c, chain, mu.p, keys[e], key_dnum, cx.p, elts[e], s, e > 0);
+        }
+        // c0' = sum sigma(c0) + ModDown(acc0), c1' = ModDown(acc1)
+        op_moddown(c, chain, cx.p, 2, out, Bases{{c0.p, nullptr}}, s);
     });
 }
 

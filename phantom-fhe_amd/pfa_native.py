@@ -45,12 +45,15 @@ SIGNATURES = {
     "pfa_apply_galois_ntt": (_i32, [_vp, _u32, _vp, _vp, _sz, _vp]),
     "pfa_apply_galois": (_i32, [_vp, _sz, _vp, _u32, _vp, _sz, _vp]),
     "pfa_hoist_rotations": (_i32, [_vp, _sz, _vp, C.POINTER(C.c_uint32), _sz, C.POINTER(_vp), _sz, _vp, _vp]),
+    "pfa_hoisting": (_i32, [_vp, _sz, _vp, C.POINTER(C.c_uint32), _sz, C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_kswitch_key": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pfa_poly_add": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_sub": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_mul": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_negate": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_from_signed": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_ckks_encode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _sz, _vp]),
+    "pfa_ckks_decode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
 }
 
 
@@ -221,6 +224,13 @@ class NativeContext:
         call("pfa_hoist_rotations", self._h, chain_index, ptr(ct), e, n, kp, keys[0].shape[0], ptr(out),
              stream or stream_of(ct))
 
+    def hoisting(self, chain_index, ct, elts, keys, out, stream=None):
+        n = len(elts)
+        e = (C.c_uint32 * n)(*elts)
+        kp = (C.c_void_p * n)(*[ptr(k) for k in keys])
+        call("pfa_hoisting", self._h, chain_index, ptr(ct), e, n, kp, keys[0].shape[0], ptr(out),
+             stream or stream_of(ct))
+
     def kswitch_key(self, new_key, s, a, e, out, stream=None):
         call("pfa_kswitch_key", self._h, ptr(new_key), ptr(s), ptr(a), ptr(e), ptr(out), stream or stream_of(s))
 
@@ -235,6 +245,24 @@ class NativeContext:
 
     def poly_negate(self, a, out, L, start=0, stream=None):
         call("pfa_poly_negate", self._h, ptr(a), ptr(out), L, start, stream or stream_of(a))
+
+    def ckks_encode(self, values_c128, scale, out, L, stream=None):
+        """values_c128: complex128 device tensor [<= N/2]; out: uint64 [L][N]."""
+        import torch
+
+        if values_c128.dtype != torch.complex128 or values_c128.device.type != "cuda":
+            raise ValueError("expected a complex128 device tensor")
+        v = values_c128.contiguous()
+        call("pfa_ckks_encode", self._h, v.data_ptr(), v.numel(), float(scale), ptr(out), L,
+             stream or stream_of(out))
+
+    def ckks_decode(self, plain, L, scale, out_c128, stream=None):
+        import torch
+
+        if out_c128.dtype != torch.complex128 or not out_c128.is_contiguous():
+            raise ValueError("expected a contiguous complex128 device tensor")
+        call("pfa_ckks_decode", self._h, ptr(plain), L, float(scale), out_c128.data_ptr(),
+             stream or stream_of(plain))
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

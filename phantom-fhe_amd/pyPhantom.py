@@ -1,0 +1,662 @@
+"""pyPhantom -- the reference's Python API (python/src/binding.cu) for the CKKS
+hot path, running on the MI355X core through the C ABI (pfa_native).
+
+Names, argument order and return conventions follow the pybind11 module
+`pyPhantom` (binding.cu:23-290): `params`, `context`, `secret_key`,
+`public_key`, `relin_key`, `galois_key`, `ckks_encoder`, `plaintext`,
+`ciphertext`, and the evaluator functions (`add`, `sub`, `negate`,
+`multiply`, `multiply_and_relin`, `relinearize`, `rescale_to_next`,
+`mod_switch_*`, `multiply_plain`, `add_plain`, `apply_galois`, `rotate`,
+`hoisting`, `hoist_rotations`, ...).  Operations return new objects, as the
+reference's by-value bindings do (include/evaluate.cuh:134-139).  Errors are
+ValueError for invalid arguments and RuntimeError otherwise, as pybind11 maps
+the reference's std::invalid_argument / std::logic_error.
+
+Every residue computation runs in libphantom_amd.so on the GPU.  Randomness
+(secret, uniform masks, errors) is sampled on the host from numpy's seedable
+generator and uploaded; the reference samples on the GPU with salsa20
+(src/prng.cu), whose streams are not reproducible anyway (seeds come from
+std::random_device).  Errors follow the reference's centred binomial
+distribution with 21 + 21 coin flips (sigma ~ 3.24, src/prng.cu:222-243).
+"""
+from __future__ import annotations
+
+import enum
+import itertools
+
+import numpy as np
+
+import pfa_native as _N
+
+__version__ = "amd-1"
+
+_seed_counter = itertools.count()
+_global_seed = None
+
+
+def set_seed(seed: int | None) -> None:
+    """Seed the host-side samplers (keys, masks, errors); None = OS entropy."""
+    global _global_seed, _seed_counter
+    _global_seed = seed
+    _seed_counter = itertools.count()
+
+
+def _rng(seed=None):
+    if seed is not None:
+        return np.random.default_rng(seed)
+    if _global_seed is not None:
+        return np.random.default_rng((_global_seed, next(_seed_counter)))
+    return np.random.default_rng()
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+class scheme_type(enum.IntEnum):
+    none = 0
+    bfv = 1
+    ckks = 2
+    bgv = 3
+
+
+class mul_tech_type(enum.IntEnum):
+    none = 0
+    behz = 1
+    hps = 2
+    hps_overq = 3
+    hps_overq_leveled = 4
+
+
+create_coeff_modulus = _N.create_coeff_modulus
+
+
+def get_elt_from_step(step: int, coeff_count: int) -> int:
+    """include/galois.cuh:16-49."""
+    return _N.galois_elt_from_step(step, coeff_count)
+
+
+def get_elts_from_steps(steps, coeff_count: int) -> list[int]:
+    return [get_elt_from_step(s, coeff_count) for s in steps]
+
+
+class params:
+    """EncryptionParameters (include/host/encryptionparams.h); CKKS only."""
+
+    def __init__(self, scheme=scheme_type.ckks):
+        if scheme != scheme_type.ckks:
+            raise ValueError("this core implements the CKKS scheme only")
+        self.scheme = scheme
+        self.poly_modulus_degree = 0
+        self.coeff_modulus = []
+        self.special_modulus_size = 1
+        self.galois_elts = []
+        self.mul_tech = mul_tech_type.none
+
+    def set_mul_tech(self, t):
+        self.mul_tech = t
+
+    def set_poly_modulus_degree(self, n):
+        self.poly_modulus_degree = int(n)
+
+    def set_special_modulus_size(self, k):
+        self.special_modulus_size = int(k)
+
+    def set_galois_elts(self, elts):
+        self.galois_elts = [int(e) for e in elts]
+
+    def set_coeff_modulus(self, mods):
+        self.coeff_modulus = [int(getattr(m, "value", m)) for m in mods]
+
+    def set_plain_modulus(self, _):
+        raise ValueError("plain modulus is a BFV/BGV parameter")
+
+
+class context:
+    """PhantomContext (src/context.cu:121-183): chain index 0 = key level,
+    chain c >= 1 holds |Q| - c + 1 data primes."""
+
+    def __init__(self, parms: params, device: int = 0):
+        if not parms.poly_modulus_degree or not parms.coeff_modulus:
+            raise ValueError("poly modulus degree and coefficient modulus must be set")
+        self.parms = parms
+        self.N = parms.poly_modulus_degree
+        self.moduli = list(parms.coeff_modulus)
+        self.size_P = parms.special_modulus_size
+        self.size_Q = len(self.moduli) - self.size_P
+        self.device = device
+        self.native = _N.NativeContext(self.N, self.moduli, self.size_P, device)
+        self.galois_elts = list(parms.galois_elts)
+
+    def total_parm_size(self) -> int:
+        return self.size_Q + 1
+
+    def get_first_index(self) -> int:
+        return 1
+
+    def size_Ql(self, chain_index: int) -> int:
+        return self.size_Q - (chain_index - 1)
+
+    @property
+    def dnum(self) -> int:
+        return self.size_Q // self.size_P
+
+    @property
+    def dev(self):
+        return _torch().device("cuda", self.device)
+
+    # ---- helpers (device tensors) ----
+    def _empty(self, *shape):
+        t = _torch()
+        return t.empty(shape, dtype=t.uint64, device=self.dev)
+
+    def _upload(self, a: np.ndarray):
+        t = _torch()
+        return t.from_numpy(np.ascontiguousarray(a, dtype=np.uint64)).to(self.dev)
+
+    def _signed_to_rns(self, coeffs: np.ndarray, L: int, start: int = 0):
+        """Signed integer coefficients [N] -> residues [L][N] (coefficient form)."""
+        t = _torch()
+        c = t.from_numpy(np.ascontiguousarray(coeffs, dtype=np.int64)).to(self.dev)
+        out = self._empty(L, self.N)
+        self.native.poly_from_signed(c, out, L, start)
+        return out
+
+    def _uniform(self, rng, L: int, start: int = 0):
+        a = np.stack([rng.integers(0, q, size=self.N, dtype=np.uint64) for q in self.moduli[start:start + L]])
+        return self._upload(a)
+
+    def _cbd(self, rng):
+        """Centred binomial error, 21 + 21 coins (src/prng.cu:222-243)."""
+        return (rng.binomial(21, 0.5, self.N) - rng.binomial(21, 0.5, self.N)).astype(np.int64)
+
+    def _ntt(self, t, L, start=0):
+        self.native.ntt_forward(t, 1, L, start)
+        return t
+
+
+class plaintext:
+    def __init__(self):
+        self.data = None
+        self._chain_index = 0
+        self._scale = 1.0
+
+    def chain_index(self) -> int:
+        return self._chain_index
+
+    def scale(self) -> float:
+        return self._scale
+
+
+class ciphertext:
+    """PhantomCiphertext (include/ciphertext.h): data [size][|Ql|][N] in NTT form."""
+
+    def __init__(self):
+        self.data = None
+        self._chain_index = 0
+        self._scale = 1.0
+        self.is_ntt_form = True
+
+    def chain_index(self) -> int:
+        return self._chain_index
+
+    def scale(self) -> float:
+        return self._scale
+
+    def set_scale(self, s: float):
+        self._scale = float(s)
+
+    def size(self) -> int:
+        return 0 if self.data is None else int(self.data.shape[0])
+
+    def _like(self, data, chain=None, scale=None):
+        c = ciphertext()
+        c.data = data
+        c._chain_index = self._chain_index if chain is None else chain
+        c._scale = self._scale if scale is None else scale
+        return c
+
+
+class _ksk:
+    """Key switching key material: [dnum][2][|QP|][N] on the device."""
+
+    def __init__(self, data):
+        self.data = data
+
+
+class relin_key(_ksk):
+    def __init__(self, data=None):
+        super().__init__(data)
+
+
+class galois_key:
+    def __init__(self):
+        self.keys = {}  # Galois element -> key tensor
+
+    def get(self, elt):
+        k = self.keys.get(elt)
+        if k is None:
+            raise RuntimeError(f"Galois key not present for element {elt}")
+        return k
+
+
+class public_key:
+    """PhantomPublicKey: (-(a s + e), a) over the data primes, NTT form."""
+
+    def __init__(self, ctx: context | None = None, data=None):
+        self.ctx = ctx
+        self.data = data
+
+    def encrypt_asymmetric(self, ctx: context, pt: plaintext, seed=None) -> ciphertext:
+        """ct = (pk0 u + e0 + m, pk1 u + e1) over the plaintext's primes."""
+        if self.data is None:
+            raise ValueError("public key is empty")
+        rng = _rng(seed)
+        L = ctx.size_Ql(pt.chain_index())
+        nat = ctx.native
+        u = ctx._ntt(ctx._signed_to_rns(rng.integers(-1, 2, ctx.N), L), L)
+        out = ctx._empty(2, L, ctx.N)
+        for k in range(2):
+            e = ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), L), L)
+            nat.poly_mul(self.data[k, :L].contiguous(), u, out[k], L)
+            nat.poly_add(out[k], e, out[k], L)
+        nat.poly_add(out[0], pt.data, out[0], L)
+        ct = ciphertext()
+        ct.data, ct._chain_index, ct._scale = out, pt.chain_index(), pt.scale()
+        return ct
+
+
+class secret_key:
+    """PhantomSecretKey (src/secretkey.cu): ternary secret, NTT form over all |QP| primes."""
+
+    def __init__(self, ctx: context | None = None, seed=None):
+        self.sk = None
+        self.coeffs = None
+        if ctx is not None:
+            rng = _rng(seed)
+            self._set(ctx, rng.integers(-1, 2, ctx.N).astype(np.int64))
+
+    def _set(self, ctx, coeffs):
+        self.ctx = ctx
+        self.coeffs = coeffs
+        QP = len(ctx.moduli)
+        self.sk = ctx._ntt(ctx._signed_to_rns(coeffs, QP), QP)
+
+    def generate_sparse(self, ctx: context, hamming_weight: int, seed=None):
+        """Sparse ternary secret with `hamming_weight` nonzeros (src/secretkey.cu:513-576)."""
+        if not 0 < hamming_weight <= ctx.N:
+            raise ValueError("hamming weight out of range")
+        rng = _rng(seed)
+        c = np.zeros(ctx.N, dtype=np.int64)
+        idx = rng.choice(ctx.N, size=hamming_weight, replace=False)
+        c[idx] = rng.choice(np.array([-1, 1], dtype=np.int64), size=hamming_weight)
+        self._set(ctx, c)
+        return self
+
+    def _require(self):
+        if self.sk is None:
+            raise ValueError("secret key is not generated")
+
+    def _kswitch_key(self, ctx, new_key, rng):
+        """generate_one_kswitch_key (src/secretkey.cu:354-398) via pfa_kswitch_key."""
+        QP = len(ctx.moduli)
+        dnum = ctx.dnum
+        a = _torch().stack([ctx._uniform(rng, QP) for _ in range(dnum)])
+        e = _torch().stack([ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), QP), QP) for _ in range(dnum)])
+        out = ctx._empty(dnum, 2, QP, ctx.N)
+        ctx.native.kswitch_key(new_key, self.sk, a.contiguous(), e.contiguous(), out)
+        return out
+
+    def gen_publickey(self, ctx: context, seed=None) -> public_key:
+        self._require()
+        rng = _rng(seed)
+        Q = ctx.size_Q
+        a = ctx._uniform(rng, Q)
+        e = ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), Q), Q)
+        pk = ctx._empty(2, Q, ctx.N)
+        nat = ctx.native
+        nat.poly_mul(a, self.sk[:Q].contiguous(), pk[0], Q)
+        nat.poly_add(pk[0], e, pk[0], Q)
+        nat.poly_negate(pk[0], pk[0], Q)
+        pk[1].copy_(a)
+        return public_key(ctx, pk)
+
+    def gen_relinkey(self, ctx: context, seed=None) -> relin_key:
+        """Key for s^2 (src/secretkey.cu:592-615)."""
+        self._require()
+        QP = len(ctx.moduli)
+        s2 = ctx._empty(QP, ctx.N)
+        ctx.native.poly_mul(self.sk, self.sk, s2, QP)
+        return relin_key(self._kswitch_key(ctx, s2, _rng(seed)))
+
+    def _galois_key_for(self, ctx, elt, rng):
+        QP = len(ctx.moduli)
+        rot = ctx._empty(QP, ctx.N)
+        ctx.native.apply_galois_ntt(elt, self.sk, rot, QP)
+        return self._kswitch_key(ctx, rot, rng)
+
+    def create_galois_keys(self, ctx: context, seed=None) -> galois_key:
+        """Keys for every element in params.galois_elts (src/secretkey.cu:642-682)."""
+        self._require()
+        rng = _rng(seed)
+        g = galois_key()
+        for elt in ctx.galois_elts:
+            g.keys[elt] = self._galois_key_for(ctx, elt, rng)
+        return g
+
+    def create_one_galois_key(self, ctx: context, galois_elt_idx: int, target_chain_index: int = 0, seed=None):
+        self._require()
+        elt = ctx.galois_elts[galois_elt_idx]
+        return relin_key(self._galois_key_for(ctx, elt, _rng(seed)))
+
+    def encrypt_symmetric(self, ctx: context, pt: plaintext, seed=None) -> ciphertext:
+        """ct = (-a s + e + m, a) over the plaintext's primes."""
+        self._require()
+        rng = _rng(seed)
+        L = ctx.size_Ql(pt.chain_index())
+        nat = ctx.native
+        a = ctx._uniform(rng, L)
+        e = ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), L), L)
+        out = ctx._empty(2, L, ctx.N)
+        nat.poly_mul(a, self.sk[:L].contiguous(), out[0], L)
+        nat.poly_negate(out[0], out[0], L)
+        nat.poly_add(out[0], e, out[0], L)
+        nat.poly_add(out[0], pt.data, out[0], L)
+        out[1].copy_(a)
+        ct = ciphertext()
+        ct.data, ct._chain_index, ct._scale = out, pt.chain_index(), pt.scale()
+        return ct
+
+    def decrypt(self, ctx: context, ct: ciphertext) -> plaintext:
+        """m = c0 + c1 s (+ c2 s^2) over the ciphertext's primes."""
+        self._require()
+        L = ctx.size_Ql(ct.chain_index())
+        nat = ctx.native
+        s = self.sk[:L].contiguous()
+        m = ct.data[0].clone()
+        t = ctx._empty(L, ctx.N)
+        sp = s.clone()
+        for i in range(1, ct.size()):
+            nat.poly_mul(ct.data[i], sp, t, L)
+            nat.poly_add(m, t, m, L)
+            if i + 1 < ct.size():
+                nat.poly_mul(sp, s, sp, L)
+        pt = plaintext()
+        pt.data, pt._chain_index, pt._scale = m, ct.chain_index(), ct.scale()
+        return pt
+
+
+class ckks_encoder:
+    """PhantomCKKSEncoder (src/ckks.cu): N/2 complex slots, rotation group 5^j."""
+
+    def __init__(self, ctx: context):
+        self.ctx = ctx
+        self._slots = ctx.N // 2
+
+    def slot_count(self) -> int:
+        return self._slots
+
+    def _encode(self, ctx, values, scale, chain_index):
+        t = _torch()
+        v = np.asarray(values, dtype=np.complex128).ravel()
+        if v.size == 0:
+            raise ValueError("Input vector is empty")
+        if v.size > self._slots:
+            raise ValueError("Input vector exceeds max slots")
+        if not 1 <= chain_index <= ctx.size_Q:
+            raise ValueError("chain index out of range")
+        L = ctx.size_Ql(chain_index)
+        out = ctx._empty(L, ctx.N)
+        ctx.native.ckks_encode(t.from_numpy(v).to(ctx.dev), scale, out, L)
+        pt = plaintext()
+        pt.data, pt._chain_index, pt._scale = out, chain_index, float(scale)
+        return pt
+
+    def encode_double_vector(self, ctx, values, scale, chain_index=1):
+        return self._encode(ctx, np.asarray(values, dtype=np.float64), scale, chain_index)
+
+    def encode_complex_vector(self, ctx, values, scale, chain_index=1):
+        return self._encode(ctx, values, scale, chain_index)
+
+    def _decode(self, ctx, pt):
+        t = _torch()
+        out = t.empty(self._slots, dtype=t.complex128, device=ctx.dev)
+        ctx.native.ckks_decode(pt.data, pt.data.shape[0], pt.scale(), out)
+        t.cuda.synchronize(ctx.dev)
+        return out.cpu().numpy()
+
+    def decode_complex_vector(self, ctx, pt):
+        return self._decode(ctx, pt).tolist()
+
+    def decode_double_vector(self, ctx, pt):
+        return self._decode(ctx, pt).real.tolist()
+
+
+# ---------------------------------------------------------------- evaluator
+def _check_same(a: ciphertext, b: ciphertext):
+    if a.chain_index() != b.chain_index():
+        raise ValueError("encrypted1 and encrypted2 parameter mismatch")
+
+
+def _check_scale(a, b):
+    if abs(a.scale() - b.scale()) > 1e-9 * max(abs(a.scale()), 1.0):
+        raise ValueError("scale mismatch")
+
+
+def negate(ctx: context, ct: ciphertext) -> ciphertext:
+    L = ctx.size_Ql(ct.chain_index())
+    out = ctx._empty(*ct.data.shape)
+    for i in range(ct.size()):
+        ctx.native.poly_negate(ct.data[i], out[i], L)
+    return ct._like(out)
+
+
+def add(ctx: context, a: ciphertext, b: ciphertext) -> ciphertext:
+    _check_same(a, b)
+    _check_scale(a, b)
+    if a.size() != b.size():
+        raise ValueError("ciphertext sizes differ")
+    L = ctx.size_Ql(a.chain_index())
+    out = ctx._empty(*a.data.shape)
+    for i in range(a.size()):
+        ctx.native.poly_add(a.data[i], b.data[i], out[i], L)
+    return a._like(out)
+
+
+def add_many(ctx: context, cts, _unused=None) -> ciphertext:
+    if not cts:
+        raise ValueError("empty list")
+    acc = cts[0]
+    for c in cts[1:]:
+        acc = add(ctx, acc, c)
+    return acc
+
+
+def sub(ctx: context, a: ciphertext, b: ciphertext, negate: bool = False) -> ciphertext:
+    _check_same(a, b)
+    _check_scale(a, b)
+    L = ctx.size_Ql(a.chain_index())
+    out = ctx._empty(*a.data.shape)
+    for i in range(a.size()):
+        if negate:
+            ctx.native.poly_sub(b.data[i], a.data[i], out[i], L)
+        else:
+            ctx.native.poly_sub(a.data[i], b.data[i], out[i], L)
+    return a._like(out)
+
+
+def add_plain(ctx: context, ct: ciphertext, pt: plaintext) -> ciphertext:
+    if ct.chain_index() != pt.chain_index():
+        raise ValueError("encrypted and plain parameter mismatch")
+    _check_scale(ct, pt)
+    L = ctx.size_Ql(ct.chain_index())
+    out = ct.data.clone()
+    ctx.native.poly_add(ct.data[0], pt.data, out[0], L)
+    return ct._like(out)
+
+
+def sub_plain(ctx: context, ct: ciphertext, pt: plaintext) -> ciphertext:
+    if ct.chain_index() != pt.chain_index():
+        raise ValueError("encrypted and plain parameter mismatch")
+    _check_scale(ct, pt)
+    L = ctx.size_Ql(ct.chain_index())
+    out = ct.data.clone()
+    ctx.native.poly_sub(ct.data[0], pt.data, out[0], L)
+    return ct._like(out)
+
+
+def multiply_plain(ctx: context, ct: ciphertext, pt: plaintext) -> ciphertext:
+    if ct.chain_index() != pt.chain_index():
+        raise ValueError("encrypted and plain parameter mismatch")
+    L = ctx.size_Ql(ct.chain_index())
+    out = ctx._empty(*ct.data.shape)
+    for i in range(ct.size()):
+        ctx.native.poly_mul(ct.data[i], pt.data, out[i], L)
+    return ct._like(out, scale=ct.scale() * pt.scale())
+
+
+def multiply(ctx: context, a: ciphertext, b: ciphertext) -> ciphertext:
+    """Tensor product of two size-2 ciphertexts -> size 3 (src/evaluate.cu:345-397)."""
+    _check_same(a, b)
+    if a.size() != 2 or b.size() != 2:
+        raise ValueError("multiply expects size-2 ciphertexts")
+    L = ctx.size_Ql(a.chain_index())
+    out = ctx._empty(3, L, ctx.N)
+    ctx.native.tensor(a.chain_index(), a.data, b.data, out)
+    return a._like(out, scale=a.scale() * b.scale())
+
+
+def relinearize(ctx: context, ct: ciphertext, rlk: relin_key) -> ciphertext:
+    if ct.size() != 3:
+        raise ValueError("relinearize expects a size-3 ciphertext")
+    L = ctx.size_Ql(ct.chain_index())
+    out = ctx._empty(2, L, ctx.N)
+    ctx.native.relinearize(ct.chain_index(), ct.data, rlk.data, out)
+    return ct._like(out)
+
+
+def multiply_and_relin(ctx: context, a: ciphertext, b: ciphertext, rlk: relin_key) -> ciphertext:
+    """src/evaluate.cu:1061-1104."""
+    _check_same(a, b)
+    if a.size() != 2 or b.size() != 2:
+        raise ValueError("multiply_and_relin expects size-2 ciphertexts")
+    L = ctx.size_Ql(a.chain_index())
+    out = ctx._empty(2, L, ctx.N)
+    ctx.native.multiply_and_relin(a.chain_index(), a.data, b.data, rlk.data, out)
+    return a._like(out, scale=a.scale() * b.scale())
+
+
+def rescale_to_next(ctx: context, ct: ciphertext) -> ciphertext:
+    """Floor division by q_last (src/evaluate.cu:1582-1602, src/rns.cu:1128-1184)."""
+    L = ctx.size_Ql(ct.chain_index())
+    if L < 2:
+        raise ValueError("end of modulus switching chain reached")
+    out = ctx._empty(ct.size(), L - 1, ctx.N)
+    ctx.native.rescale(ct.chain_index(), ct.data, out)
+    return ct._like(out, chain=ct.chain_index() + 1, scale=ct.scale() / ctx.moduli[L - 1])
+
+
+def mod_switch_to_next(ctx: context, obj):
+    """CKKS modulus drop: remove the last prime, keep the scale."""
+    chain = obj.chain_index()
+    L = ctx.size_Ql(chain)
+    if L < 2:
+        raise ValueError("end of modulus switching chain reached")
+    if isinstance(obj, plaintext):
+        pt = plaintext()
+        pt.data, pt._chain_index, pt._scale = obj.data[:L - 1].contiguous(), chain + 1, obj.scale()
+        return pt
+    return obj._like(obj.data[:, :L - 1].contiguous(), chain=chain + 1)
+
+
+def mod_switch_to(ctx: context, obj, chain_index: int):
+    if chain_index < obj.chain_index():
+        raise ValueError("cannot switch to a higher level modulus")
+    while obj.chain_index() < chain_index:
+        obj = mod_switch_to_next(ctx, obj)
+    return obj
+
+
+def mod_switch_to_inplace(ctx: context, obj, chain_index: int) -> None:
+    r = mod_switch_to(ctx, obj, chain_index)
+    obj.data, obj._chain_index = r.data, r._chain_index
+
+
+def _apply_galois_key(ctx: context, ct: ciphertext, elt: int, key) -> ciphertext:
+    if ct.size() != 2:
+        raise ValueError("ciphertext size must be 2")
+    out = ct.data.clone()
+    ctx.native.apply_galois(ct.chain_index(), out, elt, key)
+    return ct._like(out)
+
+
+def apply_galois(ctx: context, ct: ciphertext, elt: int, glk: galois_key) -> ciphertext:
+    """apply_galois_with_ksk (src/evaluate.cu:1607-1656)."""
+    return _apply_galois_key(ctx, ct, elt, glk.get(elt))
+
+
+def apply_galois_with_key(ctx: context, ct: ciphertext, elt: int, key: relin_key) -> ciphertext:
+    return _apply_galois_key(ctx, ct, elt, key.data)
+
+
+def _naf(step: int):
+    """Non-adjacent form digits (+-2^k) of step, least significant first, from
+    |step| with the sign applied afterwards (include/host/numth.h:17-34)."""
+    sign, v, out, i = step < 0, abs(step), [], 0
+    while v:
+        z = 2 - (v & 3) if v & 1 else 0
+        v = (v - z) >> 1
+        if z:
+            out.append((-z if sign else z) * (1 << i))
+        i += 1
+    return out
+
+
+def rotate(ctx: context, ct: ciphertext, step: int, glk: galois_key) -> ciphertext:
+    """rotate_internal (src/evaluate.cu:1683-1713): direct key, else NAF decomposition."""
+    elt = get_elt_from_step(step, ctx.N)
+    if elt in glk.keys:
+        return apply_galois(ctx, ct, elt, glk)
+    digits = _naf(step)
+    if len(digits) <= 1:
+        raise ValueError("Galois key not present")
+    out = ct
+    for d in digits:
+        if abs(d) != ctx.N // 2:
+            out = rotate(ctx, out, d, glk)
+    return out
+
+
+def rotate_with_key(ctx: context, ct: ciphertext, step: int, key: relin_key) -> ciphertext:
+    return apply_galois_with_key(ctx, ct, get_elt_from_step(step, ctx.N), key)
+
+
+def hoist_rotations(context: context, ct: ciphertext, glk: galois_key, steps) -> list:
+    """One ModUp of c1 shared by all rotations (src/evaluate.cu:1929-2082)."""
+    if ct.size() > 2:
+        raise ValueError("ciphertext size must be 2")
+    if not steps:
+        return []
+    elts = [get_elt_from_step(s, context.N) for s in steps]
+    keys = [glk.get(e) for e in elts]
+    L = context.size_Ql(ct.chain_index())
+    out = context._empty(len(elts), 2, L, context.N)
+    context.native.hoist_rotations(ct.chain_index(), ct.data, elts, keys, out)
+    return [ct._like(out[i]) for i in range(len(elts))]
+
+
+def hoisting(ctx: context, ct: ciphertext, glk: galois_key, steps) -> ciphertext:
+    """Sum of the rotations by `steps`: one ModUp of c1, inner products of all
+    rotations accumulated, one ModDown (src/evaluate.cu:1732-1927)."""
+    if ct.size() > 2:
+        raise ValueError("ciphertext size must be 2")
+    if not steps:
+        return ct._like(ct.data.clone())
+    elts = [get_elt_from_step(s, ctx.N) for s in steps]
+    keys = [glk.get(e) for e in elts]
+    L = ctx.size_Ql(ct.chain_index())
+    out = ctx._empty(2, L, ctx.N)
+    ctx.native.hoisting(ct.chain_index(), ct.data, elts, keys, out)
+    return ct._like(out)

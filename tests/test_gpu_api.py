@@ -1,0 +1,222 @@
+"""GPU tests of the pyPhantom drop-in module, the CKKS encoder and hoisting.
+
+* hoisting (pfa_hoisting) is bit-exact against the oracle, whose restatement of
+  src/evaluate.cu:1732-1927 is pinned in tests/test_oracle.py.
+* The encoder (pfa_ckks_encode/decode) is checked against a numpy statement of
+  the canonical embedding (slot j = m(zeta^(5^j)), evaluated directly at small N)
+  and by round trips.  The reference's special FFT cannot run here (CUDA only),
+  so the plaintext bit pattern is "parity unpinned"; decoded slots are held to
+  the north star's 1e-6 absolute tolerance.
+* The end-to-end flow mirrors the reference's python/examples/ckks.py and
+  examples/3_ckks.cu (decrypt-decode within a tolerance after mul + relin +
+  rescale, rotation and hoisting).
+"""
+import numpy as np
+import pytest
+
+import py_oracle as O
+from gpu_util import empty, first_mismatch, to_dev, to_host, uniform_limbs
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-6
+
+
+def make_ctx(logN, bits, special, steps=()):
+    import pyPhantom as ph
+
+    N = 1 << logN
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, bits))
+    p.set_special_modulus_size(special)
+    p.set_galois_elts(ph.get_elts_from_steps(list(steps), N))
+    return ph, ph.context(p)
+
+
+# ----------------------------------------------------------------- hoisting
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 6, 2, 1), (12, 5, 1, 2), (16, 6, 3, 1)])
+def test_hoisting_matches_oracle(dev, logN, nq, alpha, chain):
+    import pfa_native as P
+
+    N = 1 << logN
+    mods = O.create_coeff_modulus(N, [60] + [50] * (nq - 1) + [60] * alpha)
+    ctx = P.NativeContext(N, mods, alpha)
+    orc = O.Oracle(N, mods, alpha)
+    rng = np.random.default_rng(logN + nq)
+    Ql = orc.size_Ql(chain)
+    ct = uniform_limbs(rng, (2, Ql, N), mods)
+    steps = [1, 3, -2]
+    elts = [P.galois_elt_from_step(s, N) for s in steps]
+    keys = [uniform_limbs(rng, (orc.dnum, 2, len(mods), N), mods) for _ in steps]
+    out = empty((2, Ql, N), dev)
+    ctx.hoisting(chain, to_dev(ct, dev), elts, [to_dev(k, dev) for k in keys], out)
+    got, want = to_host(out), orc.hoisting(chain, ct, elts, keys, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+# ----------------------------------------------------------------- encoder
+def embed_direct(coeffs, n):
+    """slot_j = sum_k m_k zeta^(k 5^j), zeta = exp(2 pi i / 2n), j < n/2."""
+    m2 = 2 * n
+    ks = np.arange(n)
+    exps = np.array([pow(5, j, m2) for j in range(n // 2)])
+    return np.exp(2j * np.pi * (np.outer(exps, ks) % m2) / m2) @ coeffs
+
+
+def test_encoder_matches_direct_embedding(dev):
+    """Decode of a known integer plaintext = the canonical embedding evaluated directly."""
+    import torch
+
+    ph, ctx = make_ctx(11, [60, 50, 50, 60], 1)
+    n = ctx.N
+    rng = np.random.default_rng(1)
+    coeffs = rng.integers(-(2 ** 40), 2 ** 40, n).astype(np.int64)
+    L = ctx.size_Ql(1)
+    pt = ctx._signed_to_rns(coeffs, L)
+    ctx.native.ntt_forward(pt, 1, L, 0)
+    out = torch.empty(n // 2, dtype=torch.complex128, device=dev)
+    ctx.native.ckks_decode(pt, L, 1.0, out)
+    got = out.cpu().numpy()
+    want = embed_direct(coeffs.astype(np.float64), n)
+    assert np.max(np.abs(got - want)) / 2 ** 40 < 1e-9
+
+
+def test_encoder_encode_is_inverse_embedding(dev):
+    """Encode rounds scale * (inverse embedding); re-embedding the integer
+    coefficients gives back the values to within rounding (|err| < n / scale)."""
+    import torch
+
+    ph, ctx = make_ctx(11, [60, 50, 50, 60], 1)
+    n = ctx.N
+    rng = np.random.default_rng(2)
+    vals = rng.uniform(-1, 1, n // 2) + 1j * rng.uniform(-1, 1, n // 2)
+    scale = 2.0 ** 30
+    L = ctx.size_Ql(1)
+    pt = empty((L, n), dev)
+    ctx.native.ckks_encode(torch.from_numpy(vals).to(dev), scale, pt, L)
+    coef = O.Oracle(n, ctx.moduli, 1).ntt_inv(to_host(pt))[0].astype(np.int64)
+    q0 = ctx.moduli[0]
+    coef = np.where(coef > q0 // 2, coef - q0, coef).astype(np.float64)
+    back = embed_direct(coef, n) / scale
+    assert np.max(np.abs(back - vals)) < n / scale
+
+
+@pytest.mark.parametrize("logN,chain", [(12, 1), (16, 1), (16, 3)])
+def test_encode_decode_roundtrip(dev, logN, chain):
+    ph, ctx = make_ctx(logN, [60, 40, 40, 40, 60], 1)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(logN)
+    vals = rng.uniform(-1, 1, enc.slot_count())
+    pt = enc.encode_double_vector(ctx, vals, 2.0 ** 40, chain_index=chain)
+    dec = np.array(enc.decode_double_vector(ctx, pt))
+    assert np.max(np.abs(dec - vals)) < 1e-9
+    cv = vals[:100] + 1j * vals[100:200]
+    pc = enc.encode_complex_vector(ctx, cv, 2.0 ** 40, chain_index=chain)
+    dc = np.array(enc.decode_complex_vector(ctx, pc))
+    assert np.max(np.abs(dc[:100] - cv)) < 1e-9 and np.max(np.abs(dc[100:])) < 1e-9
+
+
+def test_encoder_errors(dev):
+    ph, ctx = make_ctx(12, [60, 40, 60], 1)
+    enc = ph.ckks_encoder(ctx)
+    with pytest.raises(ValueError):
+        enc.encode_double_vector(ctx, [], 2.0 ** 40)
+    with pytest.raises(ValueError):
+        enc.encode_double_vector(ctx, np.zeros(enc.slot_count() + 1), 2.0 ** 40)
+    with pytest.raises(ValueError):
+        enc.encode_double_vector(ctx, [1e30], 2.0 ** 40)  # coefficients beyond 2^62
+
+
+# ----------------------------------------------------------------- end to end
+def test_reference_example_flow(dev):
+    """python/examples/ckks.py of the reference, run against this module."""
+    ph, ctx = make_ctx(14, [60, 40, 40, 60], 1, steps=[1, 2, 3, 4, 5, 6, 7])
+    ph.set_seed(7)
+    scale = 2.0 ** 40
+    sk = ph.secret_key(ctx)
+    pk = sk.gen_publickey(ctx)
+    rlk = sk.gen_relinkey(ctx)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    slots = enc.slot_count()
+    msg = [1.0, 2.0, 3.0, 4.0, 5.0, 6.0, 7.0, 8.0] + [0.0] * (slots - 8)
+    pt = enc.encode_double_vector(ctx, msg, scale, chain_index=1)
+    ct = pk.encrypt_asymmetric(ctx, pt)
+    ct = ph.multiply_and_relin(ctx, ct, ct, rlk)
+    ct = ph.rescale_to_next(ctx, ct)
+    assert ct.chain_index() == 2
+    ct2 = ph.hoisting(ctx, ct, glk, [1, 2, 3, 4, 5, 6, 7])
+    ct = ph.add(ctx, ct, ct2)
+    res = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ct)))
+    sq = np.array(msg) ** 2
+    want = sq + sum(np.roll(sq, -s) for s in range(1, 8))
+    assert np.max(np.abs(res - want)) < 1e-4 * np.max(np.abs(want))
+    assert np.max(np.abs(res - want)) < TOL * 64  # values up to 204, tolerance relative to 1e-6
+
+
+@pytest.mark.parametrize("logN", [13, 16])
+def test_mul_relin_rescale_decodes_within_1e6(dev, logN):
+    """BASELINE config 3 semantics at N = 2^16 (smaller chain for time): fresh
+    ciphertexts of uniform reals in [-1, 1], HMult + relin + rescale, decode
+    within 1e-6 absolute of the exact product."""
+    ph, ctx = make_ctx(logN, [60] + [40] * 5 + [60] * 2, 2)
+    ph.set_seed(logN)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)
+    rlk = sk.gen_relinkey(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(5)
+    a = rng.uniform(-1, 1, enc.slot_count())
+    b = rng.uniform(-1, 1, enc.slot_count())
+    scale = 2.0 ** 40
+    ca = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, a, scale))
+    cb = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, b, scale))
+    fresh = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ca)))
+    assert np.max(np.abs(fresh - a)) < TOL
+    c = ph.rescale_to_next(ctx, ph.multiply_and_relin(ctx, ca, cb, rlk))
+    out = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, c)))
+    assert np.max(np.abs(out - a * b)) < TOL
+    # the same through multiply (size 3) + relinearize
+    c3 = ph.multiply(ctx, ca, cb)
+    assert c3.size() == 3
+    d3 = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, c3)))  # size-3 decrypt uses s^2
+    assert np.max(np.abs(d3 - a * b)) < TOL
+    r = ph.rescale_to_next(ctx, ph.relinearize(ctx, c3, rlk))
+    assert np.array_equal(to_host(r.data), to_host(c.data))
+
+
+def test_rotations_and_conjugation(dev):
+    steps = [1, 2, 4, -1, 0]
+    ph, ctx = make_ctx(13, [60, 40, 40, 60], 1, steps=steps)
+    ph.set_seed(3)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)  # the BASELINE configs' sparse ternary secret
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(8)
+    v = rng.uniform(-1, 1, enc.slot_count()) + 1j * rng.uniform(-1, 1, enc.slot_count())
+    ct = sk.encrypt_symmetric(ctx, enc.encode_complex_vector(ctx, v, 2.0 ** 40))
+    for s in (1, 2, -1, 3, 5):  # 3 = 4 - 1 and 5 = 4 + 1 go through the NAF decomposition
+        r = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, ph.rotate(ctx, ct, s, glk))))
+        assert np.max(np.abs(r - np.roll(v, -s))) < TOL, s
+    conj = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, ph.rotate(ctx, ct, 0, glk))))
+    assert np.max(np.abs(conj - np.conj(v))) < TOL
+    hs = ph.hoist_rotations(ctx, ct, glk, [1, 2, 4])
+    for s, h in zip([1, 2, 4], hs):
+        r = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, h)))
+        assert np.max(np.abs(r - np.roll(v, -s))) < TOL
+    with pytest.raises(RuntimeError):
+        ph.hoist_rotations(ctx, ct, glk, [5])  # no key for step 5
+
+
+def test_api_errors(dev):
+    ph, ctx = make_ctx(12, [60, 40, 40, 60], 1)
+    sk = ph.secret_key(ctx)
+    enc = ph.ckks_encoder(ctx)
+    c1 = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, [1.0], 2.0 ** 30))
+    c2 = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, [1.0], 2.0 ** 30, chain_index=2))
+    with pytest.raises(ValueError):
+        ph.add(ctx, c1, c2)
+    with pytest.raises(ValueError):
+        ph.rescale_to_next(ctx, ph.rescale_to_next(ctx, ph.rescale_to_next(ctx, c1)))
+    with pytest.raises(ValueError):
+        ph.params(ph.scheme_type.bfv)

@@ -506,3 +506,30 @@ def test_rotation_decrypts():
     dec_h = (hr[0].astype(object) + hr[1].astype(object) * sQ) % qs
     noise = centered_coeffs(o, ((dec_h - m_rot) % qs).astype(np.uint64), Ql)
     assert max(abs(x) for x in noise) < 2 ** 30
+
+
+def test_hoisting_decrypts_to_sum_of_rotations():
+    """hoisting(ct, steps) decrypts to sum_e sigma_e(m) up to key-switching noise,
+    and is not the sum of separately moved-down rotations (one ModDown of the sum)."""
+    N, nq, alpha, chain = 64, 4, 2, 1
+    mods = make_chain(N, nq, alpha)
+    o = O.Oracle(N, mods, alpha)
+    rng = np.random.default_rng(31)
+    _, s = ternary_ntt(o, rng, 16)
+    steps = [1, 2, -1]
+    elts = [O.elt_from_step(t, N) for t in steps]
+    keys = [o.kswitch_key(o.apply_galois_ntt(s, e), s, uniform_qp(o, rng, o.dnum), small_err_ntt(o, rng, o.dnum))
+            for e in elts]
+    Ql = o.size_Ql(chain)
+    ct = np.stack([np.stack([rng.integers(0, q, N, dtype=np.uint64) for q in mods[:Ql]]) for _ in range(2)])
+    h = o.hoisting(chain, ct, elts, keys)
+    sQ = s[:Ql].astype(object)
+    qs = np.array(mods[:Ql], dtype=object)[:, None]
+    m = ((ct[0].astype(object) + ct[1].astype(object) * sQ) % qs).astype(np.uint64)
+    want = sum(o.apply_galois_ntt(m, e).astype(object) for e in elts) % qs
+    dec = (h[0].astype(object) + h[1].astype(object) * sQ) % qs
+    noise = centered_coeffs(o, ((dec - want) % qs).astype(np.uint64), Ql)
+    assert max(abs(x) for x in noise) < 2 ** 30
+    rots = o.hoist_rotations(chain, ct, elts, keys)
+    summed = sum(r.astype(object) for r in rots) % qs
+    assert not np.array_equal(summed.astype(np.uint64), h)
