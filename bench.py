@@ -146,9 +146,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-hmult", action="store_true")
-    ap.add_argument("--mode", choices=["full", "ntt", "copy"], default="full",
+    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult"], default="full",
                     help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
-                         "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE)")
+                         "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
+                         "config-3 HMult + relin + rescale")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -166,6 +167,11 @@ def main():
     ctx = P.NativeContext(N, mods, 1)
     n_batches = 10  # 10 x 35 MiB > 256 MiB Infinity Cache
     batches = [uniform(torch, (POLYS, LIMBS, N), mods, dev, gen) for _ in range(n_batches)]
+    if args.mode == "hmult":
+        del batches
+        r = time_hmult(torch, P, dev, gen, 24, 4, args.steps, args.warmup)
+        log(f"bench: hmult mode, config 3: {r['ms']} ms")
+        return
     if args.mode == "copy":
         dst = torch.empty_like(batches[0])
         for i in range(args.steps):

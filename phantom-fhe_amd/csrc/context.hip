@@ -299,11 +299,49 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     }
 }
 
+static Arena &arena_for(const Ctx &c, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(c.arena_mu);
+    Arena *&a = c.arenas[{std::this_thread::get_id(), s}];
+    if (!a) a = new Arena();
+    return *a;
+}
+
+Scratch::Scratch(const Ctx &c, hipStream_t s) : a_(arena_for(c, s)) {
+    marks_.reserve(a_.chunks.size());
+    for (auto &ch : a_.chunks) marks_.push_back(ch.top);
+}
+
+Scratch::~Scratch() {
+    for (size_t i = 0; i < a_.chunks.size(); ++i) a_.chunks[i].top = i < marks_.size() ? marks_[i] : 0;
+}
+
+void *Scratch::alloc_bytes(size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    if (bytes == 0) bytes = 256;
+    for (auto &ch : a_.chunks) {
+        if (ch.cap - ch.top >= bytes) {
+            void *p = ch.base + ch.top;
+            ch.top += bytes;
+            return p;
+        }
+    }
+    const size_t cap = std::max(bytes, (size_t)256 << 20);
+    void *p = nullptr;
+    PFA_HIP(hipMalloc(&p, cap));
+    a_.chunks.push_back(Arena::Chunk{(char *)p, cap, bytes});
+    return p;
+}
+
 static void destroy(Ctx *c) {
     if (!c) return;
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c->device);
+    (void)hipDeviceSynchronize();
+    for (auto &kv : c->arenas) {
+        for (auto &ch : kv.second->chunks) (void)hipFree(ch.base);
+        delete kv.second;
+    }
     for (void *p : c->allocations) (void)hipFree(p);
     (void)hipSetDevice(prev);
     delete c;

@@ -163,10 +163,9 @@ int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_value
         require(L >= 1 && L <= c.Q, "plaintext limb count out of range");
         require(scale > 0 && std::isfinite(scale), "scale out of bounds");
         const hipStream_t s = as_stream(stream);
-        double2 *buf = nullptr;
-        uint32_t *flag = nullptr;
-        PFA_HIP(hipMallocAsync((void **)&buf, 2 * (size_t)M * sizeof(double2), s));
-        PFA_HIP(hipMallocAsync((void **)&flag, sizeof(uint32_t), s));
+        Scratch sc(c, s);
+        double2 *buf = sc.alloc<double2>(2 * (size_t)M);
+        uint32_t *flag = sc.alloc<uint32_t>(1);
         hipLaunchKernelGGL(k_zero_flag, dim3(1), dim3(1), 0, s, flag);
         hipLaunchKernelGGL(k_enc_scatter, ew_grid(M), dim3(kThreads), 0, s, (const double2 *)values,
                            (uint32_t)n_values, buf, c.slot_perm, M);
@@ -176,8 +175,6 @@ int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_value
         PFA_HIP(hipGetLastError());
         uint32_t h_flag = 0;
         PFA_HIP(hipMemcpyAsync(&h_flag, flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-        PFA_HIP(hipFreeAsync(buf, s));
-        PFA_HIP(hipFreeAsync(flag, s));
         PFA_HIP(hipStreamSynchronize(s));
         require(h_flag == 0, "encoded values are too large");
         NttLaunch fw{out, out, 0, 0, 1, (uint32_t)L};
@@ -193,11 +190,10 @@ int pfa_ckks_decode(const pfa_context *ctx, const uint64_t *in, size_t L, double
         require(scale > 0 && std::isfinite(scale), "scale out of bounds");
         const hipStream_t s = as_stream(stream);
         const uint32_t M = c.N / 2;
-        uint64_t *coef = nullptr;
-        double2 *buf = nullptr;
         const uint32_t Lc = L >= 2 ? 2 : 1;
-        PFA_HIP(hipMallocAsync((void **)&coef, (size_t)Lc * c.N * sizeof(uint64_t), s));
-        PFA_HIP(hipMallocAsync((void **)&buf, 2 * (size_t)M * sizeof(double2), s));
+        Scratch sc(c, s);
+        uint64_t *coef = sc.alloc((size_t)Lc * c.N);
+        double2 *buf = sc.alloc<double2>(2 * (size_t)M);
         NttLaunch inv{in, coef, 0, 0, 1, Lc};
         ntt_inverse(c, inv, s);
         const uint64_t q0 = c.moduli[0], q1 = c.moduli[Lc > 1 ? 1 : 0];
@@ -208,8 +204,6 @@ int pfa_ckks_decode(const pfa_context *ctx, const uint64_t *in, size_t L, double
         double2 *W = fft(buf, buf + M, M, 1.0, s);
         hipLaunchKernelGGL(k_dec_gather, ew_grid(M), dim3(kThreads), 0, s, W, (double2 *)values, c.slot_perm, M);
         PFA_HIP(hipGetLastError());
-        PFA_HIP(hipFreeAsync(buf, s));
-        PFA_HIP(hipFreeAsync(coef, s));
     });
 }
 

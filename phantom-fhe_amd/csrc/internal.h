@@ -4,8 +4,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
+#include <utility>
 #include <vector>
 
 #include "phantom_amd.h"
@@ -72,6 +76,19 @@ struct Level {
     ulonglong2 *rescale_inv = nullptr;
 };
 
+// Device workspace of one (host thread, stream): chunks grown on demand and
+// kept until the context is destroyed, handed out by a bump pointer.  Work on
+// one stream runs in order, so memory released by a finished scope can be
+// reused by the next call at once.  Keyed by thread as well as stream because
+// hipStreamPerThread is one handle value shared by every thread.
+struct Arena {
+    struct Chunk {
+        char *base;
+        size_t cap, top;
+    };
+    std::vector<Chunk> chunks;
+};
+
 struct Ctx {
     int device = 0;
     uint32_t N = 0, logN = 0;
@@ -103,6 +120,8 @@ struct Ctx {
     uint32_t *slot_perm = nullptr;   // [N/2] CKKS slot j -> DFT index (5^j mod 2N - 1) / 4
     std::vector<Level> levels;  // index = chain index (0 unused)
     std::vector<void *> allocations;
+    mutable std::mutex arena_mu;
+    mutable std::map<std::pair<std::thread::id, hipStream_t>, Arena *> arenas;
 
     uint32_t size_Ql(uint32_t chain) const { return Q - (chain - 1); }
     const Level &level(uint32_t chain) const {
@@ -126,6 +145,25 @@ T *Ctx::upload(const std::vector<T> &v) {
 
 Ctx *ctx_of(const pfa_context *c);
 void encoder_init(Ctx &c);
+
+// RAII scope over the calling thread's workspace for stream s: alloc() hands
+// out 256-byte-aligned device memory, all of it released when the scope ends.
+class Scratch {
+  public:
+    Scratch(const Ctx &c, hipStream_t s);
+    ~Scratch();
+    Scratch(const Scratch &) = delete;
+    Scratch &operator=(const Scratch &) = delete;
+    template <class T = uint64_t>
+    T *alloc(size_t elems) {
+        return (T *)alloc_bytes(elems * sizeof(T));
+    }
+
+  private:
+    void *alloc_bytes(size_t bytes);
+    Arena &a_;
+    std::vector<size_t> marks_;
+};
 
 // ---------------------------------------------------------------- launchers
 // NTT over M polys x L limbs; see NttBatch in ntt_kernels.h for the fields.

@@ -82,10 +82,9 @@ template <bool FWD>
 void fused(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     const uint32_t jobs = b.M * b.L;
     const uint32_t words = kXcds + jobs + 1;
-    uint32_t *ctl = nullptr;
-    uint64_t *scratch = nullptr;
-    PFA_HIP(hipMallocAsync((void **)&ctl, words * sizeof(uint32_t), s));
-    PFA_HIP(hipMallocAsync((void **)&scratch, (size_t)jobs * c.N * sizeof(uint64_t), s));
+    Scratch sc(c, s);
+    uint32_t *ctl = sc.alloc<uint32_t>(words);
+    uint64_t *scratch = sc.alloc((size_t)jobs * c.N);
     hipLaunchKernelGGL(k_zero_u32, dim3((words + 255) / 256), dim3(256), 0, s, ctl, words);
     FusedCtl f{ctl, ctl + kXcds, ctl + kXcds + jobs, scratch};
     const dim3 grid((uint32_t)c.n_cu * (uint32_t)c.fused_wpc);
@@ -94,8 +93,6 @@ void fused(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     else
         hipLaunchKernelGGL((ntt_inv_fused<8, 8>), grid, dim3(256), 0, s, b, t, f, (uint32_t)c.fused_lag);
     PFA_HIP(hipGetLastError());
-    PFA_HIP(hipFreeAsync(scratch, s));
-    PFA_HIP(hipFreeAsync(ctl, s));
 }
 
 #define PFA_NTT_DISPATCH(FN)                                                 \

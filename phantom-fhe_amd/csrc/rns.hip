@@ -239,20 +239,6 @@ k_kswitch_key(const uint64_t *new_key, const uint64_t *s, const uint64_t *a, con
 }
 
 // ------------------------------------------------------------ host helpers
-// Stream-ordered temporary (the counterpart of cuda_auto_ptr).
-struct Tmp {
-    uint64_t *p = nullptr;
-    hipStream_t s;
-    Tmp(size_t elems, hipStream_t st) : s(st) {
-        PFA_HIP(hipMallocAsync((void **)&p, std::max<size_t>(elems, 1) * sizeof(uint64_t), s));
-    }
-    ~Tmp() {
-        if (p) (void)hipFreeAsync(p, s);
-    }
-    Tmp(const Tmp &) = delete;
-    Tmp &operator=(const Tmp &) = delete;
-};
-
 inline dim3 grid(const Ctx &c, uint32_t y, uint32_t z = 1) { return dim3(c.N / kThreads, y, z); }
 
 void check_chain(const Ctx &c, size_t chain) {
@@ -271,11 +257,12 @@ void op_modup(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, h
     check_alpha(c);
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
-    Tmp t((size_t)Ql * c.N, s);
-    NttLaunch inv{c2, t.p, 0, 0, 1, Ql};
+    Scratch sc(c, s);
+    uint64_t *t = sc.alloc((size_t)Ql * c.N);
+    NttLaunch inv{c2, t, 0, 0, 1, Ql};
     inv.scale = lv.modup_scale;
     ntt_inverse(c, inv, s);
-    hipLaunchKernelGGL(k_modup_bconv, grid(c, lv.beta), dim3(kThreads), 0, s, t.p, c2, out, lv.modup_mat, c.mod,
+    hipLaunchKernelGGL(k_modup_bconv, grid(c, lv.beta), dim3(kThreads), 0, s, t, c2, out, lv.modup_mat, c.mod,
                        c.ratio, Ql, alpha, c.Q, c.N);
     PFA_HIP(hipGetLastError());
     // NTT every slab except its own digit's limbs (ntt_modup.cu:670-717)
@@ -308,18 +295,19 @@ void op_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, ui
     check_chain(c, chain);
     check_alpha(c);
     const uint32_t Ql = c.size_Ql(chain), alpha = c.P, QlP = Ql + alpha;
-    Tmp xP((size_t)M * alpha * c.N, s);
-    NttLaunch inv{cx + (size_t)Ql * c.N, xP.p, (uint64_t)QlP * c.N, (uint64_t)alpha * c.N, M, alpha};
+    Scratch sc(c, s);
+    uint64_t *xP = sc.alloc((size_t)M * alpha * c.N);
+    NttLaunch inv{cx + (size_t)Ql * c.N, xP, (uint64_t)QlP * c.N, (uint64_t)alpha * c.N, M, alpha};
     inv.start = c.Q;
     inv.scale = c.moddown_scale;
     ntt_inverse(c, inv, s);
-    Tmp d((size_t)M * Ql * c.N, s);
-    hipLaunchKernelGGL(k_moddown_bconv, grid(c, M), dim3(kThreads), 0, s, xP.p, d.p, c.moddown_mat, c.mod, c.ratio,
+    uint64_t *d = sc.alloc((size_t)M * Ql * c.N);
+    hipLaunchKernelGGL(k_moddown_bconv, grid(c, M), dim3(kThreads), 0, s, xP, d, c.moddown_mat, c.mod, c.ratio,
                        Ql, alpha, c.Q, c.N);
     PFA_HIP(hipGetLastError());
-    NttLaunch fw{d.p, d.p, 0, 0, M, Ql};
+    NttLaunch fw{d, d, 0, 0, M, Ql};
     ntt_forward(c, fw, s);
-    hipLaunchKernelGGL(k_moddown_final, grid(c, Ql, M), dim3(kThreads), 0, s, cx, d.p, out, base, c.mod, c.pinv,
+    hipLaunchKernelGGL(k_moddown_final, grid(c, Ql, M), dim3(kThreads), 0, s, cx, d, out, base, c.mod, c.pinv,
                        Ql, QlP, c.N);
     PFA_HIP(hipGetLastError());
 }
@@ -331,11 +319,12 @@ void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64
     const Level &lv = c.level(chain);
     const uint32_t QlP = lv.Ql + c.P;
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
-    Tmp mu((size_t)lv.beta * QlP * c.N, s);
-    op_modup(c, chain, c2, mu.p, s);
-    Tmp cx((size_t)2 * QlP * c.N, s);
-    op_inner(c, chain, mu.p, key, dnum, cx.p, 0, s);
-    op_moddown(c, chain, cx.p, 2, out, base, s);
+    Scratch sc(c, s);
+    uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
+    op_modup(c, chain, c2, mu, s);
+    uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
+    op_inner(c, chain, mu, key, dnum, cx, 0, s);
+    op_moddown(c, chain, cx, 2, out, base, s);
 }
 
 void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1,
@@ -359,17 +348,18 @@ void op_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size,
     const uint32_t L = lv.Ql;
     require(L >= 2, "cannot rescale at the last level");
     require(size >= 1 && size <= 65535, "bad ciphertext size");
-    Tmp last((size_t)size * c.N, s);
-    NttLaunch inv{in + (size_t)(L - 1) * c.N, last.p, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
+    Scratch sc(c, s);
+    uint64_t *last = sc.alloc((size_t)size * c.N);
+    NttLaunch inv{in + (size_t)(L - 1) * c.N, last, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
     inv.start = L - 1;
     ntt_inverse(c, inv, s);
-    Tmp t((size_t)size * (L - 1) * c.N, s);
-    hipLaunchKernelGGL(k_rescale_reduce, grid(c, L - 1, size), dim3(kThreads), 0, s, last.p, t.p, c.mod, c.ratio,
+    uint64_t *t = sc.alloc((size_t)size * (L - 1) * c.N);
+    hipLaunchKernelGGL(k_rescale_reduce, grid(c, L - 1, size), dim3(kThreads), 0, s, last, t, c.mod, c.ratio,
                        L - 1, c.N);
     PFA_HIP(hipGetLastError());
-    NttLaunch fw{t.p, t.p, 0, 0, size, L - 1};
+    NttLaunch fw{t, t, 0, 0, size, L - 1};
     ntt_forward(c, fw, s);
-    hipLaunchKernelGGL(k_rescale_final, grid(c, L - 1, size), dim3(kThreads), 0, s, in, t.p, out, c.mod,
+    hipLaunchKernelGGL(k_rescale_final, grid(c, L - 1, size), dim3(kThreads), 0, s, in, t, out, c.mod,
                        lv.rescale_inv, L, c.N);
     PFA_HIP(hipGetLastError());
 }
@@ -432,9 +422,10 @@ int pfa_multiply_and_relin(const pfa_context *ctx, size_t chain_index, const uin
         check_chain(c, chain_index);
         const hipStream_t s = as_stream(stream);
         const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
-        Tmp c2(LN, s);
-        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2.p, s);
-        op_keyswitch(c, (uint32_t)chain_index, c2.p, rlk, key_dnum, out, Bases{{out, out + LN}}, s);
+        Scratch sc(c, s);
+        uint64_t *c2 = sc.alloc(LN);
+        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2, s);
+        op_keyswitch(c, (uint32_t)chain_index, c2, rlk, key_dnum, out, Bases{{out, out + LN}}, s);
     });
 }
 
@@ -495,11 +486,12 @@ int pfa_apply_galois(const pfa_context *ctx, size_t chain_index, uint64_t *ct, u
         const hipStream_t s = as_stream(stream);
         const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
         const size_t LN = (size_t)Ql * c.N;
-        Tmp t(2 * LN, s);
-        op_galois(c, elt, ct, t.p, Ql, s);
-        op_galois(c, elt, ct + LN, t.p + LN, Ql, s);
+        Scratch sc(c, s);
+        uint64_t *t = sc.alloc(2 * LN);
+        op_galois(c, elt, ct, t, Ql, s);
+        op_galois(c, elt, ct + LN, t + LN, Ql, s);
         // c0' = sigma(c0) + KS0(sigma(c1)), c1' = KS1(sigma(c1))  (src/evaluate.cu:1607-1656)
-        op_keyswitch(c, (uint32_t)chain_index, t.p + LN, key, key_dnum, ct, Bases{{t.p, nullptr}}, s);
+        op_keyswitch(c, (uint32_t)chain_index, t + LN, key, key_dnum, ct, Bases{{t, nullptr}}, s);
     });
 }
 
@@ -516,14 +508,15 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
         const uint32_t Ql = lv.Ql, QlP = Ql + c.P;
         const size_t LN = (size_t)Ql * c.N;
         for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
-        Tmp mu((size_t)lv.beta * QlP * c.N, s);
-        op_modup(c, chain, ct + LN, mu.p, s);
-        Tmp cx((size_t)2 * QlP * c.N, s);
+        Scratch sc(c, s);
+        uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
+        op_modup(c, chain, ct + LN, mu, s);
+        uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
         for (size_t e = 0; e < n; ++e) {
             uint64_t *o = out + e * 2 * LN;
             op_galois(c, elts[e], ct, o, Ql, s);
-            op_inner(c, chain, mu.p, keys[e], key_dnum, cx.p, elts[e], s);
-            op_moddown(c, chain, cx.p, 2, o, Bases{{o, nullptr}}, s);
+            op_inner(c, chain, mu, keys[e], key_dnum, cx, elts[e], s);
+            op_moddown(c, chain, cx, 2, o, Bases{{o, nullptr}}, s);
         }
     });
 }
@@ -540,21 +533,22 @@ int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct,
         const uint32_t Ql = lv.Ql, QlP = Ql + c.P;
         const size_t LN = (size_t)Ql * c.N;
         for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
-        Tmp mu((size_t)lv.beta * QlP * c.N, s);
-        op_modup(c, chain, ct + LN, mu.p, s);
-        Tmp cx((size_t)2 * QlP * c.N, s);
-        Tmp c0(2 * LN, s);  // accumulated sigma(c0), and one sigma(c0) term
+        Scratch sc(c, s);
+        uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
+        op_modup(c, chain, ct + LN, mu, s);
+        uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
+        uint64_t *c0 = sc.alloc(2 * LN);  // accumulated sigma(c0), and one sigma(c0) term
         for (size_t e = 0; e < n; ++e) {
-            op_galois(c, elts[e], ct, e == 0 ? c0.p : c0.p + LN, Ql, s);
+            op_galois(c, elts[e], ct, e == 0 ? c0 : c0 + LN, Ql, s);
             if (e > 0) {
-                hipLaunchKernelGGL(k_poly_binop, grid(c, Ql), dim3(kThreads), 0, s, (int)kAdd, c0.p, c0.p + LN, c0.p,
+                hipLaunchKernelGGL(k_poly_binop, grid(c, Ql), dim3(kThreads), 0, s, (int)kAdd, c0, c0 + LN, c0,
                                    c.mod, c.ratio, 0u, c.N);
                 PFA_HIP(hipGetLastError());
             }
-            op_inner(c, chain, mu.p, keys[e], key_dnum, cx.p, elts[e], s, e > 0);
+            op_inner(c, chain, mu, keys[e], key_dnum, cx, elts[e], s, e > 0);
         }
         // c0' = sum sigma(c0) + ModDown(acc0), c1' = ModDown(acc1)
-        op_moddown(c, chain, cx.p, 2, out, Bases{{c0.p, nullptr}}, s);
+        op_moddown(c, chain, cx, 2, out, Bases{{c0, nullptr}}, s);
     });
 }
 

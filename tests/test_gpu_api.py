@@ -186,8 +186,14 @@ def test_mul_relin_rescale_decodes_within_1e6(dev, logN):
 
 
 def test_rotations_and_conjugation(dev):
+    """Rotations (direct and NAF) and conjugation decode within 1e-6.  The special
+    modulus must dominate each key digit: hybrid key switching leaves an error
+    ~ (Q_digit / P) (2N/pi) sigma sqrt(N) / scale in slot 0, because the ModUp
+    digit is the uncentred residue in [0, Q_digit) (the oracle, i.e. the
+    reference's algorithm, shows the same).  With one 60-bit special prime and a
+    60-bit first digit that term alone is ~1e-6, so P = 2 x 60-bit here."""
     steps = [1, 2, 4, -1, 0]
-    ph, ctx = make_ctx(13, [60, 40, 40, 60], 1, steps=steps)
+    ph, ctx = make_ctx(13, [60, 40, 40, 40, 60, 60], 2, steps=steps)
     ph.set_seed(3)
     sk = ph.secret_key(ctx).generate_sparse(ctx, 192)  # the BASELINE configs' sparse ternary secret
     glk = sk.create_galois_keys(ctx)
