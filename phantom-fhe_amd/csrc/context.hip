@@ -151,6 +151,8 @@ static void create_coeff_modulus(uint64_t N, const int *bits, size_t count, uint
 }
 
 // ---------------------------------------------------------------- context
+static uint64_t two32_mod(uint64_t q) { return (uint64_t)(((u128)1 << 32) % q); }
+
 static uint64_t prod_mod(const uint64_t *m, size_t n, size_t skip, uint64_t p) {
     uint64_t r = 1 % p;
     for (size_t k = 0; k < n; ++k)
@@ -246,24 +248,36 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
 
     // ModDown constants (src/rns.cu:107-138, src/rns.cu:193-194)
     {
-        std::vector<ulonglong2> sc(alpha), pinv(c.Q), pq(QP);
+        std::vector<ulonglong2> sc(alpha), pinv(c.Q), pinv_p(c.Q), pq(QP), bc((size_t)alpha * c.Q * 2),
+            unit((size_t)c.Q * 2);
         std::vector<uint64_t> mat((size_t)alpha * c.Q);
         for (uint32_t j = 0; j < alpha; ++j) {
             const uint64_t p = Pm[j];
             sc[j] = ntt_pair(invmod(prod_mod(Pm, alpha, j, p), p), p);
-            for (uint32_t i = 0; i < c.Q; ++i) mat[(size_t)j * c.Q + i] = prod_mod(Pm, alpha, j, Qm[i]);
+            for (uint32_t i = 0; i < c.Q; ++i) {
+                const uint64_t m = prod_mod(Pm, alpha, j, Qm[i]);
+                mat[(size_t)j * c.Q + i] = m;
+                bc[((size_t)j * c.Q + i) * 2] = ntt_pair(m, Qm[i]);
+                bc[((size_t)j * c.Q + i) * 2 + 1] = ntt_pair(mulmod(m, two32_mod(Qm[i]), Qm[i]), Qm[i]);
+            }
         }
         for (uint32_t i = 0; i < c.Q; ++i) {
             const uint64_t q = Qm[i];
             const uint64_t pm = prod_mod(Pm, alpha, alpha, q);
             pinv[i] = shoup_pair(invmod(pm, q), q);
+            pinv_p[i] = ntt_pair(invmod(pm, q), q);
             pq[i] = shoup_pair(pm, q);
+            unit[(size_t)i * 2] = ntt_pair(1 % q, q);
+            unit[(size_t)i * 2 + 1] = ntt_pair(two32_mod(q), q);
         }
         for (uint32_t j = 0; j < alpha; ++j) pq[c.Q + j] = ulonglong2{0, 0};
         c.moddown_scale = c.upload(sc);
         c.moddown_mat = c.upload(mat);
         c.pinv = c.upload(pinv);
         c.pmodq = c.upload(pq);
+        c.moddown_bc = c.upload(bc);
+        c.unit_bc = c.upload(unit);
+        c.pinv_p = c.upload(pinv_p);
     }
 
     encoder_init(c);
@@ -277,6 +291,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         lv.beta = (Ql + alpha - 1) / alpha;
         std::vector<ulonglong2> sc(Ql);
         std::vector<uint64_t> mat((size_t)lv.beta * alpha * QlP, 0);
+        std::vector<ulonglong2> bc((size_t)lv.beta * alpha * QlP * 2, ulonglong2{0, 0});
         for (uint32_t b = 0; b < lv.beta; ++b) {
             const uint32_t st = b * alpha, sz = std::min(alpha, Ql - st);
             for (uint32_t i = 0; i < sz; ++i) {
@@ -284,18 +299,28 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
                 sc[st + i] = ntt_pair(invmod(prod_mod(Qm + st, sz, i, q), q), q);
                 for (uint32_t r = 0; r < QlP; ++r) {
                     const uint64_t p = moduli[c.qlp_row(Ql, r)];
-                    mat[((size_t)b * alpha + i) * QlP + r] = prod_mod(Qm + st, sz, i, p);
+                    const uint64_t m = prod_mod(Qm + st, sz, i, p);
+                    const size_t k = ((size_t)b * alpha + i) * QlP + r;
+                    mat[k] = m;
+                    bc[k * 2] = ntt_pair(m, p);
+                    bc[k * 2 + 1] = ntt_pair(mulmod(m, two32_mod(p), p), p);
                 }
             }
         }
         lv.modup_scale = c.upload(sc);
         lv.modup_mat = c.upload(mat);
-        std::vector<ulonglong2> rs(Ql > 1 ? Ql - 1 : 0);
+        lv.modup_bc = c.upload(bc);
+        std::vector<ulonglong2> rs(Ql > 1 ? Ql - 1 : 0), rsp(Ql > 1 ? Ql - 1 : 0);
         if (Ql > 1) {
             const uint64_t ql = Qm[Ql - 1];
-            for (uint32_t j = 0; j + 1 < Ql; ++j) rs[j] = shoup_pair(invmod(ql % Qm[j], Qm[j]), Qm[j]);
+            for (uint32_t j = 0; j + 1 < Ql; ++j) {
+                const uint64_t v = invmod(ql % Qm[j], Qm[j]);
+                rs[j] = shoup_pair(v, Qm[j]);
+                rsp[j] = ntt_pair(v, Qm[j]);
+            }
         }
         lv.rescale_inv = c.upload(rs);
+        lv.rescale_inv_p = c.upload(rsp);
     }
 }
 

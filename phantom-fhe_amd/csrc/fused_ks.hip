@@ -1,0 +1,501 @@
+// Fused key-switching and rescale pipelines.
+//
+// The staged path (rns.hip) runs ModUp as INTT -> BConv -> NTT -> inner
+// product, and ModDown / rescale as INTT -> BConv -> NTT -> epilogue, each a
+// separate kernel with its result round-tripping through HBM.  Here the base
+// conversion is computed inside the load stage of the forward NTT's columns
+// pass, and the consumer of the forward NTT (the key-switch inner product, the
+// ModDown epilogue, the rescale epilogue) runs inside its rows pass:
+//
+//   key switch c2 -> (cx0, cx1) over QlP:
+//     1. INTT(c2) * [(Q_b/q_i)^-1]_{q_i}                       (ntt_inverse)
+//     2. k_bconv_cols: per digit b and target limb r outside digit b,
+//        y = sum_i t_i [Q_b/q_i]_{p_r} then the columns pass    -> I[b][r]
+//     3. k_inner_rows: per target limb r, for every digit b: the rows pass
+//        of I[b][r] (or c2 itself when r is in digit b), times key[b][k][r],
+//        accumulated over b                                      -> cx[k][r]
+//   ModDown cx -> out over Ql:
+//     1. INTT(cx_P) * [(P/p_j)^-1]_{p_j}                        (ntt_inverse)
+//     2. k_bconv_cols: y = sum_j xP_j [P/p_j]_{q_i}, columns pass -> D[m][i]
+//     3. k_epi_rows: rows pass of D, out = base + (cx - D) [P^-1]_{q_i}
+//   rescale c -> c' over Q_{l-1}:
+//     1. INTT of the last limb                                  (ntt_inverse)
+//     2. k_bconv_cols with one input limb and factor 1 (c_last mod q_j)
+//     3. k_epi_rows: out = (c - D) [q_last^-1]_{q_j}
+//
+// Every step is the staged path's formula (the reference's: src/rns_bconv.cu
+// :455-628 ModUp, src/eval_key_switch.cu:175-230 inner product,
+// src/rns_bconv.cu:212-229 and include/ntt_radix8_tmpl.cuh:216-233 ModDown,
+// src/rns.cu:1128-1158 rescale); only where the values live changes, and all
+// outputs are canonical residues, so results are bit-identical.
+//
+// Base conversion in FP64 (target prime q < 2^50): the products t * m mod q
+// use ArithF64::mulw with the matrix entry m as the constant.  An input residue
+// t below 2^50 is exact in a double; a wider one (a 60-bit input prime) is
+// split t = h 2^32 + l and converted as h [m 2^32]_q + l m.  Each product is
+// within (-0.875 q, 0.875 q) (|t w / q| < 2^50, so fl(t wq) is within 3/8 of
+// the true quotient); the sum is reduced after every second input limb, which
+// keeps every partial sum below 4 q < 2^53.  Targets q >= 2^50 use integer
+// Shoup products, each in [0, 2q), summed with a conditional subtraction.
+#include "internal.h"
+#include "ntt_kernels.h"
+
+namespace pfa {
+
+namespace {
+
+// Rows per workgroup of the fused rows kernels: eight rows when that still
+// makes a full wavefront, which doubles the number of work items against the
+// NTT's rows pass (the inner-product kernel has only QlP x N1/ROWS items).
+template <int S1, int S2>
+struct FGeo {
+    using G = Geo<S1, S2>;
+    static constexpr int ROWS = Sub<S2>::T * 8 >= 64 ? 8 : G::ROWS;
+    static constexpr int THREADS = ROWS * Sub<S2>::T;
+    static constexpr int TILES = G::N1 / ROWS;
+    static constexpr int LDS = ROWS * G::ROW_PITCH;
+};
+
+// Work item w of a grouped launch: G groups of J items that read the same input
+// tile.  A group's items all carry the same w mod 8, so in a grid whose size
+// is a multiple of 8 they run on workgroups of one XCD (workgroups are dealt to
+// the XCDs round-robin) and share its L2 copy of the input tile.
+__device__ __forceinline__ bool grouped_item(uint32_t w, uint32_t G, uint32_t J, uint32_t &g, uint32_t &j) {
+    const uint32_t x = w & 7u, k = w >> 3;
+    j = k % J;
+    g = (k / J) * 8u + x;
+    return g < G;
+}
+
+__host__ __device__ inline uint32_t grouped_total(uint32_t G, uint32_t J) { return ((G + 7u) / 8u) * 8u * J; }
+
+// ------------------------------------------------------------ base conversion
+// One columns-pass job: target limb (table row prow) of one output poly, with
+// inputs n_in limbs of `in` (limb stride N) over the table rows in_row0 + i.
+struct BconvCols {
+    const uint64_t *in;     // input limbs of group 0; group g adds g * in_gstride
+    uint64_t *out;          // output limbs; job (g, j) writes out + g * out_gstride + j * N
+    const ulonglong2 *bc;   // factor pairs [(m, m 2^32) in the target's policy]: see bc_of
+    uint64_t in_gstride, out_gstride;
+    uint32_t groups;        // output polys (digits for ModUp, polys for ModDown / rescale)
+    uint32_t J;             // target limbs per group (positions 0 .. J-1)
+    uint32_t n_in;          // input limbs per group (<= alpha; the last ModUp digit may be short)
+    uint32_t n_in_last;     // input limbs of the last group
+    uint32_t in_row0;       // table row of input limb 0 of group 0
+    uint32_t in_row_step;   // table rows between groups' first inputs (ModUp: alpha; else 0)
+    // target position j -> table row: j < split ? j : split_base + (j - split)
+    uint32_t split, split_base;
+    // ModUp skips the group's own limbs: positions [g * skip_step, + n_in) are not written
+    uint32_t skip;          // 1 for ModUp
+    uint32_t bc_gstride;    // pairs between groups' factor blocks
+    uint32_t bc_istride;    // pairs between one input's consecutive target factors... see bc_of
+};
+
+// factor pair index for (group g, input i, target j): bc[((g * n_in_max + i) * J + j) * 2 + h]
+// (ModUp: per digit; ModDown / rescale: shared by all groups, bc_gstride = 0)
+__device__ __forceinline__ const ulonglong2 *bc_of(const BconvCols &a, uint32_t g, uint32_t i, uint32_t j) {
+    return a.bc + (size_t)g * a.bc_gstride + ((size_t)i * a.bc_istride + j) * 2;
+}
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables &t, const A &ar, uint32_t g,
+                                             uint32_t j, uint32_t tile, typename A::T (&x)[Sub<S1>::E]) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S1>;
+    const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+    const uint32_t n_in = g + 1 == a.groups ? a.n_in_last : a.n_in;
+    const uint64_t *base = a.in + (size_t)g * a.in_gstride + tile * kCols + c;
+    const uint32_t row0 = a.in_row0 + g * a.in_row_step;
+    if constexpr (A::kF64) {
+        double acc[SB::E];
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) acc[e] = 0.0;
+        for (uint32_t i = 0; i < n_in; i++) {
+            const ulonglong2 *f = bc_of(a, g, i, j);
+            const ulonglong2 f0 = f[0];
+            const double w0 = ArithF64::as_f(f0.x), wq0 = ArithF64::as_f(f0.y);
+            const uint64_t *src = base + (size_t)i * G::N;
+            if (t.mod[row0 + i] >= kF64PrimeBound) {
+                const ulonglong2 f1 = f[1];
+                const double w1 = ArithF64::as_f(f1.x), wq1 = ArithF64::as_f(f1.y);
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) {
+                    const uint64_t v = src[(size_t)(F + SB::T * e) * G::N2];
+                    acc[e] += ar.mulw((double)(uint32_t)(v >> 32), w1, wq1) + ar.mulw((double)(uint32_t)v, w0, wq0);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) acc[e] += ar.mulw(ar.load(src[(size_t)(F + SB::T * e) * G::N2]), w0, wq0);
+            }
+            if (i & 1u) {
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) ar.reduce(acc[e]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) {
+            ar.reduce(acc[e]);
+            x[e] = acc[e];
+        }
+    } else {
+        const uint64_t q = ar.q, q2 = ar.q2;
+        uint64_t acc[SB::E];
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) acc[e] = 0;
+        for (uint32_t i = 0; i < n_in; i++) {
+            const ulonglong2 f0 = bc_of(a, g, i, j)[0];
+            const uint64_t *src = base + (size_t)i * G::N;
+#pragma unroll
+            for (int e = 0; e < SB::E; e++)
+                acc[e] = csub(acc[e] + shoup_lazy(src[(size_t)(F + SB::T * e) * G::N2], f0.x, f0.y, q), q2);
+        }
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) x[e] = acc[e];
+    }
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(BconvCols a, NttTables t) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S1>;
+    __shared__ double lds[G::COL_LDS];
+    const uint32_t NG = a.groups * G::COL_TILES;
+    const uint32_t total = grouped_total(NG, a.J);
+    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+        uint32_t gt, j;
+        if (!grouped_item(w, NG, a.J, gt, j)) continue;
+        const uint32_t g = gt / G::COL_TILES, tile = gt % G::COL_TILES;
+        if (a.skip && j >= g * a.n_in && j < g * a.n_in + (g + 1 == a.groups ? a.n_in_last : a.n_in)) continue;
+        const uint32_t prow = j < a.split ? j : a.split_base + (j - a.split);
+        const uint64_t q = t.mod[prow];
+        uint64_t *olimb = a.out + (size_t)g * a.out_gstride + (size_t)j * G::N;
+        if (q < kF64PrimeBound) {
+            const ArithF64 ar(q);
+            double x[SB::E];
+            bconv_source<ArithF64, S1, S2>(a, t, ar, g, j, tile, x);
+            fwd_cols_core<ArithF64, S1, S2>(x, ar, t, prow, lds);
+            fwd_cols_store<ArithF64, S1, S2>(x, ar, tile, olimb);
+        } else {
+            const ArithInt ar(q);
+            uint64_t x[SB::E];
+            bconv_source<ArithInt, S1, S2>(a, t, ar, g, j, tile, x);
+            fwd_cols_core<ArithInt, S1, S2>(x, ar, t, prow, reinterpret_cast<uint64_t *>(lds));
+            fwd_cols_store<ArithInt, S1, S2>(x, ar, tile, olimb);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ inner product
+struct InnerRows {
+    const uint64_t *inter;  // [beta][QlP][N] columns-pass output of the base conversion
+    const uint64_t *c2;     // [Ql][N] NTT form: the digit's own limbs
+    const uint64_t *key;    // [dnum][2][QP][N]
+    uint64_t *cx;           // [2][QlP][N]
+    const ulonglong2 *ratio;
+    uint32_t Ql, QlP, alpha, beta, Q, QP;
+};
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void inner_item(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
+                                           uint32_t prow, uint32_t k1, typename A::T *lr) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S2>;
+    using T = typename A::T;
+    const uint32_t F = threadIdx.x % SB::T;
+    const size_t rowoff = (size_t)k1 * G::N2 + F;
+    const size_t keyrow = (size_t)prow * G::N + rowoff;
+    T acc0[SB::E], acc1[SB::E];
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) acc0[e] = acc1[e] = 0;
+    for (uint32_t b = 0; b < a.beta; b++) {
+        T x[SB::E];
+        const bool own = r < a.Ql && r >= b * a.alpha && r < b * a.alpha + a.alpha;
+        if (own) {
+            const uint64_t *s = a.c2 + (size_t)r * G::N + rowoff;
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) x[e] = ar.load(ld_stream(&s[SB::T * e]));
+        } else {
+            const uint64_t *s = a.inter + ((size_t)b * a.QlP + r) * G::N + rowoff;
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(ld_stream(&s[SB::T * e]));
+            fwd_rows_core<A, S1, S2>(x, ar, t, prow, k1, lr);
+            __syncthreads();
+        }
+        const uint64_t *k0 = a.key + (size_t)b * 2 * a.QP * G::N + keyrow;
+        const uint64_t *kk1 = k0 + (size_t)a.QP * G::N;
+        if constexpr (A::kF64) {
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) {
+                ar.reduce(x[e]);
+                const double w0 = ar.load(ld_stream(&k0[SB::T * e])), w1 = ar.load(ld_stream(&kk1[SB::T * e]));
+                acc0[e] += ar.mulw(x[e], w0, w0 * ar.qinv);
+                acc1[e] += ar.mulw(x[e], w1, w1 * ar.qinv);
+            }
+            if (b & 1u) {
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) {
+                    ar.reduce(acc0[e]);
+                    ar.reduce(acc1[e]);
+                }
+            }
+        } else {
+            const ulonglong2 rt = a.ratio[prow];
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) {
+                const uint64_t w0 = ld_stream(&k0[SB::T * e]), w1 = ld_stream(&kk1[SB::T * e]);
+                U128 p0{x[e] * w0, mulhi64(x[e], w0)};
+                U128 p1{x[e] * w1, mulhi64(x[e], w1)};
+                acc0[e] = add_mod(acc0[e], barrett128(p0, ar.q, rt.x, rt.y), ar.q);
+                acc1[e] = add_mod(acc1[e], barrett128(p1, ar.q, rt.x, rt.y), ar.q);
+            }
+        }
+    }
+    uint64_t *o0 = a.cx + (size_t)r * G::N + rowoff;
+    uint64_t *o1 = o0 + (size_t)a.QlP * G::N;
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) {
+        st_stream(&o0[SB::T * e], ar.store(acc0[e]));
+        st_stream(&o1[SB::T * e], ar.store(acc1[e]));
+    }
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_inner_rows(InnerRows a, NttTables t) {
+    using G = Geo<S1, S2>;
+    using FG = FGeo<S1, S2>;
+    __shared__ double lds[FG::LDS];
+    const uint32_t rr = threadIdx.x / Sub<S2>::T;
+    const uint32_t total = a.QlP * FG::TILES;
+    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+        const uint32_t r = w / FG::TILES, tile = w % FG::TILES;
+        const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
+        const uint64_t q = t.mod[prow];
+        const uint32_t k1 = tile * FG::ROWS + rr;
+        if (q < kF64PrimeBound)
+            inner_item<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, lds + rr * G::ROW_PITCH);
+        else
+            inner_item<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1,
+                                         reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH);
+    }
+}
+
+// ------------------------------------------------------------ epilogue rows
+// out[m][j] = (base[m][j] if given) + (c[m][j] - NTT(D[m][j])) f_j   (mod q_j)
+struct EpiRows {
+    const uint64_t *inter;  // [M][J][N] columns-pass output
+    const uint64_t *c;      // [M][..][N], poly stride c_stride
+    const uint64_t *base0, *base1;  // [J][N] each, or null
+    uint64_t *out;          // [M][J][N]
+    const ulonglong2 *f;    // [J] pairs in each limb's NTT policy
+    uint64_t c_stride;
+    uint32_t M, J;
+};
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, const A &ar, uint32_t m, uint32_t j,
+                                         uint32_t k1, typename A::T *lr) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S2>;
+    using T = typename A::T;
+    const uint32_t F = threadIdx.x % SB::T;
+    const size_t rowoff = (size_t)k1 * G::N2 + F;
+    const size_t lo = ((size_t)m * a.J + j) * G::N + rowoff;
+    T x[SB::E];
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(ld_stream(&a.inter[lo + SB::T * e]));
+    fwd_rows_core<A, S1, S2>(x, ar, t, j, k1, lr);
+    const uint64_t *cp = a.c + m * a.c_stride + (size_t)j * G::N + rowoff;
+    const uint64_t *bp = m == 0 ? a.base0 : a.base1;
+    if (bp) bp += (size_t)j * G::N + rowoff;
+    const ulonglong2 f = a.f[j];
+    uint64_t *op = a.out + lo;
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) {
+        uint64_t v;
+        if constexpr (A::kF64) {
+            ar.reduce(x[e]);
+            double d = ar.load(ld_stream(&cp[SB::T * e])) - x[e];
+            ar.mul(d, f);
+            v = ar.store(d);
+            if (bp) v = add_mod(v, ld_stream(&bp[SB::T * e]), (uint64_t)ar.q);
+        } else {
+            const uint64_t d = sub_mod(ld_stream(&cp[SB::T * e]), ar.store(x[e]), ar.q);
+            v = shoup(d, f.x, f.y, ar.q);
+            if (bp) v = add_mod(v, ld_stream(&bp[SB::T * e]), ar.q);
+        }
+        st_stream(&op[SB::T * e], v);
+    }
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_epi_rows(EpiRows a, NttTables t) {
+    using G = Geo<S1, S2>;
+    using FG = FGeo<S1, S2>;
+    __shared__ double lds[FG::LDS];
+    const uint32_t rr = threadIdx.x / Sub<S2>::T;
+    const uint32_t total = a.M * a.J * FG::TILES;
+    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+        const uint32_t tile = w % FG::TILES, mj = w / FG::TILES;
+        const uint32_t m = mj % a.M, j = mj / a.M;
+        const uint64_t q = t.mod[j];
+        const uint32_t k1 = tile * FG::ROWS + rr;
+        if (q < kF64PrimeBound)
+            epi_item<ArithF64, S1, S2>(a, t, ArithF64(q), m, j, k1, lds + rr * G::ROW_PITCH);
+        else
+            epi_item<ArithInt, S1, S2>(a, t, ArithInt(q), m, j, k1,
+                                       reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH);
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ launchers
+NttTables tables_of(const Ctx &c) {
+    return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv, c.rb_fw, c.rb_inv};
+}
+
+uint32_t fgrid(const Ctx &c, uint32_t items, uint32_t wpc) {
+    const uint32_t cap = (uint32_t)c.n_cu * wpc;
+    return items < cap ? items : cap;
+}
+
+template <int S1, int S2>
+void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    const uint32_t total = grouped_total(a.groups * G::COL_TILES, a.J);
+    hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
+                       tables_of(c));
+    PFA_HIP(hipGetLastError());
+}
+
+template <int S1, int S2>
+void launch_inner(const Ctx &c, const InnerRows &a, hipStream_t s) {
+    using FG = FGeo<S1, S2>;
+    hipLaunchKernelGGL((k_inner_rows<S1, S2>), dim3(fgrid(c, a.QlP * FG::TILES, 8)), dim3(FG::THREADS), 0, s, a,
+                       tables_of(c));
+    PFA_HIP(hipGetLastError());
+}
+
+template <int S1, int S2>
+void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
+    using FG = FGeo<S1, S2>;
+    hipLaunchKernelGGL((k_epi_rows<S1, S2>), dim3(fgrid(c, a.M * a.J * FG::TILES, 8)), dim3(FG::THREADS), 0, s, a,
+                       tables_of(c));
+    PFA_HIP(hipGetLastError());
+}
+
+#define PFA_FUSED_DISPATCH(FN, ARG)                                          \
+    switch (c.logN) {                                                        \
+    case 10: FN<5, 5>(c, ARG, s); break;                                     \
+    case 11: FN<5, 6>(c, ARG, s); break;                                     \
+    case 12: FN<6, 6>(c, ARG, s); break;                                     \
+    case 13: FN<6, 7>(c, ARG, s); break;                                     \
+    case 14: FN<7, 7>(c, ARG, s); break;                                     \
+    case 15: FN<7, 8>(c, ARG, s); break;                                     \
+    case 16: FN<8, 8>(c, ARG, s); break;                                     \
+    case 17: FN<8, 9>(c, ARG, s); break;                                     \
+    default: fail(PFA_ERR_INVALID_ARGUMENT, "unsupported poly_modulus_degree"); \
+    }
+
+}  // namespace
+
+// c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp and the key-switch inner
+// product against key [dnum][2][QP][N].
+void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
+                       hipStream_t s) {
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    Scratch sc(c, s);
+    uint64_t *tin = sc.alloc((size_t)Ql * c.N);
+    uint64_t *inter = sc.alloc((size_t)lv.beta * QlP * c.N);
+    NttLaunch inv{c2, tin, 0, 0, 1, Ql};
+    inv.scale = lv.modup_scale;
+    ntt_inverse(c, inv, s);
+    BconvCols b{};
+    b.in = tin;
+    b.out = inter;
+    b.bc = lv.modup_bc;
+    b.in_gstride = (uint64_t)alpha * c.N;
+    b.out_gstride = (uint64_t)QlP * c.N;
+    b.groups = lv.beta;
+    b.J = QlP;
+    b.n_in = alpha;
+    b.n_in_last = Ql - (lv.beta - 1) * alpha;
+    b.in_row0 = 0;
+    b.in_row_step = alpha;
+    b.split = Ql;
+    b.split_base = c.Q;
+    b.skip = 1;
+    b.bc_gstride = 2 * alpha * QlP;
+    b.bc_istride = QlP;
+    PFA_FUSED_DISPATCH(launch_bconv, b);
+    InnerRows r{inter, c2, key, cx, c.ratio, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
+    PFA_FUSED_DISPATCH(launch_inner, r);
+}
+
+// cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx)  (base[m] may alias out[m] or be null)
+void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,
+                   const uint64_t *base0, const uint64_t *base1, hipStream_t s) {
+    const uint32_t Ql = c.size_Ql(chain), alpha = c.P, QlP = Ql + alpha;
+    Scratch sc(c, s);
+    uint64_t *xP = sc.alloc((size_t)M * alpha * c.N);
+    uint64_t *inter = sc.alloc((size_t)M * Ql * c.N);
+    NttLaunch inv{cx + (size_t)Ql * c.N, xP, (uint64_t)QlP * c.N, (uint64_t)alpha * c.N, M, alpha};
+    inv.start = c.Q;
+    inv.scale = c.moddown_scale;
+    ntt_inverse(c, inv, s);
+    BconvCols b{};
+    b.in = xP;
+    b.out = inter;
+    b.bc = c.moddown_bc;
+    b.in_gstride = (uint64_t)alpha * c.N;
+    b.out_gstride = (uint64_t)Ql * c.N;
+    b.groups = M;
+    b.J = Ql;
+    b.n_in = alpha;
+    b.n_in_last = alpha;
+    b.in_row0 = c.Q;
+    b.in_row_step = 0;
+    b.split = 0xffffffffu;
+    b.split_base = 0;
+    b.skip = 0;
+    b.bc_gstride = 0;
+    b.bc_istride = c.Q;
+    PFA_FUSED_DISPATCH(launch_bconv, b);
+    EpiRows e{inter, cx, base0, base1, out, c.pinv_p, (uint64_t)QlP * c.N, M, Ql};
+    PFA_FUSED_DISPATCH(launch_epi, e);
+}
+
+// in [size][L][N] -> out [size][L-1][N]: floor division by the last prime
+void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s) {
+    const Level &lv = c.level(chain);
+    const uint32_t L = lv.Ql;
+    Scratch sc(c, s);
+    uint64_t *last = sc.alloc((size_t)size * c.N);
+    uint64_t *inter = sc.alloc((size_t)size * (L - 1) * c.N);
+    NttLaunch inv{in + (size_t)(L - 1) * c.N, last, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
+    inv.start = L - 1;
+    ntt_inverse(c, inv, s);
+    BconvCols b{};
+    b.in = last;
+    b.out = inter;
+    b.bc = c.unit_bc;
+    b.in_gstride = c.N;
+    b.out_gstride = (uint64_t)(L - 1) * c.N;
+    b.groups = size;
+    b.J = L - 1;
+    b.n_in = 1;
+    b.n_in_last = 1;
+    b.in_row0 = L - 1;
+    b.in_row_step = 0;
+    b.split = 0xffffffffu;
+    b.split_base = 0;
+    b.skip = 0;
+    b.bc_gstride = 0;
+    b.bc_istride = 0;
+    PFA_FUSED_DISPATCH(launch_bconv, b);
+    EpiRows e{inter, in, nullptr, nullptr, out, lv.rescale_inv_p, (uint64_t)L * c.N, size, L - 1};
+    PFA_FUSED_DISPATCH(launch_epi, e);
+}
+
+}  // namespace pfa

@@ -74,6 +74,10 @@ struct Level {
     uint64_t *modup_mat = nullptr;
     // rescale: [q_last^-1]_{q_j} Shoup pairs, j < Ql - 1
     ulonglong2 *rescale_inv = nullptr;
+    // fused path: modup_mat entries as NTT-policy pairs of the target prime,
+    // [beta][alpha][QlP][2] = (m, [m 2^32]_{p_r}); rescale factor as NTT pairs
+    ulonglong2 *modup_bc = nullptr;
+    ulonglong2 *rescale_inv_p = nullptr;
 };
 
 // Device workspace of one (host thread, stream): chunks grown on demand and
@@ -115,6 +119,11 @@ struct Ctx {
     ulonglong2 *moddown_scale = nullptr;
     uint64_t *moddown_mat = nullptr;
     ulonglong2 *pinv = nullptr;
+    // fused path: moddown_mat as NTT-policy pairs [P][Q][2] = (m, [m 2^32]_{q_i}),
+    // (1, [2^32]_{q_i}) per Q prime [Q][2], [P^-1]_{q_i} as NTT-policy pairs [Q]
+    ulonglong2 *moddown_bc = nullptr;
+    ulonglong2 *unit_bc = nullptr;
+    ulonglong2 *pinv_p = nullptr;
     // key construction: [P]_{q_i} Shoup pairs over all QP rows (0 on P rows)
     ulonglong2 *pmodq = nullptr;
     uint32_t *slot_perm = nullptr;   // [N/2] CKKS slot j -> DFT index (5^j mod 2N - 1) / 4
@@ -178,5 +187,15 @@ struct NttLaunch {
 };
 void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s);
 void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s);
+
+// Fused key-switching / rescale pipelines (fused_ks.hip).
+// c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp then the inner product with key.
+void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
+                       hipStream_t s);
+// cx [M][QlP][N] -> out [M][Ql][N] = base_m + ModDown(cx_m); base_m may alias out_m or be null.
+void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,
+                   const uint64_t *base0, const uint64_t *base1, hipStream_t s);
+// in [size][Ql][N] -> out [size][Ql-1][N]: floor division by the level's last prime.
+void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s);
 
 }  // namespace pfa

@@ -310,20 +310,16 @@ __device__ __forceinline__ const uint64_t *cols_src(const NttBatch &b, const Til
     return base + r.m * stride + (size_t)r.l * G::N + r.tile * kCols;
 }
 
+// Forward columns pass of one tile.  In: x[e] = element (F + T e) of column c
+// of the tile, |x| <= q (any lazy representative).  Out: x[e] = element
+// (F E + e) of the column in the intermediate form (lazy).
 template <class A, int S1, int S2>
-__device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+__device__ __forceinline__ void fwd_cols_core(typename A::T (&x)[Sub<S1>::E], const A &ar, const NttTables &t,
+                                              uint32_t prow, typename A::T *lds) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
-    using T = typename A::T;
-    const A ar(q);
     const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
-    uint64_t *dst = olimb + r.tile * kCols;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
-    T x[SB::E];
-#pragma unroll
-    for (int e = 0; e < SB::E; e++) x[e] = ar.load(raw[e]);
     fwd_round_a<A, S1>(x, ar, tw, 1);
 #pragma unroll
     for (int e = 0; e < SB::E; e++) {
@@ -334,8 +330,32 @@ __device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lds[(F * SB::E + e) * kColStride + c];
     fwd_round_b<A, S1>(x, ar, tw, 1, F);
+}
+
+// store of fwd_cols_core's output into limb olimb (intermediate form)
+template <class A, int S1, int S2>
+__device__ __forceinline__ void fwd_cols_store(const typename A::T (&x)[Sub<S1>::E], const A &ar, uint32_t tile,
+                                               uint64_t *olimb) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S1>;
+    uint64_t *dst = olimb + tile * kCols;
+    const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) dst[(size_t)(F * SB::E + e) * G::N2 + c] = ar.store_mid(x[e]);
+    for (int e = 0; e < SB::E; e++) st_stream(&dst[(size_t)(F * SB::E + e) * G::N2 + c], ar.store_mid(x[e]));
+}
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
+                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
+                                              typename A::T *lds, uint64_t *olimb) {
+    using SB = Sub<S1>;
+    using T = typename A::T;
+    const A ar(q);
+    T x[SB::E];
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) x[e] = ar.load(raw[e]);
+    fwd_cols_core<A, S1, S2>(x, ar, t, prow, lds);
+    fwd_cols_store<A, S1, S2>(x, ar, r.tile, olimb);
 }
 
 template <int S1, int S2>
@@ -350,7 +370,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
     if (cur < total) {
         const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, cur), b.src, b.sstride);
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = s[(size_t)(F + SB::T * e) * G::N2 + c];
+        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[(size_t)(F + SB::T * e) * G::N2 + c]);
     }
     while (cur < total) {
         const uint32_t nxt = next_tile(b, G::COL_TILES, cur + gridDim.x, total);
@@ -359,7 +379,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
         if (nxt < total) {
             const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, nxt), b.src, b.sstride);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = s[(size_t)(F + SB::T * e) * G::N2 + c];
+            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[(size_t)(F + SB::T * e) * G::N2 + c]);
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
@@ -375,22 +395,17 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
 }
 
 // Rows pass: dst (intermediate) -> dst (canonical).
+// Forward rows pass of one tile row k1.  In: x[e] = element (F + T e) of the
+// row in the intermediate form.  Out: x[e] = element (F + T e) of the
+// transformed row (lazy; the final LDS transpose makes stores coalesced).
+// The caller separates consecutive calls on the same LDS with a barrier.
 template <class A, int S1, int S2>
-__device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+__device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], const A &ar, const NttTables &t,
+                                              uint32_t prow, uint32_t k1, typename A::T *lr) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
-    using T = typename A::T;
-    const A ar(q);
     const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
-    const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    const uint32_t k1 = r.tile * G::ROWS + rr;
-    uint64_t *rowp = olimb + (size_t)k1 * G::N2;
-    T *lr = lds + rr * G::ROW_PITCH;
-    T x[SB::E];
-#pragma unroll
-    for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(raw[e]);
+    const uint32_t F = threadIdx.x % SB::T;
     if constexpr (A::kF64)
         fwd_round_a_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1);
     else
@@ -407,13 +422,31 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
         fwd_round_b_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1, F);
     else
         fwd_round_b<A, S2>(x, ar, tw, G::N1 + k1, F);
-    // transpose back through LDS so the stores are coalesced
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < SB::E; e++) lr[rpad(F * SB::E + e)] = x[e];
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) rowp[F + SB::T * e] = ar.store(lr[rpad(F + SB::T * e)]);
+    for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F + SB::T * e)];
+}
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
+                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
+                                              typename A::T *lds, uint64_t *olimb) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S2>;
+    using T = typename A::T;
+    const A ar(q);
+    const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
+    const uint32_t k1 = r.tile * G::ROWS + rr;
+    uint64_t *rowp = olimb + (size_t)k1 * G::N2;
+    T x[SB::E];
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(raw[e]);
+    fwd_rows_core<A, S1, S2>(x, ar, t, prow, k1, lds + rr * G::ROW_PITCH);
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) st_stream(&rowp[F + SB::T * e], ar.store(x[e]));
 }
 
 template <int S1, int S2>
@@ -436,7 +469,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
     if (cur < total) {
         const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, cur), b.src, b.sstride);
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = s[F + SB::T * e];
+        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
     }
     while (cur < total) {
         const uint32_t nxt = next_tile(b, G::ROW_TILES, cur + gridDim.x, total);
@@ -445,7 +478,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
         if (nxt < total) {
             const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt), b.src, b.sstride);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = s[F + SB::T * e];
+            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[F + SB::T * e]);
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
@@ -496,7 +529,7 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     else
         inv_round_b<A, S2, false>(x, ar, itw, G::N1 + k1, ulonglong2{0, 0});
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) drow[F + SB::T * e] = ar.store_mid(x[e]);
+    for (int e = 0; e < SB::E; e++) st_stream(&drow[F + SB::T * e], ar.store_mid(x[e]));
 }
 
 template <int S1, int S2>
@@ -511,7 +544,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
     if (cur < total) {
         const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, cur), b.src, b.sstride);
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = s[F + SB::T * e];
+        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
     }
     while (cur < total) {
         const uint32_t nxt = next_tile(b, G::ROW_TILES, cur + gridDim.x, total);
@@ -520,7 +553,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
         if (nxt < total) {
             const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt), b.src, b.sstride);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = s[F + SB::T * e];
+            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[F + SB::T * e]);
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
@@ -563,7 +596,7 @@ __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
         for (int e = 0; e < SB::E; e++) ar.mul(x[e], s);
     }
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) data[(size_t)(F + SB::T * e) * G::N2 + c] = ar.store(x[e]);
+    for (int e = 0; e < SB::E; e++) st_stream(&data[(size_t)(F + SB::T * e) * G::N2 + c], ar.store(x[e]));
 }
 
 template <int S1, int S2>
@@ -578,7 +611,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBa
     if (cur < total) {
         const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, cur), b.src, b.sstride);
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = s[(size_t)(F * SB::E + e) * G::N2 + c];
+        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[(size_t)(F * SB::E + e) * G::N2 + c]);
     }
     while (cur < total) {
         const uint32_t nxt = next_tile(b, G::COL_TILES, cur + gridDim.x, total);
@@ -587,7 +620,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBa
         if (nxt < total) {
             const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, nxt), b.src, b.sstride);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = s[(size_t)(F * SB::E + e) * G::N2 + c];
+            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[(size_t)(F * SB::E + e) * G::N2 + c]);
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
@@ -725,7 +758,7 @@ __global__ void __launch_bounds__(256) ntt_fwd_fused(NttBatch b, NttTables t, Fu
                 const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
                 uint64_t raw[S1B::E];
 #pragma unroll
-                for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F + S1B::T * e) * G::N2 + c];
+                for (int e = 0; e < S1B::E; e++) raw[e] = ld_stream(&s[(size_t)(F + S1B::T * e) * G::N2 + c]);
                 if (q < kF64PrimeBound)
                     fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
                 else
@@ -775,7 +808,7 @@ __global__ void __launch_bounds__(256) ntt_inv_fused(NttBatch b, NttTables t, Fu
                 const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
                 uint64_t raw[S2B::E];
 #pragma unroll
-                for (int e = 0; e < S2B::E; e++) raw[e] = s[F + S2B::T * e];
+                for (int e = 0; e < S2B::E; e++) raw[e] = ld_stream(&s[F + S2B::T * e]);
                 if (q < kF64PrimeBound)
                     inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
                 else
@@ -798,7 +831,7 @@ __global__ void __launch_bounds__(256) ntt_inv_fused(NttBatch b, NttTables t, Fu
     }
 }
 
-__global__ void k_zero_u32(uint32_t *p, uint32_t n) {
+static __global__ void k_zero_u32(uint32_t *p, uint32_t n) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 

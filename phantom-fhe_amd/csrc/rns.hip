@@ -77,13 +77,13 @@ k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint6
     const uint64_t q = mod[l];
     const ulonglong2 r = ratio[l];
     const size_t i = (size_t)l * N + n, LN = (size_t)Ql * N;
-    const uint64_t a0 = a[i], a1 = a[LN + i], b0 = b[i], b1 = b[LN + i];
+    const uint64_t a0 = ld_stream(&a[i]), a1 = ld_stream(&a[LN + i]), b0 = ld_stream(&b[i]), b1 = ld_stream(&b[LN + i]);
     U128 m{0, 0};
     mac(m, a0, b1);
     mac(m, a1, b0);
-    d0[i] = mulmod_b(a0, b0, q, r);
-    d1[i] = barrett128(m, q, r.x, r.y);
-    d2[i] = mulmod_b(a1, b1, q, r);
+    st_stream(&d0[i], mulmod_b(a0, b0, q, r));
+    st_stream(&d1[i], barrett128(m, q, r.x, r.y));
+    st_stream(&d2[i], mulmod_b(a1, b1, q, r));
 }
 
 // ModUp base conversion per digit (src/rns_bconv.cu:455-485, :522-528, :530-628):
@@ -134,8 +134,8 @@ k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t 
     for (uint32_t b = 0; b < beta; b++) {
         const uint64_t x = t[((size_t)b * QlP + r) * N + sn];
         const uint64_t *kb = key + (size_t)b * 2 * QP * N + (size_t)row * N + n;
-        mac(a0, x, kb[0]);
-        mac(a1, x, kb[(size_t)QP * N]);
+        mac(a0, x, ld_stream(&kb[0]));
+        mac(a1, x, ld_stream(&kb[(size_t)QP * N]));
     }
     const uint64_t q = mod[row];
     const ulonglong2 rt = ratio[row];
@@ -149,64 +149,9 @@ k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t 
     *o1 = v1;
 }
 
-// ModDown base conversion P -> Ql (bConv_BEHZ, src/rns_bconv.cu:212-229):
-//   d[m][i] = sum_j xP[m][j] [P / p_j]_{q_i}  mod q_i,  xP already scaled by [(P/p_j)^-1]_{p_j}
-__global__ void __launch_bounds__(kThreads)
-k_moddown_bconv(const uint64_t *xP, uint64_t *d, const uint64_t *mat, const uint64_t *mod, const ulonglong2 *ratio,
-                uint32_t Ql, uint32_t alpha, uint32_t Q, uint32_t N) {
-    const uint32_t m = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
-    uint64_t xv[kMaxAlpha];
-#pragma unroll
-    for (uint32_t j = 0; j < kMaxAlpha; j++)
-        if (j < alpha) xv[j] = xP[((size_t)m * alpha + j) * N + n];
-    uint64_t *dm = d + (size_t)m * Ql * N;
-    for (uint32_t i = 0; i < Ql; i++) {
-        U128 acc{0, 0};
-#pragma unroll
-        for (uint32_t j = 0; j < kMaxAlpha; j++)
-            if (j < alpha) mac(acc, xv[j], mat[(size_t)j * Q + i]);
-        dm[(size_t)i * N + n] = barrett128(acc, mod[i], ratio[i].x, ratio[i].y);
-    }
-}
-
 struct Bases {
     const uint64_t *p[2];
 };
-
-// FuseModDownEpilogue (include/ntt_radix8_tmpl.cuh:216-233) plus add_to_ct_kernel
-// (src/rns_bconv.cu:763-769): out[m][i] = base[m][i] + (cx[m][i] - d[m][i]) P^-1 mod q_i
-__global__ void __launch_bounds__(kThreads)
-k_moddown_final(const uint64_t *cx, const uint64_t *d, uint64_t *out, Bases base, const uint64_t *mod,
-                const ulonglong2 *pinv, uint32_t Ql, uint32_t QlP, uint32_t N) {
-    const uint32_t i = blockIdx.y, m = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
-    const uint64_t q = mod[i];
-    const ulonglong2 pi = pinv[i];
-    const size_t o = ((size_t)m * Ql + i) * N + n;
-    uint64_t v = shoup(sub_mod(cx[((size_t)m * QlP + i) * N + n], d[o], q), pi.x, pi.y, q);
-    const uint64_t *bp = base.p[m];
-    if (bp) v = add_mod(v, bp[(size_t)i * N + n], q);
-    out[o] = v;
-}
-
-// divide_and_round_reduce_q_last_kernel (src/rns.cu:1128-1139): t[s][j] = c_last[s] mod q_j
-__global__ void __launch_bounds__(kThreads)
-k_rescale_reduce(const uint64_t *last, uint64_t *t, const uint64_t *mod, const ulonglong2 *ratio, uint32_t L1,
-                 uint32_t N) {
-    const uint32_t j = blockIdx.y, s = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
-    U128 v{last[(size_t)s * N + n], 0};
-    t[((size_t)s * L1 + j) * N + n] = barrett128(v, mod[j], ratio[j].x, ratio[j].y);
-}
-
-// divide_and_round_ntt_inv_scalar_kernel (src/rns.cu:1141-1158):
-//   out[s][j] = (c[s][j] - t[s][j]) q_last^-1 mod q_j   (floor division, no rounding term)
-__global__ void __launch_bounds__(kThreads)
-k_rescale_final(const uint64_t *in, const uint64_t *t, uint64_t *out, const uint64_t *mod, const ulonglong2 *inv,
-                uint32_t L, uint32_t N) {
-    const uint32_t j = blockIdx.y, s = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
-    const uint64_t q = mod[j];
-    const size_t o = ((size_t)s * (L - 1) + j) * N + n;
-    out[o] = shoup(sub_mod(in[((size_t)s * L + j) * N + n], t[o], q), inv[j].x, inv[j].y, q);
-}
 
 // apply_galois_ntt_permutation (src/galois.cu:11-18): dst[l][i] = src[l][pi(i)]
 __global__ void __launch_bounds__(kThreads)
@@ -293,23 +238,7 @@ void op_inner(const Ctx &c, uint32_t chain, const uint64_t *t, const uint64_t *k
 void op_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out, Bases base,
                 hipStream_t s) {
     check_chain(c, chain);
-    check_alpha(c);
-    const uint32_t Ql = c.size_Ql(chain), alpha = c.P, QlP = Ql + alpha;
-    Scratch sc(c, s);
-    uint64_t *xP = sc.alloc((size_t)M * alpha * c.N);
-    NttLaunch inv{cx + (size_t)Ql * c.N, xP, (uint64_t)QlP * c.N, (uint64_t)alpha * c.N, M, alpha};
-    inv.start = c.Q;
-    inv.scale = c.moddown_scale;
-    ntt_inverse(c, inv, s);
-    uint64_t *d = sc.alloc((size_t)M * Ql * c.N);
-    hipLaunchKernelGGL(k_moddown_bconv, grid(c, M), dim3(kThreads), 0, s, xP, d, c.moddown_mat, c.mod, c.ratio,
-                       Ql, alpha, c.Q, c.N);
-    PFA_HIP(hipGetLastError());
-    NttLaunch fw{d, d, 0, 0, M, Ql};
-    ntt_forward(c, fw, s);
-    hipLaunchKernelGGL(k_moddown_final, grid(c, Ql, M), dim3(kThreads), 0, s, cx, d, out, base, c.mod, c.pinv,
-                       Ql, QlP, c.N);
-    PFA_HIP(hipGetLastError());
+    fused_moddown(c, chain, cx, M, out, base.p[0], M > 1 ? base.p[1] : nullptr, s);
 }
 
 // out[k] = base_k + KS(c2)_k for k = 0, 1 (out [2][Ql][N]; bases may alias out or be null)
@@ -317,14 +246,12 @@ void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64
                   Bases base, hipStream_t s) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
-    const uint32_t QlP = lv.Ql + c.P;
+    require(key != nullptr, "null key");
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
     Scratch sc(c, s);
-    uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
-    op_modup(c, chain, c2, mu, s);
-    uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
-    op_inner(c, chain, mu, key, dnum, cx, 0, s);
-    op_moddown(c, chain, cx, 2, out, base, s);
+    uint64_t *cx = sc.alloc((size_t)2 * (lv.Ql + c.P) * c.N);
+    fused_modup_inner(c, chain, c2, key, cx, s);
+    fused_moddown(c, chain, cx, 2, out, base.p[0], base.p[1], s);
 }
 
 void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1,
@@ -344,24 +271,9 @@ void op_galois(const Ctx &c, uint32_t elt, const uint64_t *src, uint64_t *dst, u
 
 void op_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s) {
     check_chain(c, chain);
-    const Level &lv = c.level(chain);
-    const uint32_t L = lv.Ql;
-    require(L >= 2, "cannot rescale at the last level");
+    require(c.level(chain).Ql >= 2, "cannot rescale at the last level");
     require(size >= 1 && size <= 65535, "bad ciphertext size");
-    Scratch sc(c, s);
-    uint64_t *last = sc.alloc((size_t)size * c.N);
-    NttLaunch inv{in + (size_t)(L - 1) * c.N, last, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
-    inv.start = L - 1;
-    ntt_inverse(c, inv, s);
-    uint64_t *t = sc.alloc((size_t)size * (L - 1) * c.N);
-    hipLaunchKernelGGL(k_rescale_reduce, grid(c, L - 1, size), dim3(kThreads), 0, s, last, t, c.mod, c.ratio,
-                       L - 1, c.N);
-    PFA_HIP(hipGetLastError());
-    NttLaunch fw{t, t, 0, 0, size, L - 1};
-    ntt_forward(c, fw, s);
-    hipLaunchKernelGGL(k_rescale_final, grid(c, L - 1, size), dim3(kThreads), 0, s, in, t, out, c.mod,
-                       lv.rescale_inv, L, c.N);
-    PFA_HIP(hipGetLastError());
+    fused_rescale(c, chain, in, size, out, s);
 }
 
 }  // namespace pfa
