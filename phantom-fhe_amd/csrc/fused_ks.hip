@@ -34,8 +34,8 @@
 // t below 2^50 is exact in a double; a wider one (a 60-bit input prime) is
 // split t = h 2^32 + l and converted as h [m 2^32]_q + l m.  Each product is
 // within (-0.875 q, 0.875 q) (|t w / q| < 2^50, so fl(t wq) is within 3/8 of
-// the true quotient); the sum is reduced after every second input limb, which
-// keeps every partial sum below 4 q < 2^53.  Targets q >= 2^50 use integer
+// the true quotient); the sum is reduced whenever the next product could take
+// it past 7 x 0.875 q, which keeps every partial sum below 2^53.  Targets q >= 2^50 use integer
 // Shoup products, each in [0, 2q), summed with a conditional subtraction.
 #include "internal.h"
 #include "ntt_kernels.h"
@@ -110,12 +110,20 @@ __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables
         double acc[SB::E];
 #pragma unroll
         for (int e = 0; e < SB::E; e++) acc[e] = 0.0;
+        uint32_t units = 0;  // bound on |acc| in units of 0.875 q (a narrow product); kept <= 7
         for (uint32_t i = 0; i < n_in; i++) {
             const ulonglong2 *f = bc_of(a, g, i, j);
             const ulonglong2 f0 = f[0];
             const double w0 = ArithF64::as_f(f0.x), wq0 = ArithF64::as_f(f0.y);
             const uint64_t *src = base + (size_t)i * G::N;
-            if (t.mod[row0 + i] >= kF64PrimeBound) {
+            const bool wide = t.mod[row0 + i] >= kF64PrimeBound;
+            if (units + (wide ? 2u : 1u) > 7u) {
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) ar.reduce(acc[e]);
+                units = 1;
+            }
+            units += wide ? 2u : 1u;
+            if (wide) {
                 const ulonglong2 f1 = f[1];
                 const double w1 = ArithF64::as_f(f1.x), wq1 = ArithF64::as_f(f1.y);
 #pragma unroll
@@ -126,10 +134,6 @@ __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables
             } else {
 #pragma unroll
                 for (int e = 0; e < SB::E; e++) acc[e] += ar.mulw(ar.load(src[(size_t)(F + SB::T * e) * G::N2]), w0, wq0);
-            }
-            if (i & 1u) {
-#pragma unroll
-                for (int e = 0; e < SB::E; e++) ar.reduce(acc[e]);
             }
         }
 #pragma unroll

@@ -146,18 +146,21 @@ struct ArithF64 {
     static __device__ __forceinline__ double as_f(uint64_t b) { return __longlong_as_double((long long)b); }
     static __device__ __forceinline__ uint64_t as_u(double d) { return (uint64_t)__double_as_longlong(d); }
 
-    __device__ __forceinline__ T load(uint64_t v) const {
-        // exact for v < 2^53
-        return __fma_rn((double)(uint32_t)(v >> 32), 4294967296.0, (double)(uint32_t)v);
-    }
+    // Integer <-> double through the exponent bias: for 0 <= v < 2^52 the
+    // double with bits (0x433 << 52) | v is exactly 2^52 + v.
+    static constexpr uint64_t kBias = 0x4330000000000000ull;
+    static constexpr double kTwo52 = 4503599627370496.0;
+    static constexpr uint64_t kMant = (1ull << 52) - 1;
+    // exact for v < 2^52 (every residue of a prime below 2^50)
+    __device__ __forceinline__ T load(uint64_t v) const { return as_f(v | kBias) - kTwo52; }
+    // canonical residue of any integer-valued |v| < 2^53: with k the nearest
+    // integer to fl(v / q), v - k q lies within (0.5 + 2^-19) q of zero (and is
+    // computed exactly by the FMA), so one conditional add of q lands in [0, q).
     __device__ __forceinline__ uint64_t store(T v) const {
-        double k = floor(v * qinv);
+        const double k = rint(v * qinv);
         double r = __fma_rn(-k, q, v);
         r = r < 0.0 ? r + q : r;
-        r = r >= q ? r - q : r;
-        uint32_t hi = (uint32_t)(r * (1.0 / 4294967296.0));
-        uint32_t lo = (uint32_t)__fma_rn(-(double)hi, 4294967296.0, r);
-        return ((uint64_t)hi << 32) | lo;
+        return as_u(r + kTwo52) & kMant;
     }
     __device__ __forceinline__ uint64_t store_mid(T v) const {
         reduce(v);
