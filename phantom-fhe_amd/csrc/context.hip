@@ -231,16 +231,14 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     c.rb_inv = c.upload(rbi);
     PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
-    // The fused NTT (experimental, off unless PFA_NTT_FUSED=1) relies on the
-    // full-chip mode of MI355X: 8 XCDs, each workgroup able to name its XCD.
+    // Single-launch NTT (N = 2^16): needs the round-robin workgroup-to-XCD
+    // dealing of a full-chip MI355X partition, checked here by a probe kernel.
+    // PFA_NTT_ONEPASS=0 selects the two-launch path.
+    if (const char *w = std::getenv("PFA_ONEPASS_WPC")) c.onepass_wpc = std::max(1, std::atoi(w));
     {
-        hipDeviceProp_t prop;
-        PFA_HIP(hipGetDeviceProperties(&prop, c.device));
-        const bool can_fuse = c.N == 65536 && c.n_cu == 256 && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-        const char *f = std::getenv("PFA_NTT_FUSED");
-        c.ntt_fused = can_fuse && f && std::atoi(f) != 0;
-        if (const char *w = std::getenv("PFA_FUSED_WPC")) c.fused_wpc = std::max(1, std::atoi(w));
-        if (const char *w = std::getenv("PFA_FUSED_LAG")) c.fused_lag = std::max(1, std::atoi(w));
+        const char *f = std::getenv("PFA_NTT_ONEPASS");
+        const bool want = f ? std::atoi(f) != 0 : false;
+        c.ntt_onepass = want && c.N == 65536 && c.n_cu * c.onepass_wpc >= 128 && xcd_round_robin(c);
     }
 
     const uint64_t *Qm = moduli, *Pm = moduli + c.Q;

@@ -111,9 +111,8 @@ struct Ctx {
     ulonglong2 *rb_inv = nullptr;    // [QP][S2][N1] itw[(N1 + k1) << g]
     int n_cu = 256;                  // compute units of the device
     int ntt_wpc = 3;                 // resident NTT workgroups per CU the grid is sized for
-    bool ntt_fused = false;          // single-launch NTT with L2-resident intermediate (see ntt_kernels.h)
-    int fused_wpc = 2;               // workgroups per CU of the fused NTT
-    int fused_lag = 2;               // jobs between a job's first and second pass in an XCD queue
+    bool ntt_onepass = false;        // single-launch NTT with the intermediate kept in L2 (ntt_kernels.h)
+    int onepass_wpc = 3;             // workgroups per CU of the single-launch NTT
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
     // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
     ulonglong2 *moddown_scale = nullptr;
@@ -187,6 +186,9 @@ struct NttLaunch {
 };
 void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s);
 void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s);
+// True when the device deals workgroups to 8 XCDs round-robin (workgroup w on
+// XCD w mod 8), which the single-launch NTT relies on; runs a probe kernel.
+bool xcd_round_robin(const Ctx &c);
 
 // Fused key-switching / rescale pipelines (fused_ks.hip).
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp then the inner product with key.

@@ -1,4 +1,7 @@
 // NTT launchers and the raw-limb NTT entry points of the C ABI.
+#include <algorithm>
+#include <vector>
+
 #include "internal.h"
 #include "ntt_kernels.h"
 
@@ -77,21 +80,23 @@ void check_launch(const Ctx &c, const NttLaunch &a) {
 
 }  // namespace
 
-// Fused single-launch transform (N = 2^16 only; see ntt_kernels.h).
+// Single-launch transform (N = 2^16 only; see ntt_kernels.h).
 template <bool FWD>
-void fused(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+void onepass(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+    constexpr uint32_t T = OnePassGeo<8, 8>::T;
     const uint32_t jobs = b.M * b.L;
-    const uint32_t words = kXcds + jobs + 1;
+    const uint32_t words = jobs * (T + 1) + 1;
     Scratch sc(c, s);
     uint32_t *ctl = sc.alloc<uint32_t>(words);
-    uint64_t *scratch = sc.alloc((size_t)jobs * c.N);
-    hipLaunchKernelGGL(k_zero_u32, dim3((words + 255) / 256), dim3(256), 0, s, ctl, words);
-    FusedCtl f{ctl, ctl + kXcds, ctl + kXcds + jobs, scratch};
-    const dim3 grid((uint32_t)c.n_cu * (uint32_t)c.fused_wpc);
+    hipLaunchKernelGGL(k_zero_u32, dim3(std::min<uint32_t>((words + 255) / 256, 1024)), dim3(256), 0, s, ctl, words);
+    const OnePass o{ctl, ctl + (size_t)jobs * T, ctl + (size_t)jobs * (T + 1)};
+    // a whole number of job slots (8 XCDs x T workgroups) per launch
+    const uint32_t per = kXcds * T;
+    const uint32_t grid = std::max<uint32_t>(per, ((uint32_t)c.n_cu * (uint32_t)c.onepass_wpc) / per * per);
     if (FWD)
-        hipLaunchKernelGGL((ntt_fwd_fused<8, 8>), grid, dim3(256), 0, s, b, t, f, (uint32_t)c.fused_lag);
+        hipLaunchKernelGGL((ntt_fwd_1p<8, 8>), dim3(grid), dim3(256), 0, s, b, t, o);
     else
-        hipLaunchKernelGGL((ntt_inv_fused<8, 8>), grid, dim3(256), 0, s, b, t, f, (uint32_t)c.fused_lag);
+        hipLaunchKernelGGL((ntt_inv_1p<8, 8>), dim3(grid), dim3(256), 0, s, b, t, o);
     PFA_HIP(hipGetLastError());
 }
 
@@ -112,8 +117,8 @@ void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    if (c.ntt_fused) {
-        fused<true>(c, b, t, s);
+    if (c.ntt_onepass) {
+        onepass<true>(c, b, t, s);
         return;
     }
     PFA_NTT_DISPATCH(fwd);
@@ -124,12 +129,27 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    if (c.ntt_fused) {
-        fused<false>(c, b, t, s);
+    if (c.ntt_onepass) {
+        onepass<false>(c, b, t, s);
         return;
     }
     PFA_NTT_DISPATCH(inv);
     PFA_HIP(hipGetLastError());
+}
+
+bool xcd_round_robin(const Ctx &c) {
+    constexpr uint32_t G = 1024;
+    uint32_t *d = nullptr;
+    PFA_HIP(hipMalloc((void **)&d, G * sizeof(uint32_t)));
+    std::vector<uint32_t> h(G);
+    hipLaunchKernelGGL(k_xcc_probe, dim3(G), dim3(64), 0, 0, d);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpy(h.data(), d, G * sizeof(uint32_t), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    PFA_HIP(e);
+    for (uint32_t i = 0; i < G; i++)
+        if (h[i] != i % kXcds) return false;
+    return true;
 }
 
 }  // namespace pfa

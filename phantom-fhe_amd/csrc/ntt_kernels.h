@@ -332,8 +332,10 @@ __device__ __forceinline__ void fwd_cols_core(typename A::T (&x)[Sub<S1>::E], co
     fwd_round_b<A, S1>(x, ar, tw, 1, F);
 }
 
-// store of fwd_cols_core's output into limb olimb (intermediate form)
-template <class A, int S1, int S2>
+// store of fwd_cols_core's output into limb olimb (intermediate form); NT
+// selects streaming stores (plain stores keep the lines in L2 for a consumer
+// in the same launch)
+template <class A, int S1, int S2, bool NT = true>
 __device__ __forceinline__ void fwd_cols_store(const typename A::T (&x)[Sub<S1>::E], const A &ar, uint32_t tile,
                                                uint64_t *olimb) {
     using G = Geo<S1, S2>;
@@ -341,10 +343,16 @@ __device__ __forceinline__ void fwd_cols_store(const typename A::T (&x)[Sub<S1>:
     uint64_t *dst = olimb + tile * kCols;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) st_stream(&dst[(size_t)(F * SB::E + e) * G::N2 + c], ar.store_mid(x[e]));
+    for (int e = 0; e < SB::E; e++) {
+        uint64_t *p = &dst[(size_t)(F * SB::E + e) * G::N2 + c];
+        if (NT)
+            st_stream(p, ar.store_mid(x[e]));
+        else
+            *p = ar.store_mid(x[e]);
+    }
 }
 
-template <class A, int S1, int S2>
+template <class A, int S1, int S2, bool NT = true>
 __device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
                                               typename A::T *lds, uint64_t *olimb) {
@@ -355,7 +363,7 @@ __device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = ar.load(raw[e]);
     fwd_cols_core<A, S1, S2>(x, ar, t, prow, lds);
-    fwd_cols_store<A, S1, S2>(x, ar, r.tile, olimb);
+    fwd_cols_store<A, S1, S2, NT>(x, ar, r.tile, olimb);
 }
 
 template <int S1, int S2>
@@ -495,7 +503,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
 
 // ================================================================ inverse
 // Rows pass first: src (canonical) -> dst (intermediate).
-template <class A, int S1, int S2>
+template <class A, int S1, int S2, bool NT = true>
 __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
                                               const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
                                               typename A::T *lds, uint64_t *olimb) {
@@ -529,7 +537,12 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     else
         inv_round_b<A, S2, false>(x, ar, itw, G::N1 + k1, ulonglong2{0, 0});
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) st_stream(&drow[F + SB::T * e], ar.store_mid(x[e]));
+    for (int e = 0; e < SB::E; e++) {
+        if (NT)
+            st_stream(&drow[F + SB::T * e], ar.store_mid(x[e]));
+        else
+            drow[F + SB::T * e] = ar.store_mid(x[e]);
+    }
 }
 
 template <int S1, int S2>
@@ -639,195 +652,256 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBa
 
 namespace pfa {
 
-// ================================================================ fused
-// One launch runs both passes of every limb, with the intermediate kept in
-// the L2 of one XCD:
-//   * every workgroup reads its XCD id from the hardware register and takes
-//     work only from that XCD's queue; limb-job j belongs to XCD j mod 8;
-//   * a job is P1 tiles (first pass) then P2 tiles (second pass); the queue of
-//     an XCD is ordered P1(0), P1(1), P2(0), P1(2), P2(1), ..., P2(n-1), so a P2
-//     tile only ever waits for P1 tiles already taken by running workgroups
-//     (no deadlock, whatever the residency), and waits are rare;
-//   * P1 tiles store the intermediate into a per-job scratch limb (written
-//     through to the XCD's L2), wait for the stores' acknowledgement, then bump
-//     the job's counter (device-scope atomic); P2 tiles poll the counter and
-//     read the scratch with plain loads from the shared L2.  No CU has
-//     read a scratch line before within the launch (one limb per job), so no
-//     L1 holds a stale copy, and the lines come from the shared L2.
-// HBM sees the input read once, the output written once, plus the write-back
-// of the dead scratch lines.  Every wait is bounded; on expiry a flag is raised
-// and the kernel still terminates.
-struct FusedCtl {
-    uint32_t *queue;    // [8] per-XCD item counters, zero at launch
-    uint32_t *done;     // [jobs] finished P1 tiles per job, zero at launch
-    uint32_t *flags;    // [1] bit 0: a wait expired
-    uint64_t *scratch;  // [jobs][N] intermediate, written by P1, read by P2
+// ================================================================ single pass
+// One launch runs both passes of every limb, and a limb's intermediate never
+// leaves the L2 of the XCD that owns the limb: each first-pass tile rewrites
+// only its own tile of the output limb, and the second pass reads the limb back
+// from that L2.  HBM sees one read of the input and one write of the output.
+//
+// Ownership: limb-job j (tile order: j = l M + m) belongs to XCD j mod 8.
+// Workgroups are dealt to the XCDs round-robin (workgroup w runs on XCD w mod 8,
+// checked once per context by a probe kernel before this path is enabled), so
+// workgroup w is local workgroup u = w / 8 of XCD x = w mod 8.  With U = grid / 8
+// local workgroups and T tiles per pass, an XCD works on S = U / T jobs at a
+// time: local workgroup u takes first-pass tile u mod T of the XCD's jobs
+// u / T, u / T + S, ..., and after each the second-pass tile u mod T.
+//
+// No co-residency is assumed.  A first-pass tile is run only after claiming it
+// (agent-scope exchange on its flag), by its owner or by any workgroup of the
+// XCD that waits for the job; a workgroup waits only while every first-pass
+// tile of its job is claimed, i.e. held by running workgroups, which finish
+// them without waiting for anything.
+//
+// Visibility within the XCD: a first-pass tile's stores are acknowledged by L2
+// (s_waitcnt 0) before the job's count is raised with an atomic add (atomics
+// execute in L2); a workgroup that reads the full count invalidates its CU's L1
+// (buffer_inv sc0) before it loads the limb, so it reads the XCD's L2.  Every
+// wait is bounded: on expiry bit 0 of the flag word is set and the kernel
+// still ends.
+struct OnePass {
+    uint32_t *claim;  // [jobs][T] first-pass tile claims, zero at launch
+    uint32_t *done;   // [jobs] finished first-pass tiles, zero at launch
+    uint32_t *flags;  // [1] bit 0: a wait expired
 };
 
 constexpr uint32_t kXcds = 8;
-constexpr uint32_t kSpinLimit = 1u << 18;
+constexpr uint32_t kSpinLimit = 1u << 16;   // polls of one wait (each an agent-scope load after s_sleep 2)
+constexpr uint32_t kStealEvery = 64;         // polls between scans for unclaimed first-pass tiles
 
-__device__ __forceinline__ uint32_t xcc_id() {
-    uint32_t v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    return v & (kXcds - 1);
-}
-
-struct FusedItem {
-    uint32_t phase, k, tile;
+template <int S1, int S2>
+struct OnePassGeo {
+    using G = Geo<S1, S2>;
+    static constexpr bool OK = G::COL_THREADS == 256 && G::ROW_THREADS == 256 && G::COL_LDS == G::ROW_LDS &&
+                               G::COL_TILES == G::ROW_TILES;
+    static constexpr uint32_t T = G::COL_TILES;
 };
 
-// Queue order of one XCD with lag D (nx jobs, B tiles per phase of a job):
-//   P1(0) .. P1(D-1), then P1(D), P2(0), P1(D+1), P2(1), ..., then the last P2s.
-// P2(k) is taken about 2 D B items after P1(k) started, when its tiles are done.
-__device__ __forceinline__ FusedItem fused_item(uint32_t it, uint32_t nx, uint32_t B, uint32_t D) {
-    const uint32_t s = it / B, tile = it % B;
-    const uint32_t d = nx < D ? nx : D;
-    if (s < d) return FusedItem{1, s, tile};
-    const uint32_t u = s - d, np = nx > D ? nx - D : 0;
-    if (u < 2 * np) return (u & 1) ? FusedItem{2, u / 2, tile} : FusedItem{1, u / 2 + D, tile};
-    return FusedItem{2, np + (u - 2 * np), tile};
+// Polls are read-modify-writes (fetch_or 0): on gfx950 atomic RMWs execute in
+// the XCD's L2, where the counters live, while an agent-scope atomic load is
+// issued past L2 and costs a round trip to memory per poll.
+__device__ __forceinline__ uint32_t ld_agent(uint32_t *p) {
+    return __hip_atomic_fetch_or(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool try_claim(uint32_t *p) {
+    return __hip_atomic_exchange(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
 }
 
-// Queue and counters use device-scope atomics: on gfx950 workgroup-scope
-// atomics are not coherent between CUs, so they cannot coordinate workgroups.
-__device__ __forceinline__ uint32_t fused_take(uint32_t *queue, uint32_t xcc, uint32_t *s_slot) {
-    if (threadIdx.x == 0)
-        *s_slot = __hip_atomic_fetch_add(queue + xcc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Next first-pass tile this workgroup runs for `job` (< T), T + 1 once the job's
+// first pass is complete, or T to keep waiting.  `own` is the workgroup's own
+// tile on its first call for the job, T afterwards.  Uniform across the
+// workgroup (decided by thread 0, shared through LDS).
+template <uint32_t T>
+__device__ __forceinline__ uint32_t onepass_next(const OnePass &c, uint32_t job, uint32_t own, uint32_t spins,
+                                                 uint32_t *s_pick, uint32_t *s_free) {
+    uint32_t *cl = c.claim + (size_t)job * T;
+    if (threadIdx.x == 0) {
+        uint32_t pick = T;
+        if (own < T && try_claim(cl + own)) pick = own;
+        if (pick == T && ld_agent(c.done + job) >= T) pick = T + 1;
+        *s_pick = pick;
+    }
     __syncthreads();
-    const uint32_t it = *s_slot;
+    uint32_t pick = *s_pick;
+    if (pick == T && spins % kStealEvery == kStealEvery - 1) {
+        // look for first-pass tiles nobody has claimed (their owner is not running)
+        if (threadIdx.x < T) s_free[threadIdx.x] = ld_agent(cl + threadIdx.x) == 0u;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            for (uint32_t i = 0; i < T; i++)
+                if (s_free[i] && try_claim(cl + i)) {
+                    *s_pick = i;
+                    break;
+                }
+        __syncthreads();
+        pick = *s_pick;
+    }
     __syncthreads();
-    return it;
+    return pick;
 }
 
-// P1 side: all of this workgroup's stores are acknowledged by L2, then count the tile.
-__device__ __forceinline__ void fused_publish(uint32_t *done) {
+__device__ __forceinline__ void onepass_publish(uint32_t *done) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// P2 side: wait until all `need` P1 tiles of the job are published.
-__device__ __forceinline__ void fused_wait(uint32_t *done, uint32_t need, uint32_t *flags) {
-    if (threadIdx.x == 0) {
-        uint32_t spins = 0;
-        while (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-            __builtin_amdgcn_s_sleep(8);
-            if (++spins > kSpinLimit) {
-                __hip_atomic_fetch_or(flags, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ void onepass_expired(uint32_t *flags) {
+    if (threadIdx.x == 0) __hip_atomic_fetch_or(flags, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int S1, int S2>
-struct FusedGeo {
-    using G = Geo<S1, S2>;
-    static constexpr bool OK = G::COL_THREADS == 256 && G::ROW_THREADS == 256 && G::COL_LDS == G::ROW_LDS &&
-                               G::COL_TILES == G::ROW_TILES;
-    static constexpr int THREADS = 256;
-    static constexpr int LDS = G::COL_LDS;
-};
-
-template <int S1, int S2>
-__global__ void __launch_bounds__(256) ntt_fwd_fused(NttBatch b, NttTables t, FusedCtl ctl, uint32_t lag) {
+// The two passes of one job for the single-pass kernels; FWD selects the
+// forward (columns then rows) or inverse (rows then columns) transform.
+template <bool FWD, int S1, int S2>
+struct OnePassJob {
     using G = Geo<S1, S2>;
     using S1B = Sub<S1>;
     using S2B = Sub<S2>;
-    static_assert(FusedGeo<S1, S2>::OK, "fused NTT needs matching 256-thread passes");
-    __shared__ double lds[FusedGeo<S1, S2>::LDS];
-    __shared__ uint32_t s_slot;
-    const uint32_t xcc = xcc_id();
-    const uint32_t jobs = b.M * b.L;
-    const uint32_t nx = jobs > xcc ? (jobs - xcc + kXcds - 1) / kXcds : 0;
-    const uint32_t n1 = G::COL_TILES, n2 = G::ROW_TILES, total = nx * (n1 + n2);
-    for (;;) {
-        const uint32_t it = fused_take(ctl.queue, xcc, &s_slot);
-        if (it >= total) break;
-        const FusedItem f = fused_item(it, nx, n1, lag);
-        const uint32_t job = xcc + kXcds * f.k;
-        const TileRef r{job % b.M, job / b.M, f.tile};
-        const bool skip = b.excluded(r.m, r.l);
-        const uint32_t prow = b.map.row(r.l);
-        const uint64_t q = t.mod[prow];
-        if (f.phase == 1) {
-            if (!skip) {
-                const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
-                const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
-                uint64_t raw[S1B::E];
-#pragma unroll
-                for (int e = 0; e < S1B::E; e++) raw[e] = ld_stream(&s[(size_t)(F + S1B::T * e) * G::N2 + c]);
-                if (q < kF64PrimeBound)
-                    fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
-                else
-                    fwd_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), ctl.scratch + (size_t)job * G::N);
-            }
-            fused_publish(ctl.done + job);
-        } else if (!skip) {
-            fused_wait(ctl.done + job, n1, ctl.flags);
-            const uint32_t F = threadIdx.x % S2B::T, rr = threadIdx.x / S2B::T;
-            const uint64_t *srow = ctl.scratch + (size_t)job * G::N + (size_t)(r.tile * G::ROWS + rr) * G::N2;
-            uint64_t raw[S2B::E];
-#pragma unroll
-            for (int e = 0; e < S2B::E; e++) raw[e] = srow[F + S2B::T * e];
-            if (q < kF64PrimeBound)
-                fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
-            else
-                fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
-        }
-        __syncthreads();
-    }
-}
+    static constexpr uint32_t T = OnePassGeo<S1, S2>::T;
+    const NttBatch &b;
+    const NttTables &t;
+    uint32_t m, l, prow;
+    uint64_t q;
+    uint64_t *limb;
 
-template <int S1, int S2>
-__global__ void __launch_bounds__(256) ntt_inv_fused(NttBatch b, NttTables t, FusedCtl ctl, uint32_t lag) {
-    using G = Geo<S1, S2>;
-    using S1B = Sub<S1>;
-    using S2B = Sub<S2>;
-    static_assert(FusedGeo<S1, S2>::OK, "fused NTT needs matching 256-thread passes");
-    __shared__ double lds[FusedGeo<S1, S2>::LDS];
-    __shared__ uint32_t s_slot;
-    const uint32_t xcc = xcc_id();
-    const uint32_t jobs = b.M * b.L;
-    const uint32_t nx = jobs > xcc ? (jobs - xcc + kXcds - 1) / kXcds : 0;
-    const uint32_t n1 = G::ROW_TILES, n2 = G::COL_TILES, total = nx * (n1 + n2);
-    for (;;) {
-        const uint32_t it = fused_take(ctl.queue, xcc, &s_slot);
-        if (it >= total) break;
-        const FusedItem f = fused_item(it, nx, n1, lag);
-        const uint32_t job = xcc + kXcds * f.k;
-        const TileRef r{job % b.M, job / b.M, f.tile};
-        const bool skip = b.excluded(r.m, r.l);
-        const uint32_t prow = b.map.row(r.l);
-        const uint64_t q = t.mod[prow];
-        if (f.phase == 1) {
-            if (!skip) {
-                const uint32_t F = threadIdx.x % S2B::T;
-                const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
-                uint64_t raw[S2B::E];
-#pragma unroll
-                for (int e = 0; e < S2B::E; e++) raw[e] = ld_stream(&s[F + S2B::T * e]);
-                if (q < kF64PrimeBound)
-                    inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, ctl.scratch + (size_t)job * G::N);
-                else
-                    inv_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), ctl.scratch + (size_t)job * G::N);
-            }
-            fused_publish(ctl.done + job);
-        } else if (!skip) {
-            fused_wait(ctl.done + job, n1, ctl.flags);
+    __device__ OnePassJob(const NttBatch &b_, const NttTables &t_, uint32_t job) : b(b_), t(t_) {
+        m = job % b.M;
+        l = job / b.M;
+        prow = b.map.row(l);
+        q = t.mod[prow];
+        limb = b.dst + m * b.dstride + (size_t)l * G::N;
+    }
+    // first-pass tile `tile`: reads the source, leaves the intermediate in the
+    // tile's own part of the output limb (plain stores: the lines stay in L2)
+    __device__ void first(uint32_t tile, double *lds) const {
+        const TileRef r{m, l, tile};
+        if (FWD) {
             const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
-            const uint64_t *scol = ctl.scratch + (size_t)job * G::N + r.tile * kCols;
+            const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
             uint64_t raw[S1B::E];
 #pragma unroll
-            for (int e = 0; e < S1B::E; e++) raw[e] = scol[(size_t)(F * S1B::E + e) * G::N2 + c];
+            for (int e = 0; e < S1B::E; e++) raw[e] = ld_stream(&s[(size_t)(F + S1B::T * e) * G::N2 + c]);
             if (q < kF64PrimeBound)
-                inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+                fwd_cols_tile<ArithF64, S1, S2, false>(raw, b, t, r, prow, q, lds, limb);
             else
-                inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+                fwd_cols_tile<ArithInt, S1, S2, false>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+        } else {
+            const uint32_t F = threadIdx.x % S2B::T;
+            const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
+            uint64_t raw[S2B::E];
+#pragma unroll
+            for (int e = 0; e < S2B::E; e++) raw[e] = ld_stream(&s[F + S2B::T * e]);
+            if (q < kF64PrimeBound)
+                inv_rows_tile<ArithF64, S1, S2, false>(raw, b, t, r, prow, q, lds, limb);
+            else
+                inv_rows_tile<ArithInt, S1, S2, false>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+        }
+    }
+    // second-pass tile `tile` of the output limb, after the job's first pass
+    __device__ void second(uint32_t tile, double *lds) const {
+        asm volatile("buffer_inv sc0" ::: "memory");
+        const TileRef r{m, l, tile};
+        if (FWD) {
+            const uint32_t F = threadIdx.x % S2B::T;
+            const uint64_t *s = rows_ptr<S1, S2>(b, r, b.dst, b.dstride);
+            uint64_t raw[S2B::E];
+#pragma unroll
+            for (int e = 0; e < S2B::E; e++) raw[e] = s[F + S2B::T * e];
+            if (q < kF64PrimeBound)
+                fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, limb);
+            else
+                fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+        } else {
+            const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+            const uint64_t *s = cols_src<S1, S2>(b, r, b.dst, b.dstride);
+            uint64_t raw[S1B::E];
+#pragma unroll
+            for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F * S1B::E + e) * G::N2 + c];
+            if (q < kF64PrimeBound)
+                inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, limb);
+            else
+                inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
         }
         __syncthreads();
+    }
+};
+
+// Claims and runs first-pass tiles of `job` (its own tile `own` first, when
+// given) until the job's first pass is complete; false if a wait expired.
+template <bool FWD, int S1, int S2>
+__device__ bool onepass_complete(const OnePassJob<FWD, S1, S2> &J, const OnePass &ctl, uint32_t job, uint32_t own,
+                                 bool wait, double *lds, uint32_t *s_pick, uint32_t *s_free) {
+    constexpr uint32_t T = OnePassGeo<S1, S2>::T;
+    for (uint32_t spins = 0;; own = T) {
+        const uint32_t pick = onepass_next<T>(ctl, job, own, spins, s_pick, s_free);
+        if (pick == T + 1) return true;
+        if (pick < T) {
+            J.first(pick, lds);
+            onepass_publish(ctl.done + job);
+            if (!wait) return true;
+            continue;
+        }
+        if (!wait) return true;
+        if (++spins > kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+// Lag-one schedule of a local workgroup: first pass of job i + 1 before the
+// second pass of job i, so the wait for job i's first pass is usually over.
+template <bool FWD, int S1, int S2>
+__device__ void onepass_run(const NttBatch &b, const NttTables &t, const OnePass &ctl, double *lds, uint32_t *s_pick,
+                            uint32_t *s_free) {
+    constexpr uint32_t T = OnePassGeo<S1, S2>::T;
+    const uint32_t x = blockIdx.x % kXcds, u = blockIdx.x / kXcds;
+    const uint32_t S = (gridDim.x / kXcds) / T, slot = u / T, tau = u % T;
+    const uint32_t jobs = b.M * b.L;
+    const uint32_t nx = jobs > x ? (jobs - x + kXcds - 1) / kXcds : 0;
+    if (slot >= S) return;
+    uint32_t prev = 0xffffffffu;  // job whose second pass is pending
+    for (uint32_t kx = slot;; kx += S) {
+        uint32_t job = 0xffffffffu;
+        if (kx < nx) {
+            job = x + kXcds * kx;
+            if (b.excluded(job % b.M, job / b.M)) job = 0xffffffffu;
+        }
+        if (job != 0xffffffffu) {
+            const OnePassJob<FWD, S1, S2> J(b, t, job);
+            onepass_complete<FWD, S1, S2>(J, ctl, job, tau, false, lds, s_pick, s_free);
+        }
+        if (prev != 0xffffffffu) {
+            const OnePassJob<FWD, S1, S2> P(b, t, prev);
+            if (onepass_complete<FWD, S1, S2>(P, ctl, prev, T, true, lds, s_pick, s_free))
+                P.second(tau, lds);
+            else
+                onepass_expired(ctl.flags);
+        }
+        prev = job;
+        if (kx >= nx && prev == 0xffffffffu) break;
+    }
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__(256) ntt_fwd_1p(NttBatch b, NttTables t, OnePass ctl) {
+    static_assert(OnePassGeo<S1, S2>::OK, "single-pass NTT needs matching 256-thread passes");
+    __shared__ double lds[Geo<S1, S2>::COL_LDS];
+    __shared__ uint32_t s_pick, s_free[OnePassGeo<S1, S2>::T];
+    onepass_run<true, S1, S2>(b, t, ctl, lds, &s_pick, s_free);
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__(256) ntt_inv_1p(NttBatch b, NttTables t, OnePass ctl) {
+    static_assert(OnePassGeo<S1, S2>::OK, "single-pass NTT needs matching 256-thread passes");
+    __shared__ double lds[Geo<S1, S2>::COL_LDS];
+    __shared__ uint32_t s_pick, s_free[OnePassGeo<S1, S2>::T];
+    onepass_run<false, S1, S2>(b, t, ctl, lds, &s_pick, s_free);
+}
+
+// Records XCD ids by workgroup (the probe that enables the single-pass path).
+static __global__ void k_xcc_probe(uint32_t *out) {
+    if (threadIdx.x == 0) {
+        uint32_t v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        out[blockIdx.x] = v & 0xfu;
     }
 }
 
