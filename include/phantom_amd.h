@@ -26,8 +26,10 @@
  *     classes: INVALID_ARGUMENT = std::invalid_argument (ValueError in
  *     Python), LOGIC = std::logic_error, RUNTIME = std::runtime_error
  *     (PHANTOM_CHECK_CUDA, include/cuda_wrapper.cuh:19-43).
- *   - Temporaries are stream-ordered allocations (hipMallocAsync), as the
- *     reference's cuda_auto_ptr (include/cuda_wrapper.cuh:185-189).
+ *   - Temporaries come from a device workspace kept per (host thread, stream)
+ *     and grown on first use, where the reference makes stream-ordered
+ *     allocations (cuda_auto_ptr, include/cuda_wrapper.cuh:185-189); calls in
+ *     steady state allocate nothing.
  */
 #ifndef PHANTOM_AMD_H
 #define PHANTOM_AMD_H
