@@ -11,7 +11,7 @@
 //     1. INTT(c2) * [(Q_b/q_i)^-1]_{q_i}                       (ntt_inverse)
 //     2. k_bconv_cols: per digit b and target limb r outside digit b,
 //        y = sum_i t_i [Q_b/q_i]_{p_r} then the columns pass    -> I[b][r]
-//     3. k_inner_rows: per target limb r, for every digit b: the rows pass
+//     3. k_inner_ws: per target limb r, for every digit b: the rows pass
 //        of I[b][r] (or c2 itself when r is in digit b), times key[b][k][r],
 //        accumulated over b                                      -> cx[k][r]
 //   ModDown cx -> out over Ql:
@@ -200,60 +200,189 @@ struct InnerRows {
     uint32_t Ql, QlP, alpha, beta, Q, QP;
 };
 
+// Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
+// (already in NTT form) or the columns-pass output to transform.
+__device__ __forceinline__ const uint64_t *inner_src(const InnerRows &a, uint32_t b, uint32_t r, size_t rowoff,
+                                                     uint32_t N, bool &own) {
+    own = r < a.Ql && r >= b * a.alpha && r < b * a.alpha + a.alpha;
+    return own ? a.c2 + (size_t)r * N + rowoff : a.inter + ((size_t)b * a.QlP + r) * N + rowoff;
+}
+
+// One work item is a (target limb r, tile of ROWS rows) pair; its digits are
+// processed in turn by a warp-specialized workgroup.  The first half of the
+// workgroup (the transform waves) runs digit b's rows pass into one of two LDS
+// buffers while the second half (the accumulate waves) multiplies digit b-1's
+// transformed tile, read from the other buffer, by its key limbs.  The roles
+// keep disjoint register state (transform: the tile and the next digit's
+// prefetched tile; accumulate: the two accumulators and the key limbs), so the
+// key traffic overlaps the transforms of the other waves.  Each role's loop
+// runs beta + 1 steps with three workgroup barriers per step, in the same order
+// in both roles:
+//   A  transform: round a of digit b (or its own limb of c2) -> buffer b%2
+//   B  transform: round b;   accumulate: output 0 of digit b-1 from buffer (b-1)%2
+//   C  transform: final layout -> buffer b%2;   accumulate: output 1 of digit b-1
+// Measured against one role doing both (206 VGPRs, 2 waves per SIMD): equal at
+// config 3 (6 digits), 7-10% faster with 35 digits.
+template <int S1, int S2>
+struct WsGeo {
+    using G = Geo<S1, S2>;
+    static constexpr int ROWS = FGeo<S1, S2>::ROWS;
+    static constexpr int HALF = ROWS * Sub<S2>::T;  // threads per role
+    static constexpr int THREADS = 2 * HALF;
+    static constexpr int TILES = G::N1 / ROWS;
+    static constexpr int LDS = 2 * ROWS * G::ROW_PITCH;
+    static_assert(HALF % 64 == 0, "each role must be whole wavefronts");
+};
+
 template <class A, int S1, int S2>
-__device__ __forceinline__ void inner_item(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
-                                           uint32_t prow, uint32_t k1, typename A::T *lr) {
+__device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
+                                             uint32_t prow, uint32_t k1, typename A::T *b0, typename A::T *b1) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
-    const uint32_t F = threadIdx.x % SB::T;
+    const uint32_t F = (threadIdx.x % WsGeo<S1, S2>::HALF) % SB::T;
+    const size_t rowoff = (size_t)k1 * G::N2 + F;
+    uint64_t nraw[SB::E];
+    bool nown;
+    {
+        const uint64_t *s = inner_src(a, 0, r, rowoff, G::N, nown);
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
+    }
+    for (uint32_t b = 0; b <= a.beta; b++) {
+        T *buf = (b & 1u) ? b1 : b0;
+        const bool live = b < a.beta, own = nown;
+        // The twiddles depend on the row and the prime only; left loop-invariant,
+        // the compiler keeps every one of them live across the digit loop
+        // (~120 VGPRs) and the kernel loses a wave per SIMD.  Recomputing them
+        // per digit is cheaper.
+        uint32_t kr = k1, pr = prow;
+        asm volatile("" : "+v"(kr), "+s"(pr));
+        const ulonglong2 *tw = t.tw + (size_t)pr * G::N;
+        const ulonglong2 *rb = t.rb_fw + (size_t)pr * S2 * G::N1;
+        const ulonglong2 *small = t.small_fw + (size_t)pr * kSmall;
+        T x[SB::E];
+        // A
+        if (live) {
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) x[e] = own ? ar.load(nraw[e]) : ar.load_mid(nraw[e]);
+            if (b + 1 < a.beta) {
+                const uint64_t *s = inner_src(a, b + 1, r, rowoff, G::N, nown);
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
+            }
+            if (!own) {
+                if constexpr (A::kF64)
+                    fwd_round_a_derived<S2, G::N1>(x, ar, rb, small, kr);
+                else
+                    fwd_round_a<A, S2>(x, ar, tw, G::N1 + kr);
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) ar.reduce(x[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
+        }
+        __syncthreads();
+        // B
+        if (live && !own) {
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) x[e] = buf[rpad(F * SB::E + e)];
+            if constexpr (A::kF64)
+                fwd_round_b_derived<S2, G::N1>(x, ar, rb, small, kr, F);
+            else
+                fwd_round_b<A, S2>(x, ar, tw, G::N1 + kr, F);
+        }
+        __syncthreads();
+        // C
+        if (live && !own) {
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) buf[rpad(F * SB::E + e)] = x[e];
+        }
+        __syncthreads();
+    }
+}
+
+// Product of digit d's transformed element x (lazy) with key limb value w,
+// accumulated into acc: FP64 policy exact products (acc reduced every second
+// digit), integer policy Barrett products summed modulo q.
+template <class A>
+__device__ __forceinline__ void ws_mac(const A &ar, typename A::T &acc, typename A::T x, uint64_t w, ulonglong2 rt) {
+    if constexpr (A::kF64) {
+        ar.reduce(x);
+        const double wd = ar.load(w);
+        acc += ar.mulw(x, wd, wd * ar.qinv);
+    } else {
+        U128 p{x * w, mulhi64(x, w)};
+        acc = add_mod(acc, barrett128(p, ar.q, rt.x, rt.y), ar.q);
+    }
+}
+
+template <class A, int S1, int S2>
+__device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, uint32_t r, uint32_t prow,
+                                              uint32_t k1, const typename A::T *b0, const typename A::T *b1) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S2>;
+    using T = typename A::T;
+    const uint32_t F = (threadIdx.x % WsGeo<S1, S2>::HALF) % SB::T;
     const size_t rowoff = (size_t)k1 * G::N2 + F;
     const size_t keyrow = (size_t)prow * G::N + rowoff;
+    const uint64_t QPN = (uint64_t)a.QP * G::N;
+    // key limb k of digit d at this thread's positions
+    auto key_of = [&](uint32_t d, uint32_t k) { return a.key + ((size_t)d * 2 + k) * QPN + keyrow; };
     T acc0[SB::E], acc1[SB::E];
+    uint64_t kw0[SB::E], kw1[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) acc0[e] = acc1[e] = 0;
-    for (uint32_t b = 0; b < a.beta; b++) {
-        T x[SB::E];
-        const bool own = r < a.Ql && r >= b * a.alpha && r < b * a.alpha + a.alpha;
-        if (own) {
-            const uint64_t *s = a.c2 + (size_t)r * G::N + rowoff;
+    {
+        const uint64_t *k0 = key_of(0, 0), *kk1 = key_of(0, 1);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) x[e] = ar.load(ld_stream(&s[SB::T * e]));
-        } else {
-            const uint64_t *s = a.inter + ((size_t)b * a.QlP + r) * G::N + rowoff;
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(ld_stream(&s[SB::T * e]));
-            fwd_rows_core<A, S1, S2>(x, ar, t, prow, k1, lr);
-            __syncthreads();
+        for (int e = 0; e < SB::E; e++) {
+            kw0[e] = ld_stream(&k0[SB::T * e]);
+            kw1[e] = ld_stream(&kk1[SB::T * e]);
         }
-        const uint64_t *k0 = a.key + (size_t)b * 2 * a.QP * G::N + keyrow;
-        const uint64_t *kk1 = k0 + (size_t)a.QP * G::N;
-        if constexpr (A::kF64) {
+    }
+    const ulonglong2 rt = a.ratio[prow];
+    // Output k of digit b - 1 is accumulated in phase B (k = 0) or C (k = 1) of
+    // step b; each key register set is refilled with digit b's limb right after
+    // it is consumed, a full step before it is needed.
+    for (uint32_t b = 0; b <= a.beta; b++) {
+        const T *buf = ((b - 1) & 1u) ? b1 : b0;
+        // A
+        __syncthreads();
+        // B
+        if (b >= 1) {
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) {
-                ar.reduce(x[e]);
-                const double w0 = ar.load(ld_stream(&k0[SB::T * e])), w1 = ar.load(ld_stream(&kk1[SB::T * e]));
-                acc0[e] += ar.mulw(x[e], w0, w0 * ar.qinv);
-                acc1[e] += ar.mulw(x[e], w1, w1 * ar.qinv);
+            for (int e = 0; e < SB::E; e++) ws_mac(ar, acc0[e], buf[rpad(F + SB::T * e)], kw0[e], rt);
+            // keep the refill after the products so it can reuse their key registers
+            __builtin_amdgcn_sched_barrier(0);
+            if (b < a.beta) {
+                const uint64_t *k0 = key_of(b, 0);
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) kw0[e] = ld_stream(&k0[SB::T * e]);
             }
-            if (b & 1u) {
+        }
+        __syncthreads();
+        // C
+        if (b >= 1) {
 #pragma unroll
-                for (int e = 0; e < SB::E; e++) {
-                    ar.reduce(acc0[e]);
-                    ar.reduce(acc1[e]);
+            for (int e = 0; e < SB::E; e++) ws_mac(ar, acc1[e], buf[rpad(F + SB::T * e)], kw1[e], rt);
+            __builtin_amdgcn_sched_barrier(0);
+            if (b < a.beta) {
+                const uint64_t *kk1 = key_of(b, 1);
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) kw1[e] = ld_stream(&kk1[SB::T * e]);
+            }
+            if constexpr (A::kF64) {
+                if (!(b & 1u)) {
+#pragma unroll
+                    for (int e = 0; e < SB::E; e++) {
+                        ar.reduce(acc0[e]);
+                        ar.reduce(acc1[e]);
+                    }
                 }
             }
-        } else {
-            const ulonglong2 rt = a.ratio[prow];
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) {
-                const uint64_t w0 = ld_stream(&k0[SB::T * e]), w1 = ld_stream(&kk1[SB::T * e]);
-                U128 p0{x[e] * w0, mulhi64(x[e], w0)};
-                U128 p1{x[e] * w1, mulhi64(x[e], w1)};
-                acc0[e] = add_mod(acc0[e], barrett128(p0, ar.q, rt.x, rt.y), ar.q);
-                acc1[e] = add_mod(acc1[e], barrett128(p1, ar.q, rt.x, rt.y), ar.q);
-            }
         }
+        __syncthreads();
     }
     uint64_t *o0 = a.cx + (size_t)r * G::N + rowoff;
     uint64_t *o1 = o0 + (size_t)a.QlP * G::N;
@@ -265,24 +394,35 @@ __device__ __forceinline__ void inner_item(const InnerRows &a, const NttTables &
 }
 
 template <int S1, int S2>
-__global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_inner_rows(InnerRows a, NttTables t) {
+__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a, NttTables t) {
     using G = Geo<S1, S2>;
-    using FG = FGeo<S1, S2>;
-    __shared__ double lds[FG::LDS];
-    const uint32_t rr = threadIdx.x / Sub<S2>::T;
-    const uint32_t total = a.QlP * FG::TILES;
+    using W = WsGeo<S1, S2>;
+    __shared__ double lds[W::LDS];
+    const bool transform = threadIdx.x < W::HALF;
+    const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
+    const uint32_t total = a.QlP * W::TILES;
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
-        const uint32_t r = w / FG::TILES, tile = w % FG::TILES;
+        const uint32_t r = w / W::TILES, tile = w % W::TILES;
         const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
         const uint64_t q = t.mod[prow];
-        const uint32_t k1 = tile * FG::ROWS + rr;
-        if (q < kF64PrimeBound)
-            inner_item<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, lds + rr * G::ROW_PITCH);
-        else
-            inner_item<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1,
-                                         reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH);
+        const uint32_t k1 = tile * W::ROWS + rr;
+        if (q < kF64PrimeBound) {
+            double *b0 = lds + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
+            if (transform)
+                ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, b0, b1);
+            else
+                ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, k1, b0, b1);
+        } else {
+            uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
+            if (transform)
+                ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, b0, b1);
+            else
+                ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, k1, b0, b1);
+        }
+        __syncthreads();
     }
 }
+
 
 // ------------------------------------------------------------ epilogue rows
 // out[m][j] = (base[m][j] if given) + (c[m][j] - NTT(D[m][j])) f_j   (mod q_j)
@@ -374,8 +514,8 @@ void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
 
 template <int S1, int S2>
 void launch_inner(const Ctx &c, const InnerRows &a, hipStream_t s) {
-    using FG = FGeo<S1, S2>;
-    hipLaunchKernelGGL((k_inner_rows<S1, S2>), dim3(fgrid(c, a.QlP * FG::TILES, 8)), dim3(FG::THREADS), 0, s, a,
+    using W = WsGeo<S1, S2>;
+    hipLaunchKernelGGL((k_inner_ws<S1, S2>), dim3(fgrid(c, a.QlP * W::TILES, 4)), dim3(W::THREADS), 0, s, a,
                        tables_of(c));
     PFA_HIP(hipGetLastError());
 }

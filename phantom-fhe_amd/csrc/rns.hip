@@ -47,7 +47,15 @@ k_poly_binop(int op, const uint64_t *a, const uint64_t *b, uint64_t *out, const 
     switch (op) {
     case kAdd: r = add_mod(x, b[i], q); break;
     case kSub: r = sub_mod(x, b[i], q); break;
-    case kMul: r = mulmod_b(x, b[i], q, ratio[start + l]); break;
+    case kMul:
+        if (q < kF64PrimeBound) {
+            const ArithF64 ar(q);
+            const double y = ar.load(b[i]);
+            r = ar.store(ar.mulw(ar.load(x), y, y * ar.qinv));
+        } else {
+            r = mulmod_b(x, b[i], q, ratio[start + l]);
+        }
+        break;
     default: r = x ? q - x : 0; break;
     }
     out[i] = r;
@@ -70,14 +78,26 @@ k_from_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t st
 
 // tensor_prod_2x2_rns_poly (src/polymath.cu:463-498):
 //   d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1  (mod q_l)
+// (primes below 2^50: exact FP64 products; |a b / q| < q < 2^50 keeps
+// fl(a fl(b/q)) within 3/8 of the true quotient, so each product is within
+// 0.875 q and a sum of two stays far below 2^53)
 __global__ void __launch_bounds__(kThreads)
 k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint64_t *d2, const uint64_t *mod,
          const ulonglong2 *ratio, uint32_t Ql, uint32_t N) {
     const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     const uint64_t q = mod[l];
-    const ulonglong2 r = ratio[l];
     const size_t i = (size_t)l * N + n, LN = (size_t)Ql * N;
     const uint64_t a0 = ld_stream(&a[i]), a1 = ld_stream(&a[LN + i]), b0 = ld_stream(&b[i]), b1 = ld_stream(&b[LN + i]);
+    if (q < kF64PrimeBound) {
+        const ArithF64 ar(q);
+        const double x0 = ar.load(a0), x1 = ar.load(a1), y0 = ar.load(b0), y1 = ar.load(b1);
+        const double q0 = y0 * ar.qinv, q1 = y1 * ar.qinv;
+        st_stream(&d0[i], ar.store(ar.mulw(x0, y0, q0)));
+        st_stream(&d1[i], ar.store(ar.mulw(x0, y1, q1) + ar.mulw(x1, y0, q0)));
+        st_stream(&d2[i], ar.store(ar.mulw(x1, y1, q1)));
+        return;
+    }
+    const ulonglong2 r = ratio[l];
     U128 m{0, 0};
     mac(m, a0, b1);
     mac(m, a1, b0);

@@ -83,6 +83,31 @@ def test_ntt_config2_full_size(dev):
     assert np.array_equal(to_host(d), x)
 
 
+def test_ntt_single_launch_variant(dev, monkeypatch):
+    """The opt-in single-launch NTT (PFA_NTT_ONEPASS=1, read at context creation;
+    N = 2^16 on a device that deals workgroups to 8 XCDs round-robin) against
+    the oracle, both arithmetic policies, batches whose job count is not a
+    multiple of the XCD count, and a single limb."""
+    import pfa_native as P
+
+    monkeypatch.setenv("PFA_NTT_ONEPASS", "1")
+    N = 1 << 16
+    bits = [50, 60, 45, 50, 60, 50, 49]
+    mods = O.create_coeff_modulus(N, bits + [60])
+    ctx = P.NativeContext(N, mods, 1)
+    orc = O.Oracle(N, mods, 1)
+    rng = np.random.default_rng(11)
+    for M, L in [(2, 7), (3, 5), (1, 1)]:
+        x = uniform_limbs(rng, (M, L, N), mods)
+        d = to_dev(x, dev)
+        ctx.ntt_forward(d, M, L, 0)
+        got = to_host(d)
+        assert np.array_equal(got, orc.ntt_fwd(x, threads=8)), first_mismatch(got, orc.ntt_fwd(x, threads=8))
+        ctx.ntt_inverse(d, M, L, 0)
+        back = to_host(d)
+        assert np.array_equal(back, x), first_mismatch(back, x)
+
+
 @pytest.mark.parametrize("fill", ["zero", "qm1", "one", "two"])
 def test_ntt_edge_values(dev, fill):
     """Constant inputs (the reference's own all-1 / all-2 cases, test/ntt_test.cu:48-50,
