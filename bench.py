@@ -9,9 +9,10 @@ To keep the measurement an HBM measurement, the timed steps cycle through
 several distinct batches whose total size exceeds the 256 MiB Infinity Cache,
 so no step finds its batch cached from the previous one.
 
-Also reported (same line): inverse NTT limbs/s, and HMult + relinearize +
-rescale latency for config 3 (|Q| = 24, alpha = 4, dnum = 6) and for the
-metric's "L=35" variant (|Q| = 35, alpha = 1).
+Also reported (same line): inverse NTT limbs/s, HMult + relinearize + rescale
+latency for config 3 (|Q| = 24, alpha = 4, dnum = 6) and for the metric's
+"L=35" variant (|Q| = 35, alpha = 1), and the config-4 BSGS matrix-vector
+product (4096 x 4096 matrix, 64 baby x 64 giant steps, L = 20).
 
 cpu_baseline: the CPU oracle's forward NTT (oracle/ckks_oracle.c, a C
 restatement of the reference algorithm) on the same workload, single thread,
@@ -105,6 +106,65 @@ def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
             "chain": f"{{60, 50 x {nq - 1}, 60 x {alpha}}}", "dnum": dnum}
 
 
+def time_bsgs(torch, steps, warmup):
+    """BASELINE config 4 through the pyPhantom API: y = W x for a 4096 x 4096
+    matrix uniform in [-1/64, 1/64] (seeded), x uniform in [-1, 1] replicated over
+    the 2^15 slots with period 4096, baby 64 / giant 64, L = 20 (chain
+    {60, 40 x 19, 60 x 4}), scale 2^40, sparse ternary secret h = 192.  Times the
+    whole product (63 baby rotations, the giants' accumulation, 63 giant
+    rotations, the rescale) with the expanded diagonals resident; the one-time
+    encode and expansion are reported separately, and the decrypted result is
+    checked against numpy."""
+    import numpy as np
+
+    import pyPhantom as ph
+
+    d_pad, M = 4096, 64
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, [60] + [40] * 19 + [60] * 4))
+    p.set_special_modulus_size(4)
+    p.set_galois_elts(ph.get_elts_from_steps(ph.bsgs_required_steps(M), N))
+    ctx = ph.context(p)
+    ph.set_seed(4)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(4)
+    W = rng.uniform(-1 / 64, 1 / 64, (d_pad, d_pad))
+    xv = rng.uniform(-1, 1, d_pad)
+    scale = 2.0 ** 40
+    t0 = time.perf_counter()
+    diags = ph.pre_encode_bsgs_diagonals(ctx, enc, W.ravel(), d_pad, d_pad, d_pad, M, scale)
+    t_encode = time.perf_counter() - t0
+    x = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, np.tile(xv, enc.slot_count() // d_pad), scale))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    diags.expanded(ctx, x.chain_index())
+    torch.cuda.synchronize()
+    t_expand = time.perf_counter() - t0
+    for _ in range(warmup):
+        y = ph.bsgs_matmul_preencoded(ctx, glk, x, diags)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        y = ph.bsgs_matmul_preencoded(ctx, glk, x, diags)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, y)))
+    err = float(np.max(np.abs(got - np.tile(W @ xv, enc.slot_count() // d_pad))))
+    L = ctx.size_Ql(1)
+    # plaintext limbs read by the accumulation dominate the compulsory bytes
+    pt_bytes = d_pad * L * LIMB_BYTES
+    del diags
+    return {"ms": round(ms, 3), "max_abs_err": err, "encode_s": round(t_encode, 2),
+            "expand_ms": round(t_expand * 1e3, 1), "plaintext_bytes": pt_bytes,
+            "rotations": 2 * (M - 1), "chain": "{60, 40 x 19, 60 x 4}", "d_pad": d_pad, "baby": M,
+            "giant": d_pad // M}
+
+
 def measured_traffic():
     """HBM bytes per forward NTT from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE of both kernels, scaled by the plain-copy factor);
@@ -146,10 +206,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-hmult", action="store_true")
-    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult"], default="full",
+    ap.add_argument("--no-bsgs", action="store_true")
+    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "bsgs"], default="full",
                     help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
                          "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
-                         "config-3 HMult + relin + rescale")
+                         "config-3 HMult + relin + rescale; bsgs: only the config-4 matrix-vector product")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -167,6 +228,11 @@ def main():
     ctx = P.NativeContext(N, mods, 1)
     n_batches = 10  # 10 x 35 MiB > 256 MiB Infinity Cache
     batches = [uniform(torch, (POLYS, LIMBS, N), mods, dev, gen) for _ in range(n_batches)]
+    if args.mode == "bsgs":
+        del batches
+        r = time_bsgs(torch, max(2, args.steps // 40), 1)
+        log(f"bench: bsgs mode, config 4: {r}")
+        return
     if args.mode == "hmult":
         del batches
         r = time_hmult(torch, P, dev, gen, 24, 4, args.steps, args.warmup)
@@ -202,6 +268,12 @@ def main():
         log(f"bench: hmult L=35 {hm['L35_Q35_alpha1']['ms']} ms")
         torch.cuda.empty_cache()
 
+    bsgs = None
+    if not args.no_bsgs:
+        bsgs = time_bsgs(torch, 5, 1)
+        log(f"bench: bsgs config4 {bsgs['ms']} ms, max abs err {bsgs['max_abs_err']:.2e}")
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(mods, args.cpu_seconds)
@@ -230,6 +302,7 @@ def main():
         "ntt_forward_us": round(ev_ms * 1e3, 2),
         "ntt_inverse_us": round(ev_inv_ms * 1e3, 2),
         "hmult_relin_rescale": hm,
+        "bsgs_matvec_config4": bsgs,
     }
     print(json.dumps(line), flush=True)
 

@@ -188,6 +188,32 @@ int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_value
 int pfa_ckks_decode(const pfa_context *ctx, const uint64_t *in, size_t L, double scale, double *values,
                     void *stream);
 
+/* encode_single_chain_plaintext (src/single_chain_plaintext.cu:93-150): the
+ * same slot encoding as pfa_ckks_encode, returned as the N rounded signed
+ * coefficients (device int64) instead of residues -- the reference's
+ * level-independent plaintext.  Expand with pfa_expand_signed and
+ * pfa_ntt_forward at the level of use.  Synchronizes the stream. */
+int pfa_ckks_encode_coeffs(const pfa_context *ctx, const double *values, size_t n_values, double scale,
+                           int64_t *coeffs, void *stream);
+
+/* ------------------------------------------------------------------ BSGS */
+
+/* light_pt_expand_per_tower_kernel (src/bootstrap.cu, used by src/bsgs.cu:260-271)
+ * batched: n signed coefficient polys in[n][N] -> out[n][L][N], the residues of
+ * table rows start .. start+L-1 (coefficient form; NTT them with
+ * pfa_ntt_forward(ctx, out, n, L, start, stream)). */
+int pfa_expand_signed(const pfa_context *ctx, const int64_t *in, size_t n, uint64_t *out, size_t L, size_t start,
+                      void *stream);
+
+/* mac_accumulate_kernel (src/bsgs.cu:51-96) for every giant at once, the
+ * accumulation of bsgs_apply_giants_with_babies (src/bsgs.cu:272-296):
+ *   out[g][k] = sum_{b < M} pts[g*M + b] * babies[b][k]   (k = 0, 1; mod q_j)
+ * pts: G*M plaintexts [Ql][N]; babies: M ciphertexts [2][Ql][N]; out: G
+ * ciphertexts [2][Ql][N]; all NTT form at chain_index.  The pointer tables are
+ * host arrays of device pointers. */
+int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *const *pts,
+                 const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,27 @@ __global__ void k_enc_round(const double2 *w, uint64_t *out, const uint64_t *mod
     }
 }
 
+// z_k = w_k zeta^-k / M -> the rounded integer coefficients themselves (the
+// reference's level-independent single-chain plaintext, src/single_chain_plaintext.cu:93-150).
+__global__ void k_enc_round_signed(const double2 *w, int64_t *out, uint32_t N, double scale_over_m,
+                                   uint32_t *overflow) {
+    const uint32_t M = N / 2;
+    for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < M; k += gridDim.x * blockDim.x) {
+        double s, c;
+        sincospi(-(double)k / (double)N, &s, &c);
+        const double2 v = w[k];
+        const double r[2] = {rint((v.x * c - v.y * s) * scale_over_m), rint((v.x * s + v.y * c) * scale_over_m)};
+        for (int h = 0; h < 2; h++) {
+            if (!(fabs(r[h]) < 4611686018427387904.0)) {  // 2^62 (also catches NaN)
+                atomicOr(overflow, 1u);
+                out[k + h * M] = 0;
+            } else {
+                out[k + h * M] = (int64_t)r[h];
+            }
+        }
+    }
+}
+
 // Coefficient-form limbs -> twisted complex vector w_k = z_k zeta^k, z_k = (m_k + i m_(k+M)) / scale.
 __global__ void k_dec_compose(const uint64_t *coef, double2 *w, uint64_t q0, uint64_t q1, uint64_t q0inv_mod_q1,
                               ulonglong2 r1, uint32_t L, uint32_t N, double inv_scale) {
@@ -179,6 +200,33 @@ int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_value
         require(h_flag == 0, "encoded values are too large");
         NttLaunch fw{out, out, 0, 0, 1, (uint32_t)L};
         ntt_forward(c, fw, s);
+    });
+}
+
+int pfa_ckks_encode_coeffs(const pfa_context *ctx, const double *values, size_t n_values, double scale,
+                           int64_t *coeffs, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(coeffs && (values || n_values == 0), "null argument");
+        const uint32_t M = c.N / 2;
+        require(n_values >= 1, "Input vector is empty");
+        require(n_values <= M, "Input vector exceeds max slots");
+        require(scale > 0 && std::isfinite(scale), "scale out of bounds");
+        const hipStream_t s = as_stream(stream);
+        Scratch sc(c, s);
+        double2 *buf = sc.alloc<double2>(2 * (size_t)M);
+        uint32_t *flag = sc.alloc<uint32_t>(1);
+        hipLaunchKernelGGL(k_zero_flag, dim3(1), dim3(1), 0, s, flag);
+        hipLaunchKernelGGL(k_enc_scatter, ew_grid(M), dim3(kThreads), 0, s, (const double2 *)values,
+                           (uint32_t)n_values, buf, c.slot_perm, M);
+        double2 *w = fft(buf, buf + M, M, -1.0, s);
+        hipLaunchKernelGGL(k_enc_round_signed, ew_grid(M), dim3(kThreads), 0, s, w, coeffs, c.N, scale / (double)M,
+                           flag);
+        PFA_HIP(hipGetLastError());
+        uint32_t h_flag = 0;
+        PFA_HIP(hipMemcpyAsync(&h_flag, flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        PFA_HIP(hipStreamSynchronize(s));
+        require(h_flag == 0, "encoded values are too large");
     });
 }
 

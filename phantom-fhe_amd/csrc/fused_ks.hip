@@ -56,19 +56,6 @@ struct FGeo {
     static constexpr int LDS = ROWS * G::ROW_PITCH;
 };
 
-// Work item w of a grouped launch: G groups of J items that read the same input
-// tile.  A group's items all carry the same w mod 8, so in a grid whose size
-// is a multiple of 8 they run on workgroups of one XCD (workgroups are dealt to
-// the XCDs round-robin) and share its L2 copy of the input tile.
-__device__ __forceinline__ bool grouped_item(uint32_t w, uint32_t G, uint32_t J, uint32_t &g, uint32_t &j) {
-    const uint32_t x = w & 7u, k = w >> 3;
-    j = k % J;
-    g = (k / J) * 8u + x;
-    return g < G;
-}
-
-__host__ __device__ inline uint32_t grouped_total(uint32_t G, uint32_t J) { return ((G + 7u) / 8u) * 8u * J; }
-
 // ------------------------------------------------------------ base conversion
 // One columns-pass job: target limb (table row prow) of one output poly, with
 // inputs n_in limbs of `in` (limb stride N) over the table rows in_row0 + i.

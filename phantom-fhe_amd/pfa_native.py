@@ -54,6 +54,9 @@ SIGNATURES = {
     "pfa_poly_from_signed": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_ckks_encode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _sz, _vp]),
     "pfa_ckks_decode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
+    "pfa_ckks_encode_coeffs": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
+    "pfa_expand_signed": (_i32, [_vp, _vp, _sz, _vp, _sz, _sz, _vp]),
+    "pfa_bsgs_mac": (_i32, [_vp, _sz, C.POINTER(_vp), C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
 }
 
 
@@ -263,6 +266,37 @@ class NativeContext:
             raise ValueError("expected a contiguous complex128 device tensor")
         call("pfa_ckks_decode", self._h, ptr(plain), L, float(scale), out_c128.data_ptr(),
              stream or stream_of(plain))
+
+    def ckks_encode_coeffs(self, values_c128, scale, out_i64, stream=None):
+        """values_c128: complex128 device tensor [<= N/2]; out_i64: int64 [N] (signed coefficients)."""
+        import torch
+
+        if values_c128.dtype != torch.complex128 or values_c128.device.type != "cuda":
+            raise ValueError("expected a complex128 device tensor")
+        if out_i64.dtype != torch.int64 or not out_i64.is_contiguous():
+            raise ValueError("expected a contiguous int64 device tensor")
+        v = values_c128.contiguous()
+        call("pfa_ckks_encode_coeffs", self._h, v.data_ptr(), v.numel(), float(scale), out_i64.data_ptr(),
+             stream or stream_of(out_i64))
+
+    def expand_signed(self, coeffs_i64, n, out, L, start=0, stream=None):
+        """coeffs_i64: int64 [n][N]; out: uint64 [n][L][N] residues (coefficient form)."""
+        import torch
+
+        if coeffs_i64.dtype != torch.int64 or not coeffs_i64.is_contiguous():
+            raise ValueError("expected a contiguous int64 device tensor")
+        call("pfa_expand_signed", self._h, coeffs_i64.data_ptr(), n, ptr(out), L, start,
+             stream or stream_of(out))
+
+    def bsgs_mac(self, chain_index, pts, babies, outs, stream=None):
+        """outs[g] = sum_b pts[g * M + b] * babies[b] (M = len(babies), G = len(outs))."""
+        M, G = len(babies), len(outs)
+        if len(pts) != M * G:
+            raise ValueError("need len(babies) * len(outs) plaintexts")
+        pp = (C.c_void_p * (M * G))(*[ptr(t) for t in pts])
+        bp = (C.c_void_p * M)(*[ptr(t) for t in babies])
+        op = (C.c_void_p * G)(*[ptr(t) for t in outs])
+        call("pfa_bsgs_mac", self._h, chain_index, pp, bp, M, G, op, stream or stream_of(outs[0]))
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

@@ -660,3 +660,141 @@ def hoisting(ctx: context, ct: ciphertext, glk: galois_key, steps) -> ciphertext
     out = ctx._empty(2, L, ctx.N)
     ctx.native.hoisting(ct.chain_index(), ct.data, elts, keys, out)
     return ct._like(out)
+
+
+# ---------------------------------------------------------------- BSGS matvec
+# Encrypted matrix-vector product by baby-step giant-step diagonals
+# (include/bsgs.h, src/bsgs.cu).  y = W x for a plaintext matrix W and an
+# encrypted vector x in replicated-block layout (period d_pad).
+class bsgs_diagonals:
+    """BsgsDiagonals (include/bsgs.h:15-21): d_pad diagonals indexed
+    [g * baby_steps + b], each pre-rotated by g * baby_steps and stored as a
+    level-independent plaintext of signed coefficients (SingleChainPlaintext,
+    include/single_chain_plaintext.h:37-40).  Their NTT-form expansion at a
+    chain index is built on first use and kept on the device (d_pad x |Ql| limbs,
+    40 GiB at d_pad 4096, |Ql| 20, N 2^16), where the reference re-expands the
+    plaintexts of every giant on every product (src/bsgs.cu:245-271)."""
+
+    def __init__(self, coeffs, scale: float, d_pad: int, baby_steps: int):
+        self.coeffs = coeffs  # int64 device tensor [d_pad][N]
+        self.scale = float(scale)
+        self.d_pad = int(d_pad)
+        self.baby_steps = int(baby_steps)
+        self.giant_steps = self.d_pad // self.baby_steps
+        self._expanded = {}
+
+    def expanded(self, ctx: context, chain_index: int):
+        t = self._expanded.get(chain_index)
+        if t is None:
+            L = ctx.size_Ql(chain_index)
+            t = ctx._empty(self.d_pad, L, ctx.N)
+            step = 4096
+            for s0 in range(0, self.d_pad, step):
+                n = min(step, self.d_pad - s0)
+                ctx.native.expand_signed(self.coeffs[s0:s0 + n], n, t[s0:s0 + n], L)
+                ctx.native.ntt_forward(t[s0:s0 + n], n, L, 0)
+            self._expanded[chain_index] = t
+        return t
+
+    def release(self):
+        """Drop the cached expansions."""
+        self._expanded.clear()
+
+
+def _is_pow2(x: int) -> bool:
+    return x > 0 and (x & (x - 1)) == 0
+
+
+def pre_encode_bsgs_diagonals(context: context, encoder: ckks_encoder, matrix, num_rows: int, num_cols: int,
+                              d_pad: int, baby_steps: int, scale: float) -> bsgs_diagonals:
+    """pre_encode_bsgs_diagonals (src/bsgs.cu:99-178): diag[d][t] = W[t][(t + d) mod d_pad]
+    (zero outside num_rows x num_cols); diagonal g * M + b is rotated right by
+    g * M, tiled over the slots with period d_pad and encoded at `scale`."""
+    t = _torch()
+    if num_rows == 0 or num_cols == 0:
+        raise ValueError("pre_encode_bsgs_diagonals: dimensions must be non-zero")
+    W = np.asarray(matrix, dtype=np.float64).ravel()
+    if W.size != num_rows * num_cols:
+        raise ValueError("pre_encode_bsgs_diagonals: matrix size mismatch")
+    if not _is_pow2(d_pad):
+        raise ValueError("pre_encode_bsgs_diagonals: d_pad must be a power of 2")
+    if d_pad < num_rows or d_pad < num_cols:
+        raise ValueError("pre_encode_bsgs_diagonals: d_pad must be >= max(num_rows, num_cols)")
+    if baby_steps == 0 or d_pad % baby_steps:
+        raise ValueError("pre_encode_bsgs_diagonals: baby_steps must divide d_pad")
+    slots = encoder.slot_count()
+    if slots % d_pad:
+        raise ValueError("pre_encode_bsgs_diagonals: num_slots must be multiple of d_pad")
+    W = W.reshape(num_rows, num_cols)
+    rows = np.arange(num_rows)[:, None]
+    j = (rows + np.arange(d_pad)[None, :]) % d_pad  # [t][d]
+    vals = np.where(j < num_cols, W[rows, np.minimum(j, num_cols - 1)], 0.0)
+    diag = np.zeros((d_pad, d_pad))
+    diag[:, :num_rows] = vals.T  # diag[d][t]
+    G = d_pad // baby_steps
+    coeffs = t.empty((d_pad, context.N), dtype=t.int64, device=context.dev)
+    for g in range(G):
+        for b in range(baby_steps):
+            d = g * baby_steps + b
+            v = np.tile(np.roll(diag[d], g * baby_steps), slots // d_pad).astype(np.complex128)
+            context.native.ckks_encode_coeffs(t.from_numpy(v).to(context.dev), scale, coeffs[d])
+    return bsgs_diagonals(coeffs, scale, d_pad, baby_steps)
+
+
+def bsgs_required_steps(baby_steps: int) -> list:
+    """Rotation steps the product needs (src/bsgs.cu:180-193): powers of 2
+    below baby_steps (chained babies) and baby_steps (the giant stride)."""
+    if baby_steps <= 1:
+        return []
+    steps, s = [], 1
+    while s < baby_steps:
+        steps.append(s)
+        s <<= 1
+    return steps + [baby_steps]
+
+
+def compute_bsgs_babies(context: context, galois_key: galois_key, x: ciphertext, baby_steps: int) -> list:
+    """babies[0] = x, babies[b] = rotate(babies[b - msb(b)], msb(b)) (src/bsgs.cu:195-215)."""
+    if baby_steps == 0:
+        raise ValueError("compute_bsgs_babies: baby_steps must be > 0")
+    babies = [x]
+    for b in range(1, baby_steps):
+        bit = 1 << (b.bit_length() - 1)
+        babies.append(rotate(context, babies[b - bit], bit, galois_key))
+    return babies
+
+
+def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babies, diags: bsgs_diagonals):
+    """bsgs_apply_giants_with_babies (src/bsgs.cu:217-333): partial_g =
+    sum_b pt[g M + b] * babies[b] for every giant (one launch), then Horner
+    acc = rotate(acc, M) + partial_g from g = G - 1 down to 0, one rescale, and
+    the babies' scale restored."""
+    M, G, d_pad = diags.baby_steps, diags.giant_steps, diags.d_pad
+    if M == 0 or G == 0 or M * G != d_pad:
+        raise ValueError("bsgs_apply_giants_with_babies: M*G must equal d_pad")
+    if len(babies) != M:
+        raise ValueError("bsgs_apply_giants_with_babies: babies size != baby_steps")
+    x = babies[0]
+    chain = x.chain_index()
+    for c in babies:
+        if c.chain_index() != chain or c.size() != 2:
+            raise ValueError("babies must be size-2 ciphertexts at one chain index")
+    L = context.size_Ql(chain)
+    P = diags.expanded(context, chain)
+    partials = context._empty(G, 2, L, context.N)
+    context.native.bsgs_mac(chain, [P[i] for i in range(d_pad)], [c.data for c in babies],
+                            [partials[g] for g in range(G)])
+    scale = x.scale() * diags.scale
+    acc = x._like(partials[G - 1], scale=scale)
+    for g in range(G - 2, -1, -1):
+        acc = rotate(context, acc, M, galois_key)
+        acc = add(context, acc, x._like(partials[g], scale=scale))
+    acc = rescale_to_next(context, acc)
+    acc.set_scale(x.scale())
+    return acc
+
+
+def bsgs_matmul_preencoded(context: context, galois_key: galois_key, x: ciphertext, diags: bsgs_diagonals):
+    """bsgs_matmul_preencoded (src/bsgs.cu:335-342)."""
+    return bsgs_apply_giants_with_babies(context, galois_key,
+                                         compute_bsgs_babies(context, galois_key, x, diags.baby_steps), diags)
