@@ -19,61 +19,113 @@ namespace {
 
 constexpr int kThreads = 256;
 
-struct MacArgs {
-    const uint64_t *const *pt;    // [G M] plaintexts, [Ql][N] each (NTT form)
-    const uint64_t *const *baby;  // [M] ciphertexts, [2][Ql][N] each (NTT form)
-    uint64_t *const *out;         // [G] ciphertexts, [2][Ql][N] each
-    uint32_t M, G, Ql, N;
+// Pointer list of the accumulation: a device table, or (no table) an
+// arithmetic progression base + i * stride, which is how contiguous batches of
+// plaintexts and outputs arrive; neither needs a host-to-device copy.
+template <class P>
+struct PtrList {
+    P *const *table;
+    P *base;
+    uint64_t stride;  // elements
+    __device__ __forceinline__ P *operator[](size_t i) const { return table ? table[i] : base + i * stride; }
 };
 
+constexpr uint32_t kInlineBabies = 64;
+
+struct MacArgs {
+    PtrList<const uint64_t> pt;  // [G M] plaintexts, [Ql][N] each (NTT form)
+    PtrList<uint64_t> out;       // [G] ciphertexts, [2][Ql][N] each
+    const uint64_t *const *baby_table;          // [M] ciphertexts [2][Ql][N], when M > kInlineBabies
+    const uint64_t *baby_inline[kInlineBabies];  // the same, by value, when M <= kInlineBabies
+    uint32_t M, G, Ql, N;
+    __device__ __forceinline__ const uint64_t *baby(uint32_t b) const {
+        return baby_table ? baby_table[b] : baby_inline[b];
+    }
+};
+
+// A work item covers kSpan consecutive residues of one limb (kSpan / 256 per
+// thread, 256 apart), so every plaintext is read in 8 KiB runs.
 // FP64 policy: each product is within 0.875 q (|x y / q| < q < 2^50), so four
 // of them on top of a reduced sum stay below 4 q < 2^53; integer policy: 128-bit
 // sums of at most eight products below q^2 < 2^122, then one Barrett reduction.
+constexpr uint32_t kSpan = 1024;
+constexpr int kPer = kSpan / kThreads;
+
 __global__ void __launch_bounds__(kThreads)
 k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
-    const uint32_t T = a.N / kThreads;  // tiles per limb
+    const uint32_t T = a.N / kSpan;  // items per limb and giant
     const uint32_t groups = a.Ql * T;
     const uint32_t total = grouped_total(groups, a.G);
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
         uint32_t grp, g;
         if (!grouped_item(w, groups, a.G, grp, g)) continue;
         const uint32_t j = grp / T, tile = grp % T;
-        const size_t off0 = (size_t)j * a.N + tile * kThreads + threadIdx.x;
+        const size_t off0 = (size_t)j * a.N + tile * kSpan + threadIdx.x;
         const size_t off1 = off0 + (size_t)a.Ql * a.N;
         const uint64_t q = mod[j];
-        const uint64_t *const *pt = a.pt + (size_t)g * a.M;
+        const size_t pt0 = (size_t)g * a.M;
         uint64_t *o = a.out[g];
         if (q < kF64PrimeBound) {
             const ArithF64 ar(q);
-            double acc0 = 0.0, acc1 = 0.0;
+            double acc0[kPer], acc1[kPer];
+#pragma unroll
+            for (int e = 0; e < kPer; e++) acc0[e] = acc1[e] = 0.0;
             for (uint32_t b = 0; b < a.M; b++) {
-                const double x = ar.load(ld_stream(pt[b] + off0));
-                const double xq = x * ar.qinv;
-                const uint64_t *c = a.baby[b];
-                acc0 += ar.mulw(ar.load(c[off0]), x, xq);
-                acc1 += ar.mulw(ar.load(c[off1]), x, xq);
+                const uint64_t *p = a.pt[pt0 + b] + off0;
+                const uint64_t *c = a.baby(b);
+                double x[kPer], y0[kPer], y1[kPer];
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    x[e] = ar.load(ld_stream(p + e * kThreads));
+                    y0[e] = ar.load(c[off0 + e * kThreads]);
+                    y1[e] = ar.load(c[off1 + e * kThreads]);
+                }
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    const double xq = x[e] * ar.qinv;
+                    acc0[e] += ar.mulw(y0[e], x[e], xq);
+                    acc1[e] += ar.mulw(y1[e], x[e], xq);
+                }
                 if ((b & 3u) == 3u) {
-                    ar.reduce(acc0);
-                    ar.reduce(acc1);
+#pragma unroll
+                    for (int e = 0; e < kPer; e++) {
+                        ar.reduce(acc0[e]);
+                        ar.reduce(acc1[e]);
+                    }
                 }
             }
-            st_stream(o + off0, ar.store(acc0));
-            st_stream(o + off1, ar.store(acc1));
+#pragma unroll
+            for (int e = 0; e < kPer; e++) {
+                st_stream(o + off0 + e * kThreads, ar.store(acc0[e]));
+                st_stream(o + off1 + e * kThreads, ar.store(acc1[e]));
+            }
         } else {
             const ulonglong2 r = ratio[j];
-            U128 s0{0, 0}, s1{0, 0};
+            U128 s0[kPer], s1[kPer];
+#pragma unroll
+            for (int e = 0; e < kPer; e++) s0[e] = s1[e] = U128{0, 0};
             for (uint32_t b = 0; b < a.M; b++) {
-                const uint64_t x = ld_stream(pt[b] + off0);
-                const uint64_t *c = a.baby[b];
-                mac(s0, x, c[off0]);
-                mac(s1, x, c[off1]);
+                const uint64_t *p = a.pt[pt0 + b] + off0;
+                const uint64_t *c = a.baby(b);
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    const uint64_t x = ld_stream(p + e * kThreads);
+                    mac(s0[e], x, c[off0 + e * kThreads]);
+                    mac(s1[e], x, c[off1 + e * kThreads]);
+                }
                 if ((b & 7u) == 7u) {
-                    s0 = U128{barrett128(s0, q, r.x, r.y), 0};
-                    s1 = U128{barrett128(s1, q, r.x, r.y), 0};
+#pragma unroll
+                    for (int e = 0; e < kPer; e++) {
+                        s0[e] = U128{barrett128(s0[e], q, r.x, r.y), 0};
+                        s1[e] = U128{barrett128(s1[e], q, r.x, r.y), 0};
+                    }
                 }
             }
-            st_stream(o + off0, barrett128(s0, q, r.x, r.y));
-            st_stream(o + off1, barrett128(s1, q, r.x, r.y));
+#pragma unroll
+            for (int e = 0; e < kPer; e++) {
+                st_stream(o + off0 + e * kThreads, barrett128(s0[e], q, r.x, r.y));
+                st_stream(o + off1 + e * kThreads, barrett128(s1[e], q, r.x, r.y));
+            }
         }
     }
 }
@@ -116,14 +168,44 @@ int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *con
         const hipStream_t s = as_stream(stream);
         const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
         Scratch sc(c, s);
-        const uint64_t **dpt = sc.alloc<const uint64_t *>(M * G);
-        const uint64_t **dbaby = sc.alloc<const uint64_t *>(M);
-        uint64_t **dout = sc.alloc<uint64_t *>(G);
-        PFA_HIP(hipMemcpyAsync(dpt, pts, M * G * sizeof(void *), hipMemcpyHostToDevice, s));
-        PFA_HIP(hipMemcpyAsync(dbaby, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
-        PFA_HIP(hipMemcpyAsync(dout, out, G * sizeof(void *), hipMemcpyHostToDevice, s));
-        const MacArgs a{dpt, dbaby, dout, (uint32_t)M, (uint32_t)G, Ql, c.N};
-        const uint32_t total = grouped_total(Ql * (c.N / kThreads), (uint32_t)G);
+        MacArgs a{};
+        a.M = (uint32_t)M;
+        a.G = (uint32_t)G;
+        a.Ql = Ql;
+        a.N = c.N;
+        // a list whose addresses step by a constant multiple of 8 bytes goes as base + stride
+        auto progression = [](const void *const *v, size_t n, uint64_t &stride) {
+            const uintptr_t b0 = (uintptr_t)v[0];
+            const intptr_t d = n > 1 ? (intptr_t)((uintptr_t)v[1] - b0) : 0;
+            if (d < 0 || d % 8) return false;
+            for (size_t i = 1; i < n; i++)
+                if ((uintptr_t)v[i] != b0 + (uintptr_t)d * i) return false;
+            stride = (uint64_t)d / 8;
+            return true;
+        };
+        uint64_t st = 0;
+        if (progression((const void *const *)pts, M * G, st)) {
+            a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
+        } else {
+            const uint64_t **t = sc.alloc<const uint64_t *>(M * G);
+            PFA_HIP(hipMemcpyAsync(t, pts, M * G * sizeof(void *), hipMemcpyHostToDevice, s));
+            a.pt = PtrList<const uint64_t>{t, nullptr, 0};
+        }
+        if (progression((const void *const *)out, G, st)) {
+            a.out = PtrList<uint64_t>{nullptr, out[0], st};
+        } else {
+            uint64_t **t = sc.alloc<uint64_t *>(G);
+            PFA_HIP(hipMemcpyAsync(t, out, G * sizeof(void *), hipMemcpyHostToDevice, s));
+            a.out = PtrList<uint64_t>{t, nullptr, 0};
+        }
+        if (M <= kInlineBabies) {
+            for (size_t i = 0; i < M; i++) a.baby_inline[i] = babies[i];
+        } else {
+            const uint64_t **t = sc.alloc<const uint64_t *>(M);
+            PFA_HIP(hipMemcpyAsync(t, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
+            a.baby_table = t;
+        }
+        const uint32_t total = grouped_total(Ql * (c.N / kSpan), (uint32_t)G);
         const uint32_t cap = (uint32_t)c.n_cu * 8u;
         hipLaunchKernelGGL(k_bsgs_mac, dim3(total < cap ? total : cap), dim3(kThreads), 0, s, a, c.mod, c.ratio);
         PFA_HIP(hipGetLastError());

@@ -289,14 +289,20 @@ class NativeContext:
              stream or stream_of(out))
 
     def bsgs_mac(self, chain_index, pts, babies, outs, stream=None):
-        """outs[g] = sum_b pts[g * M + b] * babies[b] (M = len(babies), G = len(outs))."""
+        """outs[g] = sum_b pts[g * M + b] * babies[b] (M = len(babies), G = len(outs)).
+        Entries are device tensors or raw device addresses (ints); with addresses
+        only, pass `stream`."""
         M, G = len(babies), len(outs)
         if len(pts) != M * G:
             raise ValueError("need len(babies) * len(outs) plaintexts")
-        pp = (C.c_void_p * (M * G))(*[ptr(t) for t in pts])
-        bp = (C.c_void_p * M)(*[ptr(t) for t in babies])
-        op = (C.c_void_p * G)(*[ptr(t) for t in outs])
-        call("pfa_bsgs_mac", self._h, chain_index, pp, bp, M, G, op, stream or stream_of(outs[0]))
+        addr = lambda t: t if isinstance(t, int) else ptr(t)
+        pp = (C.c_void_p * (M * G))(*[addr(t) for t in pts])
+        bp = (C.c_void_p * M)(*[addr(t) for t in babies])
+        op = (C.c_void_p * G)(*[addr(t) for t in outs])
+        if stream is None:
+            first = next((t for t in list(outs) + list(babies) if not isinstance(t, int)), None)
+            stream = stream_of(first) if first is not None else None
+        call("pfa_bsgs_mac", self._h, chain_index, pp, bp, M, G, op, stream)
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

@@ -782,8 +782,10 @@ def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babi
     L = context.size_Ql(chain)
     P = diags.expanded(context, chain)
     partials = context._empty(G, 2, L, context.N)
-    context.native.bsgs_mac(chain, [P[i] for i in range(d_pad)], [c.data for c in babies],
-                            [partials[g] for g in range(G)])
+    step = L * context.N * 8  # bytes per plaintext; per partial ciphertext: 2 * step
+    base_p, base_o = P.data_ptr(), partials.data_ptr()
+    context.native.bsgs_mac(chain, [base_p + i * step for i in range(d_pad)], [c.data for c in babies],
+                            [base_o + g * 2 * step for g in range(G)])
     scale = x.scale() * diags.scale
     acc = x._like(partials[G - 1], scale=scale)
     for g in range(G - 2, -1, -1):
