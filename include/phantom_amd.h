@@ -206,13 +206,31 @@ int pfa_expand_signed(const pfa_context *ctx, const int64_t *in, size_t n, uint6
                       void *stream);
 
 /* mac_accumulate_kernel (src/bsgs.cu:51-96) for every giant at once, the
- * accumulation of bsgs_apply_giants_with_babies (src/bsgs.cu:272-296):
+ * accumulation of bsgs_apply_giants_with_babies (build_partial,
+ * src/bsgs.cu:276-342):
  *   out[g][k] = sum_{b < M} pts[g*M + b] * babies[b][k]   (k = 0, 1; mod q_j)
  * pts: G*M plaintexts [Ql][N]; babies: M ciphertexts [2][Ql][N]; out: G
  * ciphertexts [2][Ql][N]; all NTT form at chain_index.  The pointer tables are
  * host arrays of device pointers. */
 int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *const *pts,
                  const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
+
+/* compute_bsgs_babies (src/bsgs.cu:194-214): babies[0] = ct and
+ * babies[b] = rotate(babies[b - msb(b)], msb(b)) for 1 <= b < M, each rotation
+ * apply_galois_with_ksk (src/evaluate.cu:1607-1656) with the direct key.
+ * ct [2][Ql][N] at chain_index; keys[k] is the Galois key of rotation step 2^k
+ * ([key_dnum][2][QP][N]) for every 2^k < M; out receives babies 1 .. M-1 as
+ * [M-1][2][Ql][N]. */
+int pfa_bsgs_babies(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, size_t M,
+                    const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream);
+
+/* The giant-step stage of bsgs_apply_giants_with_babies (src/bsgs.cu:344-356):
+ * acc = partial[G-1]; acc = rotate(acc, step) + partial[g] for g = G-2 .. 0;
+ * out = rescale_to_next(acc).  partials [G][2][Ql][N] (NTT form, chain_index)
+ * are overwritten: partial[g] ends holding the accumulator at g.  key is the
+ * Galois key of `step` (unused when G = 1); out is [2][Ql-1][N]. */
+int pfa_bsgs_giants(const pfa_context *ctx, size_t chain_index, uint64_t *partials, size_t G, int step,
+                    const uint64_t *key, size_t key_dnum, uint64_t *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -146,6 +146,49 @@ k_expand_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t 
     st_stream(out + ((size_t)p * L + l) * N + n, r);
 }
 
+// Both polys of a ciphertext through the Galois permutation of NTT slots
+// (apply_galois_ntt_permutation, src/galois.cu:11-18):
+//   dst[k][l][i] = src[k][l][pi(i)]  (+ add0[l][i] for k = 0 when add0 is given).
+__global__ void __launch_bounds__(kThreads)
+k_galois_ct(const uint64_t *src, uint64_t *dst, const uint64_t *add0, const uint64_t *mod, uint32_t elt, uint32_t L,
+            uint32_t N, uint32_t logN) {
+    const uint32_t l = blockIdx.y, k = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    const size_t row = ((size_t)k * L + l) * N;
+    uint64_t v = src[row + galois_perm(elt, n, logN)];
+    if (k == 0 && add0) v = add_mod(v, add0[(size_t)l * N + n], mod[l]);
+    st_stream(dst + row + n, v);
+}
+
+// out = rotate(src) (+ add): the Galois permutation of both polys, then the
+// key switch of the permuted c1 whose ModDown epilogue adds the permuted c0
+// (and add[0]) to poly 0 and add[1] to poly 1 -- apply_galois_with_ksk
+// (src/evaluate.cu:1607-1656) followed by add_inplace, with the same residues.
+// out must not alias src; add[1] may alias out's poly 1.
+void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint32_t elt, const uint64_t *key,
+                 const uint64_t *add, uint64_t *out, hipStream_t s) {
+    const uint32_t Ql = c.size_Ql(chain), QlP = Ql + c.P;
+    const size_t LN = (size_t)Ql * c.N;
+    Scratch sc(c, s);
+    uint64_t *t = sc.alloc(2 * LN);
+    hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2), dim3(kThreads), 0, s, src, t, add, c.mod, elt, Ql,
+                       c.N, c.logN);
+    PFA_HIP(hipGetLastError());
+    uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
+    fused_modup_inner(c, chain, t + LN, key, cx, s);
+    fused_moddown(c, chain, cx, 2, out, t, add ? add + LN : nullptr, s);
+}
+
+uint32_t rotation_elt(const Ctx &c, int step) {
+    uint32_t e = 0;
+    if (pfa_galois_elt_from_step(step, c.N, &e) != PFA_OK) fail(PFA_ERR_INVALID_ARGUMENT, "bad rotation step");
+    return e;
+}
+
+void check_key(const Ctx &c, uint32_t chain, const uint64_t *key, size_t dnum) {
+    require(key != nullptr, "null Galois key");
+    require(c.level(chain).beta <= dnum, "key has fewer digits than the ciphertext level needs");
+}
+
 }  // namespace
 
 }  // namespace pfa
@@ -209,6 +252,54 @@ int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *con
         const uint32_t cap = (uint32_t)c.n_cu * 8u;
         hipLaunchKernelGGL(k_bsgs_mac, dim3(total < cap ? total : cap), dim3(kThreads), 0, s, a, c.mod, c.ratio);
         PFA_HIP(hipGetLastError());
+    });
+}
+
+int pfa_bsgs_babies(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, size_t M,
+                    const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && out && (M <= 1 || keys), "null argument");
+        require(M >= 1 && M <= (size_t)c.N / 2, "baby step count out of range");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        const uint32_t chain = (uint32_t)chain_index;
+        std::vector<uint32_t> elts;
+        for (size_t bit = 1, k = 0; bit < M; bit <<= 1, k++) {
+            check_key(c, chain, keys[k], key_dnum);
+            elts.push_back(rotation_elt(c, (int)bit));
+        }
+        const hipStream_t s = as_stream(stream);
+        const size_t ct_elems = (size_t)2 * c.size_Ql(chain) * c.N;
+        // babies[b] = rotate(babies[b - msb(b)], msb(b)); babies[0] = ct, babies[b] = out[b - 1]
+        for (size_t b = 1; b < M; b++) {
+            uint32_t k = 0;
+            while ((size_t)2 << k <= b) k++;
+            const size_t rem = b - ((size_t)1 << k);
+            const uint64_t *src = rem ? out + (rem - 1) * ct_elems : ct;
+            rotate_into(c, chain, src, elts[k], keys[k], nullptr, out + (b - 1) * ct_elems, s);
+        }
+    });
+}
+
+int pfa_bsgs_giants(const pfa_context *ctx, size_t chain_index, uint64_t *partials, size_t G, int step,
+                    const uint64_t *key, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(partials && out, "null argument");
+        require(G >= 1, "need at least one giant step");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        const uint32_t chain = (uint32_t)chain_index;
+        require(c.size_Ql(chain) >= 2, "cannot rescale at the last level");
+        const uint32_t elt = G > 1 ? rotation_elt(c, step) : 0;
+        if (G > 1) check_key(c, chain, key, key_dnum);
+        const hipStream_t s = as_stream(stream);
+        const size_t ct_elems = (size_t)2 * c.size_Ql(chain) * c.N;
+        // Horner from the last giant: partial[g] <- rotate(partial[g + 1], step) + partial[g]
+        for (size_t g = G - 1; g-- > 0;) {
+            uint64_t *pg = partials + g * ct_elems;
+            rotate_into(c, chain, pg + ct_elems, elt, key, pg, pg, s);
+        }
+        fused_rescale(c, chain, partials, 2, out, s);
     });
 }
 

@@ -202,14 +202,22 @@ __device__ __forceinline__ const uint64_t *inner_src(const InnerRows &a, uint32_
 // transformed tile, read from the other buffer, by its key limbs.  The roles
 // keep disjoint register state (transform: the tile and the next digit's
 // prefetched tile; accumulate: the two accumulators and the key limbs), so the
-// key traffic overlaps the transforms of the other waves.  Each role's loop
-// runs beta + 1 steps with three workgroup barriers per step, in the same order
-// in both roles:
+// key traffic overlaps the transforms of the other waves.  Both roles run
+// beta + 1 steps of three workgroup barriers each, in the same order:
 //   A  transform: round a of digit b (or its own limb of c2) -> buffer b%2
 //   B  transform: round b;   accumulate: output 0 of digit b-1 from buffer (b-1)%2
 //   C  transform: final layout -> buffer b%2;   accumulate: output 1 of digit b-1
-// Measured against one role doing both (206 VGPRs, 2 waves per SIMD): equal at
-// config 3 (6 digits), 7-10% faster with 35 digits.
+//
+// Two properties keep the prefetches a full step ahead:
+// * Global loads complete in issue order (one vmcnt counter), so a load issued
+//   after a prefetch cannot be waited for without waiting for the prefetch.
+//   The FP64 rows-pass twiddle factors therefore come from LDS: the item's
+//   rows' base factors and the small table are staged there once per item.
+//   The Barrett ratio is loaded before the first key limbs.
+// * Every prefetch is unconditional (the step after the last one reloads the
+//   rows it has just consumed, which are still in L2), so the prefetched
+//   registers are never merged with their previous values at the loop head,
+//   which would cost a copy of each and ~60 registers.
 template <int S1, int S2>
 struct WsGeo {
     using G = Geo<S1, S2>;
@@ -217,17 +225,22 @@ struct WsGeo {
     static constexpr int HALF = ROWS * Sub<S2>::T;  // threads per role
     static constexpr int THREADS = 2 * HALF;
     static constexpr int TILES = G::N1 / ROWS;
-    static constexpr int LDS = 2 * ROWS * G::ROW_PITCH;
+    static constexpr int LDS = 2 * ROWS * G::ROW_PITCH;      // doubles: the two tile buffers
+    static constexpr int TW_RB = S2 * ROWS;                   // staged base factors [S2][ROWS]
+    static constexpr int TW_SMALL = 1 << (S2 - 1);            // staged small table entries
+    static constexpr int TW = TW_RB + TW_SMALL;               // ulonglong2 entries after the buffers
     static_assert(HALF % 64 == 0, "each role must be whole wavefronts");
 };
 
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
-                                             uint32_t prow, uint32_t k1, typename A::T *b0, typename A::T *b1) {
+                                             uint32_t prow, uint32_t k1, uint32_t rr, const ulonglong2 *tws,
+                                             typename A::T *b0, typename A::T *b1) {
     using G = Geo<S1, S2>;
+    using W = WsGeo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
-    const uint32_t F = (threadIdx.x % WsGeo<S1, S2>::HALF) % SB::T;
+    const uint32_t F = (threadIdx.x % W::HALF) % SB::T;
     const size_t rowoff = (size_t)k1 * G::N2 + F;
     uint64_t nraw[SB::E];
     bool nown;
@@ -236,57 +249,62 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
 #pragma unroll
         for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
     }
-    for (uint32_t b = 0; b <= a.beta; b++) {
+    for (uint32_t b = 0; b < a.beta; b++) {
         T *buf = (b & 1u) ? b1 : b0;
-        const bool live = b < a.beta, own = nown;
-        // The twiddles depend on the row and the prime only; left loop-invariant,
-        // the compiler keeps every one of them live across the digit loop
-        // (~120 VGPRs) and the kernel loses a wave per SIMD.  Recomputing them
-        // per digit is cheaper.
-        uint32_t kr = k1, pr = prow;
-        asm volatile("" : "+v"(kr), "+s"(pr));
-        const ulonglong2 *tw = t.tw + (size_t)pr * G::N;
-        const ulonglong2 *rb = t.rb_fw + (size_t)pr * S2 * G::N1;
-        const ulonglong2 *small = t.small_fw + (size_t)pr * kSmall;
+        const bool own = nown;
         T x[SB::E];
         // A
-        if (live) {
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) x[e] = own ? ar.load(nraw[e]) : ar.load_mid(nraw[e]);
-            if (b + 1 < a.beta) {
-                const uint64_t *s = inner_src(a, b + 1, r, rowoff, G::N, nown);
+        for (int e = 0; e < SB::E; e++) x[e] = own ? ar.load(nraw[e]) : ar.load_mid(nraw[e]);
+        {
+            const uint64_t *s = inner_src(a, b + 1 < a.beta ? b + 1 : b, r, rowoff, G::N, nown);
 #pragma unroll
-                for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
-            }
-            if (!own) {
-                if constexpr (A::kF64)
-                    fwd_round_a_derived<S2, G::N1>(x, ar, rb, small, kr);
-                else
-                    fwd_round_a<A, S2>(x, ar, tw, G::N1 + kr);
-#pragma unroll
-                for (int e = 0; e < SB::E; e++) ar.reduce(x[e]);
-            }
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
+            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
         }
+        if (!own) {
+            // the twiddle addresses are made opaque per digit: left loop-invariant,
+            // the compiler would hold every twiddle live across the digit loop
+            if constexpr (A::kF64) {
+                uint32_t kr = rr;
+                asm volatile("" : "+v"(kr));
+                fwd_round_a_derived<S2, W::ROWS>(x, ar, tws, tws + W::TW_RB, kr);
+            } else {
+                uint32_t kr = k1, pr = prow;
+                asm volatile("" : "+v"(kr), "+s"(pr));
+                fwd_round_a<A, S2>(x, ar, t.tw + (size_t)pr * G::N, G::N1 + kr);
+            }
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) ar.reduce(x[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
         __syncthreads();
         // B
-        if (live && !own) {
+        if (!own) {
 #pragma unroll
             for (int e = 0; e < SB::E; e++) x[e] = buf[rpad(F * SB::E + e)];
-            if constexpr (A::kF64)
-                fwd_round_b_derived<S2, G::N1>(x, ar, rb, small, kr, F);
-            else
-                fwd_round_b<A, S2>(x, ar, tw, G::N1 + kr, F);
+            if constexpr (A::kF64) {
+                uint32_t kr = rr;
+                asm volatile("" : "+v"(kr));
+                fwd_round_b_derived<S2, W::ROWS>(x, ar, tws, tws + W::TW_RB, kr, F);
+            } else {
+                uint32_t kr = k1, pr = prow;
+                asm volatile("" : "+v"(kr), "+s"(pr));
+                fwd_round_b<A, S2>(x, ar, t.tw + (size_t)pr * G::N, G::N1 + kr, F);
+            }
         }
         __syncthreads();
         // C
-        if (live && !own) {
+        if (!own) {
 #pragma unroll
             for (int e = 0; e < SB::E; e++) buf[rpad(F * SB::E + e)] = x[e];
         }
         __syncthreads();
     }
+    // step beta: the accumulate waves consume the last digit
+    __syncthreads();
+    __syncthreads();
+    __syncthreads();
 }
 
 // Product of digit d's transformed element x (lazy) with key limb value w,
@@ -315,57 +333,66 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
     const size_t keyrow = (size_t)prow * G::N + rowoff;
     const uint64_t QPN = (uint64_t)a.QP * G::N;
     // key limb k of digit d at this thread's positions
-    auto key_of = [&](uint32_t d, uint32_t k) { return a.key + ((size_t)d * 2 + k) * QPN + keyrow; };
+    // limb i = 2 d + k of the key (digit d, output k) at this thread's positions
+    auto key_at = [&](uint32_t i) { return a.key + (size_t)i * QPN + keyrow; };
+    ulonglong2 rt = a.ratio[prow];
+    rt.x = wave_uniform(rt.x);
+    rt.y = wave_uniform(rt.y);
+    __builtin_amdgcn_sched_barrier(0);
     T acc0[SB::E], acc1[SB::E];
-    uint64_t kw0[SB::E], kw1[SB::E];
+    uint64_t kw[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) acc0[e] = acc1[e] = 0;
     {
-        const uint64_t *k0 = key_of(0, 0), *kk1 = key_of(0, 1);
+        const uint64_t *k = key_at(0);
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) {
-            kw0[e] = ld_stream(&k0[SB::T * e]);
-            kw1[e] = ld_stream(&kk1[SB::T * e]);
-        }
+        for (int e = 0; e < SB::E; e++) kw[e] = ld_stream(&k[SB::T * e]);
     }
-    const ulonglong2 rt = a.ratio[prow];
+    // step 0: the transform waves fill buffer 0
+    __syncthreads();
+    __syncthreads();
+    __syncthreads();
     // Output k of digit b - 1 is accumulated in phase B (k = 0) or C (k = 1) of
-    // step b; each key register set is refilled with digit b's limb right after
-    // it is consumed, a full step before it is needed.
-    for (uint32_t b = 0; b <= a.beta; b++) {
+    // step b.  One set of key registers: right after a limb is consumed, the
+    // next one (output 1 of the same digit, or output 0 of the next digit) is
+    // loaded, a phase ahead of its use.
+    for (uint32_t b = 1; b <= a.beta; b++) {
         const T *buf = ((b - 1) & 1u) ? b1 : b0;
         // A
         __syncthreads();
         // B
-        if (b >= 1) {
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) ws_mac(ar, acc0[e], buf[rpad(F + SB::T * e)], kw0[e], rt);
-            // keep the refill after the products so it can reuse their key registers
-            __builtin_amdgcn_sched_barrier(0);
-            if (b < a.beta) {
-                const uint64_t *k0 = key_of(b, 0);
+        for (int e = 0; e < SB::E; e++) {
+            ws_mac(ar, acc0[e], buf[rpad(F + SB::T * e)], kw[e], rt);
+            if constexpr (!A::kF64) __builtin_amdgcn_sched_barrier(0);  // one Barrett product at a time
+        }
+        // keep the refill after the products so it can reuse their key registers
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const uint64_t *k = key_at(2 * b - 1);
 #pragma unroll
-                for (int e = 0; e < SB::E; e++) kw0[e] = ld_stream(&k0[SB::T * e]);
-            }
+            for (int e = 0; e < SB::E; e++) kw[e] = ld_stream(&k[SB::T * e]);
         }
         __syncthreads();
         // C
-        if (b >= 1) {
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) ws_mac(ar, acc1[e], buf[rpad(F + SB::T * e)], kw1[e], rt);
-            __builtin_amdgcn_sched_barrier(0);
-            if (b < a.beta) {
-                const uint64_t *kk1 = key_of(b, 1);
+        for (int e = 0; e < SB::E; e++) {
+            ws_mac(ar, acc1[e], buf[rpad(F + SB::T * e)], kw[e], rt);
+            if constexpr (!A::kF64) __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            // after the last digit: reload the limb just consumed (still in L2)
+            const uint64_t *k = key_at(b < a.beta ? 2 * b : 2 * b - 1);
 #pragma unroll
-                for (int e = 0; e < SB::E; e++) kw1[e] = ld_stream(&kk1[SB::T * e]);
-            }
-            if constexpr (A::kF64) {
-                if (!(b & 1u)) {
+            for (int e = 0; e < SB::E; e++) kw[e] = ld_stream(&k[SB::T * e]);
+        }
+        if constexpr (A::kF64) {
+            if (!(b & 1u)) {
 #pragma unroll
-                    for (int e = 0; e < SB::E; e++) {
-                        ar.reduce(acc0[e]);
-                        ar.reduce(acc1[e]);
-                    }
+                for (int e = 0; e < SB::E; e++) {
+                    ar.reduce(acc0[e]);
+                    ar.reduce(acc1[e]);
                 }
             }
         }
@@ -384,25 +411,34 @@ template <int S1, int S2>
 __global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a, NttTables t) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
-    __shared__ double lds[W::LDS];
+    __shared__ double lds[W::LDS + 2 * W::TW];
+    ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + W::LDS);
     const bool transform = threadIdx.x < W::HALF;
     const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
     const uint32_t total = a.QlP * W::TILES;
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
         const uint32_t r = w / W::TILES, tile = w % W::TILES;
         const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
-        const uint64_t q = t.mod[prow];
+        const uint64_t q = wave_uniform(t.mod[prow]);
         const uint32_t k1 = tile * W::ROWS + rr;
         if (q < kF64PrimeBound) {
             double *b0 = lds + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
+            if (transform) {
+                // this item's rows' base factors rb[g][tile ROWS + i] and the small table
+                const ulonglong2 *rb = t.rb_fw + (size_t)prow * S2 * G::N1 + tile * W::ROWS;
+                const ulonglong2 *small = t.small_fw + (size_t)prow * kSmall;
+                for (uint32_t i = threadIdx.x; i < (uint32_t)W::TW; i += W::HALF)
+                    tws[i] = i < (uint32_t)W::TW_RB ? rb[(i / W::ROWS) * G::N1 + i % W::ROWS] : small[i - W::TW_RB];
+            }
+            __syncthreads();
             if (transform)
-                ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, b0, b1);
+                ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, b0, b1);
             else
                 ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, k1, b0, b1);
         } else {
             uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
             if (transform)
-                ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, b0, b1);
+                ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, b0, b1);
             else
                 ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, k1, b0, b1);
         }

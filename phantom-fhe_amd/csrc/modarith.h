@@ -208,4 +208,24 @@ struct ArithF64 {
     }
 };
 
+// A value the caller knows to be the same in every lane, moved to scalar
+// registers (a load through a pointer the compiler cannot prove read-only
+// leaves it in vector registers).
+__device__ __forceinline__ uint64_t wave_uniform(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t brv(uint32_t x, uint32_t bits) { return __builtin_bitreverse32(x) >> (32 - bits); }
+
+// Galois permutation of NTT slots (include/galois.cuh:98-113):
+//   pi(i) = brv(((elt * brv(N + i, logN + 1)) >> 1) mod N, logN),
+// with brv(N + i, logN + 1) = 2 brv(i, logN) + 1.
+__device__ __forceinline__ uint32_t galois_perm(uint32_t elt, uint32_t i, uint32_t logN) {
+    const uint64_t rev = 2ull * brv(i, logN) + 1;
+    const uint32_t raw = (uint32_t)((elt * rev) >> 1) & ((1u << logN) - 1);
+    return brv(raw, logN);
+}
+
 }  // namespace pfa

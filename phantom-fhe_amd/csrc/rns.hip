@@ -22,17 +22,6 @@ __device__ __forceinline__ uint64_t mulmod_b(uint64_t a, uint64_t b, uint64_t q,
     return barrett128(p, q, r.x, r.y);
 }
 
-__device__ __forceinline__ uint32_t brv(uint32_t x, uint32_t bits) { return __builtin_bitreverse32(x) >> (32 - bits); }
-
-// Galois permutation of NTT slots (include/galois.cuh:98-113):
-//   pi(i) = brv(((elt * brv(N + i, logN + 1)) >> 1) mod N, logN),
-// with brv(N + i, logN + 1) = 2 brv(i, logN) + 1.
-__device__ __forceinline__ uint32_t galois_perm(uint32_t elt, uint32_t i, uint32_t logN) {
-    const uint64_t rev = 2ull * brv(i, logN) + 1;
-    const uint32_t raw = (uint32_t)((elt * rev) >> 1) & ((1u << logN) - 1);
-    return brv(raw, logN);
-}
-
 // ------------------------------------------------------------ elementwise
 enum BinOp { kAdd, kSub, kMul, kNeg };
 

@@ -57,6 +57,8 @@ SIGNATURES = {
     "pfa_ckks_encode_coeffs": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
     "pfa_expand_signed": (_i32, [_vp, _vp, _sz, _vp, _sz, _sz, _vp]),
     "pfa_bsgs_mac": (_i32, [_vp, _sz, C.POINTER(_vp), C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
+    "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
+    "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
 }
 
 
@@ -303,6 +305,18 @@ class NativeContext:
             first = next((t for t in list(outs) + list(babies) if not isinstance(t, int)), None)
             stream = stream_of(first) if first is not None else None
         call("pfa_bsgs_mac", self._h, chain_index, pp, bp, M, G, op, stream)
+
+    def bsgs_babies(self, chain_index, ct, M, keys, out, stream=None):
+        """out[b - 1] = babies[b] for 1 <= b < M (chained power-of-two rotations of
+        ct); keys[k] is the Galois key of step 2^k for every 2^k < M."""
+        kp = (C.c_void_p * max(len(keys), 1))(*[ptr(k) for k in keys])
+        dnum = keys[0].shape[0] if keys else 0
+        call("pfa_bsgs_babies", self._h, chain_index, ptr(ct), M, kp, dnum, ptr(out), stream or stream_of(ct))
+
+    def bsgs_giants(self, chain_index, partials, G, step, key, out, stream=None):
+        """Horner over the giant partials (overwritten) with rotation `step`, then rescale into out."""
+        call("pfa_bsgs_giants", self._h, chain_index, ptr(partials), G, step, ptr(key) if key is not None else None,
+             key.shape[0] if key is not None else 0, ptr(out), stream or stream_of(partials))
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

@@ -757,6 +757,17 @@ def compute_bsgs_babies(context: context, galois_key: galois_key, x: ciphertext,
     """babies[0] = x, babies[b] = rotate(babies[b - msb(b)], msb(b)) (src/bsgs.cu:195-215)."""
     if baby_steps == 0:
         raise ValueError("compute_bsgs_babies: baby_steps must be > 0")
+    if x.size() != 2:
+        raise ValueError("compute_bsgs_babies: ciphertext size must be 2")
+    steps = [1 << k for k in range((baby_steps - 1).bit_length())]
+    elts = [get_elt_from_step(s, context.N) for s in steps]
+    if baby_steps == 1:
+        return [x]
+    if all(e in galois_key.keys for e in elts):
+        # every rotation has its direct key: the whole chain runs in one native call
+        out = context._empty(baby_steps - 1, 2, context.size_Ql(x.chain_index()), context.N)
+        context.native.bsgs_babies(x.chain_index(), x.data, baby_steps, [galois_key.get(e) for e in elts], out)
+        return [x] + [x._like(out[b]) for b in range(baby_steps - 1)]
     babies = [x]
     for b in range(1, baby_steps):
         bit = 1 << (b.bit_length() - 1)
@@ -787,6 +798,13 @@ def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babi
     context.native.bsgs_mac(chain, [base_p + i * step for i in range(d_pad)], [c.data for c in babies],
                             [base_o + g * 2 * step for g in range(G)])
     scale = x.scale() * diags.scale
+    elt = get_elt_from_step(M, context.N)
+    if G == 1 or elt in galois_key.keys:
+        if L < 2:
+            raise ValueError("end of modulus switching chain reached")
+        out = context._empty(2, L - 1, context.N)
+        context.native.bsgs_giants(chain, partials, G, M, galois_key.get(elt) if G > 1 else None, out)
+        return x._like(out, chain=chain + 1)
     acc = x._like(partials[G - 1], scale=scale)
     for g in range(G - 2, -1, -1):
         acc = rotate(context, acc, M, galois_key)

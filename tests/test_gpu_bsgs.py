@@ -79,6 +79,14 @@ def test_bsgs_mac_rejects_bad_arguments(dev):
         ctx.bsgs_mac(1, [x[0]], [x], [])  # no giants
     with pytest.raises(ValueError):
         ctx.bsgs_mac(5, [x[0]], [x], [x])  # chain index out of range
+    with pytest.raises(ValueError):
+        ctx.bsgs_giants(2, x, 1, 1, None, x)  # rescale at the last level
+    with pytest.raises(ValueError):
+        ctx.bsgs_giants(1, x, 2, 1, None, x)  # a rotation without a key
+    with pytest.raises(ValueError):
+        ctx.bsgs_babies(1, x, 2, [empty((0, 2, 3, N), dev)], x)  # key without digits
+    with pytest.raises(ValueError):
+        ctx.bsgs_babies(3, x, 2, [x], x)  # chain index out of range
 
 
 def test_single_chain_encode_expand_equals_encode(dev):
@@ -130,24 +138,23 @@ def _oracle_bsgs(orc, mods, chain, x, glk_host, P, M, G, N):
     return orc.rescale(chain, acc, threads=8)
 
 
-def test_bsgs_matmul_bit_exact_and_decodes(dev):
-    """d_pad 64 = 8 babies x 8 giants at N = 2^12 (2048 slots, 32 periods), a
-    48 x 40 matrix (zero padding in both directions), x in replicated-block
-    layout.  The GPU result equals the oracle's run of the same algorithm and
-    decrypts to W x."""
+@pytest.mark.parametrize("M,G,rows,cols", [(8, 8, 48, 40), (1, 8, 8, 6), (4, 1, 3, 4)])
+def test_bsgs_matmul_bit_exact_and_decodes(dev, M, G, rows, cols):
+    """d_pad = M G at N = 2^12 (2048 slots), a rows x cols matrix (zero padding
+    in both directions), x in replicated-block layout.  The GPU result equals
+    the oracle's run of the same algorithm and decrypts to W x; the babies and
+    the giant stage equal the evaluator's own rotate / add composition."""
     import torch
 
-    M, G = 8, 8
     d_pad = M * G
-    rows, cols = 48, 40
     ph, ctx = make_ctx(12, [60, 40, 40, 40, 60, 60], 2, steps=[1, 2, 4, 8])
-    assert ph.bsgs_required_steps(M) == [1, 2, 4, 8]
+    assert set(ph.bsgs_required_steps(M)) <= {1, 2, 4, 8}
     ph.set_seed(11)
     sk = ph.secret_key(ctx).generate_sparse(ctx, 64)
     glk = sk.create_galois_keys(ctx)
     enc = ph.ckks_encoder(ctx)
     slots = enc.slot_count()
-    rng = np.random.default_rng(12)
+    rng = np.random.default_rng(12 + M)
     W = rng.uniform(-1 / 8, 1 / 8, (rows, cols))
     xv = np.zeros(d_pad)
     xv[:cols] = rng.uniform(-1, 1, cols)
@@ -180,6 +187,21 @@ def test_bsgs_matmul_bit_exact_and_decodes(dev):
     babies = ph.compute_bsgs_babies(ctx, glk, x, M)
     y2 = ph.bsgs_apply_giants_with_babies(ctx, glk, babies, diags)
     assert torch.equal(y2.data, y.data)
+
+    # the native baby chain equals rotate() one step at a time
+    for b in range(1, M):
+        bit = 1 << (b.bit_length() - 1)
+        assert torch.equal(babies[b].data, ph.rotate(ctx, babies[b - bit], bit, glk).data), b
+
+    # the native giant stage equals rotate / add / rescale_to_next on the same partials
+    partials = ctx._empty(G, 2, L, ctx.N)
+    step = L * ctx.N * 8
+    ctx.native.bsgs_mac(1, [diags.expanded(ctx, 1).data_ptr() + i * step for i in range(d_pad)],
+                        [b.data for b in babies], [partials[g] for g in range(G)])
+    acc = x._like(partials[G - 1])
+    for g in range(G - 2, -1, -1):
+        acc = ph.add(ctx, ph.rotate(ctx, acc, M, glk), x._like(partials[g]))
+    assert torch.equal(ph.rescale_to_next(ctx, acc).data, y.data)
 
 
 def test_bsgs_argument_checks(dev):
