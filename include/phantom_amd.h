@@ -215,6 +215,20 @@ int pfa_expand_signed(const pfa_context *ctx, const int64_t *in, size_t n, uint6
 int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *const *pts,
                  const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
 
+/* The tiled layout of a BSGS plaintext set (D plaintexts of Ql limbs at one
+ * chain index, NTT form): limb j, residues [512 t, 512 t + 512) of plaintext d
+ * at tiled[((j (N / 512) + t) D + d) 512], D Ql N residues in all.  It stores
+ * the plaintexts the accumulation reads together next to each other.  Copies
+ * src [n][Ql][N] into positions d0 .. d0+n-1.  Layout of this library (the
+ * reference re-expands each plaintext per use, src/bsgs.cu:276-312). */
+int pfa_bsgs_tile_plaintexts(const pfa_context *ctx, size_t chain_index, const uint64_t *src, size_t n,
+                             uint64_t *tiled, size_t d0, size_t D, void *stream);
+
+/* pfa_bsgs_mac with the G*M plaintexts given as one tiled set (D = M*G,
+ * plaintext g*M + b for giant g and baby b). */
+int pfa_bsgs_mac_tiled(const pfa_context *ctx, size_t chain_index, const uint64_t *tiled,
+                       const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
+
 /* compute_bsgs_babies (src/bsgs.cu:194-214): babies[0] = ct and
  * babies[b] = rotate(babies[b - msb(b)], msb(b)) for 1 <= b < M, each rotation
  * apply_galois_with_ksk (src/evaluate.cu:1607-1656) with the direct key.

@@ -1,15 +1,18 @@
-// BSGS matrix-vector product support: the giant-step accumulation of
-// bsgs_apply_giants_with_babies (src/bsgs.cu:51-96, :272-296), for every giant
-// in one launch, and the batched expansion of level-independent plaintexts
-// (signed coefficients, light_pt_expand_per_tower_kernel, src/bsgs.cu:16-23).
+// BSGS matrix-vector product support (src/bsgs.cu):
+// * the giant-step accumulation of bsgs_apply_giants_with_babies
+//   (mac_accumulate_kernel, src/bsgs.cu:51-96, used by build_partial,
+//   :276-342) for every giant in one launch;
+// * the batched expansion of level-independent plaintexts (signed
+//   coefficients, light_pt_expand_per_tower_kernel, src/bsgs.cu:16-23);
+// * native drivers of the baby-step chain (compute_bsgs_babies, :194-214) and
+//   of the giant-step Horner loop with its rescale (:344-356), one C-ABI call
+//   each, so a product costs two host calls instead of ~1100 launches from the
+//   caller's language.
 //
 // Accumulation: out[g][k][j] = sum_{b < M} pt[g M + b][j] * baby[b][k][j]
 // (mod q_j) for giant g, ciphertext poly k in {0, 1} and limb j.  The reference
-// runs one launch per giant, reading all M babies each time; here a work item
-// is (limb tile, giant) and the items of one limb tile are grouped on one XCD,
-// so a tile of the babies is read from HBM once and then from that XCD's L2
-// for every giant.  Results are canonical residues, equal to the reference's
-// per-step Barrett sums.
+// runs one launch per giant, reading all M babies each time.  Results are
+// canonical residues, equal to the reference's per-step Barrett sums.
 #include "internal.h"
 #include "ntt_kernels.h"
 
@@ -32,8 +35,24 @@ struct PtrList {
 
 constexpr uint32_t kInlineBabies = 64;
 
+// Residues per span of the tiled plaintext layout (and per accumulation work item).
+constexpr uint32_t kSpan = 512;
+constexpr int kPer = kSpan / kThreads;  // adjacent residues per thread (one 16-byte load)
+static_assert(kPer == 2, "pair loads");
+
+typedef uint64_t Pair __attribute__((ext_vector_type(2)));
+typedef const __attribute__((address_space(1))) Pair *GlobalPair;  // pointers here are all device memory
+__device__ __forceinline__ Pair ld_pair_stream(const uint64_t *p) {
+    return __builtin_nontemporal_load((GlobalPair)p);
+}
+__device__ __forceinline__ Pair ld_pair(const uint64_t *p) { return *(GlobalPair)p; }
+__device__ __forceinline__ void st_pair_stream(uint64_t *p, Pair v) {
+    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) Pair *)p);
+}
+
 struct MacArgs {
-    PtrList<const uint64_t> pt;  // [G M] plaintexts, [Ql][N] each (NTT form)
+    PtrList<const uint64_t> pt;  // [G M] plaintexts, [Ql][N] each (NTT form), when tiled is null
+    const uint64_t *tiled;       // or the same set in the tiled layout (pfa_bsgs_tile_plaintexts)
     PtrList<uint64_t> out;       // [G] ciphertexts, [2][Ql][N] each
     const uint64_t *const *baby_table;          // [M] ciphertexts [2][Ql][N], when M > kInlineBabies
     const uint64_t *baby_inline[kInlineBabies];  // the same, by value, when M <= kInlineBabies
@@ -41,90 +60,131 @@ struct MacArgs {
     __device__ __forceinline__ const uint64_t *baby(uint32_t b) const {
         return baby_table ? baby_table[b] : baby_inline[b];
     }
+    // span `tile` of limb j of plaintext d, plus this thread's offset
+    __device__ __forceinline__ const uint64_t *span(uint32_t d, uint32_t j, uint32_t tile) const {
+        if (tiled) return tiled + (((size_t)j * (N / kSpan) + tile) * ((size_t)G * M) + d) * kSpan + kPer * threadIdx.x;
+        return pt[d] + (size_t)j * N + tile * kSpan + kPer * threadIdx.x;
+    }
 };
 
-// A work item covers kSpan consecutive residues of one limb (kSpan / 256 per
-// thread, 256 apart), so every plaintext is read in 8 KiB runs.
+// A work item is (limb j, kSpan consecutive residues, block of up to kGB
+// giants).  Baby b's residues are loaded once per item (kPer adjacent ones per
+// thread and poly) and multiplied into every giant of the block, so the
+// babies are read G / kGB times in all instead of G times.  Items of one
+// (limb, span) carry the same workgroup index mod 8 and run on one XCD, which
+// then holds that span of the babies in its L2.  The plaintexts are read once
+// each: from a pointer list they arrive in 4 KiB runs of kGB M different
+// plaintexts (4.0 TB/s measured, all of it compulsory traffic: the scattered
+// rows, not the bytes, limit it); from the tiled layout an item's plaintext
+// spans are one contiguous 2 MiB region.
 // FP64 policy: each product is within 0.875 q (|x y / q| < q < 2^50), so four
-// of them on top of a reduced sum stay below 4 q < 2^53; integer policy: 128-bit
-// sums of at most eight products below q^2 < 2^122, then one Barrett reduction.
-constexpr uint32_t kSpan = 1024;
-constexpr int kPer = kSpan / kThreads;
+// of them on top of a reduced sum stay below 4 q < 2^53; integer policy: each
+// product reduced (Barrett) and summed modulo q.
+constexpr uint32_t kGB = 8;
 
 __global__ void __launch_bounds__(kThreads)
 k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
-    const uint32_t T = a.N / kSpan;  // items per limb and giant
+    const uint32_t T = a.N / kSpan;               // spans per limb
+    const uint32_t GB = (a.G + kGB - 1) / kGB;    // giant blocks
     const uint32_t groups = a.Ql * T;
-    const uint32_t total = grouped_total(groups, a.G);
+    const uint32_t total = grouped_total(groups, GB);
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
-        uint32_t grp, g;
-        if (!grouped_item(w, groups, a.G, grp, g)) continue;
+        uint32_t grp, gb;
+        if (!grouped_item(w, groups, GB, grp, gb)) continue;
         const uint32_t j = grp / T, tile = grp % T;
-        const size_t off0 = (size_t)j * a.N + tile * kSpan + threadIdx.x;
+        const size_t off0 = (size_t)j * a.N + tile * kSpan + kPer * threadIdx.x;
         const size_t off1 = off0 + (size_t)a.Ql * a.N;
-        const uint64_t q = mod[j];
-        const size_t pt0 = (size_t)g * a.M;
-        uint64_t *o = a.out[g];
+        const uint64_t q = wave_uniform(mod[j]);
+        const uint32_t g0 = gb * kGB;
+        const uint32_t K = a.G - g0 < kGB ? a.G - g0 : kGB;  // giants in this block
         if (q < kF64PrimeBound) {
             const ArithF64 ar(q);
-            double acc0[kPer], acc1[kPer];
+            double acc0[kGB][kPer], acc1[kGB][kPer];
 #pragma unroll
-            for (int e = 0; e < kPer; e++) acc0[e] = acc1[e] = 0.0;
+            for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0.0;
             for (uint32_t b = 0; b < a.M; b++) {
-                const uint64_t *p = a.pt[pt0 + b] + off0;
                 const uint64_t *c = a.baby(b);
-                double x[kPer], y0[kPer], y1[kPer];
+                double y0[kPer], y1[kPer], y0q[kPer], y1q[kPer];
+                const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
 #pragma unroll
                 for (int e = 0; e < kPer; e++) {
-                    x[e] = ar.load(ld_stream(p + e * kThreads));
-                    y0[e] = ar.load(c[off0 + e * kThreads]);
-                    y1[e] = ar.load(c[off1 + e * kThreads]);
+                    y0[e] = ar.load(c0[e]);
+                    y1[e] = ar.load(c1[e]);
+                    y0q[e] = y0[e] * ar.qinv;
+                    y1q[e] = y1[e] * ar.qinv;
                 }
 #pragma unroll
-                for (int e = 0; e < kPer; e++) {
-                    const double xq = x[e] * ar.qinv;
-                    acc0[e] += ar.mulw(y0[e], x[e], xq);
-                    acc1[e] += ar.mulw(y1[e], x[e], xq);
+                for (uint32_t k = 0; k < kGB; k++) {
+                    if (k < K) {
+                        const uint64_t *p = a.span((g0 + k) * a.M + b, j, tile);
+                        const Pair xv = ld_pair_stream(p);
+#pragma unroll
+                        for (int e = 0; e < kPer; e++) {
+                            const double x = ar.load(xv[e]);
+                            acc0[k][e] += ar.mulw(x, y0[e], y0q[e]);
+                            acc1[k][e] += ar.mulw(x, y1[e], y1q[e]);
+                        }
+                    }
                 }
                 if ((b & 3u) == 3u) {
 #pragma unroll
-                    for (int e = 0; e < kPer; e++) {
-                        ar.reduce(acc0[e]);
-                        ar.reduce(acc1[e]);
-                    }
+                    for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                        for (int e = 0; e < kPer; e++) {
+                            ar.reduce(acc0[k][e]);
+                            ar.reduce(acc1[k][e]);
+                        }
                 }
             }
 #pragma unroll
-            for (int e = 0; e < kPer; e++) {
-                st_stream(o + off0 + e * kThreads, ar.store(acc0[e]));
-                st_stream(o + off1 + e * kThreads, ar.store(acc1[e]));
+            for (uint32_t k = 0; k < kGB; k++) {
+                if (k < K) {
+                    uint64_t *o = a.out[g0 + k];
+                    st_pair_stream(o + off0, Pair{ar.store(acc0[k][0]), ar.store(acc0[k][1])});
+                    st_pair_stream(o + off1, Pair{ar.store(acc1[k][0]), ar.store(acc1[k][1])});
+                }
             }
         } else {
-            const ulonglong2 r = ratio[j];
-            U128 s0[kPer], s1[kPer];
+            ulonglong2 r = ratio[j];
+            r.x = wave_uniform(r.x);
+            r.y = wave_uniform(r.y);
+            uint64_t acc0[kGB][kPer], acc1[kGB][kPer];
 #pragma unroll
-            for (int e = 0; e < kPer; e++) s0[e] = s1[e] = U128{0, 0};
+            for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0;
             for (uint32_t b = 0; b < a.M; b++) {
-                const uint64_t *p = a.pt[pt0 + b] + off0;
                 const uint64_t *c = a.baby(b);
+                uint64_t y0[kPer], y1[kPer];
+                const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
 #pragma unroll
                 for (int e = 0; e < kPer; e++) {
-                    const uint64_t x = ld_stream(p + e * kThreads);
-                    mac(s0[e], x, c[off0 + e * kThreads]);
-                    mac(s1[e], x, c[off1 + e * kThreads]);
+                    y0[e] = c0[e];
+                    y1[e] = c1[e];
                 }
-                if ((b & 7u) == 7u) {
 #pragma unroll
-                    for (int e = 0; e < kPer; e++) {
-                        s0[e] = U128{barrett128(s0[e], q, r.x, r.y), 0};
-                        s1[e] = U128{barrett128(s1[e], q, r.x, r.y), 0};
+                for (uint32_t k = 0; k < kGB; k++) {
+                    if (k < K) {
+                        const uint64_t *p = a.span((g0 + k) * a.M + b, j, tile);
+                        const Pair xv = ld_pair_stream(p);
+#pragma unroll
+                        for (int e = 0; e < kPer; e++) {
+                            const uint64_t x = xv[e];
+                            acc0[k][e] = add_mod(acc0[k][e], barrett128(U128{x * y0[e], mulhi64(x, y0[e])}, q, r.x, r.y), q);
+                            acc1[k][e] = add_mod(acc1[k][e], barrett128(U128{x * y1[e], mulhi64(x, y1[e])}, q, r.x, r.y), q);
+                        }
                     }
                 }
             }
 #pragma unroll
-            for (int e = 0; e < kPer; e++) {
-                st_stream(o + off0 + e * kThreads, barrett128(s0[e], q, r.x, r.y));
-                st_stream(o + off1 + e * kThreads, barrett128(s1[e], q, r.x, r.y));
+            for (uint32_t k = 0; k < kGB; k++) {
+                if (k < K) {
+                    uint64_t *o = a.out[g0 + k];
+                    st_pair_stream(o + off0, Pair{acc0[k][0], acc0[k][1]});
+                    st_pair_stream(o + off1, Pair{acc1[k][0], acc1[k][1]});
+                }
             }
         }
     }
@@ -144,6 +204,18 @@ k_expand_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t 
         r = q - 1 - r;
     }
     st_stream(out + ((size_t)p * L + l) * N + n, r);
+}
+
+// Plaintexts src[n][Ql][N] -> positions d0 .. d0+n-1 of a tiled set of D:
+//   tiled[((j T + t) D + d) kSpan + i] = pt[d][j][t kSpan + i],  T = N / kSpan.
+// One workgroup per (span, limb, plaintext): a contiguous 4 KiB read and write.
+__global__ void __launch_bounds__(kThreads)
+k_bsgs_tile(const uint64_t *src, uint64_t *tiled, uint32_t Ql, uint32_t N, uint32_t d0, uint32_t D) {
+    const uint32_t t = blockIdx.x, j = blockIdx.y, p = blockIdx.z, T = N / kSpan;
+    const uint64_t *s = src + ((size_t)p * Ql + j) * N + (size_t)t * kSpan;
+    uint64_t *o = tiled + (((size_t)j * T + t) * D + d0 + p) * kSpan;
+#pragma unroll
+    for (uint32_t i = threadIdx.x; i < kSpan; i += kThreads) st_stream(o + i, ld_stream(s + i));
 }
 
 // Both polys of a ciphertext through the Galois permutation of NTT slots
@@ -178,6 +250,63 @@ void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint32_t elt
     fused_moddown(c, chain, cx, 2, out, t, add ? add + LN : nullptr, s);
 }
 
+// One accumulation launch: plaintexts from the pointer list pts or the tiled set.
+void launch_mac(const Ctx &c, size_t chain_index, const uint64_t *const *pts, const uint64_t *tiled,
+                const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, hipStream_t s) {
+    require(babies && out, "null argument");
+    require(M >= 1 && G >= 1, "need at least one baby step and one giant step");
+    require(M * G < (1u << 24), "too many plaintexts");
+    if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+    for (size_t i = 0; i < M; i++) require(babies[i] != nullptr, "null ciphertext pointer");
+    for (size_t i = 0; i < G; i++) require(out[i] != nullptr, "null output pointer");
+    const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
+    Scratch sc(c, s);
+    MacArgs a{};
+    a.M = (uint32_t)M;
+    a.G = (uint32_t)G;
+    a.Ql = Ql;
+    a.N = c.N;
+    // a list whose addresses step by a constant multiple of 8 bytes goes as base + stride
+    auto progression = [](const void *const *v, size_t n, uint64_t &stride) {
+        const uintptr_t b0 = (uintptr_t)v[0];
+        const intptr_t d = n > 1 ? (intptr_t)((uintptr_t)v[1] - b0) : 0;
+        if (d < 0 || d % 8) return false;
+        for (size_t i = 1; i < n; i++)
+            if ((uintptr_t)v[i] != b0 + (uintptr_t)d * i) return false;
+        stride = (uint64_t)d / 8;
+        return true;
+    };
+    uint64_t st = 0;
+    a.tiled = tiled;
+    if (!tiled) {
+        if (progression((const void *const *)pts, M * G, st)) {
+            a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
+        } else {
+            const uint64_t **t = sc.alloc<const uint64_t *>(M * G);
+            PFA_HIP(hipMemcpyAsync(t, pts, M * G * sizeof(void *), hipMemcpyHostToDevice, s));
+            a.pt = PtrList<const uint64_t>{t, nullptr, 0};
+        }
+    }
+    if (progression((const void *const *)out, G, st)) {
+        a.out = PtrList<uint64_t>{nullptr, out[0], st};
+    } else {
+        uint64_t **t = sc.alloc<uint64_t *>(G);
+        PFA_HIP(hipMemcpyAsync(t, out, G * sizeof(void *), hipMemcpyHostToDevice, s));
+        a.out = PtrList<uint64_t>{t, nullptr, 0};
+    }
+    if (M <= kInlineBabies) {
+        for (size_t i = 0; i < M; i++) a.baby_inline[i] = babies[i];
+    } else {
+        const uint64_t **t = sc.alloc<const uint64_t *>(M);
+        PFA_HIP(hipMemcpyAsync(t, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
+        a.baby_table = t;
+    }
+    const uint32_t total = grouped_total(Ql * (c.N / kSpan), ((uint32_t)G + kGB - 1) / kGB);
+    const uint32_t cap = (uint32_t)c.n_cu * 4u;  // resident workgroups (4 waves per SIMD)
+    hipLaunchKernelGGL(k_bsgs_mac, dim3(total < cap ? total : cap), dim3(kThreads), 0, s, a, c.mod, c.ratio);
+    PFA_HIP(hipGetLastError());
+}
+
 uint32_t rotation_elt(const Ctx &c, int step) {
     uint32_t e = 0;
     if (pfa_galois_elt_from_step(step, c.N, &e) != PFA_OK) fail(PFA_ERR_INVALID_ARGUMENT, "bad rotation step");
@@ -200,57 +329,30 @@ extern "C" {
 int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *const *pts,
                  const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream) {
     return guarded([&] {
-        const Ctx &c = *ctx_of(ctx);
-        require(pts && babies && out, "null argument");
-        require(M >= 1 && G >= 1, "need at least one baby step and one giant step");
-        require(M * G < (1u << 24), "too many plaintexts");
-        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        require(pts != nullptr, "null argument");
         for (size_t i = 0; i < M * G; i++) require(pts[i] != nullptr, "null plaintext pointer");
-        for (size_t i = 0; i < M; i++) require(babies[i] != nullptr, "null ciphertext pointer");
-        for (size_t i = 0; i < G; i++) require(out[i] != nullptr, "null output pointer");
-        const hipStream_t s = as_stream(stream);
+        launch_mac(*ctx_of(ctx), chain_index, pts, nullptr, babies, M, G, out, as_stream(stream));
+    });
+}
+
+int pfa_bsgs_mac_tiled(const pfa_context *ctx, size_t chain_index, const uint64_t *tiled,
+                       const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream) {
+    return guarded([&] {
+        require(tiled != nullptr, "null argument");
+        launch_mac(*ctx_of(ctx), chain_index, nullptr, tiled, babies, M, G, out, as_stream(stream));
+    });
+}
+
+int pfa_bsgs_tile_plaintexts(const pfa_context *ctx, size_t chain_index, const uint64_t *src, size_t n,
+                             uint64_t *tiled, size_t d0, size_t D, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(src && tiled, "null argument");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        require(n >= 1 && n <= 65535 && d0 + n <= D && D < (1u << 24), "plaintext range out of bounds");
         const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
-        Scratch sc(c, s);
-        MacArgs a{};
-        a.M = (uint32_t)M;
-        a.G = (uint32_t)G;
-        a.Ql = Ql;
-        a.N = c.N;
-        // a list whose addresses step by a constant multiple of 8 bytes goes as base + stride
-        auto progression = [](const void *const *v, size_t n, uint64_t &stride) {
-            const uintptr_t b0 = (uintptr_t)v[0];
-            const intptr_t d = n > 1 ? (intptr_t)((uintptr_t)v[1] - b0) : 0;
-            if (d < 0 || d % 8) return false;
-            for (size_t i = 1; i < n; i++)
-                if ((uintptr_t)v[i] != b0 + (uintptr_t)d * i) return false;
-            stride = (uint64_t)d / 8;
-            return true;
-        };
-        uint64_t st = 0;
-        if (progression((const void *const *)pts, M * G, st)) {
-            a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
-        } else {
-            const uint64_t **t = sc.alloc<const uint64_t *>(M * G);
-            PFA_HIP(hipMemcpyAsync(t, pts, M * G * sizeof(void *), hipMemcpyHostToDevice, s));
-            a.pt = PtrList<const uint64_t>{t, nullptr, 0};
-        }
-        if (progression((const void *const *)out, G, st)) {
-            a.out = PtrList<uint64_t>{nullptr, out[0], st};
-        } else {
-            uint64_t **t = sc.alloc<uint64_t *>(G);
-            PFA_HIP(hipMemcpyAsync(t, out, G * sizeof(void *), hipMemcpyHostToDevice, s));
-            a.out = PtrList<uint64_t>{t, nullptr, 0};
-        }
-        if (M <= kInlineBabies) {
-            for (size_t i = 0; i < M; i++) a.baby_inline[i] = babies[i];
-        } else {
-            const uint64_t **t = sc.alloc<const uint64_t *>(M);
-            PFA_HIP(hipMemcpyAsync(t, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
-            a.baby_table = t;
-        }
-        const uint32_t total = grouped_total(Ql * (c.N / kSpan), (uint32_t)G);
-        const uint32_t cap = (uint32_t)c.n_cu * 8u;
-        hipLaunchKernelGGL(k_bsgs_mac, dim3(total < cap ? total : cap), dim3(kThreads), 0, s, a, c.mod, c.ratio);
+        hipLaunchKernelGGL(k_bsgs_tile, dim3(c.N / kSpan, Ql, (uint32_t)n), dim3(kThreads), 0, as_stream(stream), src,
+                           tiled, Ql, c.N, (uint32_t)d0, (uint32_t)D);
         PFA_HIP(hipGetLastError());
     });
 }

@@ -164,13 +164,13 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
             const ArithF64 ar(q);
             double x[SB::E];
             bconv_source<ArithF64, S1, S2>(a, t, ar, g, j, tile, x);
-            fwd_cols_core<ArithF64, S1, S2>(x, ar, t, prow, lds);
+            fwd_cols_core<ArithF64, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, lds);
             fwd_cols_store<ArithF64, S1, S2>(x, ar, tile, olimb);
         } else {
             const ArithInt ar(q);
             uint64_t x[SB::E];
             bconv_source<ArithInt, S1, S2>(a, t, ar, g, j, tile, x);
-            fwd_cols_core<ArithInt, S1, S2>(x, ar, t, prow, reinterpret_cast<uint64_t *>(lds));
+            fwd_cols_core<ArithInt, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, reinterpret_cast<uint64_t *>(lds));
             fwd_cols_store<ArithInt, S1, S2>(x, ar, tile, olimb);
         }
         __syncthreads();

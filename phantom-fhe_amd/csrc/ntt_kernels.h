@@ -314,6 +314,78 @@ __device__ __forceinline__ bool grouped_item(uint32_t w, uint32_t G, uint32_t J,
 
 __host__ __device__ inline uint32_t grouped_total(uint32_t G, uint32_t J) { return ((G + 7u) / 8u) * 8u * J; }
 
+// ================================================================ twiddles
+// Where a tile's twiddle factors come from.  Columns passes index col[0 .. N1-1]
+// (entries 1 .. N1-1 of the prime's table).  Rows passes index, in the integer
+// policy, the prime's full table `full` at base N1 + k1, and in the FP64 policy
+// the base factors rb[g * RBS + rrow] and the small table `small`.  The
+// persistent two-pass kernels stage the entries a tile needs in LDS (RBS =
+// ROWS, rrow = the row within the tile); other callers read the global tables
+// (RBS = N1, rrow = k1).
+struct TileTw {
+    const ulonglong2 *col;
+    const ulonglong2 *full;
+    const ulonglong2 *rb;
+    const ulonglong2 *small;
+    uint32_t rrow;
+};
+
+template <int S1, int S2>
+__device__ __forceinline__ TileTw global_tw(const NttTables &t, uint32_t prow, uint32_t k1, bool fwd) {
+    using G = Geo<S1, S2>;
+    const ulonglong2 *tab = (fwd ? t.tw : t.itw) + (size_t)prow * G::N;
+    return TileTw{tab, tab, (fwd ? t.rb_fw : t.rb_inv) + (size_t)prow * S2 * G::N1,
+                  (fwd ? t.small_fw : t.small_inv) + (size_t)prow * kSmall, k1};
+}
+
+// A gather of N twiddle entries into LDS, split in two so the caller can issue
+// its data prefetch in between: global loads complete in issue order, so a load
+// issued after the prefetch could not be waited for without waiting for the
+// prefetch.  load() issues every thread's loads, store() writes them to LDS
+// (the caller then synchronizes the workgroup).
+template <int N, int THREADS>
+struct TwStage {
+    static constexpr int PER = (N + THREADS - 1) / THREADS;
+    ulonglong2 v[PER];
+    // every lane loads (surplus lanes a duplicate of the last entry): a load
+    // under a branch would make the wait for it a wait for all loads
+    template <class Src>
+    __device__ __forceinline__ void load(Src src) {
+#pragma unroll
+        for (int p = 0; p < PER; p++) {
+            const uint32_t i = threadIdx.x + p * THREADS;
+            v[p] = src(i < (uint32_t)N ? i : (uint32_t)N - 1);
+        }
+    }
+    __device__ __forceinline__ void store(ulonglong2 *dst) const {
+#pragma unroll
+        for (int p = 0; p < PER; p++) {
+            const uint32_t i = threadIdx.x + p * THREADS;
+            if (i < (uint32_t)N) dst[i] = v[p];
+        }
+    }
+};
+
+// Staged entries of a rows-pass tile: rb[g][tile ROWS + i] for g < S2, i < ROWS,
+// then the small table's first 2^(S2-1) entries.
+template <int S1, int S2>
+struct RowStage {
+    using G = Geo<S1, S2>;
+    static constexpr int RB = S2 * G::ROWS;
+    static constexpr int N = RB + (1 << (S2 - 1));
+    TwStage<N, G::ROW_THREADS> st;
+    __device__ __forceinline__ void load(const NttTables &t, uint32_t prow, uint32_t tile, bool fwd) {
+        const ulonglong2 *rb = (fwd ? t.rb_fw : t.rb_inv) + (size_t)prow * S2 * G::N1 + tile * G::ROWS;
+        const ulonglong2 *small = (fwd ? t.small_fw : t.small_inv) + (size_t)prow * kSmall;
+        st.load([&](uint32_t i) { return i < (uint32_t)RB ? rb[(i / G::ROWS) * G::N1 + i % G::ROWS] : small[i - RB]; });
+    }
+    // LDS copy -> the tile's twiddle view (full: the prime's global table, for
+    // the integer policy)
+    __device__ __forceinline__ static TileTw view(const ulonglong2 *lds, const ulonglong2 *full, uint32_t rr) {
+        return TileTw{nullptr, full, lds, lds + RB, rr};
+    }
+};
+
 // ================================================================ forward
 // Columns pass: src (canonical) -> dst (intermediate form).
 template <int S1, int S2>
@@ -325,13 +397,12 @@ __device__ __forceinline__ const uint64_t *cols_src(const NttBatch &b, const Til
 
 // Forward columns pass of one tile.  In: x[e] = element (F + T e) of column c
 // of the tile, |x| <= q (any lazy representative).  Out: x[e] = element
-// (F E + e) of the column in the intermediate form (lazy).
+// (F E + e) of the column in the intermediate form (lazy).  tw: the prime's
+// table (entries 1 .. N1-1 are read).
 template <class A, int S1, int S2>
-__device__ __forceinline__ void fwd_cols_core(typename A::T (&x)[Sub<S1>::E], const A &ar, const NttTables &t,
-                                              uint32_t prow, typename A::T *lds) {
-    using G = Geo<S1, S2>;
+__device__ __forceinline__ void fwd_cols_core(typename A::T (&x)[Sub<S1>::E], const A &ar, const ulonglong2 *tw,
+                                              typename A::T *lds) {
     using SB = Sub<S1>;
-    const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     fwd_round_a<A, S1>(x, ar, tw, 1);
 #pragma unroll
@@ -366,16 +437,15 @@ __device__ __forceinline__ void fwd_cols_store(const typename A::T (&x)[Sub<S1>:
 }
 
 template <class A, int S1, int S2, bool NT = true>
-__device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+__device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const ulonglong2 *tw,
+                                              const TileRef &r, uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using SB = Sub<S1>;
     using T = typename A::T;
     const A ar(q);
     T x[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = ar.load(raw[e]);
-    fwd_cols_core<A, S1, S2>(x, ar, t, prow, lds);
+    fwd_cols_core<A, S1, S2>(x, ar, tw, lds);
     fwd_cols_store<A, S1, S2, NT>(x, ar, r.tile, olimb);
 }
 
@@ -404,10 +474,12 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
+        const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
+        uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            fwd_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            fwd_cols_tile<ArithF64, S1, S2>(raw, tw, r, q, lds, olimb);
         else
-            fwd_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            fwd_cols_tile<ArithInt, S1, S2>(raw, tw, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -420,17 +492,16 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
 // row in the intermediate form.  Out: x[e] = element (F + T e) of the
 // transformed row (lazy; the final LDS transpose makes stores coalesced).
 // The caller separates consecutive calls on the same LDS with a barrier.
-template <class A, int S1, int S2>
-__device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], const A &ar, const NttTables &t,
-                                              uint32_t prow, uint32_t k1, typename A::T *lr) {
+template <class A, int S1, int S2, int RBS>
+__device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], const A &ar, const TileTw &w,
+                                              uint32_t k1, typename A::T *lr) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
-    const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
     const uint32_t F = threadIdx.x % SB::T;
     if constexpr (A::kF64)
-        fwd_round_a_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1);
+        fwd_round_a_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow);
     else
-        fwd_round_a<A, S2>(x, ar, tw, G::N1 + k1);
+        fwd_round_a<A, S2>(x, ar, w.full, G::N1 + k1);
 #pragma unroll
     for (int e = 0; e < SB::E; e++) {
         ar.reduce(x[e]);
@@ -440,9 +511,9 @@ __device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], co
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
     if constexpr (A::kF64)
-        fwd_round_b_derived<S2, G::N1>(x, ar, t.rb_fw + (size_t)prow * S2 * G::N1, t.small_fw + (size_t)prow * kSmall, k1, F);
+        fwd_round_b_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow, F);
     else
-        fwd_round_b<A, S2>(x, ar, tw, G::N1 + k1, F);
+        fwd_round_b<A, S2>(x, ar, w.full, G::N1 + k1, F);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < SB::E; e++) lr[rpad(F * SB::E + e)] = x[e];
@@ -451,10 +522,16 @@ __device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], co
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F + SB::T * e)];
 }
 
+// the same with the twiddles read from the global tables
 template <class A, int S1, int S2>
-__device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+__device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], const A &ar, const NttTables &t,
+                                              uint32_t prow, uint32_t k1, typename A::T *lr) {
+    fwd_rows_core<A, S1, S2, Geo<S1, S2>::N1>(x, ar, global_tw<S1, S2>(t, prow, k1, true), k1, lr);
+}
+
+template <class A, int S1, int S2, int RBS>
+__device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
+                                              uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -465,7 +542,7 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     T x[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(raw[e]);
-    fwd_rows_core<A, S1, S2>(x, ar, t, prow, k1, lds + rr * G::ROW_PITCH);
+    fwd_rows_core<A, S1, S2, RBS>(x, ar, w, k1, lds + rr * G::ROW_PITCH);
 #pragma unroll
     for (int e = 0; e < SB::E; e++) st_stream(&rowp[F + SB::T * e], ar.store(x[e]));
 }
@@ -482,9 +559,11 @@ template <int S1, int S2>
 __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
+    using RS = RowStage<S1, S2>;
     __shared__ double lds[G::ROW_LDS];
+    __shared__ ulonglong2 twl[RS::N];
     const uint32_t total = b.M * b.L * G::ROW_TILES;
-    const uint32_t F = threadIdx.x % SB::T;
+    const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
     uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total);
     uint64_t raw[SB::E];
     if (cur < total) {
@@ -495,18 +574,29 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
     while (cur < total) {
         const uint32_t nxt = next_tile(b, G::ROW_TILES, cur + gridDim.x, total);
         const TileRef r = decode_tile(b, G::ROW_TILES, cur);
+        const uint32_t prow = b.map.row(r.l);
+        // the tile's prime and twiddles first, then the next tile's prefetch
+        const uint64_t q = t.mod[prow];
+        RS stage;
+        stage.load(t, prow, r.tile, true);
+        __builtin_amdgcn_sched_barrier(0);
+        // unconditional (the last tile reloads itself): a prefetch under a branch
+        // would make the wait for the staged twiddles a wait for everything
         uint64_t nraw[SB::E];
-        if (nxt < total) {
-            const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt), b.src, b.sstride);
+        {
+            const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt < total ? nxt : cur), b.src, b.sstride);
 #pragma unroll
             for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[F + SB::T * e]);
         }
-        const uint32_t prow = b.map.row(r.l);
-        const uint64_t q = t.mod[prow];
+        __builtin_amdgcn_sched_barrier(0);
+        stage.st.store(twl);
+        __syncthreads();
+        const TileTw w = RS::view(twl, t.tw + (size_t)prow * G::N, rr);
+        uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            fwd_rows_tile<ArithF64, S1, S2, G::ROWS>(raw, w, r, q, lds, olimb);
         else
-            fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            fwd_rows_tile<ArithInt, S1, S2, G::ROWS>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -516,15 +606,13 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
 
 // ================================================================ inverse
 // Rows pass first: src (canonical) -> dst (intermediate).
-template <class A, int S1, int S2, bool NT = true>
-__device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+template <class A, int S1, int S2, int RBS, bool NT = true>
+__device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
+                                              uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
     const A ar(q);
-    const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
     const uint32_t k1 = r.tile * G::ROWS + rr;
     uint64_t *drow = olimb + (size_t)k1 * G::N2;
@@ -536,9 +624,9 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
     if constexpr (A::kF64)
-        inv_round_a_derived<S2, G::N1>(x, ar, t.rb_inv + (size_t)prow * S2 * G::N1, t.small_inv + (size_t)prow * kSmall, k1, F);
+        inv_round_a_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow, F);
     else
-        inv_round_a<A, S2>(x, ar, itw, G::N1 + k1, F);
+        inv_round_a<A, S2>(x, ar, w.full, G::N1 + k1, F);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < SB::E; e++) lr[rpad(F * SB::E + e)] = x[e];
@@ -546,9 +634,9 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F + SB::T * e)];
     if constexpr (A::kF64)
-        inv_round_b_derived<S2, G::N1>(x, ar, t.rb_inv + (size_t)prow * S2 * G::N1, t.small_inv + (size_t)prow * kSmall, k1);
+        inv_round_b_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow);
     else
-        inv_round_b<A, S2, false>(x, ar, itw, G::N1 + k1, ulonglong2{0, 0});
+        inv_round_b<A, S2, false>(x, ar, w.full, G::N1 + k1, ulonglong2{0, 0});
 #pragma unroll
     for (int e = 0; e < SB::E; e++) {
         if (NT)
@@ -564,7 +652,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
     using SB = Sub<S2>;
     __shared__ double lds[G::ROW_LDS];
     const uint32_t total = b.M * b.L * G::ROW_TILES;
-    const uint32_t F = threadIdx.x % SB::T;
+    const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
     uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total);
     uint64_t raw[SB::E];
     if (cur < total) {
@@ -583,10 +671,12 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
+        const TileTw w = global_tw<S1, S2>(t, prow, r.tile * G::ROWS + rr, false);
+        uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            inv_rows_tile<ArithF64, S1, S2, G::N1>(raw, w, r, q, lds, olimb);
         else
-            inv_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            inv_rows_tile<ArithInt, S1, S2, G::N1>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -594,16 +684,16 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
     }
 }
 
-// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and optional scale.
+// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and optional scale
+// (scale: the pair for this limb, or null).
 template <class A, int S1, int S2>
-__device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const NttBatch &b,
-                                              const NttTables &t, const TileRef &r, uint32_t prow, uint64_t q,
+__device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const ulonglong2 *itw,
+                                              ulonglong2 ninv, const ulonglong2 *scale, const TileRef &r, uint64_t q,
                                               typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     using T = typename A::T;
     const A ar(q);
-    const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
     uint64_t *data = olimb + r.tile * kCols;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     T x[SB::E];
@@ -615,9 +705,9 @@ __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lds[(F + SB::T * e) * kColStride + c];
-    inv_round_b<A, S1, true>(x, ar, itw, 1, t.ninv[prow]);
-    if (b.scale) {
-        const ulonglong2 s = b.scale[r.l];
+    inv_round_b<A, S1, true>(x, ar, itw, 1, ninv);
+    if (scale) {
+        const ulonglong2 s = *scale;
 #pragma unroll
         for (int e = 0; e < SB::E; e++) ar.mul(x[e], s);
     }
@@ -650,10 +740,13 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBa
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
+        const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
+        const ulonglong2 *scale = b.scale ? b.scale + r.l : nullptr;
+        uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            inv_cols_tile<ArithF64, S1, S2>(raw, itw, t.ninv[prow], scale, r, q, lds, olimb);
         else
-            inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), b.dst + r.m * b.dstride + (size_t)r.l * G::N);
+            inv_cols_tile<ArithInt, S1, S2>(raw, itw, t.ninv[prow], scale, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
@@ -794,9 +887,10 @@ struct OnePassJob {
 #pragma unroll
             for (int e = 0; e < S1B::E; e++) raw[e] = ld_stream(&s[(size_t)(F + S1B::T * e) * G::N2 + c]);
             if (q < kF64PrimeBound)
-                fwd_cols_tile<ArithF64, S1, S2, false>(raw, b, t, r, prow, q, lds, limb);
+                fwd_cols_tile<ArithF64, S1, S2, false>(raw, t.tw + (size_t)prow * G::N, r, q, lds, limb);
             else
-                fwd_cols_tile<ArithInt, S1, S2, false>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+                fwd_cols_tile<ArithInt, S1, S2, false>(raw, t.tw + (size_t)prow * G::N, r, q,
+                                                       reinterpret_cast<uint64_t *>(lds), limb);
         } else {
             const uint32_t F = threadIdx.x % S2B::T;
             const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
@@ -804,9 +898,10 @@ struct OnePassJob {
 #pragma unroll
             for (int e = 0; e < S2B::E; e++) raw[e] = ld_stream(&s[F + S2B::T * e]);
             if (q < kF64PrimeBound)
-                inv_rows_tile<ArithF64, S1, S2, false>(raw, b, t, r, prow, q, lds, limb);
+                inv_rows_tile<ArithF64, S1, S2, G::N1, false>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, false), r, q, lds, limb);
             else
-                inv_rows_tile<ArithInt, S1, S2, false>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+                inv_rows_tile<ArithInt, S1, S2, G::N1, false>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, false), r, q,
+                                                              reinterpret_cast<uint64_t *>(lds), limb);
         }
     }
     // second-pass tile `tile` of the output limb, after the job's first pass
@@ -820,9 +915,10 @@ struct OnePassJob {
 #pragma unroll
             for (int e = 0; e < S2B::E; e++) raw[e] = s[F + S2B::T * e];
             if (q < kF64PrimeBound)
-                fwd_rows_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, limb);
+                fwd_rows_tile<ArithF64, S1, S2, G::N1>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, true), r, q, lds, limb);
             else
-                fwd_rows_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+                fwd_rows_tile<ArithInt, S1, S2, G::N1>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, true), r, q,
+                                                       reinterpret_cast<uint64_t *>(lds), limb);
         } else {
             const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
             const uint64_t *s = cols_src<S1, S2>(b, r, b.dst, b.dstride);
@@ -830,9 +926,10 @@ struct OnePassJob {
 #pragma unroll
             for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F * S1B::E + e) * G::N2 + c];
             if (q < kF64PrimeBound)
-                inv_cols_tile<ArithF64, S1, S2>(raw, b, t, r, prow, q, lds, limb);
+                inv_cols_tile<ArithF64, S1, S2>(raw, t.itw + (size_t)prow * G::N, t.ninv[prow], b.scale ? b.scale + l : nullptr, r, q, lds, limb);
             else
-                inv_cols_tile<ArithInt, S1, S2>(raw, b, t, r, prow, q, reinterpret_cast<uint64_t *>(lds), limb);
+                inv_cols_tile<ArithInt, S1, S2>(raw, t.itw + (size_t)prow * G::N, t.ninv[prow], b.scale ? b.scale + l : nullptr, r, q,
+                                                reinterpret_cast<uint64_t *>(lds), limb);
         }
         __syncthreads();
     }

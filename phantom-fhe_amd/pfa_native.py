@@ -57,6 +57,8 @@ SIGNATURES = {
     "pfa_ckks_encode_coeffs": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
     "pfa_expand_signed": (_i32, [_vp, _vp, _sz, _vp, _sz, _sz, _vp]),
     "pfa_bsgs_mac": (_i32, [_vp, _sz, C.POINTER(_vp), C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
+    "pfa_bsgs_tile_plaintexts": (_i32, [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp]),
+    "pfa_bsgs_mac_tiled": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
     "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
 }
@@ -305,6 +307,19 @@ class NativeContext:
             first = next((t for t in list(outs) + list(babies) if not isinstance(t, int)), None)
             stream = stream_of(first) if first is not None else None
         call("pfa_bsgs_mac", self._h, chain_index, pp, bp, M, G, op, stream)
+
+    def bsgs_tile_plaintexts(self, chain_index, src, n, tiled, d0, D, stream=None):
+        """src [n][Ql][N] -> positions d0 .. d0+n-1 of the tiled set `tiled` of D plaintexts."""
+        call("pfa_bsgs_tile_plaintexts", self._h, chain_index, ptr(src), n, ptr(tiled), d0, D,
+             stream or stream_of(src))
+
+    def bsgs_mac_tiled(self, chain_index, tiled, babies, outs, stream=None):
+        """bsgs_mac with the len(babies) * len(outs) plaintexts in one tiled set."""
+        M, G = len(babies), len(outs)
+        addr = lambda t: t if isinstance(t, int) else ptr(t)
+        bp = (C.c_void_p * M)(*[addr(t) for t in babies])
+        op = (C.c_void_p * G)(*[addr(t) for t in outs])
+        call("pfa_bsgs_mac_tiled", self._h, chain_index, ptr(tiled), bp, M, G, op, stream or stream_of(tiled))
 
     def bsgs_babies(self, chain_index, ct, M, keys, out, stream=None):
         """out[b - 1] = babies[b] for 1 <= b < M (chained power-of-two rotations of

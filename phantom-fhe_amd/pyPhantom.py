@@ -684,15 +684,21 @@ class bsgs_diagonals:
         self._expanded = {}
 
     def expanded(self, ctx: context, chain_index: int):
+        """The diagonals as NTT-form plaintexts at chain_index, in the tiled
+        layout the accumulation reads (pfa_bsgs_tile_plaintexts), built once
+        per level and kept on the device."""
         t = self._expanded.get(chain_index)
         if t is None:
             L = ctx.size_Ql(chain_index)
-            t = ctx._empty(self.d_pad, L, ctx.N)
-            step = 4096
+            t = ctx._empty(self.d_pad * L * ctx.N)
+            step = min(self.d_pad, 256)
+            tmp = ctx._empty(step, L, ctx.N)
             for s0 in range(0, self.d_pad, step):
                 n = min(step, self.d_pad - s0)
-                ctx.native.expand_signed(self.coeffs[s0:s0 + n], n, t[s0:s0 + n], L)
-                ctx.native.ntt_forward(t[s0:s0 + n], n, L, 0)
+                ctx.native.expand_signed(self.coeffs[s0:s0 + n], n, tmp[:n], L)
+                ctx.native.ntt_forward(tmp[:n], n, L, 0)
+                ctx.native.bsgs_tile_plaintexts(chain_index, tmp[:n], n, t, s0, self.d_pad)
+            del tmp
             self._expanded[chain_index] = t
         return t
 
@@ -793,10 +799,9 @@ def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babi
     L = context.size_Ql(chain)
     P = diags.expanded(context, chain)
     partials = context._empty(G, 2, L, context.N)
-    step = L * context.N * 8  # bytes per plaintext; per partial ciphertext: 2 * step
-    base_p, base_o = P.data_ptr(), partials.data_ptr()
-    context.native.bsgs_mac(chain, [base_p + i * step for i in range(d_pad)], [c.data for c in babies],
-                            [base_o + g * 2 * step for g in range(G)])
+    step = 2 * L * context.N * 8  # bytes per partial ciphertext
+    base_o = partials.data_ptr()
+    context.native.bsgs_mac_tiled(chain, P, [c.data for c in babies], [base_o + g * step for g in range(G)])
     scale = x.scale() * diags.scale
     elt = get_elt_from_step(M, context.N)
     if G == 1 or elt in galois_key.keys:

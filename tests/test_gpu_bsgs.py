@@ -42,7 +42,7 @@ def add_mod(a, b, mods):
     return out
 
 
-@pytest.mark.parametrize("M,G,chain", [(5, 3, 1), (8, 1, 2), (1, 4, 1), (9, 2, 1)])
+@pytest.mark.parametrize("M,G,chain", [(5, 3, 1), (8, 1, 2), (1, 4, 1), (9, 2, 1), (3, 19, 1)])
 def test_bsgs_mac_matches_oracle(dev, M, G, chain):
     import pfa_native as P
 
@@ -68,6 +68,39 @@ def test_bsgs_mac_matches_oracle(dev, M, G, chain):
         assert np.array_equal(got, want), (g, first_mismatch(got, want))
 
 
+@pytest.mark.parametrize("M,G,chunk", [(4, 19, 7), (64, 2, 128), (1, 9, 9)])
+def test_bsgs_tiled_mac_equals_pointer_mac(dev, M, G, chunk):
+    """The tiled plaintext layout, filled in chunks, gives the same sums as the
+    pointer-list accumulation (and so as the oracle)."""
+    import pfa_native as P
+    import torch
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 50, 45, 60, 50, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    chain = 1
+    Ql = len(mods) - 1
+    rng = np.random.default_rng(M + G)
+    D = M * G
+    pts = to_dev(np.stack([uniform_limbs(rng, (Ql, N), mods[:Ql]) for _ in range(D)]), dev)
+    babies = [to_dev(uniform_limbs(rng, (2, Ql, N), mods[:Ql]), dev) for _ in range(M)]
+    tiled = empty((D * Ql * N,), dev)
+    for d0 in range(0, D, chunk):
+        n = min(chunk, D - d0)
+        ctx.bsgs_tile_plaintexts(chain, pts[d0:d0 + n], n, tiled, d0, D)
+    # the layout itself: limb j, span t of plaintext d at ((j T + t) D + d) 512
+    T = N // 512
+    view = tiled.view(Ql, T, D, 512)
+    d, j, t = D - 1, Ql - 1, T - 1
+    assert torch.equal(view[j, t, d], pts[d, j, t * 512:(t + 1) * 512])
+    want = [empty((2, Ql, N), dev) for _ in range(G)]
+    got = [empty((2, Ql, N), dev) for _ in range(G)]
+    ctx.bsgs_mac(chain, [pts[i] for i in range(D)], babies, want)
+    ctx.bsgs_mac_tiled(chain, tiled, babies, got)
+    for g in range(G):
+        assert torch.equal(got[g], want[g]), g
+
+
 def test_bsgs_mac_rejects_bad_arguments(dev):
     import pfa_native as P
 
@@ -79,6 +112,8 @@ def test_bsgs_mac_rejects_bad_arguments(dev):
         ctx.bsgs_mac(1, [x[0]], [x], [])  # no giants
     with pytest.raises(ValueError):
         ctx.bsgs_mac(5, [x[0]], [x], [x])  # chain index out of range
+    with pytest.raises(ValueError):
+        ctx.bsgs_tile_plaintexts(1, x[0], 2, x, 1, 2)  # positions past the set
     with pytest.raises(ValueError):
         ctx.bsgs_giants(2, x, 1, 1, None, x)  # rescale at the last level
     with pytest.raises(ValueError):
@@ -195,9 +230,7 @@ def test_bsgs_matmul_bit_exact_and_decodes(dev, M, G, rows, cols):
 
     # the native giant stage equals rotate / add / rescale_to_next on the same partials
     partials = ctx._empty(G, 2, L, ctx.N)
-    step = L * ctx.N * 8
-    ctx.native.bsgs_mac(1, [diags.expanded(ctx, 1).data_ptr() + i * step for i in range(d_pad)],
-                        [b.data for b in babies], [partials[g] for g in range(G)])
+    ctx.native.bsgs_mac_tiled(1, diags.expanded(ctx, 1), [b.data for b in babies], [partials[g] for g in range(G)])
     acc = x._like(partials[G - 1])
     for g in range(G - 2, -1, -1):
         acc = ph.add(ctx, ph.rotate(ctx, acc, M, glk), x._like(partials[g]))
