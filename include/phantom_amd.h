@@ -233,8 +233,10 @@ int pfa_bsgs_mac_tiled(const pfa_context *ctx, size_t chain_index, const uint64_
  * babies[b] = rotate(babies[b - msb(b)], msb(b)) for 1 <= b < M, each rotation
  * apply_galois_with_ksk (src/evaluate.cu:1607-1656) with the direct key.
  * ct [2][Ql][N] at chain_index; keys[k] is the Galois key of rotation step 2^k
- * ([key_dnum][2][QP][N]) for every 2^k < M; out receives babies 1 .. M-1 as
- * [M-1][2][Ql][N]. */
+ * ([key_dnum][2][QP][N]) for every 2^k < M; out receives all M babies as
+ * [M][2][Ql][N] (out[0] a copy of ct; ct may be out itself).  The babies with
+ * msb(b) = 2^k are independent, so each such level runs as one batched
+ * rotation. */
 int pfa_bsgs_babies(const pfa_context *ctx, size_t chain_index, const uint64_t *ct, size_t M,
                     const uint64_t *const *keys, size_t key_dnum, uint64_t *out, void *stream);
 
@@ -245,6 +247,16 @@ int pfa_bsgs_babies(const pfa_context *ctx, size_t chain_index, const uint64_t *
  * Galois key of `step` (unused when G = 1); out is [2][Ql-1][N]. */
 int pfa_bsgs_giants(const pfa_context *ctx, size_t chain_index, uint64_t *partials, size_t G, int step,
                     const uint64_t *key, size_t key_dnum, uint64_t *out, void *stream);
+
+/* bsgs_apply_giants_with_babies (src/bsgs.cu:216-357) over a tiled plaintext
+ * set (D = M*G, see pfa_bsgs_tile_plaintexts): the accumulation of every
+ * giant's partial (pfa_bsgs_mac_tiled), the Horner loop with rotation step M
+ * and the rescale (pfa_bsgs_giants), in one call.  babies: M ciphertexts
+ * [2][Ql][N]; key: the Galois key of step M (unused when G = 1); out
+ * [2][Ql-1][N].  Temporaries: G ciphertexts of workspace. */
+int pfa_bsgs_apply_giants(const pfa_context *ctx, size_t chain_index, const uint64_t *tiled,
+                          const uint64_t *const *babies, size_t M, size_t G, const uint64_t *key, size_t key_dnum,
+                          uint64_t *out, void *stream);
 
 #ifdef __cplusplus
 }

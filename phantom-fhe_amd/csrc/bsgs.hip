@@ -57,6 +57,7 @@ struct MacArgs {
     const uint64_t *const *baby_table;          // [M] ciphertexts [2][Ql][N], when M > kInlineBabies
     const uint64_t *baby_inline[kInlineBabies];  // the same, by value, when M <= kInlineBabies
     uint32_t M, G, Ql, N;
+    uint32_t gb_begin, gb_end;  // giant blocks [gb_begin, gb_end) of kGB giants this launch covers
     __device__ __forceinline__ const uint64_t *baby(uint32_t b) const {
         return baby_table ? baby_table[b] : baby_inline[b];
     }
@@ -85,12 +86,13 @@ constexpr uint32_t kGB = 8;
 __global__ void __launch_bounds__(kThreads)
 k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
     const uint32_t T = a.N / kSpan;               // spans per limb
-    const uint32_t GB = (a.G + kGB - 1) / kGB;    // giant blocks
+    const uint32_t GB = a.gb_end - a.gb_begin;    // giant blocks of this launch
     const uint32_t groups = a.Ql * T;
     const uint32_t total = grouped_total(groups, GB);
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
         uint32_t grp, gb;
         if (!grouped_item(w, groups, GB, grp, gb)) continue;
+        gb += a.gb_begin;
         const uint32_t j = grp / T, tile = grp % T;
         const size_t off0 = (size_t)j * a.N + tile * kSpan + kPer * threadIdx.x;
         const size_t off1 = off0 + (size_t)a.Ql * a.N;
@@ -218,54 +220,61 @@ k_bsgs_tile(const uint64_t *src, uint64_t *tiled, uint32_t Ql, uint32_t N, uint3
     for (uint32_t i = threadIdx.x; i < kSpan; i += kThreads) st_stream(o + i, ld_stream(s + i));
 }
 
-// Both polys of a ciphertext through the Galois permutation of NTT slots
-// (apply_galois_ntt_permutation, src/galois.cu:11-18):
-//   dst[k][l][i] = src[k][l][pi(i)]  (+ add0[l][i] for k = 0 when add0 is given).
+// Both polys of B ciphertexts through the Galois permutation of NTT slots
+// (apply_galois_ntt_permutation, src/galois.cu:11-18): ciphertext i of src
+// (stride src_stride) -> ciphertext i of dst (contiguous [B][2][L][N]),
+//   dst[i][k][l][n] = src[i][k][l][pi(n)]  (+ add0[l][n] for k = 0 when add0 is given, B = 1).
 __global__ void __launch_bounds__(kThreads)
-k_galois_ct(const uint64_t *src, uint64_t *dst, const uint64_t *add0, const uint64_t *mod, uint32_t elt, uint32_t L,
-            uint32_t N, uint32_t logN) {
-    const uint32_t l = blockIdx.y, k = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+k_galois_ct(const uint64_t *src, uint64_t src_stride, uint64_t *dst, const uint64_t *add0, const uint64_t *mod,
+            uint32_t elt, uint32_t L, uint32_t N, uint32_t logN) {
+    const uint32_t l = blockIdx.y, k = blockIdx.z & 1u, i = blockIdx.z >> 1, n = blockIdx.x * kThreads + threadIdx.x;
     const size_t row = ((size_t)k * L + l) * N;
-    uint64_t v = src[row + galois_perm(elt, n, logN)];
+    uint64_t v = src[i * src_stride + row + galois_perm(elt, n, logN)];
     if (k == 0 && add0) v = add_mod(v, add0[(size_t)l * N + n], mod[l]);
-    st_stream(dst + row + n, v);
+    st_stream(dst + (size_t)i * 2 * L * N + row + n, v);
 }
 
-// out = rotate(src) (+ add): the Galois permutation of both polys, then the
-// key switch of the permuted c1 whose ModDown epilogue adds the permuted c0
-// (and add[0]) to poly 0 and add[1] to poly 1 -- apply_galois_with_ksk
-// (src/evaluate.cu:1607-1656) followed by add_inplace, with the same residues.
-// out must not alias src; add[1] may alias out's poly 1.
-void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint32_t elt, const uint64_t *key,
-                 const uint64_t *add, uint64_t *out, hipStream_t s) {
+// out[i] = rotate(src[i]) for B ciphertexts with one key (+ add, B = 1): the
+// Galois permutation of both polys, then the key switch of the permuted c1s
+// whose ModDown epilogue adds the permuted c0 (and add[0]) to poly 0 and
+// add[1] to poly 1 -- apply_galois_with_ksk (src/evaluate.cu:1607-1656),
+// followed by add_inplace, with the same residues.  src[i] is at
+// src + i src_stride, out is contiguous [B][2][Ql][N] and must not overlap
+// src; add[1] may alias out's poly 1.
+void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src_stride, uint32_t B, uint32_t elt,
+                 const uint64_t *key, const uint64_t *add, uint64_t *out, hipStream_t s) {
     const uint32_t Ql = c.size_Ql(chain), QlP = Ql + c.P;
-    const size_t LN = (size_t)Ql * c.N;
+    const uint64_t LN = (uint64_t)Ql * c.N;
+    require(B >= 1 && B <= 32767 && (B == 1 || add == nullptr), "bad rotation batch");
     Scratch sc(c, s);
-    uint64_t *t = sc.alloc(2 * LN);
-    hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2), dim3(kThreads), 0, s, src, t, add, c.mod, elt, Ql,
-                       c.N, c.logN);
+    uint64_t *t = sc.alloc((size_t)B * 2 * LN);
+    hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2 * B), dim3(kThreads), 0, s, src, src_stride, t, add,
+                       c.mod, elt, Ql, c.N, c.logN);
     PFA_HIP(hipGetLastError());
-    uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
-    fused_modup_inner(c, chain, t + LN, key, cx, s);
-    fused_moddown(c, chain, cx, 2, out, t, add ? add + LN : nullptr, s);
+    uint64_t *cx = sc.alloc((size_t)B * 2 * QlP * c.N);
+    fused_modup_inner(c, chain, t + LN, key, cx, s, B, 2 * LN, (uint64_t)2 * QlP * c.N);
+    fused_moddown(c, chain, cx, 2 * B, out, t, add ? add + LN : nullptr, s, 2 * LN);
 }
 
-// One accumulation launch: plaintexts from the pointer list pts or the tiled set.
-void launch_mac(const Ctx &c, size_t chain_index, const uint64_t *const *pts, const uint64_t *tiled,
-                const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, hipStream_t s) {
+// Accumulation arguments: plaintexts from the pointer list pts or the tiled
+// set, pointer tables (when a list is not an arithmetic progression) copied to
+// workspace memory on stream s.
+MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, const uint64_t *tiled,
+                 const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, Scratch &sc,
+                 hipStream_t s) {
     require(babies && out, "null argument");
     require(M >= 1 && G >= 1, "need at least one baby step and one giant step");
     require(M * G < (1u << 24), "too many plaintexts");
     if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
     for (size_t i = 0; i < M; i++) require(babies[i] != nullptr, "null ciphertext pointer");
     for (size_t i = 0; i < G; i++) require(out[i] != nullptr, "null output pointer");
-    const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
-    Scratch sc(c, s);
     MacArgs a{};
     a.M = (uint32_t)M;
     a.G = (uint32_t)G;
-    a.Ql = Ql;
+    a.Ql = c.size_Ql((uint32_t)chain_index);
     a.N = c.N;
+    a.gb_begin = 0;
+    a.gb_end = ((uint32_t)G + kGB - 1) / kGB;
     // a list whose addresses step by a constant multiple of 8 bytes goes as base + stride
     auto progression = [](const void *const *v, size_t n, uint64_t &stride) {
         const uintptr_t b0 = (uintptr_t)v[0];
@@ -301,8 +310,13 @@ void launch_mac(const Ctx &c, size_t chain_index, const uint64_t *const *pts, co
         PFA_HIP(hipMemcpyAsync(t, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
         a.baby_table = t;
     }
-    const uint32_t total = grouped_total(Ql * (c.N / kSpan), ((uint32_t)G + kGB - 1) / kGB);
-    const uint32_t cap = (uint32_t)c.n_cu * 4u;  // resident workgroups (4 waves per SIMD)
+    return a;
+}
+
+// one launch over giant blocks [a.gb_begin, a.gb_end), at most wpc workgroups per CU
+void launch_mac(const Ctx &c, const MacArgs &a, uint32_t wpc, hipStream_t s) {
+    const uint32_t total = grouped_total(a.Ql * (c.N / kSpan), a.gb_end - a.gb_begin);
+    const uint32_t cap = (uint32_t)c.n_cu * wpc;
     hipLaunchKernelGGL(k_bsgs_mac, dim3(total < cap ? total : cap), dim3(kThreads), 0, s, a, c.mod, c.ratio);
     PFA_HIP(hipGetLastError());
 }
@@ -331,7 +345,11 @@ int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *con
     return guarded([&] {
         require(pts != nullptr, "null argument");
         for (size_t i = 0; i < M * G; i++) require(pts[i] != nullptr, "null plaintext pointer");
-        launch_mac(*ctx_of(ctx), chain_index, pts, nullptr, babies, M, G, out, as_stream(stream));
+        const Ctx &c = *ctx_of(ctx);
+        const hipStream_t s = as_stream(stream);
+        Scratch sc(c, s);
+        // 4 resident workgroups per CU (119 VGPRs: 4 waves per SIMD)
+        launch_mac(c, mac_args(c, chain_index, pts, nullptr, babies, M, G, out, sc, s), 4, s);
     });
 }
 
@@ -339,7 +357,10 @@ int pfa_bsgs_mac_tiled(const pfa_context *ctx, size_t chain_index, const uint64_
                        const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream) {
     return guarded([&] {
         require(tiled != nullptr, "null argument");
-        launch_mac(*ctx_of(ctx), chain_index, nullptr, tiled, babies, M, G, out, as_stream(stream));
+        const Ctx &c = *ctx_of(ctx);
+        const hipStream_t s = as_stream(stream);
+        Scratch sc(c, s);
+        launch_mac(c, mac_args(c, chain_index, nullptr, tiled, babies, M, G, out, sc, s), 4, s);
     });
 }
 
@@ -371,14 +392,17 @@ int pfa_bsgs_babies(const pfa_context *ctx, size_t chain_index, const uint64_t *
             elts.push_back(rotation_elt(c, (int)bit));
         }
         const hipStream_t s = as_stream(stream);
-        const size_t ct_elems = (size_t)2 * c.size_Ql(chain) * c.N;
-        // babies[b] = rotate(babies[b - msb(b)], msb(b)); babies[0] = ct, babies[b] = out[b - 1]
-        for (size_t b = 1; b < M; b++) {
-            uint32_t k = 0;
-            while ((size_t)2 << k <= b) k++;
-            const size_t rem = b - ((size_t)1 << k);
-            const uint64_t *src = rem ? out + (rem - 1) * ct_elems : ct;
-            rotate_into(c, chain, src, elts[k], keys[k], nullptr, out + (b - 1) * ct_elems, s);
+        const uint64_t ct_elems = (uint64_t)2 * c.size_Ql(chain) * c.N;
+        if (out != ct) PFA_HIP(hipMemcpyAsync(out, ct, ct_elems * 8, hipMemcpyDeviceToDevice, s));
+        // babies[b] = rotate(babies[b - msb(b)], msb(b)): the babies with msb(b) = 2^k
+        // are one rotation by 2^k of babies 0 .. 2^k - 1, run as one batch
+        for (size_t bit = 1, k = 0; bit < M; bit <<= 1, k++) {
+            const size_t B = std::min(bit, M - bit);
+            for (size_t b0 = 0; b0 < B; b0 += 32767) {
+                const size_t n = std::min<size_t>(32767, B - b0);
+                rotate_into(c, chain, out + b0 * ct_elems, ct_elems, (uint32_t)n, elts[k], keys[k], nullptr,
+                            out + (bit + b0) * ct_elems, s);
+            }
         }
     });
 }
@@ -399,7 +423,38 @@ int pfa_bsgs_giants(const pfa_context *ctx, size_t chain_index, uint64_t *partia
         // Horner from the last giant: partial[g] <- rotate(partial[g + 1], step) + partial[g]
         for (size_t g = G - 1; g-- > 0;) {
             uint64_t *pg = partials + g * ct_elems;
-            rotate_into(c, chain, pg + ct_elems, elt, key, pg, pg, s);
+            rotate_into(c, chain, pg + ct_elems, 0, 1, elt, key, pg, pg, s);
+        }
+        fused_rescale(c, chain, partials, 2, out, s);
+    });
+}
+
+int pfa_bsgs_apply_giants(const pfa_context *ctx, size_t chain_index, const uint64_t *tiled,
+                          const uint64_t *const *babies, size_t M, size_t G, const uint64_t *key, size_t key_dnum,
+                          uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(tiled && out, "null argument");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        const uint32_t chain = (uint32_t)chain_index;
+        require(c.size_Ql(chain) >= 2, "cannot rescale at the last level");
+        require(M <= (size_t)INT32_MAX, "baby step count out of range");
+        const uint32_t elt = G > 1 ? rotation_elt(c, (int)M) : 0;
+        if (G > 1) check_key(c, chain, key, key_dnum);
+        const hipStream_t s = as_stream(stream);
+        const uint64_t ct_elems = (uint64_t)2 * c.size_Ql(chain) * c.N;
+        Scratch sc(c, s);
+        uint64_t *partials = G >= 1 ? sc.alloc((size_t)G * ct_elems) : nullptr;
+        std::vector<uint64_t *> outs(G);
+        for (size_t g = 0; g < G; g++) outs[g] = partials + g * ct_elems;
+        // Every partial in one launch, then the Horner loop.  (Running the
+        // accumulation in giant blocks on a second stream, overlapped with the
+        // Horner steps, measured no faster: both halves slowed down ~2x.)
+        launch_mac(c, mac_args(c, chain_index, nullptr, tiled, babies, M, G, outs.data(), sc, s), 4, s);
+        // Horner from the last giant: partial[g] <- rotate(partial[g + 1], M) + partial[g]
+        for (size_t g = G - 1; g-- > 0;) {
+            uint64_t *pg = partials + g * ct_elems;
+            rotate_into(c, chain, pg + ct_elems, 0, 1, elt, key, pg, pg, s);
         }
         fused_rescale(c, chain, partials, 2, out, s);
     });

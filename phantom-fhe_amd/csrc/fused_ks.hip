@@ -64,6 +64,9 @@ struct BconvCols {
     uint64_t *out;          // output limbs; job (g, j) writes out + g * out_gstride + j * N
     const ulonglong2 *bc;   // factor pairs [(m, m 2^32) in the target's policy]: see bc_of
     uint64_t in_gstride, out_gstride;
+    // independent conversions of the same shape: member i adds i * in_bstride / out_bstride
+    uint32_t batch = 1;
+    uint64_t in_bstride = 0, out_bstride = 0;
     uint32_t groups;        // output polys (digits for ModUp, polys for ModDown / rescale)
     uint32_t J;             // target limbs per group (positions 0 .. J-1)
     uint32_t n_in;          // input limbs per group (<= alpha; the last ModUp digit may be short)
@@ -85,13 +88,13 @@ __device__ __forceinline__ const ulonglong2 *bc_of(const BconvCols &a, uint32_t 
 }
 
 template <class A, int S1, int S2>
-__device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables &t, const A &ar, uint32_t g,
-                                             uint32_t j, uint32_t tile, typename A::T (&x)[Sub<S1>::E]) {
+__device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables &t, const A &ar, uint32_t mi,
+                                             uint32_t g, uint32_t j, uint32_t tile, typename A::T (&x)[Sub<S1>::E]) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     const uint32_t n_in = g + 1 == a.groups ? a.n_in_last : a.n_in;
-    const uint64_t *base = a.in + (size_t)g * a.in_gstride + tile * kCols + c;
+    const uint64_t *base = a.in + (size_t)mi * a.in_bstride + (size_t)g * a.in_gstride + tile * kCols + c;
     const uint32_t row0 = a.in_row0 + g * a.in_row_step;
     if constexpr (A::kF64) {
         double acc[SB::E];
@@ -150,26 +153,27 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     __shared__ double lds[G::COL_LDS];
-    const uint32_t NG = a.groups * G::COL_TILES;
+    const uint32_t NG = a.batch * a.groups * G::COL_TILES;
     const uint32_t total = grouped_total(NG, a.J);
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
         uint32_t gt, j;
         if (!grouped_item(w, NG, a.J, gt, j)) continue;
-        const uint32_t g = gt / G::COL_TILES, tile = gt % G::COL_TILES;
+        const uint32_t mg = gt / G::COL_TILES, tile = gt % G::COL_TILES;
+        const uint32_t mi = mg / a.groups, g = mg % a.groups;
         if (a.skip && j >= g * a.n_in && j < g * a.n_in + (g + 1 == a.groups ? a.n_in_last : a.n_in)) continue;
         const uint32_t prow = j < a.split ? j : a.split_base + (j - a.split);
         const uint64_t q = t.mod[prow];
-        uint64_t *olimb = a.out + (size_t)g * a.out_gstride + (size_t)j * G::N;
+        uint64_t *olimb = a.out + (size_t)mi * a.out_bstride + (size_t)g * a.out_gstride + (size_t)j * G::N;
         if (q < kF64PrimeBound) {
             const ArithF64 ar(q);
             double x[SB::E];
-            bconv_source<ArithF64, S1, S2>(a, t, ar, g, j, tile, x);
+            bconv_source<ArithF64, S1, S2>(a, t, ar, mi, g, j, tile, x);
             fwd_cols_core<ArithF64, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, lds);
             fwd_cols_store<ArithF64, S1, S2>(x, ar, tile, olimb);
         } else {
             const ArithInt ar(q);
             uint64_t x[SB::E];
-            bconv_source<ArithInt, S1, S2>(a, t, ar, g, j, tile, x);
+            bconv_source<ArithInt, S1, S2>(a, t, ar, mi, g, j, tile, x);
             fwd_cols_core<ArithInt, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, reinterpret_cast<uint64_t *>(lds));
             fwd_cols_store<ArithInt, S1, S2>(x, ar, tile, olimb);
         }
@@ -185,6 +189,9 @@ struct InnerRows {
     uint64_t *cx;           // [2][QlP][N]
     const ulonglong2 *ratio;
     uint32_t Ql, QlP, alpha, beta, Q, QP;
+    // independent key switches with the same key: member i adds i * the stride
+    uint32_t batch = 1;
+    uint64_t inter_bstride = 0, c2_bstride = 0, cx_bstride = 0;
 };
 
 // Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
@@ -408,15 +415,21 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
 }
 
 template <int S1, int S2>
-__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a, NttTables t) {
+__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a0, NttTables t) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
     __shared__ double lds[W::LDS + 2 * W::TW];
     ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + W::LDS);
     const bool transform = threadIdx.x < W::HALF;
     const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
-    const uint32_t total = a.QlP * W::TILES;
-    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+    const uint32_t per = a0.QlP * W::TILES;
+    const uint32_t total = a0.batch * per;
+    for (uint32_t w0 = blockIdx.x; w0 < total; w0 += gridDim.x) {
+        const uint32_t mi = w0 / per, w = w0 % per;
+        InnerRows a = a0;
+        a.inter += mi * a0.inter_bstride;
+        a.c2 += mi * a0.c2_bstride;
+        a.cx += mi * a0.cx_bstride;
         const uint32_t r = w / W::TILES, tile = w % W::TILES;
         const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
         const uint64_t q = wave_uniform(t.mod[prow]);
@@ -452,11 +465,12 @@ __global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows
 struct EpiRows {
     const uint64_t *inter;  // [M][J][N] columns-pass output
     const uint64_t *c;      // [M][..][N], poly stride c_stride
-    const uint64_t *base0, *base1;  // [J][N] each, or null
+    const uint64_t *base0, *base1;  // [J][N] each, or null: polys 2i and 2i+1 add base0/base1 + i base_stride
     uint64_t *out;          // [M][J][N]
     const ulonglong2 *f;    // [J] pairs in each limb's NTT policy
     uint64_t c_stride;
     uint32_t M, J;
+    uint64_t base_stride = 0;
 };
 
 template <class A, int S1, int S2>
@@ -473,8 +487,8 @@ __device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, c
     for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(ld_stream(&a.inter[lo + SB::T * e]));
     fwd_rows_core<A, S1, S2>(x, ar, t, j, k1, lr);
     const uint64_t *cp = a.c + m * a.c_stride + (size_t)j * G::N + rowoff;
-    const uint64_t *bp = m == 0 ? a.base0 : a.base1;
-    if (bp) bp += (size_t)j * G::N + rowoff;
+    const uint64_t *bp = (m & 1u) ? a.base1 : a.base0;
+    if (bp) bp += (size_t)(m >> 1) * a.base_stride + (size_t)j * G::N + rowoff;
     const ulonglong2 f = a.f[j];
     uint64_t *op = a.out + lo;
 #pragma unroll
@@ -529,7 +543,7 @@ uint32_t fgrid(const Ctx &c, uint32_t items, uint32_t wpc) {
 template <int S1, int S2>
 void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
     using G = Geo<S1, S2>;
-    const uint32_t total = grouped_total(a.groups * G::COL_TILES, a.J);
+    const uint32_t total = grouped_total(a.batch * a.groups * G::COL_TILES, a.J);
     hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
                        tables_of(c));
     PFA_HIP(hipGetLastError());
@@ -538,7 +552,7 @@ void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
 template <int S1, int S2>
 void launch_inner(const Ctx &c, const InnerRows &a, hipStream_t s) {
     using W = WsGeo<S1, S2>;
-    hipLaunchKernelGGL((k_inner_ws<S1, S2>), dim3(fgrid(c, a.QlP * W::TILES, 4)), dim3(W::THREADS), 0, s, a,
+    hipLaunchKernelGGL((k_inner_ws<S1, S2>), dim3(fgrid(c, a.batch * a.QlP * W::TILES, 4)), dim3(W::THREADS), 0, s, a,
                        tables_of(c));
     PFA_HIP(hipGetLastError());
 }
@@ -569,13 +583,14 @@ void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp and the key-switch inner
 // product against key [dnum][2][QP][N].
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s) {
+                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride) {
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    const uint64_t LN = (uint64_t)Ql * c.N, IN = (uint64_t)lv.beta * QlP * c.N;
     Scratch sc(c, s);
-    uint64_t *tin = sc.alloc((size_t)Ql * c.N);
-    uint64_t *inter = sc.alloc((size_t)lv.beta * QlP * c.N);
-    NttLaunch inv{c2, tin, 0, 0, 1, Ql};
+    uint64_t *tin = sc.alloc((size_t)batch * LN);
+    uint64_t *inter = sc.alloc((size_t)batch * IN);
+    NttLaunch inv{c2, tin, c2_stride, LN, batch, Ql};
     inv.scale = lv.modup_scale;
     ntt_inverse(c, inv, s);
     BconvCols b{};
@@ -595,14 +610,22 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.skip = 1;
     b.bc_gstride = 2 * alpha * QlP;
     b.bc_istride = QlP;
+    b.batch = batch;
+    b.in_bstride = LN;
+    b.out_bstride = IN;
     PFA_FUSED_DISPATCH(launch_bconv, b);
     InnerRows r{inter, c2, key, cx, c.ratio, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
+    r.batch = batch;
+    r.inter_bstride = IN;
+    r.c2_bstride = c2_stride;
+    r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
     PFA_FUSED_DISPATCH(launch_inner, r);
 }
 
-// cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx)  (base[m] may alias out[m] or be null)
+// cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx): poly 2i + k adds
+// base_k + i base_stride (base_k may alias out's polys or be null)
 void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,
-                   const uint64_t *base0, const uint64_t *base1, hipStream_t s) {
+                   const uint64_t *base0, const uint64_t *base1, hipStream_t s, uint64_t base_stride) {
     const uint32_t Ql = c.size_Ql(chain), alpha = c.P, QlP = Ql + alpha;
     Scratch sc(c, s);
     uint64_t *xP = sc.alloc((size_t)M * alpha * c.N);
@@ -630,6 +653,7 @@ void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M,
     b.bc_istride = c.Q;
     PFA_FUSED_DISPATCH(launch_bconv, b);
     EpiRows e{inter, cx, base0, base1, out, c.pinv_p, (uint64_t)QlP * c.N, M, Ql};
+    e.base_stride = base_stride;
     PFA_FUSED_DISPATCH(launch_epi, e);
 }
 

@@ -192,11 +192,14 @@ bool xcd_round_robin(const Ctx &c);
 
 // Fused key-switching / rescale pipelines (fused_ks.hip).
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp then the inner product with key.
+// With batch > 1, member i reads c2 + i c2_stride and writes cx + i cx_stride
+// (default 2 QlP N), all with the same key.
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s);
-// cx [M][QlP][N] -> out [M][Ql][N] = base_m + ModDown(cx_m); base_m may alias out_m or be null.
+                       hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0);
+// cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx): poly 2i + k adds
+// base_k + i base_stride; the bases may alias out's polys or be null.
 void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,
-                   const uint64_t *base0, const uint64_t *base1, hipStream_t s);
+                   const uint64_t *base0, const uint64_t *base1, hipStream_t s, uint64_t base_stride = 0);
 // in [size][Ql][N] -> out [size][Ql-1][N]: floor division by the level's last prime.
 void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s);
 

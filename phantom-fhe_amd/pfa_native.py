@@ -61,6 +61,7 @@ SIGNATURES = {
     "pfa_bsgs_mac_tiled": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
     "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
+    "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
 }
 
 
@@ -322,8 +323,8 @@ class NativeContext:
         call("pfa_bsgs_mac_tiled", self._h, chain_index, ptr(tiled), bp, M, G, op, stream or stream_of(tiled))
 
     def bsgs_babies(self, chain_index, ct, M, keys, out, stream=None):
-        """out[b - 1] = babies[b] for 1 <= b < M (chained power-of-two rotations of
-        ct); keys[k] is the Galois key of step 2^k for every 2^k < M."""
+        """out[b] = babies[b] for 0 <= b < M (out[0] = ct, then chained
+        power-of-two rotations); keys[k] is the Galois key of step 2^k for every 2^k < M."""
         kp = (C.c_void_p * max(len(keys), 1))(*[ptr(k) for k in keys])
         dnum = keys[0].shape[0] if keys else 0
         call("pfa_bsgs_babies", self._h, chain_index, ptr(ct), M, kp, dnum, ptr(out), stream or stream_of(ct))
@@ -332,6 +333,16 @@ class NativeContext:
         """Horner over the giant partials (overwritten) with rotation `step`, then rescale into out."""
         call("pfa_bsgs_giants", self._h, chain_index, ptr(partials), G, step, ptr(key) if key is not None else None,
              key.shape[0] if key is not None else 0, ptr(out), stream or stream_of(partials))
+
+    def bsgs_apply_giants(self, chain_index, tiled, babies, G, key, out, stream=None):
+        """Accumulation of the G giants' partials (tiled plaintext set), Horner
+        rotations by M = len(babies) and the rescale into out [2][Ql-1][N]."""
+        M = len(babies)
+        addr = lambda t: t if isinstance(t, int) else ptr(t)
+        bp = (C.c_void_p * M)(*[addr(t) for t in babies])
+        call("pfa_bsgs_apply_giants", self._h, chain_index, ptr(tiled), bp, M, G,
+             ptr(key) if key is not None else None, key.shape[0] if key is not None else 0, ptr(out),
+             stream or stream_of(tiled))
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

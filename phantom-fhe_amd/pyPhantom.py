@@ -771,9 +771,9 @@ def compute_bsgs_babies(context: context, galois_key: galois_key, x: ciphertext,
         return [x]
     if all(e in galois_key.keys for e in elts):
         # every rotation has its direct key: the whole chain runs in one native call
-        out = context._empty(baby_steps - 1, 2, context.size_Ql(x.chain_index()), context.N)
+        out = context._empty(baby_steps, 2, context.size_Ql(x.chain_index()), context.N)
         context.native.bsgs_babies(x.chain_index(), x.data, baby_steps, [galois_key.get(e) for e in elts], out)
-        return [x] + [x._like(out[b]) for b in range(baby_steps - 1)]
+        return [x] + [x._like(out[b]) for b in range(1, baby_steps)]
     babies = [x]
     for b in range(1, baby_steps):
         bit = 1 << (b.bit_length() - 1)
@@ -798,18 +798,20 @@ def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babi
             raise ValueError("babies must be size-2 ciphertexts at one chain index")
     L = context.size_Ql(chain)
     P = diags.expanded(context, chain)
+    elt = get_elt_from_step(M, context.N)
+    if G == 1 or elt in galois_key.keys:
+        # accumulation, Horner rotations and rescale in one native call
+        if L < 2:
+            raise ValueError("end of modulus switching chain reached")
+        out = context._empty(2, L - 1, context.N)
+        context.native.bsgs_apply_giants(chain, P, [c.data for c in babies], G,
+                                         galois_key.get(elt) if G > 1 else None, out)
+        return x._like(out, chain=chain + 1)
     partials = context._empty(G, 2, L, context.N)
     step = 2 * L * context.N * 8  # bytes per partial ciphertext
     base_o = partials.data_ptr()
     context.native.bsgs_mac_tiled(chain, P, [c.data for c in babies], [base_o + g * step for g in range(G)])
     scale = x.scale() * diags.scale
-    elt = get_elt_from_step(M, context.N)
-    if G == 1 or elt in galois_key.keys:
-        if L < 2:
-            raise ValueError("end of modulus switching chain reached")
-        out = context._empty(2, L - 1, context.N)
-        context.native.bsgs_giants(chain, partials, G, M, galois_key.get(elt) if G > 1 else None, out)
-        return x._like(out, chain=chain + 1)
     acc = x._like(partials[G - 1], scale=scale)
     for g in range(G - 2, -1, -1):
         acc = rotate(context, acc, M, galois_key)

@@ -119,9 +119,13 @@ def test_bsgs_mac_rejects_bad_arguments(dev):
     with pytest.raises(ValueError):
         ctx.bsgs_giants(1, x, 2, 1, None, x)  # a rotation without a key
     with pytest.raises(ValueError):
-        ctx.bsgs_babies(1, x, 2, [empty((0, 2, 3, N), dev)], x)  # key without digits
+        ctx.bsgs_babies(1, x, 2, [empty((0, 2, 3, N), dev)], empty((2, 2, 2, N), dev))  # key without digits
     with pytest.raises(ValueError):
         ctx.bsgs_babies(3, x, 2, [x], x)  # chain index out of range
+    with pytest.raises(ValueError):
+        ctx.bsgs_apply_giants(1, x, [x], 2, None, x)  # a rotation without a key
+    with pytest.raises(ValueError):
+        ctx.bsgs_apply_giants(2, x, [x], 1, None, x)  # rescale at the last level
 
 
 def test_single_chain_encode_expand_equals_encode(dev):
@@ -235,6 +239,11 @@ def test_bsgs_matmul_bit_exact_and_decodes(dev, M, G, rows, cols):
     for g in range(G - 2, -1, -1):
         acc = ph.add(ctx, ph.rotate(ctx, acc, M, glk), x._like(partials[g]))
     assert torch.equal(ph.rescale_to_next(ctx, acc).data, y.data)
+    # and so does the Horner-only entry point on the same partials
+    out = ctx._empty(2, L - 1, ctx.N)
+    key = glk.get(ph.get_elt_from_step(M, ctx.N)) if G > 1 else None
+    ctx.native.bsgs_giants(1, partials, G, M, key, out)
+    assert torch.equal(out, y.data)
 
 
 def test_bsgs_argument_checks(dev):
