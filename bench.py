@@ -207,10 +207,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-hmult", action="store_true")
     ap.add_argument("--no-bsgs", action="store_true")
-    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "bsgs"], default="full",
+    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "hmult35", "bsgs"], default="full",
                     help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
                          "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
-                         "config-3 HMult + relin + rescale; bsgs: only the config-4 matrix-vector product")
+                         "config-3 HMult + relin + rescale; hmult35: only the L=35 variant; bsgs: only the "
+                         "config-4 matrix-vector product")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -237,6 +238,11 @@ def main():
         del batches
         r = time_hmult(torch, P, dev, gen, 24, 4, args.steps, args.warmup)
         log(f"bench: hmult mode, config 3: {r['ms']} ms")
+        return
+    if args.mode == "hmult35":
+        del batches
+        r = time_hmult(torch, P, dev, gen, 35, 1, args.steps, args.warmup)
+        log(f"bench: hmult35 mode, L=35: {r['ms']} ms")
         return
     if args.mode == "copy":
         dst = torch.empty_like(batches[0])

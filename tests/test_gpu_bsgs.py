@@ -42,7 +42,7 @@ def add_mod(a, b, mods):
     return out
 
 
-@pytest.mark.parametrize("M,G,chain", [(5, 3, 1), (8, 1, 2), (1, 4, 1), (9, 2, 1), (3, 19, 1)])
+@pytest.mark.parametrize("M,G,chain", [(5, 3, 1), (8, 1, 2), (1, 4, 1), (9, 2, 1), (3, 19, 1), (70, 2, 1)])
 def test_bsgs_mac_matches_oracle(dev, M, G, chain):
     import pfa_native as P
 
@@ -244,6 +244,29 @@ def test_bsgs_matmul_bit_exact_and_decodes(dev, M, G, rows, cols):
     key = glk.get(ph.get_elt_from_step(M, ctx.N)) if G > 1 else None
     ctx.native.bsgs_giants(1, partials, G, M, key, out)
     assert torch.equal(out, y.data)
+
+
+@pytest.mark.parametrize("M", [6, 70])
+def test_bsgs_babies_any_count(dev, M):
+    """compute_bsgs_babies for baby counts that are not powers of two and above
+    the 64 babies passed by value (the reference takes any count,
+    src/bsgs.cu:194-214): the batched native chain equals rotate() one step
+    at a time."""
+    import torch
+
+    steps = [1 << k for k in range((M - 1).bit_length())]
+    ph, ctx = make_ctx(12, [60, 40, 40, 60], 1, steps=steps)
+    ph.set_seed(5)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 64)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(M)
+    x = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, rng.uniform(-1, 1, enc.slot_count()), 2.0 ** 40))
+    babies = ph.compute_bsgs_babies(ctx, glk, x, M)
+    assert len(babies) == M and babies[0] is x
+    for b in range(1, M):
+        bit = 1 << (b.bit_length() - 1)
+        assert torch.equal(babies[b].data, ph.rotate(ctx, babies[b - bit], bit, glk).data), b
 
 
 def test_bsgs_argument_checks(dev):
