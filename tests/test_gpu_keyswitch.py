@@ -147,6 +147,22 @@ def test_multiply_and_relin(dev, logN, nq, alpha, chain):
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("alias", ["a", "b", "ab"])
+def test_multiply_and_relin_in_place(dev, alias):
+    """multiply_and_relin in place (out aliasing a, b or both): the tensor
+    product is formed before the key switch overwrites out, so the residues
+    equal the oracle's."""
+    st = Setup(12, 6, 2, seed=8)
+    a, b = st.ct(1), st.ct(1)
+    key = st.key()
+    da = to_dev(a, dev)
+    db = da if alias == "ab" else to_dev(b, dev)
+    out = db if alias == "b" else da
+    st.ctx.multiply_and_relin(1, da, db, to_dev(key, dev), out)
+    got, want = to_host(out), st.orc.multiply_and_relin(1, a, a if alias == "ab" else b, key, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
 def test_multiply_and_relin_config3(dev):
     """BASELINE config 3 shape: N = 2^16, chain {60, 50 x 23, 60 x 4}: |Q| = 24,
     alpha = 4, dnum = beta = 6, fresh ciphertexts at chain index 1."""
