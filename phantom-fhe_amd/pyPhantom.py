@@ -673,7 +673,7 @@ class bsgs_diagonals:
     include/single_chain_plaintext.h:37-40).  Their NTT-form expansion at a
     chain index is built on first use and kept on the device (d_pad x |Ql| limbs,
     40 GiB at d_pad 4096, |Ql| 20, N 2^16), where the reference re-expands the
-    plaintexts of every giant on every product (src/bsgs.cu:245-271)."""
+    plaintexts of every giant on every product (src/bsgs.cu:276-312)."""
 
     def __init__(self, coeffs, scale: float, d_pad: int, baby_steps: int):
         self.coeffs = coeffs  # int64 device tensor [d_pad][N]
@@ -711,12 +711,35 @@ def _is_pow2(x: int) -> bool:
     return x > 0 and (x & (x - 1)) == 0
 
 
+def _encode_bsgs_diagonals(context: context, encoder: ckks_encoder, rows, d_pad: int, baby_steps: int,
+                           scale: float) -> bsgs_diagonals:
+    """Shared tail of the pre-encoders (src/bsgs.cu:133-176, :465-513): with the
+    matrix `rows` (complex, shape [num_rows][num_cols]) diag[d][t] =
+    rows[t][(t + d) mod d_pad] (zero outside), diagonal g * M + b rotated right by
+    g * M, tiled over the slots with period d_pad and encoded at `scale` as a
+    single-chain plaintext."""
+    t = _torch()
+    num_rows, num_cols = rows.shape
+    r = np.arange(num_rows)[:, None]
+    j = (r + np.arange(d_pad)[None, :]) % d_pad  # [t][d]
+    vals = np.where(j < num_cols, rows[r, np.minimum(j, num_cols - 1)], 0.0)
+    diag = np.zeros((d_pad, d_pad), dtype=np.complex128)
+    diag[:, :num_rows] = vals.T  # diag[d][t]
+    slots = encoder.slot_count()
+    coeffs = t.empty((d_pad, context.N), dtype=t.int64, device=context.dev)
+    for g in range(d_pad // baby_steps):
+        for b in range(baby_steps):
+            d = g * baby_steps + b
+            v = np.tile(np.roll(diag[d], g * baby_steps), slots // d_pad)
+            context.native.ckks_encode_coeffs(t.from_numpy(v).to(context.dev), scale, coeffs[d])
+    return bsgs_diagonals(coeffs, scale, d_pad, baby_steps)
+
+
 def pre_encode_bsgs_diagonals(context: context, encoder: ckks_encoder, matrix, num_rows: int, num_cols: int,
                               d_pad: int, baby_steps: int, scale: float) -> bsgs_diagonals:
     """pre_encode_bsgs_diagonals (src/bsgs.cu:99-178): diag[d][t] = W[t][(t + d) mod d_pad]
     (zero outside num_rows x num_cols); diagonal g * M + b is rotated right by
     g * M, tiled over the slots with period d_pad and encoded at `scale`."""
-    t = _torch()
     if num_rows == 0 or num_cols == 0:
         raise ValueError("pre_encode_bsgs_diagonals: dimensions must be non-zero")
     W = np.asarray(matrix, dtype=np.float64).ravel()
@@ -728,23 +751,63 @@ def pre_encode_bsgs_diagonals(context: context, encoder: ckks_encoder, matrix, n
         raise ValueError("pre_encode_bsgs_diagonals: d_pad must be >= max(num_rows, num_cols)")
     if baby_steps == 0 or d_pad % baby_steps:
         raise ValueError("pre_encode_bsgs_diagonals: baby_steps must divide d_pad")
-    slots = encoder.slot_count()
-    if slots % d_pad:
+    if encoder.slot_count() % d_pad:
         raise ValueError("pre_encode_bsgs_diagonals: num_slots must be multiple of d_pad")
-    W = W.reshape(num_rows, num_cols)
-    rows = np.arange(num_rows)[:, None]
-    j = (rows + np.arange(d_pad)[None, :]) % d_pad  # [t][d]
-    vals = np.where(j < num_cols, W[rows, np.minimum(j, num_cols - 1)], 0.0)
-    diag = np.zeros((d_pad, d_pad))
-    diag[:, :num_rows] = vals.T  # diag[d][t]
-    G = d_pad // baby_steps
-    coeffs = t.empty((d_pad, context.N), dtype=t.int64, device=context.dev)
-    for g in range(G):
-        for b in range(baby_steps):
-            d = g * baby_steps + b
-            v = np.tile(np.roll(diag[d], g * baby_steps), slots // d_pad).astype(np.complex128)
-            context.native.ckks_encode_coeffs(t.from_numpy(v).to(context.dev), scale, coeffs[d])
-    return bsgs_diagonals(coeffs, scale, d_pad, baby_steps)
+    return _encode_bsgs_diagonals(context, encoder, W.reshape(num_rows, num_cols).astype(np.complex128), d_pad,
+                                  baby_steps, scale)
+
+
+class ComplexFoldMode(enum.Enum):
+    """ComplexFoldMode (include/bsgs.h:81-97).  Rows: rows i and i + ceil(R/2)
+    share complex row i (re(y)[i] = (W x)[i], im(y)[i] = (W x)[i + ceil(R/2)]).
+    ColsConj: columns j and j + ceil(C/2) share complex column j with the second
+    conjugated, for x packed as x[j] + i x[j + ceil(C/2)] (re(y) = W x)."""
+    Rows = 0
+    ColsConj = 1
+
+
+class complex_bsgs_diagonals:
+    """ComplexBsgsDiagonals (include/bsgs.h:77-79): the same structure as
+    bsgs_diagonals, with complex-folded diagonals."""
+
+    def __init__(self, inner: bsgs_diagonals):
+        self.inner = inner
+
+
+def _complex_fold(W: np.ndarray, mode: ComplexFoldMode) -> np.ndarray:
+    """apply_complex_fold (src/bsgs.cu:373-413): the folded complex matrix."""
+    R, C = W.shape
+    if mode == ComplexFoldMode.Rows:
+        h = (R + 1) // 2
+        out = W[:h].astype(np.complex128)
+        out[:R - h] += 1j * W[h:]
+        return out
+    h = (C + 1) // 2
+    out = W[:, :h].astype(np.complex128)
+    out[:, :C - h] -= 1j * W[:, h:]
+    return out
+
+
+def pre_encode_bsgs_diagonals_complex(context: context, encoder: ckks_encoder, matrix, num_rows: int,
+                                      num_cols: int, d_pad: int, baby_steps: int, scale: float,
+                                      mode: ComplexFoldMode) -> complex_bsgs_diagonals:
+    """pre_encode_bsgs_diagonals_complex (src/bsgs.cu:415-514): the matrix folded
+    to complex (Rows or ColsConj), then diagonal-encoded as in the real case."""
+    if num_rows == 0 or num_cols == 0:
+        raise ValueError("pre_encode_bsgs_diagonals_complex: dimensions must be non-zero")
+    W = np.asarray(matrix, dtype=np.float64).ravel()
+    if W.size != num_rows * num_cols:
+        raise ValueError("pre_encode_bsgs_diagonals_complex: matrix size mismatch")
+    if not _is_pow2(d_pad):
+        raise ValueError("pre_encode_bsgs_diagonals_complex: d_pad must be a power of 2")
+    if baby_steps == 0 or d_pad % baby_steps:
+        raise ValueError("pre_encode_bsgs_diagonals_complex: baby_steps must divide d_pad")
+    folded = _complex_fold(W.reshape(num_rows, num_cols), ComplexFoldMode(mode))
+    if d_pad < folded.shape[0] or d_pad < folded.shape[1]:
+        raise ValueError("pre_encode_bsgs_diagonals_complex: d_pad must be >= max(folded_rows, folded_cols)")
+    if encoder.slot_count() % d_pad:
+        raise ValueError("pre_encode_bsgs_diagonals_complex: num_slots must be multiple of d_pad")
+    return complex_bsgs_diagonals(_encode_bsgs_diagonals(context, encoder, folded, d_pad, baby_steps, scale))
 
 
 def bsgs_required_steps(baby_steps: int) -> list:
@@ -760,7 +823,7 @@ def bsgs_required_steps(baby_steps: int) -> list:
 
 
 def compute_bsgs_babies(context: context, galois_key: galois_key, x: ciphertext, baby_steps: int) -> list:
-    """babies[0] = x, babies[b] = rotate(babies[b - msb(b)], msb(b)) (src/bsgs.cu:195-215)."""
+    """babies[0] = x, babies[b] = rotate(babies[b - msb(b)], msb(b)) (src/bsgs.cu:194-214)."""
     if baby_steps == 0:
         raise ValueError("compute_bsgs_babies: baby_steps must be > 0")
     if x.size() != 2:
@@ -782,7 +845,7 @@ def compute_bsgs_babies(context: context, galois_key: galois_key, x: ciphertext,
 
 
 def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babies, diags: bsgs_diagonals):
-    """bsgs_apply_giants_with_babies (src/bsgs.cu:217-333): partial_g =
+    """bsgs_apply_giants_with_babies (src/bsgs.cu:216-357): partial_g =
     sum_b pt[g M + b] * babies[b] for every giant (one launch), then Horner
     acc = rotate(acc, M) + partial_g from g = G - 1 down to 0, one rescale, and
     the babies' scale restored."""
@@ -822,6 +885,18 @@ def bsgs_apply_giants_with_babies(context: context, galois_key: galois_key, babi
 
 
 def bsgs_matmul_preencoded(context: context, galois_key: galois_key, x: ciphertext, diags: bsgs_diagonals):
-    """bsgs_matmul_preencoded (src/bsgs.cu:335-342)."""
+    """bsgs_matmul_preencoded (src/bsgs.cu:361-368)."""
     return bsgs_apply_giants_with_babies(context, galois_key,
                                          compute_bsgs_babies(context, galois_key, x, diags.baby_steps), diags)
+
+
+def bsgs_matmul_preencoded_complex(context: context, galois_key: galois_key, x: ciphertext,
+                                   diags: complex_bsgs_diagonals):
+    """bsgs_matmul_preencoded_complex (src/bsgs.cu:517-524): the real-path product."""
+    return bsgs_matmul_preencoded(context, galois_key, x, diags.inner)
+
+
+def bsgs_apply_giants_with_babies_complex(context: context, galois_key: galois_key, babies,
+                                          diags: complex_bsgs_diagonals):
+    """bsgs_apply_giants_with_babies_complex (src/bsgs.cu:526-532)."""
+    return bsgs_apply_giants_with_babies(context, galois_key, babies, diags.inner)

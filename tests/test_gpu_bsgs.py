@@ -269,6 +269,51 @@ def test_bsgs_babies_any_count(dev, M):
         assert torch.equal(babies[b].data, ph.rotate(ctx, babies[b - bit], bit, glk).data), b
 
 
+@pytest.mark.parametrize("mode", ["Rows", "ColsConj"])
+def test_bsgs_complex_fold_decodes(dev, mode):
+    """pre_encode_bsgs_diagonals_complex (src/bsgs.cu:415-514) + the complex
+    product: Rows packs (W x)[i] and (W x)[i + ceil(R/2)] into one slot's real
+    and imaginary parts; ColsConj takes x packed as x[j] + i x[j + ceil(C/2)]
+    and returns W x in the real parts."""
+    M, G = 4, 4
+    d_pad = M * G
+    R, C = (24, 12) if mode == "Rows" else (10, 20)
+    ph, ctx = make_ctx(12, [60, 40, 40, 40, 60, 60], 2, steps=[1, 2, 4])
+    ph.set_seed(13)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 64)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    slots = enc.slot_count()
+    rng = np.random.default_rng(14)
+    W = rng.uniform(-1 / 8, 1 / 8, (R, C))
+    x = rng.uniform(-1, 1, C)
+    scale = 2.0 ** 40
+    fold = getattr(ph.ComplexFoldMode, mode)
+    diags = ph.pre_encode_bsgs_diagonals_complex(ctx, enc, W.ravel(), R, C, d_pad, M, scale, fold)
+    xv = np.zeros(d_pad, dtype=np.complex128)
+    if mode == "Rows":
+        xv[:C] = x
+    else:
+        h = (C + 1) // 2
+        xv[:h] = x[:h]
+        xv[:C - h] += 1j * x[h:]
+    ct = sk.encrypt_symmetric(ctx, enc.encode_complex_vector(ctx, np.tile(xv, slots // d_pad), scale))
+    y = ph.bsgs_matmul_preencoded_complex(ctx, glk, ct, diags)
+    got = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, y)))[:d_pad]
+    want = W @ x
+    if mode == "Rows":
+        h = (R + 1) // 2
+        assert np.max(np.abs(got[:h].real - want[:h])) < 1e-5
+        assert np.max(np.abs(got[:R - h].imag - want[h:])) < 1e-5
+    else:
+        assert np.max(np.abs(got[:R].real - want)) < 1e-5
+    # the split API gives the same residues
+    babies = ph.compute_bsgs_babies(ctx, glk, ct, M)
+    y2 = ph.bsgs_apply_giants_with_babies_complex(ctx, glk, babies, diags)
+    import torch
+    assert torch.equal(y2.data, y.data)
+
+
 def test_bsgs_argument_checks(dev):
     ph, ctx = make_ctx(12, [60, 40, 60], 1)
     enc = ph.ckks_encoder(ctx)
@@ -281,3 +326,5 @@ def test_bsgs_argument_checks(dev):
         ph.pre_encode_bsgs_diagonals(ctx, enc, W.ravel(), 4, 4, 8, 3, 2.0 ** 30)  # baby steps must divide
     with pytest.raises(ValueError):
         ph.pre_encode_bsgs_diagonals(ctx, enc, W.ravel()[:15], 4, 4, 8, 2, 2.0 ** 30)  # size mismatch
+    with pytest.raises(ValueError):  # folded 4 x 2 needs d_pad >= 4
+        ph.pre_encode_bsgs_diagonals_complex(ctx, enc, W.ravel(), 4, 4, 2, 1, 2.0 ** 30, ph.ComplexFoldMode.ColsConj)
