@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import enum
 import itertools
+import struct
 
 import numpy as np
 
@@ -177,6 +178,62 @@ class context:
         return t
 
 
+# ---------------------------------------------------------------- binary format
+# The reference's save/load layout (include/ciphertext.h:173-214,
+# include/plaintext.h:73-101, include/secretkey.h:99-111, :192-228, :290-318,
+# :537-575): raw little-endian fields, no padding, then the residues as
+# uint64 limbs in [poly][limb][N] order.
+_CT_HEADER = struct.Struct("<QQQQdQQ??")  # chain_index, size, N, |Ql|, scale, correction_factor,
+#                                           noiseScaleDeg, is_ntt_form, is_asymmetric
+_PT_HEADER = struct.Struct("<QQQd")  # chain_index, N, |Ql|, scale
+_SK_HEADER = struct.Struct("<QQQ")  # sk_max_power, N, |QP|
+_COUNT = struct.Struct("<Q")  # dnum of a relin key, key count of a Galois key
+
+
+def _read_exact(stream, n: int) -> bytes:
+    b = stream.read(n)
+    if len(b) != n:
+        raise ValueError("unexpected end of stream")
+    return b
+
+
+def _write_limbs(stream, tensor):
+    stream.write(np.ascontiguousarray(tensor.cpu().numpy(), dtype=np.uint64).tobytes())
+
+
+def _read_limbs(stream, shape, dev):
+    n = int(np.prod(shape))
+    a = np.frombuffer(_read_exact(stream, 8 * n), dtype=np.uint64).reshape(shape)
+    return _torch().from_numpy(a.copy()).to(dev)
+
+
+def _device(ctx):
+    t = _torch()
+    return ctx.dev if ctx is not None else t.device("cuda", t.cuda.current_device())
+
+
+def _opened(stream, mode):
+    """A path opens a file; a file object is used as given."""
+    if isinstance(stream, (str, bytes)) or hasattr(stream, "__fspath__"):
+        return open(stream, mode), True
+    return stream, False
+
+
+def _save_ct_record(stream, data, chain, scale, is_ntt=True, correction_factor=1, noise_scale_deg=1,
+                    is_asymmetric=False):
+    size, L, N = (int(x) for x in data.shape)
+    stream.write(_CT_HEADER.pack(chain, size, N, L, float(scale), correction_factor, noise_scale_deg, bool(is_ntt),
+                                 bool(is_asymmetric)))
+    _write_limbs(stream, data)
+
+
+def _load_ct_record(stream, dev):
+    chain, size, N, L, scale, cf, nsd, ntt, asym = _CT_HEADER.unpack(_read_exact(stream, _CT_HEADER.size))
+    if size < 1 or L < 1 or N < 2 or N & (N - 1) or size * L * N > (1 << 36):
+        raise ValueError("corrupt ciphertext header")
+    return _read_limbs(stream, (size, L, N), dev), chain, scale, cf, nsd, ntt, asym
+
+
 class plaintext:
     def __init__(self):
         self.data = None
@@ -188,6 +245,29 @@ class plaintext:
 
     def scale(self) -> float:
         return self._scale
+
+    def save(self, stream):
+        """PhantomPlaintext::save (include/plaintext.h:73-85)."""
+        f, own = _opened(stream, "wb")
+        try:
+            L, N = (int(x) for x in self.data.shape)
+            f.write(_PT_HEADER.pack(self._chain_index, N, L, float(self._scale)))
+            _write_limbs(f, self.data)
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context | None = None):
+        """PhantomPlaintext::load (include/plaintext.h:87-101)."""
+        f, own = _opened(stream, "rb")
+        try:
+            chain, N, L, scale = _PT_HEADER.unpack(_read_exact(f, _PT_HEADER.size))
+            self.data = _read_limbs(f, (L, N), _device(ctx))
+            self._chain_index, self._scale = chain, scale
+        finally:
+            if own:
+                f.close()
+        return self
 
 
 class ciphertext:
@@ -218,6 +298,28 @@ class ciphertext:
         c._scale = self._scale if scale is None else scale
         return c
 
+    def save(self, stream):
+        """PhantomCiphertext::save (include/ciphertext.h:173-191)."""
+        f, own = _opened(stream, "wb")
+        try:
+            _save_ct_record(f, self.data, self._chain_index, self._scale, self.is_ntt_form,
+                            getattr(self, "correction_factor", 1), getattr(self, "noise_scale_deg", 1),
+                            getattr(self, "is_asymmetric", False))
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context | None = None):
+        """PhantomCiphertext::load (include/ciphertext.h:193-214); ctx picks the device."""
+        f, own = _opened(stream, "rb")
+        try:
+            (self.data, self._chain_index, self._scale, self.correction_factor, self.noise_scale_deg,
+             self.is_ntt_form, self.is_asymmetric) = _load_ct_record(f, _device(ctx))
+        finally:
+            if own:
+                f.close()
+        return self
+
 
 class _ksk:
     """Key switching key material: [dnum][2][|QP|][N] on the device."""
@@ -226,14 +328,50 @@ class _ksk:
         self.data = data
 
 
+def _save_ksk(stream, data):
+    """PhantomRelinKey::save (include/secretkey.h:192-204): dnum, then each
+    digit as a key-level ciphertext [2][|QP|][N]."""
+    if data is None:
+        raise ValueError("key has not been generated")
+    stream.write(_COUNT.pack(int(data.shape[0])))
+    for d in range(int(data.shape[0])):
+        _save_ct_record(stream, data[d], 0, 1.0)
+
+
+def _load_ksk(stream, dev):
+    (dnum,) = _COUNT.unpack(_read_exact(stream, _COUNT.size))
+    digits = [_load_ct_record(stream, dev)[0] for _ in range(dnum)]
+    if not digits:
+        raise ValueError("key has no digits")
+    return _torch().stack(digits).contiguous()
+
+
 class relin_key(_ksk):
     def __init__(self, data=None):
         super().__init__(data)
 
+    def save(self, stream):
+        f, own = _opened(stream, "wb")
+        try:
+            _save_ksk(f, self.data)
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context | None = None):
+        """PhantomRelinKey::load (include/secretkey.h:206-228)."""
+        f, own = _opened(stream, "rb")
+        try:
+            self.data = _load_ksk(f, _device(ctx))
+        finally:
+            if own:
+                f.close()
+        return self
+
 
 class galois_key:
     def __init__(self):
-        self.keys = {}  # Galois element -> key tensor
+        self.keys = {}  # Galois element -> key tensor, in the context's galois_elts order
 
     def get(self, elt):
         k = self.keys.get(elt)
@@ -241,13 +379,62 @@ class galois_key:
             raise RuntimeError(f"Galois key not present for element {elt}")
         return k
 
+    def save(self, stream):
+        """PhantomGaloisKey::save (include/secretkey.h:290-302): the key count,
+        then one relin-key record per Galois element in the context's order."""
+        f, own = _opened(stream, "wb")
+        try:
+            if not self.keys:
+                raise ValueError("PhantomGaloisKey has not been generated")
+            f.write(_COUNT.pack(len(self.keys)))
+            for k in self.keys.values():
+                _save_ksk(f, k)
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context):
+        """PhantomGaloisKey::load (include/secretkey.h:304-318); the elements
+        come from ctx.galois_elts, as the file holds only the keys."""
+        f, own = _opened(stream, "rb")
+        try:
+            (n,) = _COUNT.unpack(_read_exact(f, _COUNT.size))
+            if n != len(ctx.galois_elts):
+                raise ValueError(f"file holds {n} Galois keys, the context has {len(ctx.galois_elts)} elements")
+            self.keys = {e: _load_ksk(f, ctx.dev) for e in ctx.galois_elts}
+        finally:
+            if own:
+                f.close()
+        return self
+
 
 class public_key:
-    """PhantomPublicKey: (-(a s + e), a) over the data primes, NTT form."""
+    """PhantomPublicKey: (-(a s + e), a) over every prime of the key level, NTT form."""
 
     def __init__(self, ctx: context | None = None, data=None):
         self.ctx = ctx
         self.data = data
+
+    def save(self, stream):
+        """PhantomPublicKey::save (include/secretkey.h:99-104): one ciphertext record."""
+        if self.data is None:
+            raise ValueError("PhantomPublicKey has not been generated")
+        f, own = _opened(stream, "wb")
+        try:
+            _save_ct_record(f, self.data, 0, 1.0)
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context | None = None):
+        f, own = _opened(stream, "rb")
+        try:
+            self.data = _load_ct_record(f, _device(ctx))[0]
+            self.ctx = ctx
+        finally:
+            if own:
+                f.close()
+        return self
 
     def encrypt_asymmetric(self, ctx: context, pt: plaintext, seed=None) -> ciphertext:
         """ct = (pk0 u + e0 + m, pk1 u + e1) over the plaintext's primes."""
@@ -299,6 +486,34 @@ class secret_key:
         if self.sk is None:
             raise ValueError("secret key is not generated")
 
+    def save(self, stream):
+        """PhantomSecretKey::save (include/secretkey.h:537-554): sk_max_power
+        (1 for CKKS), N, |QP|, then s in NTT form over every prime."""
+        self._require()
+        f, own = _opened(stream, "wb")
+        try:
+            QP, N = (int(x) for x in self.sk.shape)
+            f.write(_SK_HEADER.pack(1, N, QP))
+            _write_limbs(f, self.sk)
+        finally:
+            if own:
+                f.close()
+
+    def load(self, stream, ctx: context):
+        """PhantomSecretKey::load (include/secretkey.h:556-575); only the first
+        power is kept (CKKS uses s alone)."""
+        f, own = _opened(stream, "rb")
+        try:
+            power, N, QP = _SK_HEADER.unpack(_read_exact(f, _SK_HEADER.size))
+            if N != ctx.N or QP != len(ctx.moduli) or power < 1:
+                raise ValueError("secret key does not match the context")
+            data = _read_limbs(f, (power, QP, N), ctx.dev)
+            self.ctx, self.sk, self.coeffs = ctx, data[0].contiguous(), None
+        finally:
+            if own:
+                f.close()
+        return self
+
     def _kswitch_key(self, ctx, new_key, rng):
         """generate_one_kswitch_key (src/secretkey.cu:354-398) via pfa_kswitch_key."""
         QP = len(ctx.moduli)
@@ -310,16 +525,17 @@ class secret_key:
         return out
 
     def gen_publickey(self, ctx: context, seed=None) -> public_key:
+        """(-(a s + e), a) at the key level, over every prime (src/secretkey.cu:578-590)."""
         self._require()
         rng = _rng(seed)
-        Q = ctx.size_Q
-        a = ctx._uniform(rng, Q)
-        e = ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), Q), Q)
-        pk = ctx._empty(2, Q, ctx.N)
+        QP = len(ctx.moduli)
+        a = ctx._uniform(rng, QP)
+        e = ctx._ntt(ctx._signed_to_rns(ctx._cbd(rng), QP), QP)
+        pk = ctx._empty(2, QP, ctx.N)
         nat = ctx.native
-        nat.poly_mul(a, self.sk[:Q].contiguous(), pk[0], Q)
-        nat.poly_add(pk[0], e, pk[0], Q)
-        nat.poly_negate(pk[0], pk[0], Q)
+        nat.poly_mul(a, self.sk, pk[0], QP)
+        nat.poly_add(pk[0], e, pk[0], QP)
+        nat.poly_negate(pk[0], pk[0], QP)
         pk[1].copy_(a)
         return public_key(ctx, pk)
 
@@ -662,6 +878,74 @@ def hoisting(ctx: context, ct: ciphertext, glk: galois_key, steps) -> ciphertext
     return ct._like(out)
 
 
+class single_chain_plaintext:
+    """SingleChainPlaintext (include/single_chain_plaintext.h:37-40,
+    python/src/binding.cu:405-426): a plaintext kept as its N rounded signed
+    coefficients and scale, expanded to residues at the level of use.  The
+    coefficients are held on the device (int64 [N])."""
+
+    def __init__(self, coeffs, scale: float):
+        self.coeffs = coeffs
+        self._scale = float(scale)
+
+    @property
+    def scale(self) -> float:
+        return self._scale
+
+    @property
+    def N(self) -> int:
+        return int(self.coeffs.shape[0])
+
+    @property
+    def nbytes(self) -> int:
+        return 8 * self.N
+
+    def get_scale(self) -> float:
+        return self._scale
+
+    def coeffs_bytes(self) -> bytes:
+        """The int64 coefficients as raw bytes (N * 8); scp_from_bytes inverts it."""
+        return np.ascontiguousarray(self.coeffs.cpu().numpy(), dtype=np.int64).tobytes()
+
+
+def encode_single_chain_plaintext(context: context, encoder: ckks_encoder, slots, scale: float):
+    """encode_single_chain_plaintext (src/single_chain_plaintext.cu:93-150): the
+    CKKS slot encoding of `slots` (complex or real) at `scale`, kept as signed
+    coefficients."""
+    t = _torch()
+    v = np.asarray(slots)
+    if v.ndim != 1:
+        raise RuntimeError("encode_single_chain_plaintext: array must be 1-D")
+    if len(v) > encoder.slot_count():
+        raise ValueError("encode_single_chain_plaintext: too many values")
+    coeffs = t.empty(context.N, dtype=t.int64, device=context.dev)
+    context.native.ckks_encode_coeffs(t.from_numpy(v.astype(np.complex128)).to(context.dev), scale, coeffs)
+    return single_chain_plaintext(coeffs, scale)
+
+
+def scp_from_bytes(data: bytes, scale: float, N: int, context: context | None = None):
+    """scp_from_bytes (python/src/binding.cu:496-519): the inverse of coeffs_bytes."""
+    if len(data) != N * 8:
+        raise RuntimeError(f"scp_from_bytes: byte length mismatch (got {len(data)}, expected {N * 8})")
+    t = _torch()
+    c = t.from_numpy(np.frombuffer(data, dtype=np.int64).copy()).to(_device(context))
+    return single_chain_plaintext(c, scale)
+
+
+def expand_single_chain_to_full(context: context, scp: single_chain_plaintext, target_chain_index: int):
+    """expand_single_chain_to_full (src/single_chain_plaintext.cu:150-192): the
+    coefficients reduced into every prime of the level, then the forward NTT."""
+    if scp.N != context.N:
+        raise ValueError("expand_single_chain_to_full: coeff length != N")
+    L = context.size_Ql(target_chain_index)
+    out = context._empty(1, L, context.N)
+    context.native.expand_signed(scp.coeffs.to(context.dev).view(1, -1).contiguous(), 1, out, L)
+    context.native.ntt_forward(out, 1, L, 0)
+    pt = plaintext()
+    pt.data, pt._chain_index, pt._scale = out[0], target_chain_index, scp.scale
+    return pt
+
+
 # ---------------------------------------------------------------- BSGS matvec
 # Encrypted matrix-vector product by baby-step giant-step diagonals
 # (include/bsgs.h, src/bsgs.cu).  y = W x for a plaintext matrix W and an
@@ -705,6 +989,11 @@ class bsgs_diagonals:
     def release(self):
         """Drop the cached expansions."""
         self._expanded.clear()
+
+    @property
+    def diagonals(self) -> list:
+        """The d_pad single-chain plaintexts (views of the coefficient array)."""
+        return [single_chain_plaintext(self.coeffs[d], self.scale) for d in range(self.d_pad)]
 
 
 def _is_pow2(x: int) -> bool:

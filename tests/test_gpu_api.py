@@ -226,3 +226,116 @@ def test_api_errors(dev):
         ph.rescale_to_next(ctx, ph.rescale_to_next(ctx, ph.rescale_to_next(ctx, c1)))
     with pytest.raises(ValueError):
         ph.params(ph.scheme_type.bfv)
+
+
+def test_serialization_reference_layout(dev):
+    """save/load in the reference's binary layout (include/ciphertext.h:173-214,
+    include/plaintext.h:73-101, include/secretkey.h:99-111, :192-228, :290-318,
+    :537-575): the headers carry the reference's fields in its order, the
+    objects round-trip exactly, and loaded keys work."""
+    import io
+    import struct
+
+    import torch
+
+    ph, ctx = make_ctx(12, [60, 40, 40, 60], 1, steps=[1, -1])
+    ph.set_seed(21)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 64)
+    pk = sk.gen_publickey(ctx)
+    rlk = sk.gen_relinkey(ctx)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(22)
+    v = rng.uniform(-1, 1, enc.slot_count())
+    pt = enc.encode_double_vector(ctx, v, 2.0 ** 40)
+    ct = sk.encrypt_symmetric(ctx, pt)
+    N, L, QP = ctx.N, ctx.size_Ql(1), len(ctx.moduli)
+
+    # ciphertext: 7 x 8-byte fields + 2 bools (58 bytes), then [2][L][N] uint64
+    buf = io.BytesIO()
+    ct.save(buf)
+    raw = buf.getvalue()
+    assert len(raw) == 58 + 2 * L * N * 8
+    assert struct.unpack("<QQQQdQQ??", raw[:58]) == (1, 2, N, L, 2.0 ** 40, 1, 1, True, False)
+    assert raw[58:66] == to_host(ct.data)[0, 0, 0].tobytes()
+    ct2 = ph.ciphertext().load(io.BytesIO(raw), ctx)
+    assert torch.equal(ct2.data, ct.data) and ct2.chain_index() == 1 and ct2.scale() == ct.scale()
+
+    # plaintext: chain, N, L, scale, then [L][N]
+    buf = io.BytesIO()
+    pt.save(buf)
+    raw = buf.getvalue()
+    assert len(raw) == 32 + L * N * 8 and struct.unpack("<QQQd", raw[:32]) == (1, N, L, 2.0 ** 40)
+    assert torch.equal(ph.plaintext().load(io.BytesIO(raw), ctx).data, pt.data)
+
+    # secret key: power 1, N, |QP|, then s over every prime
+    buf = io.BytesIO()
+    sk.save(buf)
+    raw = buf.getvalue()
+    assert struct.unpack("<QQQ", raw[:24]) == (1, N, QP) and len(raw) == 24 + QP * N * 8
+    sk2 = ph.secret_key().load(io.BytesIO(raw), ctx)
+    got = np.array(enc.decode_double_vector(ctx, sk2.decrypt(ctx, ct2)))
+    assert np.max(np.abs(got - v)) < 1e-6
+
+    # public key: one key-level ciphertext record [2][QP][N]
+    buf = io.BytesIO()
+    pk.save(buf)
+    raw = buf.getvalue()
+    assert struct.unpack("<QQQQdQQ??", raw[:58])[:4] == (0, 2, N, QP)
+    pk2 = ph.public_key().load(io.BytesIO(raw), ctx)
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, pk2.encrypt_asymmetric(ctx, pt))))
+    assert np.max(np.abs(got - v)) < 1e-6
+
+    # relin key: dnum, then dnum key-level ciphertexts; galois key: count, then relin keys
+    buf = io.BytesIO()
+    rlk.save(buf)
+    raw = buf.getvalue()
+    dnum = int(rlk.data.shape[0])
+    assert struct.unpack("<Q", raw[:8]) == (dnum,) and len(raw) == 8 + dnum * (58 + 2 * QP * N * 8)
+    rlk2 = ph.relin_key().load(io.BytesIO(raw), ctx)
+    assert torch.equal(rlk2.data, rlk.data)
+    y1 = ph.multiply_and_relin(ctx, ct, ct, rlk)
+    y2 = ph.multiply_and_relin(ctx, ct2, ct2, rlk2)
+    assert torch.equal(y1.data, y2.data)
+    buf = io.BytesIO()
+    glk.save(buf)
+    raw = buf.getvalue()
+    assert struct.unpack("<Q", raw[:8]) == (len(ctx.galois_elts),)
+    glk2 = ph.galois_key().load(io.BytesIO(raw), ctx)
+    assert list(glk2.keys) == list(glk.keys)
+    assert torch.equal(ph.rotate(ctx, ct, 1, glk2).data, ph.rotate(ctx, ct, 1, glk).data)
+
+    # a truncated stream or a corrupt header is an error, not a short object
+    buf = io.BytesIO()
+    ct.save(buf)
+    raw = buf.getvalue()
+    with pytest.raises(ValueError):
+        ph.ciphertext().load(io.BytesIO(raw[:-8]), ctx)
+    with pytest.raises(ValueError):
+        ph.ciphertext().load(io.BytesIO(struct.pack("<QQQQdQQ??", 1, 2, 0, L, 1.0, 1, 1, True, False)), ctx)
+
+
+def test_single_chain_plaintext_api(dev):
+    """encode_single_chain_plaintext / expand_single_chain_to_full
+    (src/single_chain_plaintext.cu:93-192) and the bytes round trip of the
+    Python binding (python/src/binding.cu:405-519): the expansion at a level
+    equals encode at that level, residue for residue."""
+    import torch
+
+    ph, ctx = make_ctx(13, [60, 40, 40, 60], 1)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(23)
+    v = rng.uniform(-1, 1, enc.slot_count()) + 1j * rng.uniform(-1, 1, enc.slot_count())
+    scale = 2.0 ** 40
+    scp = ph.encode_single_chain_plaintext(ctx, enc, v, scale)
+    assert scp.N == ctx.N and scp.nbytes == 8 * ctx.N and scp.scale == scale == scp.get_scale()
+    for chain in (1, 2):
+        full = ph.expand_single_chain_to_full(ctx, scp, chain)
+        ref = enc.encode_complex_vector(ctx, v, scale, chain)
+        assert full.chain_index() == chain and full.scale() == scale
+        assert torch.equal(full.data, ref.data)
+    scp2 = ph.scp_from_bytes(scp.coeffs_bytes(), scale, ctx.N, ctx)
+    assert torch.equal(ph.expand_single_chain_to_full(ctx, scp2, 1).data,
+                       ph.expand_single_chain_to_full(ctx, scp, 1).data)
+    with pytest.raises(RuntimeError):
+        ph.scp_from_bytes(b"\0" * 8, scale, ctx.N, ctx)
