@@ -258,6 +258,15 @@ int pfa_bsgs_apply_giants(const pfa_context *ctx, size_t chain_index, const uint
                           const uint64_t *const *babies, size_t M, size_t G, const uint64_t *key, size_t key_dnum,
                           uint64_t *out, void *stream);
 
+/* ------------------------------------------------------------ bootstrapping */
+
+/* The raise step of mod_raise_inplace (src/bootstrap.cu): `in` holds `size`
+ * polys [size][1][N] at the bottom of the chain (the single prime q0, table
+ * row 0, NTT form); out [size][|Q|][N] receives, over every prime of the
+ * first data level (chain index 1), the centred lift of each coefficient
+ * (in (-q0/2, q0/2]), in NTT form. */
+int pfa_mod_raise(const pfa_context *ctx, const uint64_t *in, size_t size, uint64_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -184,6 +184,21 @@ class Oracle:
         lib().orc_ntt_inv(self._ctx, _p(d), M, L, start, threads or threads_default())
         return d
 
+    def mod_raise(self, ct_bottom: np.ndarray, L: int) -> np.ndarray:
+        """mod_raise_extend_modulus (src/bootstrap.cu:37-75, :105-180): [size][1][N]
+        mod q0 in NTT form -> INTT, residue v read as v - q0 when v >= q0 >> 1,
+        reduced into primes 0 .. L-1, forward NTT.  [size][L][N]."""
+        coef = self.ntt_inv(u64(ct_bottom))
+        q0 = self.moduli[0]
+        neg = coef >= np.uint64(q0 >> 1)
+        mag = np.where(neg, np.uint64(q0) - coef, coef)
+        out = np.empty((coef.shape[0], L, self.N), dtype=np.uint64)
+        for l in range(L):
+            q = np.uint64(self.moduli[l])
+            r = mag[:, 0, :] % q
+            out[:, l, :] = np.where(neg[:, 0, :] & (r != 0), q - r, r)
+        return self.ntt_fwd(out)
+
     def tensor(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
         a, b = u64(a), u64(b)
         L = a.shape[-2]

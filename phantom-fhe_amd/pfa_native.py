@@ -62,6 +62,7 @@ SIGNATURES = {
     "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
     "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
+    "pfa_mod_raise": (_i32, [_vp, _vp, _sz, _vp, _vp]),
 }
 
 
@@ -80,6 +81,14 @@ def lib():
             raise ImportError(
                 f"libphantom_amd.so not found at {LIB_PATH}: build it with "
                 "`python -c 'import __graft_entry__ as g; g.build()'` (there is no CPU fallback)")
+        # torch first: its wheel carries its own HIP runtime, which torch loads as
+        # "libamdhip64.so".  Loaded after it, this library binds to that same
+        # runtime (soname libamdhip64.so.7); loaded before, it brings in the
+        # system copy and torch then starts a second runtime that sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)
@@ -343,6 +352,10 @@ class NativeContext:
         call("pfa_bsgs_apply_giants", self._h, chain_index, ptr(tiled), bp, M, G,
              ptr(key) if key is not None else None, key.shape[0] if key is not None else 0, ptr(out),
              stream or stream_of(tiled))
+
+    def mod_raise(self, ct_bottom, out, stream=None):
+        """ct_bottom [size][1][N] mod q0 -> out [size][|Q|][N], centred lift (NTT form)."""
+        call("pfa_mod_raise", self._h, ptr(ct_bottom), ct_bottom.shape[0], ptr(out), stream or stream_of(out))
 
     def poly_from_signed(self, coeffs_i64, out, L, start=0, stream=None):
         import torch

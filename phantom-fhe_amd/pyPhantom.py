@@ -1189,3 +1189,534 @@ def bsgs_apply_giants_with_babies_complex(context: context, galois_key: galois_k
                                           diags: complex_bsgs_diagonals):
     """bsgs_apply_giants_with_babies_complex (src/bsgs.cu:526-532)."""
     return bsgs_apply_giants_with_babies(context, galois_key, babies, diags.inner)
+
+
+# ---------------------------------------------------------------- bootstrapping
+# CKKS bootstrapping with the API of include/bootstrap.h / python/src/binding.cu
+# (create_bootstrap_key, bootstrap, bootstrap_required_galois_elts,
+# build_c2s_diagonals, ...), on the chain layout
+#     [q0 | user levels | SlotToCoeff x 3 | EvalMod x 10 | CoeffToSlot x 3] + special
+# (bootstrap_coeff_bits).  The pipeline follows the reference's order
+# (src/bootstrap.cu:1703-1800): ModRaise, CoeffToSlot, conjugate split into
+# real and imaginary tracks, the modular reduction on both, recombination,
+# SlotToCoeff.  The reduction is EvalMod (sin(2 pi x) / (2 pi) ~ x - round(x)
+# through a Chebyshev approximation of cos(2 pi (x - 1/4) / 2^r) and r
+# double-angle steps) where the reference runs the lapis EvalRound tables
+# (src/evalmod.cu); the secret is used as generated (sparse, so |I| < K), where
+# the reference switches to a sparse secret around ModRaise.  Parity is the
+# reference's own acceptance test: decoded slots within 1e-3
+# (test/ckks_engine_test.cu:182).
+#
+# Scales are tracked exactly: diagonal plaintexts are encoded at the prime the
+# following rescale drops, and every constant at the scale that makes the sum
+# it joins line up, so no addition ever mixes scales.
+
+BOOT_K = 28            # |x| bound of EvalMod's input (|I| < K for the sparse secret)
+BOOT_R = 3             # double-angle steps
+BOOT_DEG = 63          # Chebyshev degree (depth 7)
+BOOT_EVALMOD_LEVELS = 10
+BOOT_MSG_BITS = 12     # bootstrapping lifts the message to about q0 / 2^12 first
+# The transforms run at 2^b times their output scale (an exact integer multiple):
+# b more bits above their rotations' key-switching noise, b fewer in the last
+# layer's diagonals.  CoeffToSlot's slots (~sum |I|, hundreds) make those
+# diagonals' rounding count; SlotToCoeff's slots are the small message.
+BOOT_C2S_BOOST = 5
+BOOT_S2C_BOOST = 10
+BOOT_LT_LEVELS = 3
+
+
+def bootstrap_coeff_bits(user_levels: int = 13, q0_bits: int = 60, user_bits: int = 40, s2c_bits: int = 50,
+                         evalmod_bits: int = 60, c2s_bits: int = 60, special: int = 6, special_bits: int = 60):
+    """Prime sizes of a bootstrappable chain, bottom to top, then the special
+    primes: q0 | user levels | SlotToCoeff x 3 | EvalMod x 10 | CoeffToSlot x 3.
+    CoeffToSlot's diagonals are encoded at the scale of the prime its rescale
+    drops and act on slots of size ~sum |I| (hundreds to thousands), so its
+    primes are the widest; SlotToCoeff acts on the small refreshed message."""
+    return ([q0_bits] + [user_bits] * user_levels + [s2c_bits] * BOOT_LT_LEVELS + [evalmod_bits] * BOOT_EVALMOD_LEVELS
+            + [c2s_bits] * BOOT_LT_LEVELS + [special_bits] * special)
+
+
+def _brv_index(x: int, bits: int) -> int:
+    r = 0
+    for _ in range(bits):
+        r = (r << 1) | (x & 1)
+        x >>= 1
+    return r
+
+
+def _fft_stages(N: int, inverse: bool):
+    """The special FFT z = B_L ... B_1 P u (z_j = sum_k u_k zeta^(5^j k), P the
+    bit reversal) as butterfly stages B_s (or their inverses), each a dict
+    offset -> diagonal (entry (r, r + offset))."""
+    n, M = N // 2, 2 * N
+    rot = np.array([pow(5, j, M) for j in range(n)], dtype=np.int64)
+    out = []
+    length = 2
+    while length <= n:
+        lenh, lenq = length // 2, length * 4
+        j = np.arange(lenh)
+        w = np.exp(1j * np.pi * ((rot[j] % lenq) * (M // lenq)) / N)
+        top = (np.arange(0, n, length)[:, None] + j[None, :]).ravel()
+        wt = np.tile(w, n // length)
+        d0 = np.zeros(n, complex)
+        dp = np.zeros(n, complex)
+        dm = np.zeros(n, complex)
+        if not inverse:   # out[t] = in[t] + w in[t+h]; out[t+h] = in[t] - w in[t+h]
+            d0[top], dp[top], d0[top + lenh], dm[top + lenh] = 1, wt, -wt, 1
+        else:             # in[t] = (out[t] + out[t+h]) / 2; in[t+h] = (out[t] - out[t+h]) / (2 w)
+            d0[top], dp[top], d0[top + lenh], dm[top + lenh] = 0.5, 0.5, -0.5 / wt, 0.5 / wt
+        st = {0: d0, lenh: dp}
+        st[n - lenh] = st.get(n - lenh, 0) + dm  # the last stage's +-n/2 diagonals coincide
+        out.append(st)
+        length <<= 1
+    return out
+
+
+def _diag_product(A, B, n):
+    """(A B) from diagonal forms: (A B)[r][r+d] = sum A_d1[r] B_d2[r + d1], d = d1 + d2 mod n."""
+    C = {}
+    for d1, a in A.items():
+        for d2, b in B.items():
+            d = (d1 + d2) % n
+            C[d] = C.get(d, 0) + a * np.roll(b, -d1)
+    return {d: v for d, v in C.items() if np.max(np.abs(v)) > 1e-300}
+
+
+class _LTLayers:
+    """LinearTransformDiagonals (include/bootstrap.h): per layer, diagonals
+    {offset: values} of the product of its butterfly stages, the stage unit
+    2^s0 and the baby-step count."""
+
+    def __init__(self, log_n: int, stages_per_layer, inverse: bool):
+        N = 1 << log_n
+        n = N // 2
+        logn = n.bit_length() - 1
+        if sum(stages_per_layer) != logn:
+            raise ValueError(f"stages_per_layer must sum to log2(slots) = {logn}")
+        st = _fft_stages(N, inverse)
+        if inverse:   # CoeffToSlot applies B_L^-1 first
+            st = st[::-1]
+        self.N, self.n, self.layers, self.units = N, n, [], []
+        k = 0
+        for g in stages_per_layer:
+            L = {0: np.ones(n, complex)}
+            for s in st[k:k + g]:
+                L = _diag_product(s, L, n)
+            lo = k if not inverse else logn - k - g  # lowest stage index of the layer
+            self.layers.append(L)
+            self.units.append(1 << lo)
+            k += g
+        self.stages_per_layer = list(stages_per_layer)
+
+    def baby_giant(self, i):
+        """(n1, {giant: [(baby, offset)]}) of layer i, offsets in units of 2^s0."""
+        unit, n = self.units[i], self.n
+        e = sorted(d // unit for d in self.layers[i])
+        span = n // unit
+        n1 = 1
+        while n1 * n1 < len(e):
+            n1 <<= 1
+        groups = {}
+        for x in e:
+            g, b = divmod(x, n1)
+            groups.setdefault(g, []).append((b, x * unit))
+        return n1, groups, span
+
+    def rotation_steps(self):
+        steps = set()
+        for i in range(len(self.layers)):
+            n1, groups, span = self.baby_giant(i)
+            unit = self.units[i]
+            for g, terms in groups.items():
+                for b, _ in terms:
+                    if b:
+                        steps.add(b * unit)
+                if g:
+                    steps.add(_signed_step(g * n1 * unit, self.n))
+        return sorted(steps)
+
+
+def _signed_step(step: int, n: int) -> int:
+    step %= n
+    return step - n if step > n // 2 else step
+
+
+def build_c2s_diagonals(log_n: int, stages_per_layer=(5, 5, 5)) -> _LTLayers:
+    """CoeffToSlot as layered butterflies (src/bootstrap.cu:256-387): slots ->
+    the packed coefficients u_k = m_k + i m_(k+N/2), in bit-reversed order."""
+    return _LTLayers(log_n, stages_per_layer, True)
+
+
+def build_s2c_diagonals(log_n: int, stages_per_layer=(5, 5, 5)) -> _LTLayers:
+    """SlotToCoeff (src/bootstrap.cu:389-437): the inverse of CoeffToSlot."""
+    return _LTLayers(log_n, stages_per_layer, False)
+
+
+def c2s_required_rotation_steps(diags: _LTLayers, num_slots: int) -> list:
+    return diags.rotation_steps()
+
+
+def bootstrap_required_galois_elts(log_n: int, stages_per_layer=(5, 5, 5)) -> list:
+    """Galois elements of the CoeffToSlot and SlotToCoeff rotations plus
+    conjugation (python/src/binding.cu:301-318)."""
+    N = 1 << log_n
+    steps = sorted(set(build_c2s_diagonals(log_n, stages_per_layer).rotation_steps())
+                   | set(build_s2c_diagonals(log_n, stages_per_layer).rotation_steps()))
+    return get_elts_from_steps(steps, N) + [2 * N - 1]
+
+
+def _default_stages(log_n: int):
+    logn = log_n - 1
+    return [logn // 3 + (1 if i < logn % 3 else 0) for i in range(3)]
+
+
+def _const_plain(ctx: context, value: complex, scale: float, chain: int) -> plaintext:
+    """The constant `value` in every slot, exactly: coefficient 0 = Re(value) scale
+    and coefficient N/2 = Im(value) scale (X^(N/2) is i at every slot)."""
+    c = np.zeros(ctx.N, dtype=np.int64)
+    c[0] = int(round(complex(value).real * scale))
+    c[ctx.N // 2] = int(round(complex(value).imag * scale))
+    L = ctx.size_Ql(chain)
+    pt = plaintext()
+    pt.data, pt._chain_index, pt._scale = ctx._ntt(ctx._signed_to_rns(c, L), L), chain, float(scale)
+    return pt
+
+
+class small_bootstrap_key:
+    """SmallBootstrapKey (include/bootstrap.h): the key-switching pair that
+    moves a ciphertext from the user's dense secret to a transient sparse one
+    (ksk_to_sparse) and back (ksk_to_dense)."""
+
+    def __init__(self, ksk_to_sparse=None, ksk_to_dense=None):
+        self.ksk_to_sparse = ksk_to_sparse
+        self.ksk_to_dense = ksk_to_dense
+
+
+def _small_bootstrap_key(context: context, dense_sk: secret_key, sparse_hamming_weight: int, seed=None):
+    if sparse_hamming_weight <= 0:
+        raise ValueError("create_small_bootstrap_key: hamming_weight must be > 0")
+    dense_sk._require()
+    rng = _rng(seed)
+    sparse = secret_key().generate_sparse(context, sparse_hamming_weight, seed=rng)
+    small = small_bootstrap_key(relin_key(sparse._kswitch_key(context, dense_sk.sk, rng)),
+                                relin_key(dense_sk._kswitch_key(context, sparse.sk, rng)))
+    return small, sparse
+
+
+def create_small_bootstrap_key(context: context, dense_sk: secret_key, sparse_hamming_weight: int = 128,
+                               seed=None) -> small_bootstrap_key:
+    """create_small_bootstrap_key (src/bootstrap.cu:185-202): the sparse
+    secret exists only inside this call."""
+    return _small_bootstrap_key(context, dense_sk, sparse_hamming_weight, seed)[0]
+
+
+def apply_kswitch(context: context, ct: ciphertext, key: relin_key) -> ciphertext:
+    """apply_kswitch_inplace: (c0, c1) under s -> under the key's target secret
+    (the Galois path with the identity element 1)."""
+    return _apply_galois_key(context, ct, 1, key.data)
+
+
+class bootstrap_key:
+    """BootstrapKey (include/bootstrap.h): the encapsulation pair, the Galois
+    keys of CoeffToSlot, SlotToCoeff and conjugation, the relinearization
+    key, and the layers' diagonal plaintexts, encoded at the levels they are
+    applied at."""
+
+    def __init__(self):
+        self.small = None
+        self.glk = None
+        self.rlk = None
+        self.c2s = None
+        self.s2c = None
+        self.c2s_pts = []   # per layer: {giant: [(baby, plaintext)]}
+        self.s2c_pts = []
+        self.cheb = None
+        self.K, self.r = BOOT_K, BOOT_R
+
+
+def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1):
+    """Layer i's diagonals, each pre-rotated by minus its giant step, encoded
+    at `chain` with the scale of the prime the following rescale drops,
+    divided by scale_div (a power of two, so the scale stays exact)."""
+    n1, groups, span = lt.baby_giant(i)
+    L = ctx.size_Ql(chain)
+    scale = float(ctx.moduli[L - 1]) / scale_div
+    out = {}
+    for g, terms in groups.items():
+        shift = g * n1 * lt.units[i]
+        lst = []
+        for b, d in terms:
+            v = np.roll(lt.layers[i][d % lt.n] * factor, shift)
+            lst.append((b, enc.encode_complex_vector(ctx, v, scale, chain)))
+        out[g] = lst
+    return out
+
+
+def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secret_key,
+                         sparse_hamming_weight: int = 128, eval_mod_levels: int = 0, user_scale: float = 0.0,
+                         split_scale_down: bool = False, stages_per_layer=None, seed=None) -> bootstrap_key:
+    """create_bootstrap_key (src/bootstrap.cu:895-960, python/src/binding.cu:320-327).
+    The context must use the bootstrap_coeff_bits layout and carry
+    bootstrap_required_galois_elts.  The ModRaise runs under a transient
+    sparse secret of weight sparse_hamming_weight (|I| < K = 28 holds up to a
+    few hundred); the rotation and relinearization keys are the dense
+    secret's.  eval_mod_levels, user_scale and split_scale_down are
+    accepted for the reference's signature (EvalMod here always takes 10
+    levels)."""
+    ctx, enc = context, encoder
+    log_n = ctx.N.bit_length() - 1
+    stages = list(stages_per_layer or _default_stages(log_n))
+    need = 2 * len(stages) + BOOT_EVALMOD_LEVELS + 1
+    if ctx.size_Q < need:
+        raise ValueError(f"bootstrapping needs at least {need} primes (bootstrap_coeff_bits)")
+    missing = [e for e in bootstrap_required_galois_elts(log_n, stages) if e not in ctx.galois_elts]
+    if missing:
+        raise ValueError("the context's galois_elts lack bootstrap_required_galois_elts")
+    rng = _rng(seed)
+    bk = bootstrap_key()
+    bk.small = _small_bootstrap_key(ctx, dense_sk, sparse_hamming_weight, rng)[0]
+    bk.rlk = dense_sk.gen_relinkey(ctx, seed=rng)
+    bk.glk = galois_key()
+    for elt in bootstrap_required_galois_elts(log_n, stages):
+        bk.glk.keys[elt] = dense_sk._galois_key_for(ctx, elt, rng)
+    bk.c2s = build_c2s_diagonals(log_n, stages)
+    bk.s2c = build_s2c_diagonals(log_n, stages)
+    nl = len(stages)
+    # CoeffToSlot at chains 1 .. nl, with 1 / (2K) in its last layer;
+    # SlotToCoeff starts after EvalMod, with 1 / (2 pi) in its first layer.  The
+    # last layer of each takes the 2^BOOT_LT_BOOST the input carries back out.
+    bk.c2s_pts = [_encode_layer(ctx, enc, bk.c2s, i, 1 + i, 1 / (2 * BOOT_K) if i == nl - 1 else 1.0,
+                                1 << BOOT_C2S_BOOST if i == nl - 1 else 1)
+                  for i in range(nl)]
+    s2c0 = 1 + nl + BOOT_EVALMOD_LEVELS
+    bk.s2c_pts = [_encode_layer(ctx, enc, bk.s2c, i, s2c0 + i, 1 / (2 * np.pi) if i == 0 else 1.0,
+                                1 << BOOT_S2C_BOOST if i == nl - 1 else 1)
+                  for i in range(nl)]
+    bk.cheb = evalmod_chebyshev(BOOT_K, BOOT_R, BOOT_DEG)
+    return bk
+
+
+def _apply_layer(ctx, ct: ciphertext, lt: _LTLayers, pts, i: int, glk, rescale: bool = True) -> ciphertext:
+    """sum_d D_d . rot(ct, d) by baby steps (hoisted) and giant steps.  The
+    giant rotations and the sum run before the one rescale, where the scale is
+    q_drop times larger and their key-switching noise q_drop times smaller
+    next to it."""
+    n1, groups, span = lt.baby_giant(i)
+    unit = lt.units[i]
+    babies = sorted({b for terms in groups.values() for b, _ in terms})
+    rotated = {0: ct}
+    steps = [b * unit for b in babies if b]
+    if steps:
+        for b, r in zip([b for b in babies if b], hoist_rotations(ctx, ct, glk, steps)):
+            rotated[b] = r
+    acc = None
+    for g, terms in sorted(pts[i].items()):
+        part = None
+        for b, pt in terms:
+            term = multiply_plain(ctx, rotated[b], pt)
+            part = term if part is None else add(ctx, part, term)
+        if g:
+            part = rotate(ctx, part, _signed_step(g * n1 * unit, lt.n), glk)
+        acc = part if acc is None else add(ctx, acc, part)
+    return rescale_to_next(ctx, acc) if rescale else acc
+
+
+def _boosted(ctx, ct: ciphertext, bits: int) -> ciphertext:
+    """ct times the integer 2^bits, read at 2^bits its scale: the same message,
+    with the noise a transform adds that much smaller next to it."""
+    out = multiply_plain(ctx, ct, _const_plain(ctx, 1 << bits, 1.0, ct.chain_index()))
+    out.set_scale(ct.scale() * (1 << bits))
+    return out
+
+
+def _transform(ctx, ct, lt, pts, glk, boost, last_rescale=True):
+    ct = _boosted(ctx, ct, boost)
+    nl = len(lt.layers)
+    for i in range(nl):
+        ct = _apply_layer(ctx, ct, lt, pts, i, glk, rescale=last_rescale or i < nl - 1)
+    return ct
+
+
+def apply_c2s_inplace(context: context, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
+    """CoeffToSlot (src/bootstrap.cu apply_c2s_inplace): slots -> the packed
+    coefficients in bit-reversed order, times 1 / (2K), at ct's scale."""
+    return _transform(context, ct, bk.c2s, bk.c2s_pts, bk.glk, BOOT_C2S_BOOST)
+
+
+def apply_s2c_inplace(context: context, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
+    """SlotToCoeff (src/bootstrap.cu apply_s2c_inplace): the inverse layout
+    change, times 1 / (2 pi), at ct's scale."""
+    return _transform(context, ct, bk.s2c, bk.s2c_pts, bk.glk, BOOT_S2C_BOOST)
+
+
+def mod_raise_inplace(context: context, ct: ciphertext, bk) -> ciphertext:
+    """mod_raise_inplace (src/bootstrap.cu:204-215): a ciphertext (brought to the
+    bottom of the chain first) is switched to the sparse secret, each residue
+    mod q0 lifted centred into every prime of chain index 1 (pfa_mod_raise),
+    and switched back to the dense secret.  bk is a small_bootstrap_key or a
+    bootstrap_key.  Returns the raised ciphertext (chain index 1)."""
+    small = bk.small if isinstance(bk, bootstrap_key) else bk
+    bottom = context.size_Q
+    if ct.chain_index() != bottom:
+        ct = mod_switch_to(context, ct, bottom)
+    ct = apply_kswitch(context, ct, small.ksk_to_sparse)
+    out = context._empty(ct.size(), context.size_Q, context.N)
+    context.native.mod_raise(ct.data, out)
+    return apply_kswitch(context, ct._like(out, chain=1), small.ksk_to_dense)
+
+
+class _ExactScale:
+    """Ciphertext arithmetic that lands on exact target scales (see above)."""
+
+    def __init__(self, ctx, rlk):
+        self.ctx, self.rlk = ctx, rlk
+
+    def q_drop(self, chain):
+        return self.ctx.moduli[self.ctx.size_Ql(chain) - 1]
+
+    def down(self, ct, chain):
+        return mod_switch_to(self.ctx, ct, chain) if ct.chain_index() < chain else ct
+
+    def mul(self, a, b):
+        c = max(a.chain_index(), b.chain_index())
+        r = rescale_to_next(self.ctx, multiply_and_relin(self.ctx, self.down(a, c), self.down(b, c), self.rlk))
+        return r
+
+    def add_const(self, ct, value):
+        return add_plain(self.ctx, ct, _const_plain(self.ctx, value, ct.scale(), ct.chain_index()))
+
+    def mul_const_to(self, ct, value, target_scale, target_chain):
+        """value * ct at exactly target_scale, target_chain (ct above target_chain)."""
+        ct = self.down(ct, target_chain - 1)
+        s = target_scale * self.q_drop(target_chain - 1) / ct.scale()
+        r = rescale_to_next(self.ctx, multiply_plain(self.ctx, ct, _const_plain(self.ctx, value, s, target_chain - 1)))
+        r.set_scale(target_scale)
+        return r
+
+    def match(self, ct, target_scale, target_chain):
+        if ct.scale() == target_scale:
+            return self.down(ct, target_chain)
+        return self.mul_const_to(ct, 1.0, target_scale, target_chain)
+
+
+def evalmod_chebyshev(K: int = BOOT_K, r: int = BOOT_R, deg: int = BOOT_DEG) -> np.ndarray:
+    """Chebyshev coefficients (interpolation at the deg + 1 Chebyshev nodes) of
+    cos(2 pi (K t - 1/4) / 2^r) on [-1, 1]; r double angles c <- 2 c^2 - 1 then
+    give sin(2 pi K t) (the role of src/evalmod.cu's EvalRound tables)."""
+    from numpy.polynomial import chebyshev as _C
+
+    k = np.arange(deg + 1)
+    nodes = np.cos(np.pi * (k + 0.5) / (deg + 1))
+    return _C.chebfit(nodes, np.cos(2 * np.pi * (K * nodes - 0.25) / 2 ** r), deg)
+
+
+def _cheb_split(c):
+    """p = sum c_j T_j of degree d >= 8 as T_m hi + lo, m the largest power of two
+    <= d (T_(m+i) = 2 T_m T_i - T_(m-i)); returns (m, hi, lo)."""
+    deg = len(c) - 1
+    m = 1 << (deg.bit_length() - 1)
+    hi = [c[m]] + [2 * c[m + i] for i in range(1, deg - m + 1)]
+    lo = [c[i] - (c[2 * m - i] if 2 * m - i <= deg else 0.0) for i in range(m)]
+    return m, hi, lo
+
+
+def _cheb_depth(deg: int) -> int:
+    """Levels the evaluation in _eval_mod consumes for a degree-deg polynomial."""
+    if deg < 8:
+        return max(1, (deg - 1).bit_length() + 1)
+    m = 1 << (deg.bit_length() - 1)
+    return max(_cheb_depth(deg - m) + 1, m.bit_length(), _cheb_depth(m - 1))
+
+
+def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
+    """cos(2 pi (K t - 1/4) / 2^r) by Chebyshev (Paterson-Stockmeyer splitting at
+    powers of two), then r double angles: sin(2 pi K t) for t in [-1, 1]."""
+    E = _ExactScale(ctx, bk.rlk)
+    T = {1: ct}
+
+    def cheb_T(k):
+        if k in T:
+            return T[k]
+        if k % 2 == 0:
+            h = cheb_T(k // 2)
+            sq = E.mul(h, h)
+            T[k] = E.add_const(add(ctx, sq, sq), -1.0)
+        else:
+            a, b = (k + 1) // 2, (k - 1) // 2
+            p = E.mul(cheb_T(a), cheb_T(b))
+            two = add(ctx, p, p)
+            T[k] = sub(ctx, two, E.match(cheb_T(1), two.scale(), two.chain_index()))
+        return T[k]
+
+    def evaluate(c, target_scale, target_chain):
+        deg = len(c) - 1
+        if deg < 8:
+            acc = None
+            for j in range(1, deg + 1):
+                if c[j] != 0.0:
+                    term = E.mul_const_to(cheb_T(j), c[j], target_scale, target_chain)
+                    acc = term if acc is None else add(ctx, acc, term)
+            if acc is None:
+                acc = E.mul_const_to(cheb_T(1), 0.0, target_scale, target_chain)
+            return E.add_const(acc, c[0])
+        m, hi, lo = _cheb_split(c)
+        Tm = E.down(cheb_T(m), target_chain - 1)
+        hi_ct = evaluate(hi, target_scale * E.q_drop(target_chain - 1) / Tm.scale(), target_chain - 1)
+        prod = rescale_to_next(ctx, multiply_and_relin(ctx, Tm, hi_ct, bk.rlk))
+        prod.set_scale(target_scale)
+        return add(ctx, prod, evaluate(lo, target_scale, target_chain))
+
+    y = evaluate(list(bk.cheb), ct.scale(), ct.chain_index() + _cheb_depth(len(bk.cheb) - 1))
+    for _ in range(bk.r):
+        sq = E.mul(y, y)
+        y = E.add_const(add(ctx, sq, sq), -1.0)
+    return y
+
+
+def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
+    """ct * (sign i): the plaintext polynomial times sign X^(N/2), exact."""
+    L = ctx.size_Ql(ct.chain_index())
+    c = np.zeros(ctx.N, dtype=np.int64)
+    c[ctx.N // 2] = sign
+    mono = ctx._ntt(ctx._signed_to_rns(c, L), L)
+    out = ctx._empty(*ct.data.shape)
+    for k in range(ct.size()):
+        ctx.native.poly_mul(ct.data[k], mono, out[k], L)
+    return ct._like(out)
+
+
+def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: bootstrap_key, user_scale: float,
+              split_scale_down: bool = False) -> ciphertext:
+    """bootstrap (src/bootstrap.cu:1703-1951): a ciphertext at scale user_scale,
+    at any level (it is brought to the bottom of the chain first) -> the same
+    message at chain index 1 + 2 * (transform layers) + 10, at a scale within a
+    few parts in 10^12 of user_scale (the exact value is carried)."""
+    ctx = context
+    if ct.size() != 2:
+        raise ValueError("bootstrap expects a size-2 ciphertext")
+    if abs(ct.scale() - user_scale) > 1e-6 * user_scale:
+        raise ValueError("ciphertext scale differs from user_scale")
+    q0 = ctx.moduli[0]
+    ct = mod_switch_to(ctx, ct, ctx.size_Q)
+    # exact integer lift of the message to ~q0 / 2^BOOT_MSG_BITS: EvalMod's
+    # sin(2 pi x) / (2 pi) ~ x then holds to (2 pi 2^-12)^2 / 6 ~ 4e-7 relative,
+    # and the noise that the transforms add is magnified q0 / scale times less
+    k = max(0, int(np.floor(np.log2(q0 / user_scale))) - BOOT_MSG_BITS)
+    scale = float(user_scale)
+    if k:
+        ct = multiply_plain(ctx, ct, _const_plain(ctx, 1 << k, 1.0, ctx.size_Q))
+        scale *= 2.0 ** k
+    raised = mod_raise_inplace(ctx, ct, bk.small)
+    raised.set_scale(float(q0))  # slots now read coefficients / q0 = I + m scale / q0
+    # CoeffToSlot; its last rescale waits until the conjugate split is done,
+    # so the conjugation's key-switching noise lands at the larger scale too
+    u = _transform(ctx, raised, bk.c2s, bk.c2s_pts, bk.glk, BOOT_C2S_BOOST, last_rescale=False)
+    conj = apply_galois(ctx, u, 2 * ctx.N - 1, bk.glk)
+    real = rescale_to_next(ctx, add(ctx, u, conj))                     # Re(x) / K
+    imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))  # Im(x) / K
+    real = _eval_mod(ctx, real, bk)
+    imag = _eval_mod(ctx, imag, bk)
+    y = add(ctx, real, _times_i(ctx, imag, 1))
+    out = apply_s2c_inplace(ctx, y, bk)
+    out.set_scale(scale * out.scale() / q0)
+    return out

@@ -339,3 +339,27 @@ def test_single_chain_plaintext_api(dev):
                        ph.expand_single_chain_to_full(ctx, scp, 1).data)
     with pytest.raises(RuntimeError):
         ph.scp_from_bytes(b"\0" * 8, scale, ctx.N, ctx)
+
+
+def test_library_loaded_before_torch(dev):
+    """A fresh process that uses pyPhantom without importing torch itself: the
+    loader imports torch before the library, so both share torch's HIP runtime
+    and the device is visible to both."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = (
+        "import sys; sys.path[:0] = [%r, %r]\n"
+        "import numpy as np, pyPhantom as ph\n"
+        "p = ph.params(ph.scheme_type.ckks); N = 1 << 12\n"
+        "p.set_poly_modulus_degree(N); p.set_coeff_modulus(ph.create_coeff_modulus(N, [60, 40, 60]))\n"
+        "p.set_special_modulus_size(1); ctx = ph.context(p); enc = ph.ckks_encoder(ctx)\n"
+        "z = np.linspace(-1, 1, N // 2)\n"
+        "got = enc.decode_double_vector(ctx, enc.encode_double_vector(ctx, z, 2.0 ** 40))\n"
+        "print('max err', float(np.max(np.abs(np.array(got) - z))))\n"
+    ) % (root, os.path.join(root, "phantom-fhe_amd"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert float(r.stdout.split()[-1]) < 1e-6

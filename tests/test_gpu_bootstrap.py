@@ -1,0 +1,95 @@
+"""GPU tests of CKKS bootstrapping (src/bootstrap.cu:1703-1951).
+
+* pfa_mod_raise is bit-exact against the oracle's restatement of
+  mod_raise_signed_tile_kernel (src/bootstrap.cu:37-75), itself pinned against
+  Python integers in tests/test_bootstrap_math.py.
+* End to end, the reference's acceptance test is the bar: decoded slots after
+  bootstrap within 1e-3 of the input (test/ckks_engine_test.cu:182-188); the
+  refreshed ciphertext must also take a further multiplication.
+"""
+import numpy as np
+import pytest
+
+import py_oracle as O
+from gpu_util import empty, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def test_mod_raise_matches_oracle(dev):
+    import pfa_native as P
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 40, 40, 50, 60, 60])
+    ctx = P.NativeContext(N, mods, 2)
+    orc = O.Oracle(N, mods, 2)
+    q0 = mods[0]
+    rng = np.random.default_rng(21)
+    coef = rng.integers(0, q0, (2, 1, N), dtype=np.uint64)
+    coef[0, 0, :4] = [0, q0 >> 1, (q0 >> 1) - 1, q0 - 1]
+    ct = orc.ntt_fwd(coef)
+    Q = len(mods) - 2
+    out = empty((2, Q, N), dev)
+    ctx.mod_raise(to_dev(ct, dev), out)
+    got, want = to_host(out), orc.mod_raise(ct, Q)
+    assert np.array_equal(got, want)
+
+
+def boot_setup(logN, user_levels, special, seed=4):
+    import pyPhantom as ph
+
+    N = 1 << logN
+    stages = ph._default_stages(logN)
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, ph.bootstrap_coeff_bits(user_levels, special=special)))
+    p.set_special_modulus_size(special)
+    p.set_galois_elts(ph.bootstrap_required_galois_elts(logN, stages))
+    ctx = ph.context(p)
+    sk = ph.secret_key(ctx, seed=seed)
+    enc = ph.ckks_encoder(ctx)
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=seed + 1)
+    return ph, ctx, sk, enc, bk
+
+
+@pytest.fixture(scope="module")
+def boot12(dev):
+    return boot_setup(12, 3, 4)
+
+
+@pytest.mark.parametrize("kind", ["real", "complex"])
+def test_bootstrap_refreshes(boot12, kind):
+    ph, ctx, sk, enc, bk = boot12
+    n = enc.slot_count()
+    rng = np.random.default_rng(7)
+    z = rng.uniform(-1, 1, n)
+    if kind == "complex":
+        z = z + 1j * rng.uniform(-1, 1, n)
+    scale = 2.0 ** 40
+    bottom = ctx.size_Q
+    ct = sk.encrypt_symmetric(ctx, enc.encode_complex_vector(ctx, z, scale, bottom), seed=8)
+    out = ph.bootstrap(ctx, enc, ct, bk, scale)
+    assert out.chain_index() == 1 + 2 * 3 + ph.BOOT_EVALMOD_LEVELS
+    got = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, out)))
+    err = np.max(np.abs(got - z))
+    print(f"bootstrap N=2^12 {kind}: max |err| {err:.3e} ({-np.log2(err):.1f} bits)")
+    assert err < 1e-3
+    # the refreshed ciphertext takes a further multiplication
+    sq = ph.rescale_to_next(ctx, ph.multiply_and_relin(ctx, out, out, bk.rlk))
+    got2 = np.array(enc.decode_complex_vector(ctx, sk.decrypt(ctx, sq)))
+    assert np.max(np.abs(got2 - z * z)) < 4e-3
+
+
+def test_mod_raise_api_keeps_message(boot12):
+    """mod_raise_inplace through the encapsulation keys: the raised ciphertext
+    decrypts to m + q0 I with I small and integral."""
+    ph, ctx, sk, enc, bk = boot12
+    z = np.random.default_rng(2).uniform(-1, 1, enc.slot_count())
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, 2.0 ** 40, ctx.size_Q), seed=3)
+    raised = ph.mod_raise_inplace(ctx, ct, bk.small)
+    assert raised.chain_index() == 1
+    # reading the raised plaintext at scale 2^40 after dropping all primes but
+    # q0 gives the message back
+    low = ph.mod_switch_to(ctx, raised, ctx.size_Q)
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, low)))
+    assert np.max(np.abs(got - z)) < 1e-6
