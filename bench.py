@@ -12,7 +12,8 @@ so no step finds its batch cached from the previous one.
 Also reported (same line): inverse NTT limbs/s, HMult + relinearize + rescale
 latency for config 3 (|Q| = 24, alpha = 4, dnum = 6) and for the metric's
 "L=35" variant (|Q| = 35, alpha = 1), and the config-4 BSGS matrix-vector
-product (4096 x 4096 matrix, 64 baby x 64 giant steps, L = 20).
+product (4096 x 4096 matrix, 64 baby x 64 giant steps, L = 20) and the
+config-5 bootstrap (latency and refreshed precision bits).
 
 cpu_baseline: the CPU oracle's forward NTT (oracle/ckks_oracle.c, a C
 restatement of the reference algorithm) on the same workload, single thread,
@@ -165,6 +166,58 @@ def time_bsgs(torch, steps, warmup):
             "giant": d_pad // M}
 
 
+def time_bootstrap(torch, steps, warmup):
+    """BASELINE config 5 through the pyPhantom API: N = 2^16, the 2^15 slots
+    uniform in [-1, 1] (seeded), scale 2^40, chain bootstrap_coeff_bits()
+    (|Q| = 30: q0 60 | 13 x 40 | SlotToCoeff 3 x 50 | EvalMod 10 x 60 |
+    CoeffToSlot 3 x 60, then 6 special primes of 60 bits, dnum = 5), sparse
+    ternary secret h = 192 with the ModRaise under an h = 192 encapsulation
+    secret.  Times whole bootstraps (the ciphertext enters at the bottom of
+    the chain) with the keys and diagonals resident; reports the refreshed
+    precision -log2(max |decrypted - input|)."""
+    import math
+
+    import numpy as np
+
+    import pyPhantom as ph
+
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, ph.bootstrap_coeff_bits()))
+    p.set_special_modulus_size(6)
+    p.set_galois_elts(ph.bootstrap_required_galois_elts(16))
+    ctx = ph.context(p)
+    ph.set_seed(5)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)
+    enc = ph.ckks_encoder(ctx)
+    t0 = time.perf_counter()
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192)
+    torch.cuda.synchronize()
+    t_key = time.perf_counter() - t0
+    rng = np.random.default_rng(5)
+    z = rng.uniform(-1, 1, enc.slot_count())
+    scale = 2.0 ** 40
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, scale, ctx.size_Q))
+    for _ in range(warmup):
+        out = ph.bootstrap(ctx, enc, ct, bk, scale)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        out = ph.bootstrap(ctx, enc, ct, bk, scale)
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = e0.elapsed_time(e1) / steps
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, out)))
+    err = float(np.max(np.abs(got - z)))
+    return {"ms": round(ms, 2), "wall_ms": round(wall_ms, 2), "precision_bits": round(-math.log2(err), 2),
+            "max_abs_err": err, "keygen_s": round(t_key, 1), "galois_keys": len(bk.glk.keys),
+            "levels_left": ctx.size_Ql(out.chain_index()) - 1,
+            "chain": "q0 60 | 13 x 40 | 3 x 50 | 10 x 60 | 3 x 60 + 6 x 60 special", "secret_h": 192}
+
+
 def measured_traffic():
     """HBM bytes per forward NTT from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE of both kernels, scaled by the plain-copy factor);
@@ -207,11 +260,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-hmult", action="store_true")
     ap.add_argument("--no-bsgs", action="store_true")
-    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "hmult35", "bsgs"], default="full",
+    ap.add_argument("--no-boot", action="store_true")
+    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "hmult35", "bsgs", "bootstrap"],
+                    default="full",
                     help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
                          "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
                          "config-3 HMult + relin + rescale; hmult35: only the L=35 variant; bsgs: only the "
-                         "config-4 matrix-vector product")
+                         "config-4 matrix-vector product; bootstrap: only the config-5 bootstrap")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
@@ -233,6 +288,11 @@ def main():
         del batches
         r = time_bsgs(torch, max(2, args.steps // 40), 1)
         log(f"bench: bsgs mode, config 4: {r}")
+        return
+    if args.mode == "bootstrap":
+        del batches
+        r = time_bootstrap(torch, max(2, args.steps // 40), 1)
+        log(f"bench: bootstrap mode, config 5: {r}")
         return
     if args.mode == "hmult":
         del batches
@@ -280,6 +340,12 @@ def main():
         log(f"bench: bsgs config4 {bsgs['ms']} ms, max abs err {bsgs['max_abs_err']:.2e}")
         torch.cuda.empty_cache()
 
+    boot = None
+    if not args.no_boot:
+        boot = time_bootstrap(torch, 3, 1)
+        log(f"bench: bootstrap config5 {boot['ms']} ms, {boot['precision_bits']} bits")
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(mods, args.cpu_seconds)
@@ -309,6 +375,7 @@ def main():
         "ntt_inverse_us": round(ev_inv_ms * 1e3, 2),
         "hmult_relin_rescale": hm,
         "bsgs_matvec_config4": bsgs,
+        "bootstrap_config5": boot,
     }
     print(json.dumps(line), flush=True)
 
