@@ -260,12 +260,27 @@ int pfa_bsgs_apply_giants(const pfa_context *ctx, size_t chain_index, const uint
 
 /* ------------------------------------------------------------ bootstrapping */
 
-/* The raise step of mod_raise_inplace (src/bootstrap.cu): `in` holds `size`
- * polys [size][1][N] at the bottom of the chain (the single prime q0, table
- * row 0, NTT form); out [size][|Q|][N] receives, over every prime of the
- * first data level (chain index 1), the centred lift of each coefficient
- * (in (-q0/2, q0/2]), in NTT form. */
+/* The raise step of mod_raise_inplace (mod_raise_extend_modulus and
+ * mod_raise_signed_tile_kernel, src/bootstrap.cu:37-75, :105-180): `in` holds
+ * `size` polys [size][1][N] at the bottom of the chain (the single prime q0,
+ * table row 0, NTT form); out [size][|Q|][N] receives, over every prime of the
+ * first data level (chain index 1), each coefficient read as the centred
+ * integer (v - q0 when v >= floor(q0 / 2)), in NTT form.  Temporaries:
+ * size x N words of workspace. */
 int pfa_mod_raise(const pfa_context *ctx, const uint64_t *in, size_t size, uint64_t *out, void *stream);
+
+/* Linear combination of ciphertexts with integer constants, the weighted sum
+ * of Chebyshev terms before its one rescale (weighted_sum_chebyshev,
+ * src/evalmod.cu:277-335):
+ *   out[k][l] = sum_t consts[t] ins[t][k][l]  (+ bias on poly 0)  mod q_l
+ * for polys k < size and limbs l < L (table rows 0 .. L-1), NTT form.
+ * ins[t] is [size][in_limbs[t]][N] with in_limbs[t] >= L: a ciphertext at a
+ * lower chain index enters as it is (its first L limbs are read).  consts are
+ * signed; bias points to a signed 128-bit integer as two words (low, high;
+ * two's complement) or is NULL.  n <= 8.  out may be one of the inputs when
+ * that input has exactly L limbs. */
+int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, const uint64_t *const *ins, const size_t *in_limbs,
+                   const int64_t *consts, size_t n, const uint64_t *bias, uint64_t *out, void *stream);
 
 #ifdef __cplusplus
 }

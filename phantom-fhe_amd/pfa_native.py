@@ -63,6 +63,7 @@ SIGNATURES = {
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
     "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
     "pfa_mod_raise": (_i32, [_vp, _vp, _sz, _vp, _vp]),
+    "pfa_ct_lincomb": (_i32, [_vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
 }
 
 
@@ -352,6 +353,27 @@ class NativeContext:
         call("pfa_bsgs_apply_giants", self._h, chain_index, ptr(tiled), bp, M, G,
              ptr(key) if key is not None else None, key.shape[0] if key is not None else 0, ptr(out),
              stream or stream_of(tiled))
+
+    def ct_lincomb(self, L, ins, consts, out, bias=None, stream=None):
+        """out [size][L][N] = sum_t consts[t] ins[t] (+ bias on poly 0); ins are
+        [size][L_t][N] tensors with L_t >= L; consts Python ints in int64 range,
+        bias a Python int in the signed 128-bit range or None."""
+        n = len(ins)
+        size = out.shape[0]
+        for t in ins:
+            if t.shape[0] != size or t.shape[2] != out.shape[2] or not t.is_contiguous():
+                raise ValueError("inputs must be contiguous [size][L_t][N] like the output")
+        ip = (C.c_void_p * max(n, 1))(*[ptr(t) for t in ins])
+        il = (C.c_size_t * max(n, 1))(*[t.shape[1] for t in ins])
+        kc = (C.c_int64 * max(n, 1))(*[int(k) for k in consts])
+        bp = None
+        if bias is not None:
+            b = int(bias)
+            if not -(1 << 127) <= b < (1 << 127):
+                raise ValueError("bias out of the signed 128-bit range")
+            b &= (1 << 128) - 1
+            bp = (C.c_uint64 * 2)(b & 0xFFFFFFFFFFFFFFFF, b >> 64)
+        call("pfa_ct_lincomb", self._h, L, size, ip, il, kc, n, bp, ptr(out), stream or stream_of(out))
 
     def mod_raise(self, ct_bottom, out, stream=None):
         """ct_bottom [size][1][N] mod q0 -> out [size][|Q|][N], centred lift (NTT form)."""

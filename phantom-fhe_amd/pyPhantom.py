@@ -1372,13 +1372,22 @@ def _default_stages(log_n: int):
 
 def _const_plain(ctx: context, value: complex, scale: float, chain: int) -> plaintext:
     """The constant `value` in every slot, exactly: coefficient 0 = Re(value) scale
-    and coefficient N/2 = Im(value) scale (X^(N/2) is i at every slot)."""
-    c = np.zeros(ctx.N, dtype=np.int64)
-    c[0] = int(round(complex(value).real * scale))
-    c[ctx.N // 2] = int(round(complex(value).imag * scale))
+    and coefficient N/2 = Im(value) scale (X^(N/2) is i at every slot).  A real
+    constant is the same residue at every NTT point, so it is written directly."""
+    value = complex(value)
     L = ctx.size_Ql(chain)
     pt = plaintext()
-    pt.data, pt._chain_index, pt._scale = ctx._ntt(ctx._signed_to_rns(c, L), L), chain, float(scale)
+    pt._chain_index, pt._scale = chain, float(scale)
+    re = int(round(value.real * scale))
+    if value.imag == 0:
+        t = _torch()
+        r = np.array([re % q for q in ctx.moduli[:L]], dtype=np.uint64)
+        pt.data = t.from_numpy(r).to(ctx.dev).view(L, 1).expand(L, ctx.N).contiguous()
+        return pt
+    c = np.zeros(ctx.N, dtype=np.int64)
+    c[0] = re
+    c[ctx.N // 2] = int(round(value.imag * scale))
+    pt.data = ctx._ntt(ctx._signed_to_rns(c, L), L)
     return pt
 
 
@@ -1428,28 +1437,44 @@ class bootstrap_key:
         self.rlk = None
         self.c2s = None
         self.s2c = None
-        self.c2s_pts = []   # per layer: {giant: [(baby, plaintext)]}
+        self.c2s_pts = []   # per layer: a _LayerPlan
         self.s2c_pts = []
         self.cheb = None
         self.K, self.r = BOOT_K, BOOT_R
 
 
-def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1):
+class _LayerPlan:
+    """One transform layer, ready for pfa_bsgs_mac: the baby offsets b (in
+    units), the giant indices g, and the diagonal plaintexts as a [G][M] grid
+    (a shared zero plaintext where (g, b) has no diagonal)."""
+
+    def __init__(self, babies, giants, grid, scale, zero):
+        self.babies, self.giants, self.grid, self.scale, self.zero = babies, giants, grid, scale, zero
+
+
+def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1) -> _LayerPlan:
     """Layer i's diagonals, each pre-rotated by minus its giant step, encoded
     at `chain` with the scale of the prime the following rescale drops,
     divided by scale_div (a power of two, so the scale stays exact)."""
     n1, groups, span = lt.baby_giant(i)
     L = ctx.size_Ql(chain)
     scale = float(ctx.moduli[L - 1]) / scale_div
-    out = {}
-    for g, terms in groups.items():
+    babies = sorted({b for terms in groups.values() for b, _ in terms})
+    giants = sorted(groups)
+    zero = None
+    grid = []
+    for g in giants:
         shift = g * n1 * lt.units[i]
-        lst = []
-        for b, d in terms:
-            v = np.roll(lt.layers[i][d % lt.n] * factor, shift)
-            lst.append((b, enc.encode_complex_vector(ctx, v, scale, chain)))
-        out[g] = lst
-    return out
+        have = {b: d for b, d in groups[g]}
+        for b in babies:
+            if b in have:
+                v = np.roll(lt.layers[i][have[b] % lt.n] * factor, shift)
+                grid.append(enc.encode_complex_vector(ctx, v, scale, chain).data)
+            else:
+                if zero is None:
+                    zero = ctx._empty(L, ctx.N).zero_()
+                grid.append(zero)
+    return _LayerPlan(babies, giants, grid, scale, zero)
 
 
 def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secret_key,
@@ -1497,24 +1522,26 @@ def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secr
 
 
 def _apply_layer(ctx, ct: ciphertext, lt: _LTLayers, pts, i: int, glk, rescale: bool = True) -> ciphertext:
-    """sum_d D_d . rot(ct, d) by baby steps (hoisted) and giant steps.  The
-    giant rotations and the sum run before the one rescale, where the scale is
-    q_drop times larger and their key-switching noise q_drop times smaller
-    next to it."""
-    n1, groups, span = lt.baby_giant(i)
+    """sum_d D_d . rot(ct, d) by baby steps (hoisted rotations) and giant steps:
+    one pfa_bsgs_mac forms every giant's sum of diagonal x baby products, the
+    giant rotations follow.  The giant rotations and the sum run before the
+    one rescale, where the scale is q_drop times larger and their
+    key-switching noise q_drop times smaller next to it."""
+    plan = pts[i]
+    n1, _, _ = lt.baby_giant(i)
     unit = lt.units[i]
-    babies = sorted({b for terms in groups.values() for b, _ in terms})
     rotated = {0: ct}
-    steps = [b * unit for b in babies if b]
+    steps = [b * unit for b in plan.babies if b]
     if steps:
-        for b, r in zip([b for b in babies if b], hoist_rotations(ctx, ct, glk, steps)):
+        for b, r in zip([b for b in plan.babies if b], hoist_rotations(ctx, ct, glk, steps)):
             rotated[b] = r
+    L = ctx.size_Ql(ct.chain_index())
+    parts = ctx._empty(len(plan.giants), 2, L, ctx.N)
+    ctx.native.bsgs_mac(ct.chain_index(), plan.grid, [rotated[b].data for b in plan.babies],
+                        [parts[k] for k in range(len(plan.giants))])
     acc = None
-    for g, terms in sorted(pts[i].items()):
-        part = None
-        for b, pt in terms:
-            term = multiply_plain(ctx, rotated[b], pt)
-            part = term if part is None else add(ctx, part, term)
+    for k, g in enumerate(plan.giants):
+        part = ct._like(parts[k], scale=ct.scale() * plan.scale)
         if g:
             part = rotate(ctx, part, _signed_step(g * n1 * unit, lt.n), glk)
         acc = part if acc is None else add(ctx, acc, part)
@@ -1565,40 +1592,6 @@ def mod_raise_inplace(context: context, ct: ciphertext, bk) -> ciphertext:
     return apply_kswitch(context, ct._like(out, chain=1), small.ksk_to_dense)
 
 
-class _ExactScale:
-    """Ciphertext arithmetic that lands on exact target scales (see above)."""
-
-    def __init__(self, ctx, rlk):
-        self.ctx, self.rlk = ctx, rlk
-
-    def q_drop(self, chain):
-        return self.ctx.moduli[self.ctx.size_Ql(chain) - 1]
-
-    def down(self, ct, chain):
-        return mod_switch_to(self.ctx, ct, chain) if ct.chain_index() < chain else ct
-
-    def mul(self, a, b):
-        c = max(a.chain_index(), b.chain_index())
-        r = rescale_to_next(self.ctx, multiply_and_relin(self.ctx, self.down(a, c), self.down(b, c), self.rlk))
-        return r
-
-    def add_const(self, ct, value):
-        return add_plain(self.ctx, ct, _const_plain(self.ctx, value, ct.scale(), ct.chain_index()))
-
-    def mul_const_to(self, ct, value, target_scale, target_chain):
-        """value * ct at exactly target_scale, target_chain (ct above target_chain)."""
-        ct = self.down(ct, target_chain - 1)
-        s = target_scale * self.q_drop(target_chain - 1) / ct.scale()
-        r = rescale_to_next(self.ctx, multiply_plain(self.ctx, ct, _const_plain(self.ctx, value, s, target_chain - 1)))
-        r.set_scale(target_scale)
-        return r
-
-    def match(self, ct, target_scale, target_chain):
-        if ct.scale() == target_scale:
-            return self.down(ct, target_chain)
-        return self.mul_const_to(ct, 1.0, target_scale, target_chain)
-
-
 def evalmod_chebyshev(K: int = BOOT_K, r: int = BOOT_R, deg: int = BOOT_DEG) -> np.ndarray:
     """Chebyshev coefficients (interpolation at the deg + 1 Chebyshev nodes) of
     cos(2 pi (K t - 1/4) / 2^r) on [-1, 1]; r double angles c <- 2 c^2 - 1 then
@@ -1630,46 +1623,72 @@ def _cheb_depth(deg: int) -> int:
 
 def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     """cos(2 pi (K t - 1/4) / 2^r) by Chebyshev (Paterson-Stockmeyer splitting at
-    powers of two), then r double angles: sin(2 pi K t) for t in [-1, 1]."""
-    E = _ExactScale(ctx, bk.rlk)
+    powers of two, src/evalmod.cu:196-335 for the pattern), then r double
+    angles: sin(2 pi K t) for t in [-1, 1].
+
+    Every weighted sum is one pfa_ct_lincomb over the Chebyshev terms at their
+    own levels, with the integer weights round(c_j S q / scale_j) that land it
+    at the exact scale S q, followed by one rescale to S: scales never drift
+    and no addition mixes them.  T_k = 2 T_a T_b - T_1 and 2 y^2 - 1 are formed
+    the same way before their rescale."""
+    nat = ctx.native
+    N = ctx.N
     T = {1: ct}
+
+    def q_drop(chain):
+        return ctx.moduli[ctx.size_Ql(chain) - 1]
+
+    def lincomb(terms, bias, chain, scale):
+        L = ctx.size_Ql(chain)
+        for _, k in terms:
+            if not -(1 << 63) <= k < (1 << 63):
+                raise ValueError("Chebyshev weight outside int64")
+        out = ctx._empty(2, L, N)
+        nat.ct_lincomb(L, [c.data for c, _ in terms], [k for _, k in terms], out, bias)
+        return ct._like(out, chain=chain, scale=scale)
+
+    def product(a, b):
+        c = max(a.chain_index(), b.chain_index())
+        return multiply_and_relin(ctx, mod_switch_to(ctx, a, c), mod_switch_to(ctx, b, c), bk.rlk)
 
     def cheb_T(k):
         if k in T:
             return T[k]
         if k % 2 == 0:
-            h = cheb_T(k // 2)
-            sq = E.mul(h, h)
-            T[k] = E.add_const(add(ctx, sq, sq), -1.0)
+            p = product(cheb_T(k // 2), cheb_T(k // 2))
+            pre = lincomb([(p, 2)], -round(p.scale()), p.chain_index(), p.scale())
         else:
-            a, b = (k + 1) // 2, (k - 1) // 2
-            p = E.mul(cheb_T(a), cheb_T(b))
-            two = add(ctx, p, p)
-            T[k] = sub(ctx, two, E.match(cheb_T(1), two.scale(), two.chain_index()))
+            p = product(cheb_T((k + 1) // 2), cheb_T((k - 1) // 2))
+            t1 = cheb_T(1)
+            pre = lincomb([(p, 2), (t1, -round(p.scale() / t1.scale()))], None, p.chain_index(), p.scale())
+        T[k] = rescale_to_next(ctx, pre)
         return T[k]
 
     def evaluate(c, target_scale, target_chain):
         deg = len(c) - 1
+        chain = target_chain - 1
+        q = q_drop(chain)
         if deg < 8:
-            acc = None
+            terms = []
             for j in range(1, deg + 1):
                 if c[j] != 0.0:
-                    term = E.mul_const_to(cheb_T(j), c[j], target_scale, target_chain)
-                    acc = term if acc is None else add(ctx, acc, term)
-            if acc is None:
-                acc = E.mul_const_to(cheb_T(1), 0.0, target_scale, target_chain)
-            return E.add_const(acc, c[0])
+                    t = cheb_T(j)
+                    terms.append((t, round(c[j] * target_scale * q / t.scale())))
+            pre = lincomb(terms, round(c[0] * target_scale * q), chain, target_scale * q)
+            r = rescale_to_next(ctx, pre)
+            r.set_scale(target_scale)
+            return r
         m, hi, lo = _cheb_split(c)
-        Tm = E.down(cheb_T(m), target_chain - 1)
-        hi_ct = evaluate(hi, target_scale * E.q_drop(target_chain - 1) / Tm.scale(), target_chain - 1)
+        Tm = mod_switch_to(ctx, cheb_T(m), chain)
+        hi_ct = evaluate(hi, target_scale * q / Tm.scale(), chain)
         prod = rescale_to_next(ctx, multiply_and_relin(ctx, Tm, hi_ct, bk.rlk))
         prod.set_scale(target_scale)
         return add(ctx, prod, evaluate(lo, target_scale, target_chain))
 
     y = evaluate(list(bk.cheb), ct.scale(), ct.chain_index() + _cheb_depth(len(bk.cheb) - 1))
     for _ in range(bk.r):
-        sq = E.mul(y, y)
-        y = E.add_const(add(ctx, sq, sq), -1.0)
+        p = product(y, y)
+        y = rescale_to_next(ctx, lincomb([(p, 2)], -round(p.scale()), p.chain_index(), p.scale()))
     return y
 
 

@@ -3,6 +3,8 @@
 * pfa_mod_raise is bit-exact against the oracle's restatement of
   mod_raise_signed_tile_kernel (src/bootstrap.cu:37-75), itself pinned against
   Python integers in tests/test_bootstrap_math.py.
+* pfa_ct_lincomb (the integer-weighted sums of EvalMod) is bit-exact against
+  Python integers.
 * End to end, the reference's acceptance test is the bar: decoded slots after
   bootstrap within 1e-3 of the input (test/ckks_engine_test.cu:182-188); the
   refreshed ciphertext must also take a further multiplication.
@@ -33,6 +35,53 @@ def test_mod_raise_matches_oracle(dev):
     ctx.mod_raise(to_dev(ct, dev), out)
     got, want = to_host(out), orc.mod_raise(ct, Q)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bias", [None, 0, (1 << 119) + 12345, -(1 << 126) + 7])
+def test_ct_lincomb_matches_integers(dev, bias):
+    """pfa_ct_lincomb against Python integers: inputs at several limb counts,
+    signed constants up to the int64 ends, signed 128-bit biases."""
+    import pfa_native as P
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 40, 50, 60, 60, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    rng = np.random.default_rng(31)
+    L = 3
+    limbs = [3, 5, 4, 3]
+    ins = [np.stack([np.stack([rng.integers(0, q, N, dtype=np.uint64) for q in mods[:Lt]]) for _ in range(2)])
+           for Lt in limbs]
+    consts = [2, -(1 << 63), (1 << 63) - 1, -987654321987]
+    out = empty((2, L, N), dev)
+    ctx.ct_lincomb(L, [to_dev(x, dev) for x in ins], consts, out, bias)
+    got = to_host(out)
+    for k in range(2):
+        for l in range(L):
+            q = mods[l]
+            acc = [0] * N
+            for x, c in zip(ins, consts):
+                row = x[k, l].tolist()
+                acc = [(a + c * v) for a, v in zip(acc, row)]
+            if k == 0 and bias is not None:
+                acc = [a + bias for a in acc]
+            assert got[k, l].tolist() == [a % q for a in acc], (k, l)
+
+
+def test_ct_lincomb_in_place(dev):
+    import pfa_native as P
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 40, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    rng = np.random.default_rng(5)
+    x = np.stack([np.stack([rng.integers(0, q, N, dtype=np.uint64) for q in mods[:2]]) for _ in range(2)])
+    t = to_dev(x, dev)
+    ctx.ct_lincomb(2, [t], [-3], t, -5)
+    got = to_host(t)
+    for k in range(2):
+        for l in range(2):
+            q = mods[l]
+            assert got[k, l].tolist() == [(-3 * v - (5 if k == 0 else 0)) % q for v in x[k, l].tolist()]
 
 
 def boot_setup(logN, user_levels, special, seed=4):
