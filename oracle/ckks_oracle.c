@@ -10,7 +10,9 @@
  * inputs < 2^126) are exact, so canonical residues of the same formulas are
  * bit-identical to what the reference computes.
  *
- * Parity pinning of each function lives in tests/test_oracle_*.py.
+ * Parity pinning of each function lives in tests/test_oracle.py (closed
+ * forms, brute force, big-integer CRT identities) and tests/test_golden.py
+ * (vectors computed independently in plain Python integers).
  */
 #include "ckks_oracle.h"
 
