@@ -124,6 +124,21 @@ int pfa_relinearize(const pfa_context *ctx, size_t chain_index, const uint64_t *
 int pfa_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *in, size_t size, uint64_t *out,
                 void *stream);
 
+/* multiply_and_relin_inplace then rescale_to_next_inplace (src/evaluate.cu:1061-1104,
+ * :1582-1602) as one call: out [2][|Ql|-1][N] = rescale(multiply_and_relin(a, b)),
+ * bit-identical to pfa_multiply_and_relin followed by pfa_rescale.  The ModDown
+ * output is never formed: its last limb's coefficients come from the ModDown
+ * inputs and the two forward NTTs of the rescale and the ModDown merge by
+ * linearity.  out must not alias a or b; |Ql| >= 2. */
+int pfa_multiply_relin_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
+                               const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream);
+
+/* relinearize_inplace then rescale_to_next_inplace (src/evaluate.cu:1342-1374,
+ * :1582-1602) as one call: ct3 [3][|Ql|][N] -> out [2][|Ql|-1][N], bit-identical to
+ * pfa_relinearize followed by pfa_rescale.  out must not alias ct3. */
+int pfa_relinearize_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *ct3, const uint64_t *rlk,
+                            size_t key_dnum, uint64_t *out, void *stream);
+
 /* get_elt_from_step (include/galois.cuh:16-49): 5^step mod 2N, step 0 -> 2N-1. */
 int pfa_galois_elt_from_step(int step, uint64_t poly_degree, uint32_t *elt);
 

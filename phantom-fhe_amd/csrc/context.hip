@@ -245,9 +245,10 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     const uint32_t alpha = c.P;
 
     // ModDown constants (src/rns.cu:107-138, src/rns.cu:193-194)
+    std::vector<ulonglong2> md_scale_host;
     {
         std::vector<ulonglong2> sc(alpha), pinv(c.Q), pinv_p(c.Q), pq(QP), bc((size_t)alpha * c.Q * 2),
-            unit((size_t)c.Q * 2);
+            unit((size_t)c.Q * 2), mdr((size_t)(alpha + 1) * c.Q * 2);
         std::vector<uint64_t> mat((size_t)alpha * c.Q);
         for (uint32_t j = 0; j < alpha; ++j) {
             const uint64_t p = Pm[j];
@@ -267,6 +268,14 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             pq[i] = shoup_pair(pm, q);
             unit[(size_t)i * 2] = ntt_pair(1 % q, q);
             unit[(size_t)i * 2 + 1] = ntt_pair(two32_mod(q), q);
+            mdr[(size_t)i * 2] = unit[(size_t)i * 2];
+            mdr[(size_t)i * 2 + 1] = unit[(size_t)i * 2 + 1];
+            for (uint32_t j = 0; j < alpha; ++j) {
+                const uint64_t g = invmod(Pm[j] % q, q);
+                const size_t k = ((size_t)(1 + j) * c.Q + i) * 2;
+                mdr[k] = ntt_pair(g, q);
+                mdr[k + 1] = ntt_pair(mulmod(g, two32_mod(q), q), q);
+            }
         }
         for (uint32_t j = 0; j < alpha; ++j) pq[c.Q + j] = ulonglong2{0, 0};
         c.moddown_scale = c.upload(sc);
@@ -276,6 +285,8 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         c.moddown_bc = c.upload(bc);
         c.unit_bc = c.upload(unit);
         c.pinv_p = c.upload(pinv_p);
+        c.mdr_bc = c.upload(mdr);
+        md_scale_host = sc;
     }
 
     encoder_init(c);
@@ -319,6 +330,18 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         }
         lv.rescale_inv = c.upload(rs);
         lv.rescale_inv_p = c.upload(rsp);
+        {
+            const uint64_t ql = Qm[Ql - 1];
+            std::vector<ulonglong2> ms(alpha + 1);
+            std::vector<uint64_t> gl(alpha);
+            ms[0] = ntt_pair(1 % ql, ql);
+            for (uint32_t j = 0; j < alpha; ++j) {
+                ms[1 + j] = md_scale_host[j];
+                gl[j] = invmod(Pm[j] % ql, ql);
+            }
+            lv.mdr_scale = c.upload(ms);
+            lv.mdr_glast = c.upload(gl);
+        }
     }
 }
 

@@ -79,7 +79,16 @@ struct BconvCols {
     uint32_t skip;          // 1 for ModUp
     uint32_t bc_gstride;    // pairs between groups' factor blocks
     uint32_t bc_istride;    // pairs between one input's consecutive target factors... see bc_of
+    // table row of input 0 when it differs from the run in_row0 + i (the fused
+    // ModDown + rescale puts the rescale's last-limb coefficients first);
+    // inputs i >= 1 then sit at rows in_row0 + i - 1.  ~0u: no such input
+    uint32_t first_row = ~0u;
 };
+
+__device__ __forceinline__ uint32_t bconv_in_row(const BconvCols &a, uint32_t row0, uint32_t i) {
+    if (a.first_row == ~0u) return row0 + i;
+    return i == 0 ? a.first_row : row0 + i - 1;
+}
 
 // factor pair index for (group g, input i, target j): bc[((g * n_in_max + i) * J + j) * 2 + h]
 // (ModUp: per digit; ModDown / rescale: shared by all groups, bc_gstride = 0)
@@ -106,7 +115,7 @@ __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables
             const ulonglong2 f0 = f[0];
             const double w0 = ArithF64::as_f(f0.x), wq0 = ArithF64::as_f(f0.y);
             const uint64_t *src = base + (size_t)i * G::N;
-            const bool wide = t.mod[row0 + i] >= kF64PrimeBound;
+            const bool wide = t.mod[bconv_in_row(a, row0, i)] >= kF64PrimeBound;
             if (units + (wide ? 2u : 1u) > 7u) {
 #pragma unroll
                 for (int e = 0; e < SB::E; e++) ar.reduce(acc[e]);
@@ -192,6 +201,12 @@ struct InnerRows {
     // independent key switches with the same key: member i adds i * the stride
     uint32_t batch = 1;
     uint64_t inter_bstride = 0, c2_bstride = 0, cx_bstride = 0;
+    // ModDown + rescale fusion (batch 1 only): output k of target limb fold_r
+    // (the level's last prime) is written as base_k[fold_r] + acc * fold_f,
+    // fold_f = [P^-1]_q as an integer Shoup pair; ~0u = no folding
+    uint32_t fold_r = ~0u;
+    const uint64_t *fold_base0 = nullptr, *fold_base1 = nullptr;
+    const ulonglong2 *fold_f = nullptr;
 };
 
 // Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
@@ -409,10 +424,24 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
     }
     uint64_t *o0 = a.cx + (size_t)r * G::N + rowoff;
     uint64_t *o1 = o0 + (size_t)a.QlP * G::N;
+    // fold (see InnerRows): e_k = base_k + cx_k [P^-1]_q, the NTT-form limb whose
+    // INTT, less the base conversion of the P limbs times P^-1, is the
+    // coefficient form of the ModDown output's last limb
+    const bool fold = r == a.fold_r;
+    ulonglong2 f{0, 0};
+    const uint64_t *fb0 = a.fold_base0 + (size_t)r * G::N + rowoff;
+    const uint64_t *fb1 = a.fold_base1 + (size_t)r * G::N + rowoff;
+    if (fold) f = *a.fold_f;
+    const uint64_t q = (uint64_t)ar.q;
 #pragma unroll
     for (int e = 0; e < SB::E; e++) {
-        st_stream(&o0[SB::T * e], ar.store(acc0[e]));
-        st_stream(&o1[SB::T * e], ar.store(acc1[e]));
+        uint64_t v0 = ar.store(acc0[e]), v1 = ar.store(acc1[e]);
+        if (fold) {
+            v0 = add_mod(shoup(v0, f.x, f.y, q), fb0[SB::T * e], q);
+            v1 = add_mod(shoup(v1, f.x, f.y, q), fb1[SB::T * e], q);
+        }
+        st_stream(&o0[SB::T * e], v0);
+        st_stream(&o1[SB::T * e], v1);
     }
 }
 
@@ -473,6 +502,9 @@ struct EpiRows {
     uint64_t c_stride;
     uint32_t M, J;
     uint64_t base_stride = 0;
+    // fused ModDown + rescale: when set ([J] pairs in each limb's NTT policy),
+    // out = (c f1 + base - NTT(D)) f instead
+    const ulonglong2 *f1 = nullptr;
 };
 
 template <class A, int S1, int S2>
@@ -493,6 +525,27 @@ __device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, c
     if (bp) bp += (size_t)(m >> 1) * a.base_stride + (size_t)j * G::N + rowoff;
     const ulonglong2 f = a.f[j];
     uint64_t *op = a.out + lo;
+    if (a.f1) {
+        const ulonglong2 f1 = a.f1[j];
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) {
+            uint64_t v;
+            if constexpr (A::kF64) {
+                ar.reduce(x[e]);
+                double d = ar.load(ld_stream(&cp[SB::T * e]));
+                ar.mul(d, f1);
+                d += ar.load(ld_stream(&bp[SB::T * e])) - x[e];
+                ar.mul(d, f);
+                v = ar.store(d);
+            } else {
+                const uint64_t cf = shoup(ld_stream(&cp[SB::T * e]), f1.x, f1.y, ar.q);
+                const uint64_t d = sub_mod(add_mod(cf, ld_stream(&bp[SB::T * e]), ar.q), ar.store(x[e]), ar.q);
+                v = shoup(d, f.x, f.y, ar.q);
+            }
+            st_stream(&op[SB::T * e], v);
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < SB::E; e++) {
         uint64_t v;
@@ -529,6 +582,27 @@ __global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_epi_rows(EpiRows a,
             epi_item<ArithInt, S1, S2>(a, t, ArithInt(q), m, j, k1,
                                        reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH);
         __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ rescale's last limb
+// Fused ModDown + rescale: over M groups of [1 + alpha][N] coefficient-form
+// limbs x (x_0 = INTT(base + cx [P^-1]) of the last limb, x_(1+i) = the scaled
+// INTT of P limb i), x_0 := (x_0 - sum_i x_(1+i) g_i) mod q with
+// g_i = [p_i^-1]_q: the canonical coefficients of the ModDown output's last
+// limb.  128-bit products, one Barrett reduction (alpha < 64 keeps the sum
+// below 2^128 for residues below 2^61).
+__global__ void k_mdr_last(uint64_t *x, const uint64_t *g, const uint64_t *mod, const ulonglong2 *ratio,
+                           uint32_t row, uint32_t alpha, uint32_t N, uint32_t M) {
+    const uint64_t q = mod[row];
+    const ulonglong2 rt = ratio[row];
+    const uint32_t total = M * N;
+    for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const uint32_t m = idx / N, k = idx % N;
+        uint64_t *base = x + (size_t)m * (alpha + 1) * N + k;
+        U128 acc{0, 0};
+        for (uint32_t i = 0; i < alpha; i++) mac(acc, base[(size_t)(i + 1) * N], g[i]);
+        base[0] = sub_mod(base[0], barrett128(acc, q, rt.x, rt.y), q);
     }
 }
 
@@ -585,7 +659,7 @@ void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp and the key-switch inner
 // product against key [dnum][2][QP][N].
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride) {
+                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold) {
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
     const uint64_t LN = (uint64_t)Ql * c.N, IN = (uint64_t)lv.beta * QlP * c.N;
@@ -621,7 +695,62 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.inter_bstride = IN;
     r.c2_bstride = c2_stride;
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
+    if (fold) {
+        require(batch == 1 && fold->base0 && fold->base1 && Ql >= 2, "bad ModDown + rescale fold");
+        r.fold_r = Ql - 1;
+        r.fold_base0 = fold->base0;
+        r.fold_base1 = fold->base1;
+        r.fold_f = c.pinv + (Ql - 1);
+    }
     PFA_FUSED_DISPATCH(launch_inner, r);
+}
+
+// The rescale of base + ModDown(cx) without forming the ModDown output.  With
+// q_l the last prime, v_i the scaled INTT of P limb i and
+// t = INTT(base + cx [P^-1])_(l) - sum_i v_i [p_i^-1]_(q_l) mod q_l (the
+// ModDown output's last limb in coefficient form), for j < l:
+//   out_j = (cx_j [P^-1] + base_j - NTT(sum_i v_i [p_i^-1]_(q_j) + t)) [q_l^-1]
+// which is ModDown's (cx - NTT(delta)) P^-1 + base followed by the rescale's
+// (c - NTT(t mod q_j)) q_l^-1 with the two NTTs merged by linearity.
+void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, const uint64_t *base0,
+                           const uint64_t *base1, uint64_t *out, hipStream_t s) {
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha, J = Ql - 1;
+    require(Ql >= 2, "cannot rescale at the last level");
+    Scratch sc(c, s);
+    uint64_t *x = sc.alloc((size_t)2 * (alpha + 1) * c.N);
+    uint64_t *inter = sc.alloc((size_t)2 * J * c.N);
+    NttLaunch inv{cx + (size_t)(Ql - 1) * c.N, x, (uint64_t)QlP * c.N, (uint64_t)(alpha + 1) * c.N, 2, alpha + 1};
+    inv.start = Ql - 1;
+    inv.split = 1;
+    inv.split_base = c.Q;
+    inv.scale = lv.mdr_scale;
+    ntt_inverse(c, inv, s);
+    hipLaunchKernelGGL(k_mdr_last, dim3((2 * c.N + 255) / 256), dim3(256), 0, s, x, lv.mdr_glast, c.mod, c.ratio,
+                       Ql - 1, alpha, c.N, 2u);
+    PFA_HIP(hipGetLastError());
+    BconvCols b{};
+    b.in = x;
+    b.out = inter;
+    b.bc = c.mdr_bc;
+    b.in_gstride = (uint64_t)(alpha + 1) * c.N;
+    b.out_gstride = (uint64_t)J * c.N;
+    b.groups = 2;
+    b.J = J;
+    b.n_in = alpha + 1;
+    b.n_in_last = alpha + 1;
+    b.in_row0 = c.Q;
+    b.in_row_step = 0;
+    b.first_row = Ql - 1;
+    b.split = 0xffffffffu;
+    b.split_base = 0;
+    b.skip = 0;
+    b.bc_gstride = 0;
+    b.bc_istride = c.Q;
+    PFA_FUSED_DISPATCH(launch_bconv, b);
+    EpiRows e{inter, cx, base0, base1, out, lv.rescale_inv_p, (uint64_t)QlP * c.N, 2, J};
+    e.f1 = c.pinv_p;
+    PFA_FUSED_DISPATCH(launch_epi, e);
 }
 
 // cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx): poly 2i + k adds

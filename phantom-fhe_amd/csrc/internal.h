@@ -78,6 +78,11 @@ struct Level {
     // [beta][alpha][QlP][2] = (m, [m 2^32]_{p_r}); rescale factor as NTT pairs
     ulonglong2 *modup_bc = nullptr;
     ulonglong2 *rescale_inv_p = nullptr;
+    // fused ModDown + rescale, with q_l = this level's last prime:
+    // INTT scales [1 + alpha] (unit pair of q_l, then the ModDown scales) and
+    // [p_i^-1]_{q_l} for i < alpha (plain residues)
+    ulonglong2 *mdr_scale = nullptr;
+    uint64_t *mdr_glast = nullptr;
 };
 
 // Device workspace of one (host thread, stream): chunks grown on demand and
@@ -123,6 +128,10 @@ struct Ctx {
     ulonglong2 *moddown_bc = nullptr;
     ulonglong2 *unit_bc = nullptr;
     ulonglong2 *pinv_p = nullptr;
+    // fused ModDown + rescale base conversion [1 + P][Q][2]: input 0 (the
+    // rescale's last limb) with (1, [2^32]_{q_i}), input 1 + j with
+    // ([p_j^-1]_{q_i}, [p_j^-1 2^32]_{q_i}), NTT-policy pairs
+    ulonglong2 *mdr_bc = nullptr;
     // key construction: [P]_{q_i} Shoup pairs over all QP rows (0 on P rows)
     ulonglong2 *pmodq = nullptr;
     uint32_t *slot_perm = nullptr;   // [N/2] CKKS slot j -> DFT index (5^j mod 2N - 1) / 4
@@ -194,8 +203,18 @@ bool xcd_round_robin(const Ctx &c);
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp then the inner product with key.
 // With batch > 1, member i reads c2 + i c2_stride and writes cx + i cx_stride
 // (default 2 QlP N), all with the same key.
+// With fold (batch 1), limb Ql - 1 of output k is written as
+// fold->base_k[Ql - 1] + cx_k[Ql - 1] [P^-1]: the input fused_moddown_rescale expects.
+struct KsFold {
+    const uint64_t *base0 = nullptr, *base1 = nullptr;
+};
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0);
+                       hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0,
+                       const KsFold *fold = nullptr);
+// cx [2][QlP][N] from fused_modup_inner with a fold over base -> out [2][Ql-1][N]
+// = rescale(base + ModDown(cx)), bit-identical to fused_moddown then fused_rescale.
+void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, const uint64_t *base0,
+                           const uint64_t *base1, uint64_t *out, hipStream_t s);
 // cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx): poly 2i + k adds
 // base_k + i base_stride; the bases may alias out's polys or be null.
 void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,

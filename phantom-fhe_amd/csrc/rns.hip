@@ -263,6 +263,22 @@ void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64
     fused_moddown(c, chain, cx, 2, out, base.p[0], base.p[1], s);
 }
 
+// out [2][Ql-1][N] = rescale(base + KS(c2)): bit-identical to op_keyswitch
+// followed by op_rescale, without forming the key-switched ciphertext
+void op_keyswitch_rescale(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum,
+                          const uint64_t *base0, const uint64_t *base1, uint64_t *out, hipStream_t s) {
+    check_chain(c, chain);
+    const Level &lv = c.level(chain);
+    require(key != nullptr, "null key");
+    require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
+    require(lv.Ql >= 2, "cannot rescale at the last level");
+    Scratch sc(c, s);
+    uint64_t *cx = sc.alloc((size_t)2 * (lv.Ql + c.P) * c.N);
+    const KsFold fold{base0, base1};
+    fused_modup_inner(c, chain, c2, key, cx, s, 1, 0, 0, &fold);
+    fused_moddown_rescale(c, chain, cx, base0, base1, out, s);
+}
+
 void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1,
                uint64_t *d2, hipStream_t s) {
     check_chain(c, chain);
@@ -359,6 +375,36 @@ int pfa_relinearize(const pfa_context *ctx, size_t chain_index, const uint64_t *
         const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
         op_keyswitch(c, (uint32_t)chain_index, ct3 + 2 * LN, rlk, key_dnum, out, Bases{{ct3, ct3 + LN}},
                      as_stream(stream));
+    });
+}
+
+int pfa_multiply_relin_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
+                               const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && b && out && rlk, "null argument");
+        require(out != a && out != b, "output must not alias an input");
+        check_chain(c, chain_index);
+        require(c.size_Ql((uint32_t)chain_index) >= 2, "cannot rescale at the last level");
+        const hipStream_t s = as_stream(stream);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        Scratch sc(c, s);
+        uint64_t *d = sc.alloc(3 * LN);
+        op_tensor(c, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s);
+        op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s);
+    });
+}
+
+int pfa_relinearize_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *ct3, const uint64_t *rlk,
+                            size_t key_dnum, uint64_t *out, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct3 && out && rlk, "null argument");
+        require(out != ct3, "output must not alias the input");
+        check_chain(c, chain_index);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        op_keyswitch_rescale(c, (uint32_t)chain_index, ct3 + 2 * LN, rlk, key_dnum, ct3, ct3 + LN, out,
+                             as_stream(stream));
     });
 }
 

@@ -41,6 +41,8 @@ SIGNATURES = {
     "pfa_multiply_and_relin": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
     "pfa_relinearize": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
     "pfa_rescale": (_i32, [_vp, _sz, _vp, _sz, _vp, _vp]),
+    "pfa_multiply_relin_rescale": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_relinearize_rescale": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
     "pfa_galois_elt_from_step": (_i32, [_i32, _u64, C.POINTER(C.c_uint32)]),
     "pfa_apply_galois_ntt": (_i32, [_vp, _u32, _vp, _vp, _sz, _vp]),
     "pfa_apply_galois": (_i32, [_vp, _sz, _vp, _u32, _vp, _sz, _vp]),
@@ -223,6 +225,14 @@ class NativeContext:
 
     def relinearize(self, chain_index, ct3, rlk, out, stream=None):
         call("pfa_relinearize", self._h, chain_index, ptr(ct3), ptr(rlk), rlk.shape[0], ptr(out),
+             stream or stream_of(ct3))
+
+    def multiply_relin_rescale(self, chain_index, a, b, rlk, out, stream=None):
+        call("pfa_multiply_relin_rescale", self._h, chain_index, ptr(a), ptr(b), ptr(rlk), rlk.shape[0], ptr(out),
+             stream or stream_of(a))
+
+    def relinearize_rescale(self, chain_index, ct3, rlk, out, stream=None):
+        call("pfa_relinearize_rescale", self._h, chain_index, ptr(ct3), ptr(rlk), rlk.shape[0], ptr(out),
              stream or stream_of(ct3))
 
     def rescale(self, chain_index, ct, out, stream=None):

@@ -774,6 +774,35 @@ def rescale_to_next(ctx: context, ct: ciphertext) -> ciphertext:
     return ct._like(out, chain=ct.chain_index() + 1, scale=ct.scale() / ctx.moduli[L - 1])
 
 
+def multiply_and_relin_rescale(ctx: context, a: ciphertext, b: ciphertext, rlk: relin_key) -> ciphertext:
+    """rescale_to_next(multiply_and_relin(a, b)) as one native call
+    (pfa_multiply_relin_rescale), bit-identical to the two calls: the
+    relinearized product at full level is never formed.  The reference has no
+    single call for this pair (src/evaluate.cu:1061-1104 then :1582-1602)."""
+    _check_same(a, b)
+    if a.size() != 2 or b.size() != 2:
+        raise ValueError("multiply_and_relin expects size-2 ciphertexts")
+    L = ctx.size_Ql(a.chain_index())
+    if L < 2:
+        raise ValueError("end of modulus switching chain reached")
+    out = ctx._empty(2, L - 1, ctx.N)
+    ctx.native.multiply_relin_rescale(a.chain_index(), a.data, b.data, rlk.data, out)
+    return a._like(out, chain=a.chain_index() + 1, scale=a.scale() * b.scale() / ctx.moduli[L - 1])
+
+
+def relinearize_rescale(ctx: context, ct: ciphertext, rlk: relin_key) -> ciphertext:
+    """rescale_to_next(relinearize(ct)) as one native call (pfa_relinearize_rescale),
+    bit-identical to the two calls."""
+    if ct.size() != 3:
+        raise ValueError("relinearize expects a size-3 ciphertext")
+    L = ctx.size_Ql(ct.chain_index())
+    if L < 2:
+        raise ValueError("end of modulus switching chain reached")
+    out = ctx._empty(2, L - 1, ctx.N)
+    ctx.native.relinearize_rescale(ct.chain_index(), ct.data, rlk.data, out)
+    return ct._like(out, chain=ct.chain_index() + 1, scale=ct.scale() / ctx.moduli[L - 1])
+
+
 def mod_switch_to_next(ctx: context, obj):
     """CKKS modulus drop: remove the last prime, keep the scale."""
     chain = obj.chain_index()
@@ -1681,7 +1710,7 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
         m, hi, lo = _cheb_split(c)
         Tm = mod_switch_to(ctx, cheb_T(m), chain)
         hi_ct = evaluate(hi, target_scale * q / Tm.scale(), chain)
-        prod = rescale_to_next(ctx, multiply_and_relin(ctx, Tm, hi_ct, bk.rlk))
+        prod = multiply_and_relin_rescale(ctx, Tm, hi_ct, bk.rlk)
         prod.set_scale(target_scale)
         return add(ctx, prod, evaluate(lo, target_scale, target_chain))
 

@@ -183,6 +183,10 @@ def test_mul_relin_rescale_decodes_within_1e6(dev, logN):
     assert np.max(np.abs(d3 - a * b)) < TOL
     r = ph.rescale_to_next(ctx, ph.relinearize(ctx, c3, rlk))
     assert np.array_equal(to_host(r.data), to_host(c.data))
+    # the fused single calls give the same ciphertext (residues, level and scale)
+    for f in (ph.multiply_and_relin_rescale(ctx, ca, cb, rlk), ph.relinearize_rescale(ctx, c3, rlk)):
+        assert np.array_equal(to_host(f.data), to_host(c.data))
+        assert f.chain_index() == c.chain_index() and f.scale() == c.scale()
 
 
 def test_rotations_and_conjugation(dev):

@@ -39,11 +39,11 @@ def chain_bits(nq, alpha):
 
 
 class Setup:
-    def __init__(self, logN, nq, alpha, seed=0):
+    def __init__(self, logN, nq, alpha, seed=0, bits=None):
         import pfa_native as P
 
         self.N = 1 << logN
-        self.mods = O.create_coeff_modulus(self.N, chain_bits(nq, alpha))
+        self.mods = O.create_coeff_modulus(self.N, bits or chain_bits(nq, alpha))
         self.nq, self.alpha = nq, alpha
         self.ctx = P.NativeContext(self.N, self.mods, alpha)
         self.orc = O.Oracle(self.N, self.mods, alpha)
@@ -173,6 +173,66 @@ def test_multiply_and_relin_config3(dev):
     st.ctx.multiply_and_relin(1, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
     got, want = to_host(out), st.orc.multiply_and_relin(1, a, b, key, threads=8)
     assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+# (logN, nq, alpha, chain, bits): the fused rescale's last prime in the FP64
+# policy (50-bit) and in the integer policy (60-bit), |Ql| = 2 (one limb left)
+FUSED_SHAPES = [(logN, nq, alpha, chain, None) for logN, nq, alpha, chain in SHAPES] + [
+    (12, 4, 2, 1, [60] * 6),
+    (13, 6, 3, 2, [60, 50, 50, 50, 60, 50, 60, 60, 60]),
+    (12, 3, 1, 2, None),
+]
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain,bits", FUSED_SHAPES)
+def test_multiply_relin_rescale(dev, logN, nq, alpha, chain, bits):
+    """pfa_multiply_relin_rescale equals multiply_and_relin followed by rescale."""
+    st = Setup(logN, nq, alpha, seed=11, bits=bits)
+    Ql = st.orc.size_Ql(chain)
+    a, b = st.ct(chain), st.ct(chain)
+    key = st.key()
+    out = empty((2, Ql - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    want = st.orc.rescale(chain, st.orc.multiply_and_relin(chain, a, b, key, threads=8), threads=8)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("logN,nq,alpha,chain,bits", FUSED_SHAPES[:3] + FUSED_SHAPES[-3:])
+def test_relinearize_rescale(dev, logN, nq, alpha, chain, bits):
+    """pfa_relinearize_rescale equals relinearize followed by rescale."""
+    st = Setup(logN, nq, alpha, seed=12, bits=bits)
+    Ql = st.orc.size_Ql(chain)
+    ct3 = st.ct(chain, 3)
+    key = st.key()
+    out = empty((2, Ql - 1, st.N), dev)
+    st.ctx.relinearize_rescale(chain, to_dev(ct3, dev), to_dev(key, dev), out)
+    want = st.orc.rescale(chain, st.orc.keyswitch(chain, ct3[:2], ct3[2], key, threads=8), threads=8)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_multiply_relin_rescale_config3(dev):
+    """The fused path at the BASELINE config-3 shape (N = 2^16, |Q| = 24, alpha = 4)."""
+    st = Setup(16, 24, 4, seed=13)
+    a, b = st.ct(1), st.ct(1)
+    key = st.key()
+    out = empty((2, 23, st.N), dev)
+    st.ctx.multiply_relin_rescale(1, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    want = st.orc.rescale(1, st.orc.multiply_and_relin(1, a, b, key, threads=8), threads=8)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_multiply_relin_rescale_errors(dev):
+    st = Setup(12, 3, 1)
+    key = to_dev(st.key(), dev)
+    a = to_dev(st.ct(3), dev)
+    with pytest.raises(ValueError):  # one limb left: nothing to rescale
+        st.ctx.multiply_relin_rescale(3, a, a, key, empty((2, 1, st.N), dev))
+    a1 = to_dev(st.ct(1), dev)
+    with pytest.raises(ValueError):  # the output may not alias an input
+        st.ctx.multiply_relin_rescale(1, a1, a1, key, a1)
 
 
 @pytest.mark.parametrize("chain,size", [(1, 2), (2, 3), (4, 2)])
