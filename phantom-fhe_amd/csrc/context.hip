@@ -231,6 +231,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     c.rb_inv = c.upload(rbi);
     PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
+    if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
     // Single-launch NTT (N = 2^16): needs the round-robin workgroup-to-XCD
     // dealing of a full-chip MI355X partition, checked here by a probe kernel.
     // PFA_NTT_ONEPASS=0 selects the two-launch path.

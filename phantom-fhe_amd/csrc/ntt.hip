@@ -30,9 +30,10 @@ NttTables tables(const Ctx &c) {
     return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv, c.rb_fw, c.rb_inv};
 }
 
-// persistent grid: at most n_cu * ntt_wpc workgroups, each walking its tiles
-uint32_t grid_for(const Ctx &c, uint32_t tiles) {
-    const uint32_t cap = (uint32_t)c.n_cu * (uint32_t)c.ntt_wpc;
+// persistent grid: at most n_cu * wpc workgroups, each walking its tiles
+// (wpc: ntt_wpc for the inverse passes, ntt_wpc_fwd for the forward ones)
+uint32_t grid_for(const Ctx &c, uint32_t tiles, int wpc) {
+    const uint32_t cap = (uint32_t)c.n_cu * (uint32_t)wpc;
     return tiles < cap ? tiles : cap;
 }
 
@@ -40,12 +41,12 @@ template <int S1, int S2>
 void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
     const uint32_t ml = b.M * b.L;
-    hipLaunchKernelGGL((ntt_fwd_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES)), dim3(G::COL_THREADS), 0, s, b,
+    hipLaunchKernelGGL((ntt_fwd_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES, c.ntt_wpc_fwd)), dim3(G::COL_THREADS), 0, s, b,
                        t);
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES)), dim3(G::ROW_THREADS), 0, s, b2,
+    hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc_fwd)), dim3(G::ROW_THREADS), 0, s, b2,
                        t);
 }
 
@@ -53,12 +54,12 @@ template <int S1, int S2>
 void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
     const uint32_t ml = b.M * b.L;
-    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES)), dim3(G::ROW_THREADS), 0, s, b,
+    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc)), dim3(G::ROW_THREADS), 0, s, b,
                        t);
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES)), dim3(G::COL_THREADS), 0, s, b2,
+    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES, c.ntt_wpc)), dim3(G::COL_THREADS), 0, s, b2,
                        t);
 }
 

@@ -275,9 +275,9 @@ struct Geo {
 __device__ __forceinline__ int rpad(int k) { return k + (k >> 4); }
 
 // Tiles are numbered limb-major, poly-minor, tile-innermost.  Each workgroup
-// walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... and prefetches the next
-// tile's residues into registers while it transforms the current one, so HBM
-// traffic overlaps the butterflies.
+// walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the inverse passes
+// prefetch the next tile's residues into registers while they transform the
+// current one, the forward passes run more workgroups instead.
 struct TileRef {
     uint32_t m, l, tile;
 };
@@ -449,29 +449,25 @@ __device__ __forceinline__ void fwd_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
     fwd_cols_store<A, S1, S2, NT>(x, ar, r.tile, olimb);
 }
 
+// The forward passes keep no register prefetch: without it they fit 4 waves
+// per SIMD (102 / 126 VGPRs, against 135 / 158 with a prefetched tile at 3),
+// and the extra resident workgroups hide the load latency better (measured on
+// the 2 x 35-limb config-2 batch: 43-44.5 -> 40.8-41 us per forward NTT).
 template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBatch b, NttTables t) {
+__global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) __attribute__((amdgpu_waves_per_eu(4, 8)))
+ntt_fwd_cols(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     __shared__ double lds[G::COL_LDS];
     const uint32_t total = b.M * b.L * G::COL_TILES;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
-    uint32_t cur = next_tile(b, G::COL_TILES, blockIdx.x, total);
-    uint64_t raw[SB::E];
-    if (cur < total) {
-        const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, cur), b.src, b.sstride);
+    for (uint32_t cur = next_tile(b, G::COL_TILES, blockIdx.x, total); cur < total;
+         cur = next_tile(b, G::COL_TILES, cur + gridDim.x, total)) {
+        const TileRef r = decode_tile(b, G::COL_TILES, cur);
+        uint64_t raw[SB::E];
+        const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[(size_t)(F + SB::T * e) * G::N2 + c]);
-    }
-    while (cur < total) {
-        const uint32_t nxt = next_tile(b, G::COL_TILES, cur + gridDim.x, total);
-        const TileRef r = decode_tile(b, G::COL_TILES, cur);
-        uint64_t nraw[SB::E];
-        if (nxt < total) {
-            const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, nxt), b.src, b.sstride);
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[(size_t)(F + SB::T * e) * G::N2 + c]);
-        }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
@@ -480,9 +476,6 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_fwd_cols(NttBa
             fwd_cols_tile<ArithF64, S1, S2>(raw, tw, r, q, lds, olimb);
         else
             fwd_cols_tile<ArithInt, S1, S2>(raw, tw, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
-#pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
-        cur = nxt;
         __syncthreads();
     }
 }
@@ -556,7 +549,8 @@ __device__ __forceinline__ const uint64_t *rows_ptr(const NttBatch &b, const Til
 }
 
 template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBatch b, NttTables t) {
+__global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) __attribute__((amdgpu_waves_per_eu(4, 8)))
+ntt_fwd_rows(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using RS = RowStage<S1, S2>;
@@ -564,31 +558,19 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
     __shared__ ulonglong2 twl[RS::N];
     const uint32_t total = b.M * b.L * G::ROW_TILES;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total);
-    uint64_t raw[SB::E];
-    if (cur < total) {
-        const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, cur), b.src, b.sstride);
-#pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
-    }
-    while (cur < total) {
-        const uint32_t nxt = next_tile(b, G::ROW_TILES, cur + gridDim.x, total);
+    for (uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total); cur < total;
+         cur = next_tile(b, G::ROW_TILES, cur + gridDim.x, total)) {
         const TileRef r = decode_tile(b, G::ROW_TILES, cur);
         const uint32_t prow = b.map.row(r.l);
-        // the tile's prime and twiddles first, then the next tile's prefetch
         const uint64_t q = t.mod[prow];
+        // the tile's twiddles are requested before its residues, so both are
+        // in flight together and staged in LDS once
         RS stage;
         stage.load(t, prow, r.tile, true);
-        __builtin_amdgcn_sched_barrier(0);
-        // unconditional (the last tile reloads itself): a prefetch under a branch
-        // would make the wait for the staged twiddles a wait for everything
-        uint64_t nraw[SB::E];
-        {
-            const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt < total ? nxt : cur), b.src, b.sstride);
+        uint64_t raw[SB::E];
+        const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[F + SB::T * e]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
         stage.st.store(twl);
         __syncthreads();
         const TileTw w = RS::view(twl, t.tw + (size_t)prow * G::N, rr);
@@ -597,9 +579,6 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_fwd_rows(NttBa
             fwd_rows_tile<ArithF64, S1, S2, G::ROWS>(raw, w, r, q, lds, olimb);
         else
             fwd_rows_tile<ArithInt, S1, S2, G::ROWS>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
-#pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
-        cur = nxt;
         __syncthreads();
     }
 }
