@@ -509,7 +509,7 @@ struct EpiRows {
 
 template <class A, int S1, int S2>
 __device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, const A &ar, uint32_t m, uint32_t j,
-                                         uint32_t k1, typename A::T *lr) {
+                                         uint32_t k1, typename A::T *lr, ulonglong2 *twl) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -519,7 +519,24 @@ __device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, c
     T x[SB::E];
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = ar.load_mid(ld_stream(&a.inter[lo + SB::T * e]));
-    fwd_rows_core<A, S1, S2>(x, ar, t, j, k1, lr);
+    if constexpr (A::kF64) {
+        // stage this item's rows' base factors rb[g][tile ROWS + i] and the
+        // small table in LDS (requested after the residues, so the one wait
+        // covers both) instead of dependent global reads inside the rounds
+        using FG = FGeo<S1, S2>;
+        constexpr int RB = S2 * FG::ROWS, NS = RB + (1 << (S2 - 1));
+        const uint32_t tile0 = k1 - k1 % FG::ROWS;
+        const ulonglong2 *rb = t.rb_fw + (size_t)j * S2 * G::N1 + tile0;
+        const ulonglong2 *small = t.small_fw + (size_t)j * kSmall;
+        TwStage<NS, FG::THREADS> st;
+        st.load([&](uint32_t i) { return i < (uint32_t)RB ? rb[(i / FG::ROWS) * G::N1 + i % FG::ROWS] : small[i - RB]; });
+        st.store(twl);
+        __syncthreads();
+        const TileTw w{nullptr, nullptr, twl, twl + RB, k1 % FG::ROWS};
+        fwd_rows_core<A, S1, S2, FG::ROWS>(x, ar, w, k1, lr);
+    } else {
+        fwd_rows_core<A, S1, S2>(x, ar, t, j, k1, lr);
+    }
     const uint64_t *cp = a.c + m * a.c_stride + (size_t)j * G::N + rowoff;
     const uint64_t *bp = (m & 1u) ? a.base1 : a.base0;
     if (bp) bp += (size_t)(m >> 1) * a.base_stride + (size_t)j * G::N + rowoff;
@@ -569,6 +586,7 @@ __global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_epi_rows(EpiRows a,
     using G = Geo<S1, S2>;
     using FG = FGeo<S1, S2>;
     __shared__ double lds[FG::LDS];
+    __shared__ ulonglong2 twl[S2 * FG::ROWS + (1 << (S2 - 1))];
     const uint32_t rr = threadIdx.x / Sub<S2>::T;
     const uint32_t total = a.M * a.J * FG::TILES;
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
@@ -577,10 +595,10 @@ __global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_epi_rows(EpiRows a,
         const uint64_t q = t.mod[j];
         const uint32_t k1 = tile * FG::ROWS + rr;
         if (q < kF64PrimeBound)
-            epi_item<ArithF64, S1, S2>(a, t, ArithF64(q), m, j, k1, lds + rr * G::ROW_PITCH);
+            epi_item<ArithF64, S1, S2>(a, t, ArithF64(q), m, j, k1, lds + rr * G::ROW_PITCH, twl);
         else
             epi_item<ArithInt, S1, S2>(a, t, ArithInt(q), m, j, k1,
-                                       reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH);
+                                       reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, twl);
         __syncthreads();
     }
 }
