@@ -83,6 +83,9 @@ struct BconvCols {
     // ModDown + rescale puts the rescale's last-limb coefficients first);
     // inputs i >= 1 then sit at rows in_row0 + i - 1.  ~0u: no such input
     uint32_t first_row = ~0u;
+    // every factor is 1 (ModUp with alpha = 1: Q_b = q_i; the rescale's single
+    // input): a lone input below 2^50 is then only reduced, not multiplied
+    uint32_t unit = 0;
 };
 
 __device__ __forceinline__ uint32_t bconv_in_row(const BconvCols &a, uint32_t row0, uint32_t i) {
@@ -106,6 +109,16 @@ __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables
     const uint64_t *base = a.in + (size_t)mi * a.in_bstride + (size_t)g * a.in_gstride + tile * kCols + c;
     const uint32_t row0 = a.in_row0 + g * a.in_row_step;
     if constexpr (A::kF64) {
+        if (a.unit && n_in == 1 && t.mod[bconv_in_row(a, row0, 0)] < kF64PrimeBound) {
+            // x = v mod q with v < 2^50: the FMA remainder of the nearest
+            // quotient is exact and within (0.5 + 2^-20) q of zero
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) {
+                x[e] = ar.load(base[(size_t)(F + SB::T * e) * G::N2]);
+                ar.reduce(x[e]);
+            }
+            return;
+        }
         double acc[SB::E];
 #pragma unroll
         for (int e = 0; e < SB::E; e++) acc[e] = 0.0;
@@ -704,6 +717,7 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.skip = 1;
     b.bc_gstride = 2 * alpha * QlP;
     b.bc_istride = QlP;
+    b.unit = alpha == 1;
     b.batch = batch;
     b.in_bstride = LN;
     b.out_bstride = IN;
@@ -820,6 +834,7 @@ void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t si
     b.in = last;
     b.out = inter;
     b.bc = c.unit_bc;
+    b.unit = 1;
     b.in_gstride = c.N;
     b.out_gstride = (uint64_t)(L - 1) * c.N;
     b.groups = size;
