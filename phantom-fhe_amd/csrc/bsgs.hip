@@ -292,7 +292,7 @@ MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, c
             a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
         } else {
             const uint64_t **t = sc.alloc<const uint64_t *>(M * G);
-            PFA_HIP(hipMemcpyAsync(t, pts, M * G * sizeof(void *), hipMemcpyHostToDevice, s));
+            upload_async(c, t, pts, M * G * sizeof(void *), s);
             a.pt = PtrList<const uint64_t>{t, nullptr, 0};
         }
     }
@@ -300,14 +300,14 @@ MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, c
         a.out = PtrList<uint64_t>{nullptr, out[0], st};
     } else {
         uint64_t **t = sc.alloc<uint64_t *>(G);
-        PFA_HIP(hipMemcpyAsync(t, out, G * sizeof(void *), hipMemcpyHostToDevice, s));
+        upload_async(c, t, out, G * sizeof(void *), s);
         a.out = PtrList<uint64_t>{t, nullptr, 0};
     }
     if (M <= kInlineBabies) {
         for (size_t i = 0; i < M; i++) a.baby_inline[i] = babies[i];
     } else {
         const uint64_t **t = sc.alloc<const uint64_t *>(M);
-        PFA_HIP(hipMemcpyAsync(t, babies, M * sizeof(void *), hipMemcpyHostToDevice, s));
+        upload_async(c, t, babies, M * sizeof(void *), s);
         a.baby_table = t;
     }
     return a;

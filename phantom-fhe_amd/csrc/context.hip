@@ -230,6 +230,8 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     c.rb_fw = c.upload(rbf);
     c.rb_inv = c.upload(rbi);
     PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
+    PFA_HIP(hipHostMalloc((void **)&c.stage, Ctx::kStageSlots * Ctx::kStageSlotBytes, hipHostMallocDefault));
+    for (auto &e : c.stage_ev) PFA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
     // Single-launch NTT (N = 2^16): needs the round-robin workgroup-to-XCD
@@ -379,12 +381,30 @@ void *Scratch::alloc_bytes(size_t bytes) {
     return p;
 }
 
+void upload_async(const Ctx &c, void *dst, const void *src, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    if (!c.stage || n > Ctx::kStageSlotBytes) {
+        PFA_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, s));
+        return;
+    }
+    std::lock_guard<std::mutex> lock(c.stage_mu);
+    const size_t i = c.stage_next++ % Ctx::kStageSlots;
+    PFA_HIP(hipEventSynchronize(c.stage_ev[i]));  // the slot's previous copy is done
+    char *slot = c.stage + i * Ctx::kStageSlotBytes;
+    std::memcpy(slot, src, n);
+    PFA_HIP(hipMemcpyAsync(dst, slot, n, hipMemcpyHostToDevice, s));
+    PFA_HIP(hipEventRecord(c.stage_ev[i], s));
+}
+
 static void destroy(Ctx *c) {
     if (!c) return;
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c->device);
     (void)hipDeviceSynchronize();
+    for (auto &e : c->stage_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->stage) (void)hipHostFree(c->stage);
     for (auto &kv : c->arenas) {
         for (auto &ch : kv.second->chunks) (void)hipFree(ch.base);
         delete kv.second;

@@ -140,6 +140,15 @@ struct Ctx {
     std::vector<void *> allocations;
     mutable std::mutex arena_mu;
     mutable std::map<std::pair<std::thread::id, hipStream_t>, Arena *> arenas;
+    // Pinned host staging for small host-to-device uploads (pointer tables):
+    // a copy from pageable memory would make the host wait for the stream's
+    // earlier work; from pinned memory it is queued like a kernel.  Slots are
+    // reused round-robin once their previous copy has completed (its event).
+    static constexpr size_t kStageSlots = 64, kStageSlotBytes = 64 << 10;
+    char *stage = nullptr;                       // hipHostMalloc'd, kStageSlots * kStageSlotBytes
+    hipEvent_t stage_ev[kStageSlots] = {};
+    mutable std::mutex stage_mu;
+    mutable size_t stage_next = 0;
 
     uint32_t size_Ql(uint32_t chain) const { return Q - (chain - 1); }
     const Level &level(uint32_t chain) const {
@@ -166,6 +175,11 @@ void encoder_init(Ctx &c);
 
 // RAII scope over the calling thread's workspace for stream s: alloc() hands
 // out 256-byte-aligned device memory, all of it released when the scope ends.
+// Copies n bytes from host memory to device memory dst in stream order
+// without waiting for the stream (pinned staging; larger copies than a slot
+// fall back to a plain asynchronous copy).
+void upload_async(const Ctx &c, void *dst, const void *src, size_t n, hipStream_t s);
+
 class Scratch {
   public:
     Scratch(const Ctx &c, hipStream_t s);

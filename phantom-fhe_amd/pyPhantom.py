@@ -130,6 +130,9 @@ class context:
         self.device = device
         self.native = _N.NativeContext(self.N, self.moduli, self.size_P, device)
         self.galois_elts = list(parms.galois_elts)
+        # device constants made on first use (monomials, constant plaintexts):
+        # each upload would otherwise be one more host-to-device copy per call
+        self._const_cache = {}
 
     def total_parm_size(self) -> int:
         return self.size_Q + 1
@@ -154,13 +157,11 @@ class context:
         return t.empty(shape, dtype=t.uint64, device=self.dev)
 
     def _upload(self, a: np.ndarray):
-        t = _torch()
-        return t.from_numpy(np.ascontiguousarray(a, dtype=np.uint64)).to(self.dev)
+        return _to_dev(np.ascontiguousarray(a, dtype=np.uint64), self.dev)
 
     def _signed_to_rns(self, coeffs: np.ndarray, L: int, start: int = 0):
         """Signed integer coefficients [N] -> residues [L][N] (coefficient form)."""
-        t = _torch()
-        c = t.from_numpy(np.ascontiguousarray(coeffs, dtype=np.int64)).to(self.dev)
+        c = _to_dev(np.ascontiguousarray(coeffs, dtype=np.int64), self.dev)
         out = self._empty(L, self.N)
         self.native.poly_from_signed(c, out, L, start)
         return out
@@ -199,6 +200,14 @@ def _read_exact(stream, n: int) -> bytes:
 
 def _write_limbs(stream, tensor):
     stream.write(np.ascontiguousarray(tensor.cpu().numpy(), dtype=np.uint64).tobytes())
+
+
+def _to_dev(a: np.ndarray, dev):
+    """Host array -> device tensor through pinned memory, queued on the current
+    stream: a copy from pageable memory would make the host wait for all the
+    work already queued, leaving the GPU idle while the next calls are issued."""
+    t = _torch()
+    return t.from_numpy(a).pin_memory().to(dev, non_blocking=True)
 
 
 def _read_limbs(stream, shape, dev):
@@ -1408,15 +1417,20 @@ def _const_plain(ctx: context, value: complex, scale: float, chain: int) -> plai
     pt = plaintext()
     pt._chain_index, pt._scale = chain, float(scale)
     re = int(round(value.real * scale))
-    if value.imag == 0:
-        t = _torch()
-        r = np.array([re % q for q in ctx.moduli[:L]], dtype=np.uint64)
-        pt.data = t.from_numpy(r).to(ctx.dev).view(L, 1).expand(L, ctx.N).contiguous()
-        return pt
-    c = np.zeros(ctx.N, dtype=np.int64)
-    c[0] = re
-    c[ctx.N // 2] = int(round(value.imag * scale))
-    pt.data = ctx._ntt(ctx._signed_to_rns(c, L), L)
+    im = int(round(value.imag * scale))
+    key = ("const", re, im, L)
+    data = ctx._const_cache.get(key)
+    if data is None:
+        if im == 0:
+            r = np.array([re % q for q in ctx.moduli[:L]], dtype=np.uint64)
+            data = _to_dev(r, ctx.dev).view(L, 1).expand(L, ctx.N).contiguous()
+        else:
+            c = np.zeros(ctx.N, dtype=np.int64)
+            c[0] = re
+            c[ctx.N // 2] = im
+            data = ctx._ntt(ctx._signed_to_rns(c, L), L)
+        ctx._const_cache[key] = data
+    pt.data = data
     return pt
 
 
@@ -1724,9 +1738,12 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
 def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
     """ct * (sign i): the plaintext polynomial times sign X^(N/2), exact."""
     L = ctx.size_Ql(ct.chain_index())
-    c = np.zeros(ctx.N, dtype=np.int64)
-    c[ctx.N // 2] = sign
-    mono = ctx._ntt(ctx._signed_to_rns(c, L), L)
+    mono = ctx._const_cache.get(("times_i", sign, L))
+    if mono is None:
+        c = np.zeros(ctx.N, dtype=np.int64)
+        c[ctx.N // 2] = sign
+        mono = ctx._ntt(ctx._signed_to_rns(c, L), L)
+        ctx._const_cache[("times_i", sign, L)] = mono
     out = ctx._empty(*ct.data.shape)
     for k in range(ct.size()):
         ctx.native.poly_mul(ct.data[k], mono, out[k], L)
