@@ -171,9 +171,9 @@ def time_bsgs(torch, steps, warmup):
     ms = e0.elapsed_time(e1) / steps
     got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, y)))
     err = float(np.max(np.abs(got - np.tile(W @ xv, enc.slot_count() // d_pad))))
-    L = ctx.size_Ql(1)
-    # plaintext limbs read by the accumulation dominate the compulsory bytes
-    pt_bytes = d_pad * L * LIMB_BYTES
+    # the tiled plaintext set the accumulation reads dominates the compulsory
+    # bytes (5 bytes per residue on the 40-bit limbs, 8 on the 60-bit one)
+    pt_bytes = ctx.native.bsgs_tiled_size(1, d_pad)
     del diags
     return {"ms": round(ms, 3), "max_abs_err": err, "encode_s": round(t_encode, 2),
             "expand_ms": round(t_expand * 1e3, 1), "plaintext_bytes": pt_bytes,

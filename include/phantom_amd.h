@@ -230,14 +230,21 @@ int pfa_expand_signed(const pfa_context *ctx, const int64_t *in, size_t n, uint6
 int pfa_bsgs_mac(const pfa_context *ctx, size_t chain_index, const uint64_t *const *pts,
                  const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
 
-/* The tiled layout of a BSGS plaintext set (D plaintexts of Ql limbs at one
- * chain index, NTT form): limb j, residues [512 t, 512 t + 512) of plaintext d
- * at tiled[((j (N / 512) + t) D + d) 512], D Ql N residues in all.  It stores
- * the plaintexts the accumulation reads together next to each other.  Copies
- * src [n][Ql][N] into positions d0 .. d0+n-1.  Layout of this library (the
+/* The tiled layout of a BSGS plaintext set (D plaintexts of Ql <= 64 limbs at
+ * one chain index, NTT form): one region per limb, in limb order; in limb j's
+ * region, residues [512 t, 512 t + 512) of plaintext d sit at position
+ * (t D + d) 512.  A limb whose prime is 2^40 or more stores 8 bytes per
+ * residue; a limb whose prime is below 2^40 stores D N 32-bit low words
+ * followed by D N bytes of bits 32..39 (5 bytes per residue).  It stores the
+ * plaintexts the accumulation reads together next to each other, as few bytes
+ * as the residues need.  Copies src [n][Ql][N] into positions d0 .. d0+n-1 of
+ * a buffer of at least pfa_bsgs_tiled_size bytes.  Layout of this library (the
  * reference re-expands each plaintext per use, src/bsgs.cu:276-312). */
 int pfa_bsgs_tile_plaintexts(const pfa_context *ctx, size_t chain_index, const uint64_t *src, size_t n,
                              uint64_t *tiled, size_t d0, size_t D, void *stream);
+
+/* Bytes of a tiled set of D plaintexts at chain_index (see pfa_bsgs_tile_plaintexts). */
+int pfa_bsgs_tiled_size(const pfa_context *ctx, size_t chain_index, size_t D, size_t *bytes);
 
 /* pfa_bsgs_mac with the G*M plaintexts given as one tiled set (D = M*G,
  * plaintext g*M + b for giant g and baby b). */

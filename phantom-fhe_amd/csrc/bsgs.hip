@@ -50,9 +50,36 @@ __device__ __forceinline__ void st_pair_stream(uint64_t *p, Pair v) {
     __builtin_nontemporal_store(v, (__attribute__((address_space(1))) Pair *)p);
 }
 
+// The tiled plaintext layout (pfa_bsgs_tile_plaintexts) of a set of D
+// plaintexts: one region per limb j at byte offset off[j], holding span t of
+// plaintext d at position (t D + d) kSpan.  A limb whose prime is below 2^40
+// is packed: its region is D N 32-bit low words, then D N bytes of bits
+// 32..39 (5 bytes per residue instead of 8); the accumulation is bound by
+// reading this set, so packing cuts its time with its size.
+constexpr uint32_t kMaxTiledLimbs = 64;
+constexpr uint64_t kPackBound = 1ull << 40;
+struct TiledLayout {
+    uint64_t off[kMaxTiledLimbs];
+    uint64_t packed;  // bit j: limb j is packed
+    uint64_t bytes;   // total size
+};
+
+TiledLayout tiled_layout(const Ctx &c, uint32_t Ql, uint64_t D) {
+    require(Ql <= kMaxTiledLimbs, "too many limbs for the tiled plaintext layout");
+    TiledLayout t{};
+    for (uint32_t j = 0; j < Ql; j++) {
+        const bool pk = c.moduli[j] < kPackBound;
+        t.off[j] = t.bytes;
+        if (pk) t.packed |= 1ull << j;
+        t.bytes += D * c.N * (pk ? 5 : 8);
+    }
+    return t;
+}
+
 struct MacArgs {
     PtrList<const uint64_t> pt;  // [G M] plaintexts, [Ql][N] each (NTT form), when tiled is null
-    const uint64_t *tiled;       // or the same set in the tiled layout (pfa_bsgs_tile_plaintexts)
+    const uint8_t *tiled;        // or the same set in the tiled layout (pfa_bsgs_tile_plaintexts)
+    TiledLayout lay;
     PtrList<uint64_t> out;       // [G] ciphertexts, [2][Ql][N] each
     const uint64_t *const *baby_table;          // [M] ciphertexts [2][Ql][N], when M > kInlineBabies
     const uint64_t *baby_inline[kInlineBabies];  // the same, by value, when M <= kInlineBabies
@@ -61,12 +88,19 @@ struct MacArgs {
     __device__ __forceinline__ const uint64_t *baby(uint32_t b) const {
         return baby_table ? baby_table[b] : baby_inline[b];
     }
-    // span `tile` of limb j of plaintext d, plus this thread's offset
-    __device__ __forceinline__ const uint64_t *span(uint32_t d, uint32_t j, uint32_t tile) const {
-        if (tiled) return tiled + (((size_t)j * (N / kSpan) + tile) * ((size_t)G * M) + d) * kSpan + kPer * threadIdx.x;
-        return pt[d] + (size_t)j * N + tile * kSpan + kPer * threadIdx.x;
-    }
+    // this thread's kPer residues of span `tile` of limb j of plaintext d
+    __device__ __forceinline__ Pair span(uint32_t d, uint32_t j, uint32_t tile) const;
 };
+
+__device__ __forceinline__ Pair MacArgs::span(uint32_t d, uint32_t j, uint32_t tile) const {
+    if (!tiled) return ld_pair_stream(pt[d] + (size_t)j * N + tile * kSpan + kPer * threadIdx.x);
+    const size_t i = ((size_t)tile * ((size_t)G * M) + d) * kSpan + kPer * threadIdx.x;
+    const uint8_t *r = tiled + lay.off[j];
+    if (!((lay.packed >> j) & 1u)) return ld_pair_stream(reinterpret_cast<const uint64_t *>(r) + i);
+    const uint64_t lo = __builtin_nontemporal_load(reinterpret_cast<const uint64_t *>(r) + i / 2);
+    const uint32_t hi = __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(r + (size_t)G * M * N * 4) + i / 2);
+    return Pair{(lo & 0xffffffffull) | ((uint64_t)(hi & 0xffu) << 32), (lo >> 32) | ((uint64_t)(hi >> 8) << 32)};
+}
 
 // A work item is (limb j, kSpan consecutive residues, block of up to kGB
 // giants).  Baby b's residues are loaded once per item (kPer adjacent ones per
@@ -120,8 +154,7 @@ k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
 #pragma unroll
                 for (uint32_t k = 0; k < kGB; k++) {
                     if (k < K) {
-                        const uint64_t *p = a.span((g0 + k) * a.M + b, j, tile);
-                        const Pair xv = ld_pair_stream(p);
+                        const Pair xv = a.span((g0 + k) * a.M + b, j, tile);
 #pragma unroll
                         for (int e = 0; e < kPer; e++) {
                             const double x = ar.load(xv[e]);
@@ -169,8 +202,7 @@ k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
 #pragma unroll
                 for (uint32_t k = 0; k < kGB; k++) {
                     if (k < K) {
-                        const uint64_t *p = a.span((g0 + k) * a.M + b, j, tile);
-                        const Pair xv = ld_pair_stream(p);
+                        const Pair xv = a.span((g0 + k) * a.M + b, j, tile);
 #pragma unroll
                         for (int e = 0; e < kPer; e++) {
                             const uint64_t x = xv[e];
@@ -208,14 +240,28 @@ k_expand_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t 
     st_stream(out + ((size_t)p * L + l) * N + n, r);
 }
 
-// Plaintexts src[n][Ql][N] -> positions d0 .. d0+n-1 of a tiled set of D:
-//   tiled[((j T + t) D + d) kSpan + i] = pt[d][j][t kSpan + i],  T = N / kSpan.
-// One workgroup per (span, limb, plaintext): a contiguous 4 KiB read and write.
+// Plaintexts src[n][Ql][N] -> positions d0 .. d0+n-1 of a tiled set of D
+// (TiledLayout): residue i of span t of limb j of plaintext d at position
+// (t D + d) kSpan + i of limb j's region.  One workgroup per (span, limb,
+// plaintext): a contiguous 4 KiB read, a contiguous 4 KiB (or 2.5 KiB) write.
 __global__ void __launch_bounds__(kThreads)
-k_bsgs_tile(const uint64_t *src, uint64_t *tiled, uint32_t Ql, uint32_t N, uint32_t d0, uint32_t D) {
-    const uint32_t t = blockIdx.x, j = blockIdx.y, p = blockIdx.z, T = N / kSpan;
+k_bsgs_tile(const uint64_t *src, uint8_t *tiled, TiledLayout lay, uint32_t Ql, uint32_t N, uint32_t d0, uint32_t D) {
+    const uint32_t t = blockIdx.x, j = blockIdx.y, p = blockIdx.z;
     const uint64_t *s = src + ((size_t)p * Ql + j) * N + (size_t)t * kSpan;
-    uint64_t *o = tiled + (((size_t)j * T + t) * D + d0 + p) * kSpan;
+    const size_t pos = ((size_t)t * D + d0 + p) * kSpan;
+    uint8_t *r = tiled + lay.off[j];
+    if ((lay.packed >> j) & 1u) {
+        uint32_t *lo = reinterpret_cast<uint32_t *>(r) + pos;
+        uint8_t *hi = r + (size_t)D * N * 4 + pos;
+#pragma unroll
+        for (uint32_t i = threadIdx.x; i < kSpan; i += kThreads) {
+            const uint64_t v = ld_stream(s + i);
+            lo[i] = (uint32_t)v;
+            hi[i] = (uint8_t)(v >> 32);
+        }
+        return;
+    }
+    uint64_t *o = reinterpret_cast<uint64_t *>(r) + pos;
 #pragma unroll
     for (uint32_t i = threadIdx.x; i < kSpan; i += kThreads) st_stream(o + i, ld_stream(s + i));
 }
@@ -286,7 +332,8 @@ MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, c
         return true;
     };
     uint64_t st = 0;
-    a.tiled = tiled;
+    a.tiled = reinterpret_cast<const uint8_t *>(tiled);
+    if (tiled) a.lay = tiled_layout(c, a.Ql, (uint64_t)M * G);
     if (!tiled) {
         if (progression((const void *const *)pts, M * G, st)) {
             a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
@@ -372,9 +419,20 @@ int pfa_bsgs_tile_plaintexts(const pfa_context *ctx, size_t chain_index, const u
         if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
         require(n >= 1 && n <= 65535 && d0 + n <= D && D < (1u << 24), "plaintext range out of bounds");
         const uint32_t Ql = c.size_Ql((uint32_t)chain_index);
+        const TiledLayout lay = tiled_layout(c, Ql, D);
         hipLaunchKernelGGL(k_bsgs_tile, dim3(c.N / kSpan, Ql, (uint32_t)n), dim3(kThreads), 0, as_stream(stream), src,
-                           tiled, Ql, c.N, (uint32_t)d0, (uint32_t)D);
+                           reinterpret_cast<uint8_t *>(tiled), lay, Ql, c.N, (uint32_t)d0, (uint32_t)D);
         PFA_HIP(hipGetLastError());
+    });
+}
+
+int pfa_bsgs_tiled_size(const pfa_context *ctx, size_t chain_index, size_t D, size_t *bytes) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(bytes != nullptr, "null argument");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        require(D >= 1 && D < (1u << 24), "plaintext count out of range");
+        *bytes = (size_t)tiled_layout(c, c.size_Ql((uint32_t)chain_index), D).bytes;
     });
 }
 

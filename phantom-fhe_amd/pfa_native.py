@@ -61,6 +61,7 @@ SIGNATURES = {
     "pfa_bsgs_mac": (_i32, [_vp, _sz, C.POINTER(_vp), C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
     "pfa_bsgs_tile_plaintexts": (_i32, [_vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp]),
     "pfa_bsgs_mac_tiled": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
+    "pfa_bsgs_tiled_size": (_i32, [_vp, _sz, _sz, C.POINTER(_sz)]),
     "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
     "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
@@ -333,6 +334,12 @@ class NativeContext:
         """src [n][Ql][N] -> positions d0 .. d0+n-1 of the tiled set `tiled` of D plaintexts."""
         call("pfa_bsgs_tile_plaintexts", self._h, chain_index, ptr(src), n, ptr(tiled), d0, D,
              stream or stream_of(src))
+
+    def bsgs_tiled_size(self, chain_index, D) -> int:
+        """Bytes of a tiled set of D plaintexts at chain_index."""
+        n = C.c_size_t(0)
+        call("pfa_bsgs_tiled_size", self._h, chain_index, D, C.byref(n))
+        return int(n.value)
 
     def bsgs_mac_tiled(self, chain_index, tiled, babies, outs, stream=None):
         """bsgs_mac with the len(babies) * len(outs) plaintexts in one tiled set."""

@@ -1012,7 +1012,7 @@ class bsgs_diagonals:
         t = self._expanded.get(chain_index)
         if t is None:
             L = ctx.size_Ql(chain_index)
-            t = ctx._empty(self.d_pad * L * ctx.N)
+            t = ctx._empty((ctx.native.bsgs_tiled_size(chain_index, self.d_pad) + 7) // 8)
             step = min(self.d_pad, 256)
             tmp = ctx._empty(step, L, ctx.N)
             for s0 in range(0, self.d_pad, step):

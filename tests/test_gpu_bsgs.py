@@ -101,6 +101,38 @@ def test_bsgs_tiled_mac_equals_pointer_mac(dev, M, G, chunk):
         assert torch.equal(got[g], want[g]), g
 
 
+@pytest.mark.parametrize("M,G", [(8, 5), (64, 2)])
+def test_bsgs_tiled_packed_limbs(dev, M, G):
+    """Limbs whose prime is below 2^40 are stored in 5 bytes per residue in the
+    tiled set; the accumulation over such a set equals the pointer-list one, and
+    the set's size is 5 / 8 of the unpacked size on those limbs."""
+    import pfa_native as P
+    import torch
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 40, 38, 40, 50, 40, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    chain = 1
+    Ql = len(mods) - 1
+    D = M * G
+    packed = sum(1 for q in mods[:Ql] if q < (1 << 40))
+    assert packed == 4
+    assert ctx.bsgs_tiled_size(chain, D) == D * N * (5 * packed + 8 * (Ql - packed))
+    rng = np.random.default_rng(M * G + 1)
+    pts = uniform_limbs(rng, (D, Ql, N), mods[:Ql])
+    pts[0, 1, :4] = [0, mods[1] - 1, (1 << 32) - 1, 1 << 32]  # the packing's edges
+    dpts = to_dev(pts, dev)
+    babies = [to_dev(uniform_limbs(rng, (2, Ql, N), mods[:Ql]), dev) for _ in range(M)]
+    tiled = empty(((ctx.bsgs_tiled_size(chain, D) + 7) // 8,), dev)
+    ctx.bsgs_tile_plaintexts(chain, dpts, D, tiled, 0, D)
+    want = [empty((2, Ql, N), dev) for _ in range(G)]
+    got = [empty((2, Ql, N), dev) for _ in range(G)]
+    ctx.bsgs_mac(chain, [dpts[i] for i in range(D)], babies, want)
+    ctx.bsgs_mac_tiled(chain, tiled, babies, got)
+    for g in range(G):
+        assert torch.equal(got[g], want[g]), g
+
+
 def test_bsgs_mac_rejects_bad_arguments(dev):
     import pfa_native as P
 
