@@ -50,12 +50,19 @@ void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
                        t);
 }
 
+// batches of at least this many limbs take the inverse rows pass with staged twiddles
+constexpr uint32_t kInvStagedLimbs = 48;
+
 template <int S1, int S2>
 void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
     const uint32_t ml = b.M * b.L;
-    hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc)), dim3(G::ROW_THREADS), 0, s, b,
-                       t);
+    if (ml >= kInvStagedLimbs)
+        hipLaunchKernelGGL((ntt_inv_rows_staged<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, 3)),
+                           dim3(G::ROW_THREADS), 0, s, b, t);
+    else
+        hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc)),
+                           dim3(G::ROW_THREADS), 0, s, b, t);
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;

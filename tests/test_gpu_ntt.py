@@ -108,6 +108,24 @@ def test_ntt_single_launch_variant(dev, monkeypatch):
         assert np.array_equal(back, x), first_mismatch(back, x)
 
 
+@pytest.mark.parametrize("logn,M,L", [(12, 2, 26), (16, 2, 25), (13, 4, 12)])
+def test_ntt_large_batches_both_policies(dev, logn, M, L):
+    """Batches of 48 limbs or more take the inverse rows pass with staged
+    twiddles: forward and inverse against the oracle with 50- and 60-bit primes
+    (FP64 and integer policies) mixed in one batch."""
+    N = 1 << logn
+    mods, ctx, orc = make(N, [50, 60] * (L // 2) + [50] * (L % 2) + [60])
+    rng = np.random.default_rng(logn + M + L)
+    x = uniform_limbs(rng, (M, L, N), mods)
+    d = to_dev(x, dev)
+    ctx.ntt_forward(d, M, L, 0)
+    got, want = to_host(d), orc.ntt_fwd(x, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    ctx.ntt_inverse(d, M, L, 0)
+    back = to_host(d)
+    assert np.array_equal(back, x), first_mismatch(back, x)
+
+
 @pytest.mark.parametrize("fill", ["zero", "qm1", "one", "two"])
 def test_ntt_edge_values(dev, fill):
     """Constant inputs (the reference's own all-1 / all-2 cases, test/ntt_test.cu:48-50,
