@@ -1,6 +1,6 @@
 """Benchmark of the MI355X CKKS hot path (one JSON line on stdout).
 
-Headline (BASELINE.json metric, config 2): batched forward negacyclic NTT at
+Headline (the project metric, config 2): batched forward negacyclic NTT at
 N = 2^16 over a batch of 2 polys x 35 limbs (35 x 50-bit primes; the 60-bit
 special prime is in the table but not transformed).  One step = one forward
 NTT of one batch, inputs resident in HBM.  value = limbs transformed per second.
@@ -123,7 +123,7 @@ def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
 
 
 def time_bsgs(torch, steps, warmup):
-    """BASELINE config 4 through the pyPhantom API: y = W x for a 4096 x 4096
+    """benchmark config 4 through the pyPhantom API: y = W x for a 4096 x 4096
     matrix uniform in [-1/64, 1/64] (seeded), x uniform in [-1, 1] replicated over
     the 2^15 slots with period 4096, baby 64 / giant 64, L = 20 (chain
     {60, 40 x 19, 60 x 4}), scale 2^40, sparse ternary secret h = 192.  Times the
@@ -182,7 +182,7 @@ def time_bsgs(torch, steps, warmup):
 
 
 def time_bootstrap(torch, steps, warmup):
-    """BASELINE config 5 through the pyPhantom API: N = 2^16, the 2^15 slots
+    """benchmark config 5 through the pyPhantom API: N = 2^16, the 2^15 slots
     uniform in [-1, 1] (seeded), scale 2^40, chain bootstrap_coeff_bits()
     (|Q| = 30: q0 60 | 13 x 40 | SlotToCoeff 3 x 50 | EvalMod 10 x 60 |
     CoeffToSlot 3 x 60, then 6 special primes of 60 bits, dnum = 5), sparse
@@ -284,8 +284,9 @@ def main():
                          "config-4 matrix-vector product; bootstrap: only the config-5 bootstrap")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
-              "the path's sharding is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the hot path "
+              "would shard by RNS limb or by independent ciphertexts, neither of which is built here",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

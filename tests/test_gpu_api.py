@@ -157,7 +157,7 @@ def test_reference_example_flow(dev):
 
 @pytest.mark.parametrize("logN", [13, 16])
 def test_mul_relin_rescale_decodes_within_1e6(dev, logN):
-    """BASELINE config 3 semantics at N = 2^16 (smaller chain for time): fresh
+    """benchmark config 3 semantics at N = 2^16 (smaller chain for time): fresh
     ciphertexts of uniform reals in [-1, 1], HMult + relin + rescale, decode
     within 1e-6 absolute of the exact product."""
     ph, ctx = make_ctx(logN, [60] + [40] * 5 + [60] * 2, 2)
@@ -199,7 +199,7 @@ def test_rotations_and_conjugation(dev):
     steps = [1, 2, 4, -1, 0]
     ph, ctx = make_ctx(13, [60, 40, 40, 40, 60, 60], 2, steps=steps)
     ph.set_seed(3)
-    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)  # the BASELINE configs' sparse ternary secret
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)  # the benchmark configs' sparse ternary secret
     glk = sk.create_galois_keys(ctx)
     enc = ph.ckks_encoder(ctx)
     rng = np.random.default_rng(8)

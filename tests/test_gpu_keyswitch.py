@@ -10,7 +10,7 @@ the CPU oracle, bit-exact on every RNS residue:
   (src/evaluate.cu:1929-2082) and key construction (src/secretkey.cu:354-398).
 
 Shapes cover alpha = 1 (the single-special-prime BConv), a short last digit
-(|Ql| not a multiple of alpha), lower levels (chain index > 1) and the BASELINE
+(|Ql| not a multiple of alpha), lower levels (chain index > 1) and the benchmark
 config-3 shape (N = 2^16, |Q| = 24, alpha = 4, dnum = 6).
 """
 import numpy as np
@@ -164,7 +164,7 @@ def test_multiply_and_relin_in_place(dev, alias):
 
 
 def test_multiply_and_relin_config3(dev):
-    """BASELINE config 3 shape: N = 2^16, chain {60, 50 x 23, 60 x 4}: |Q| = 24,
+    """benchmark config 3 shape: N = 2^16, chain {60, 50 x 23, 60 x 4}: |Q| = 24,
     alpha = 4, dnum = beta = 6, fresh ciphertexts at chain index 1."""
     st = Setup(16, 24, 4, seed=7)
     a, b = st.ct(1), st.ct(1)
@@ -213,7 +213,7 @@ def test_relinearize_rescale(dev, logN, nq, alpha, chain, bits):
 
 
 def test_multiply_relin_rescale_config3(dev):
-    """The fused path at the BASELINE config-3 shape (N = 2^16, |Q| = 24, alpha = 4)."""
+    """The fused path at the benchmark config-3 shape (N = 2^16, |Q| = 24, alpha = 4)."""
     st = Setup(16, 24, 4, seed=13)
     a, b = st.ct(1), st.ct(1)
     key = st.key()

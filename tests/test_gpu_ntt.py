@@ -50,7 +50,7 @@ def test_ntt_fwd_inv_all_degrees(dev, logn):
 
 
 def test_ntt_config1_cpu_case(dev):
-    """BASELINE config 1: N = 2^13, CoeffModulus::Create(8192, {50,50,55,60})."""
+    """benchmark config 1: N = 2^13, CoeffModulus::Create(8192, {50,50,55,60})."""
     N = 8192
     mods = O.create_coeff_modulus(N, [50, 50, 55, 60])
     import pfa_native as P
@@ -68,7 +68,7 @@ def test_ntt_config1_cpu_case(dev):
 
 
 def test_ntt_config2_full_size(dev):
-    """N = 2^16, 35 x 50-bit primes + one 60-bit special prime,
+    """benchmark config 2: N = 2^16, 35 x 50-bit primes + one 60-bit special prime,
     batch of 2 polys x 35 limbs, bit-exact against the oracle."""
     N = 1 << 16
     mods, ctx, orc = make(N, [50] * 35 + [60])
