@@ -88,3 +88,15 @@ def test_null_context_is_an_error():
     bad = (C.c_uint64 * 2)(97, 193)
     rc = P.lib().pfa_context_create(1024, bad, 2, 1, 0, C.byref(out))
     assert rc == P.PFA_ERR_INVALID_ARGUMENT
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message (no GPU needed)."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
