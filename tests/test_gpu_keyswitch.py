@@ -212,6 +212,26 @@ def test_relinearize_rescale(dev, logN, nq, alpha, chain, bits):
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 20, 1, 1), (12, 18, 1, 2), (13, 34, 2, 1)])
+def test_many_digits(dev, logN, nq, alpha, chain):
+    """16 or more digits per key switch (long digit loops in the inner
+    product): multiply_and_relin and the fused call against the oracle."""
+    st = Setup(logN, nq, alpha, seed=14)
+    assert st.orc.beta(chain) >= 16
+    Ql = st.orc.size_Ql(chain)
+    a, b = st.ct(chain), st.ct(chain)
+    key = st.key()
+    want = st.orc.multiply_and_relin(chain, a, b, key, threads=8)
+    out = empty((2, Ql, st.N), dev)
+    st.ctx.multiply_and_relin(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    fused = empty((2, Ql - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), fused)
+    got, want = to_host(fused), st.orc.rescale(chain, want, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
 def test_multiply_relin_rescale_config3(dev):
     """The fused path at the benchmark config-3 shape (N = 2^16, |Q| = 24, alpha = 4)."""
     st = Setup(16, 24, 4, seed=13)
