@@ -245,8 +245,9 @@ def measured_traffic():
         return None
 
 
-def cpu_baseline(mods, seconds):
-    """Oracle forward NTT, one thread, repeated over the config-2 batch for ~`seconds`."""
+def cpu_baseline(mods, seconds, threads=1):
+    """Oracle forward NTT on `threads` host threads (OpenMP over limbs), repeated
+    over the config-2 batch for ~`seconds`."""
     import numpy as np
 
     import py_oracle as O
@@ -256,14 +257,25 @@ def cpu_baseline(mods, seconds):
     x = np.stack([rng.integers(0, q, size=(POLYS, N), dtype=np.uint64) for q in mods[:LIMBS]], axis=1)
     limbs, t0 = 0, time.perf_counter()
     while True:
-        orc.ntt_fwd(x, threads=1)
+        orc.ntt_fwd(x, threads=threads)
         limbs += POLYS * LIMBS
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    return {"value": round(limbs / el, 2), "unit": "limbs/s", "cores": 1, "kind": "port",
+    return {"value": round(limbs / el, 2), "unit": "limbs/s", "cores": threads, "kind": "port",
             "sample": f"{limbs // (POLYS * LIMBS)} forward NTTs of the 2x35-limb N=2^16 batch "
-                      f"({limbs} limbs, {el:.1f} s) by oracle/ckks_oracle.c (radix-2, Shoup), 1 thread"}
+                      f"({limbs} limbs, {el:.1f} s) by oracle/ckks_oracle.c (radix-2, Shoup), "
+                      f"{threads} thread{'s' if threads > 1 else ''}"}
+
+
+def host_threads():
+    """Host threads this process may use (its CPU affinity, at most 16: the GPU
+    box's share of the host for one GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def main():
@@ -362,10 +374,14 @@ def main():
         log(f"bench: bootstrap config5 {boot['ms']} ms, {boot['precision_bits']} bits")
         torch.cuda.empty_cache()
 
-    cpu = None
+    cpu = cpu_all = None
     if not args.no_cpu:
         cpu = cpu_baseline(mods, args.cpu_seconds)
         log(f"bench: cpu baseline {cpu['value']} limbs/s")
+        nt = host_threads()
+        if nt > 1:
+            cpu_all = cpu_baseline(mods, args.cpu_seconds / 2, nt)
+            log(f"bench: cpu baseline on {nt} threads {cpu_all['value']} limbs/s")
 
     line = {
         "metric": "NTT limbs/s at N=2^16; HMult+relin+rescale ms (L=35); % HBM roofline",
@@ -386,6 +402,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "forward NTT (ntt_fwd_cols + ntt_fwd_rows), 16 B/residue algorithmic"},
         "cpu_baseline": cpu,
+        "cpu_baseline_all_threads": cpu_all,
         "ntt_inverse_limbs_per_s": round(limbs / (ev_inv_ms * 1e-3), 1),
         "ntt_forward_us": round(ev_ms * 1e3, 2),
         "ntt_inverse_us": round(ev_inv_ms * 1e3, 2),
