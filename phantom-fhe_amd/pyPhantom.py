@@ -556,11 +556,36 @@ class secret_key:
         ctx.native.poly_mul(self.sk, self.sk, s2, QP)
         return relin_key(self._kswitch_key(ctx, s2, _rng(seed)))
 
-    def _galois_key_for(self, ctx, elt, rng):
+    def _galois_key_for(self, ctx, elt, rng, digits=None):
+        """Key for sigma_elt(s); with `digits`, only that many leading partitions
+        (generate_one_kswitch_key_at_level, src/secretkey.cu:400-472: the same
+        structure over every prime, the partitions a level does not use left out)."""
         QP = len(ctx.moduli)
         rot = ctx._empty(QP, ctx.N)
         ctx.native.apply_galois_ntt(elt, self.sk, rot, QP)
-        return self._kswitch_key(ctx, rot, rng)
+        key = self._kswitch_key(ctx, rot, rng)
+        return key if digits is None or digits == key.shape[0] else key[:digits].contiguous()
+
+    @staticmethod
+    def _level_digits(ctx, target_chain_index: int):
+        """Partitions a key for target_chain_index needs (0: the key level, all
+        of them): ceil(|Ql| / |P|), src/secretkey.cu:423-435."""
+        if target_chain_index == 0:
+            return None
+        if not 1 <= target_chain_index <= ctx.size_Q:
+            raise ValueError("generate_one_kswitch_key_at_level: target_chain_index out of range")
+        beta = -(-ctx.size_Ql(target_chain_index) // ctx.size_P)
+        if beta > ctx.dnum:
+            raise RuntimeError("generate_one_kswitch_key_at_level: computed beta_k is invalid")
+        return beta
+
+    def _elt_at(self, ctx, idx: int, what: str) -> int:
+        if not 0 <= idx < len(ctx.galois_elts):
+            raise IndexError(f"{what}: index out of range")
+        elt = ctx.galois_elts[idx]
+        if not (elt & 1) or elt >= 2 * ctx.N:
+            raise ValueError(f"{what}: Galois element is not valid")
+        return elt
 
     def create_galois_keys(self, ctx: context, seed=None) -> galois_key:
         """Keys for every element in params.galois_elts (src/secretkey.cu:642-682)."""
@@ -571,10 +596,28 @@ class secret_key:
             g.keys[elt] = self._galois_key_for(ctx, elt, rng)
         return g
 
-    def create_one_galois_key(self, ctx: context, galois_elt_idx: int, target_chain_index: int = 0, seed=None):
+    def create_galois_keys_per_level(self, ctx: context, indices, target_chain_indices, seed=None) -> galois_key:
+        """create_galois_keys_per_level (src/secretkey.cu:726-775): keys for the
+        Galois elements at positions `indices` of params.galois_elts, each with
+        the partitions its target chain index needs (0: all); the other
+        elements get no key."""
         self._require()
-        elt = ctx.galois_elts[galois_elt_idx]
-        return relin_key(self._galois_key_for(ctx, elt, _rng(seed)))
+        indices, targets = list(indices), list(target_chain_indices)
+        if len(indices) != len(targets):
+            raise ValueError("create_galois_keys_per_level: indices and target_chain_indices must have the same length")
+        rng = _rng(seed)
+        g = galois_key()
+        for idx, tci in zip(indices, targets):
+            elt = self._elt_at(ctx, idx, "create_galois_keys_per_level")
+            g.keys[elt] = self._galois_key_for(ctx, elt, rng, self._level_digits(ctx, tci))
+        return g
+
+    def create_one_galois_key(self, ctx: context, galois_elt_idx: int, target_chain_index: int = 0, seed=None):
+        """create_one_galois_key (src/secretkey.cu:777-811): the key of one
+        element, with the partitions target_chain_index needs (0: all)."""
+        self._require()
+        elt = self._elt_at(ctx, galois_elt_idx, "create_one_galois_key")
+        return relin_key(self._galois_key_for(ctx, elt, _rng(seed), self._level_digits(ctx, target_chain_index)))
 
     def encrypt_symmetric(self, ctx: context, pt: plaintext, seed=None) -> ciphertext:
         """ct = (-a s + e + m, a) over the plaintext's primes."""

@@ -218,6 +218,38 @@ def test_rotations_and_conjugation(dev):
         ph.hoist_rotations(ctx, ct, glk, [5])  # no key for step 5
 
 
+def test_galois_keys_per_level(dev):
+    """create_galois_keys_per_level / create_one_galois_key with a target chain
+    index: keys with only the partitions that level needs rotate correctly
+    there, are refused at a level that needs more, and the argument errors
+    match the reference's exception classes."""
+    ph, ctx = make_ctx(13, [60, 40, 40, 40, 40, 40, 60, 60], 2, steps=[1, 2])
+    ph.set_seed(9)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192)
+    enc = ph.ckks_encoder(ctx)
+    assert ctx.dnum == 3
+    g = sk.create_galois_keys_per_level(ctx, [0, 1], [3, 0])  # step 1 at chain index 3, step 2 full
+    elt1, elt2 = ctx.galois_elts
+    assert g.keys[elt1].shape[0] == 2 and g.keys[elt2].shape[0] == 3  # ceil(4 / 2) = 2 partitions
+    rng = np.random.default_rng(10)
+    v = rng.uniform(-1, 1, enc.slot_count())
+    ct3 = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, v, 2.0 ** 40, chain_index=3))
+    r = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ph.rotate(ctx, ct3, 1, g))))
+    assert np.max(np.abs(r - np.roll(v, -1))) < TOL
+    one = sk.create_one_galois_key(ctx, 0, 3)
+    r = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ph.rotate_with_key(ctx, ct3, 1, one))))
+    assert np.max(np.abs(r - np.roll(v, -1))) < TOL
+    ct1 = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, v, 2.0 ** 40))
+    with pytest.raises(ValueError):  # chain index 1 needs 3 partitions
+        ph.rotate(ctx, ct1, 1, g)
+    with pytest.raises(ValueError):
+        sk.create_galois_keys_per_level(ctx, [0, 1], [3])
+    with pytest.raises(IndexError):
+        sk.create_one_galois_key(ctx, 2)
+    with pytest.raises(ValueError):
+        sk.create_one_galois_key(ctx, 0, ctx.size_Q + 1)
+
+
 def test_api_errors(dev):
     ph, ctx = make_ctx(12, [60, 40, 40, 60], 1)
     sk = ph.secret_key(ctx)
