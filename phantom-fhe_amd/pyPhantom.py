@@ -74,6 +74,23 @@ class mul_tech_type(enum.IntEnum):
 create_coeff_modulus = _N.create_coeff_modulus
 
 
+def set_cuda_device(device_id: int) -> None:
+    """set_cuda_device (python/src/binding.cu:387-395): make device_id current for
+    the calling thread (contexts and tensors created afterwards default to it)."""
+    t = _torch()
+    if not 0 <= int(device_id) < t.cuda.device_count():
+        raise RuntimeError(f"set_cuda_device failed: no device {device_id}")
+    t.cuda.set_device(int(device_id))
+
+
+def get_cuda_device_count() -> int:
+    """get_cuda_device_count (python/src/binding.cu:397-402): visible devices, 0 on error."""
+    try:
+        return int(_torch().cuda.device_count())
+    except Exception:
+        return 0
+
+
 def get_elt_from_step(step: int, coeff_count: int) -> int:
     """include/galois.cuh:16-49."""
     return _N.galois_elt_from_step(step, coeff_count)
@@ -119,7 +136,7 @@ class context:
     """PhantomContext (src/context.cu:121-183): chain index 0 = key level,
     chain c >= 1 holds |Q| - c + 1 data primes."""
 
-    def __init__(self, parms: params, device: int = 0):
+    def __init__(self, parms: params, device: int | None = None):
         if not parms.poly_modulus_degree or not parms.coeff_modulus:
             raise ValueError("poly modulus degree and coefficient modulus must be set")
         self.parms = parms
@@ -127,8 +144,9 @@ class context:
         self.moduli = list(parms.coeff_modulus)
         self.size_P = parms.special_modulus_size
         self.size_Q = len(self.moduli) - self.size_P
-        self.device = device
-        self.native = _N.NativeContext(self.N, self.moduli, self.size_P, device)
+        # the calling thread's current device unless given (set_cuda_device)
+        self.device = _torch().cuda.current_device() if device is None else int(device)
+        self.native = _N.NativeContext(self.N, self.moduli, self.size_P, self.device)
         self.galois_elts = list(parms.galois_elts)
         # device constants made on first use (monomials, constant plaintexts):
         # each upload would otherwise be one more host-to-device copy per call

@@ -250,6 +250,18 @@ def test_galois_keys_per_level(dev):
         sk.create_one_galois_key(ctx, 0, ctx.size_Q + 1)
 
 
+def test_device_helpers(dev):
+    import pyPhantom as ph
+
+    n = ph.get_cuda_device_count()
+    assert n >= 1
+    ph.set_cuda_device(0)
+    with pytest.raises(RuntimeError):
+        ph.set_cuda_device(n)
+    _, ctx = make_ctx(12, [60, 40, 60], 1)
+    assert ctx.device == 0
+
+
 def test_api_errors(dev):
     ph, ctx = make_ctx(12, [60, 40, 40, 60], 1)
     sk = ph.secret_key(ctx)
