@@ -175,6 +175,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     __shared__ double lds[G::COL_LDS];
+    __shared__ ulonglong2 twl[G::N1];  // the target prime's columns-pass twiddles
     const uint32_t NG = a.batch * a.groups * G::COL_TILES;
     const uint32_t total = grouped_total(NG, a.J);
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
@@ -186,17 +187,24 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
         const uint32_t prow = j < a.split ? j : a.split_base + (j - a.split);
         const uint64_t q = t.mod[prow];
         uint64_t *olimb = a.out + (size_t)mi * a.out_bstride + (size_t)g * a.out_gstride + (size_t)j * G::N;
+        // the twiddles are requested before the inputs and staged in LDS
+        TwStage<G::N1, G::COL_THREADS> st;
+        st.load([&](uint32_t i) { return t.tw[(size_t)prow * G::N + i]; });
         if (q < kF64PrimeBound) {
             const ArithF64 ar(q);
             double x[SB::E];
             bconv_source<ArithF64, S1, S2>(a, t, ar, mi, g, j, tile, x);
-            fwd_cols_core<ArithF64, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, lds);
+            st.store(twl);
+            __syncthreads();
+            fwd_cols_core<ArithF64, S1, S2>(x, ar, twl, lds);
             fwd_cols_store<ArithF64, S1, S2>(x, ar, tile, olimb);
         } else {
             const ArithInt ar(q);
             uint64_t x[SB::E];
             bconv_source<ArithInt, S1, S2>(a, t, ar, mi, g, j, tile, x);
-            fwd_cols_core<ArithInt, S1, S2>(x, ar, t.tw + (size_t)prow * G::N, reinterpret_cast<uint64_t *>(lds));
+            st.store(twl);
+            __syncthreads();
+            fwd_cols_core<ArithInt, S1, S2>(x, ar, twl, reinterpret_cast<uint64_t *>(lds));
             fwd_cols_store<ArithInt, S1, S2>(x, ar, tile, olimb);
         }
         __syncthreads();

@@ -459,18 +459,27 @@ ntt_fwd_cols(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     __shared__ double lds[G::COL_LDS];
+    // the tile's twiddle factors (entries 1 .. N1-1 of its prime's table),
+    // requested before its residues and staged in LDS: one wait covers both,
+    // and the rounds read LDS instead of L1/L2 (config-2 forward NTT
+    // 39.4-39.9 -> 37.4-38.0 us)
+    __shared__ ulonglong2 twl[G::N1];
     const uint32_t total = b.M * b.L * G::COL_TILES;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
     for (uint32_t cur = next_tile(b, G::COL_TILES, blockIdx.x, total); cur < total;
          cur = next_tile(b, G::COL_TILES, cur + gridDim.x, total)) {
         const TileRef r = decode_tile(b, G::COL_TILES, cur);
+        const uint32_t prow = b.map.row(r.l);
+        TwStage<G::N1, G::COL_THREADS> st;
+        st.load([&](uint32_t i) { return t.tw[(size_t)prow * G::N + i]; });
         uint64_t raw[SB::E];
         const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[(size_t)(F + SB::T * e) * G::N2 + c]);
-        const uint32_t prow = b.map.row(r.l);
+        st.store(twl);
+        __syncthreads();
         const uint64_t q = t.mod[prow];
-        const ulonglong2 *tw = t.tw + (size_t)prow * G::N;
+        const ulonglong2 *tw = twl;
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
             fwd_cols_tile<ArithF64, S1, S2>(raw, tw, r, q, lds, olimb);
