@@ -115,8 +115,8 @@ struct Ctx {
     ulonglong2 *rb_fw = nullptr;     // [QP][S2][N1] rows-pass stage bases tw[(N1 + k1) << g]
     ulonglong2 *rb_inv = nullptr;    // [QP][S2][N1] itw[(N1 + k1) << g]
     int n_cu = 256;                  // compute units of the device
-    int ntt_wpc = 3;                 // resident inverse-NTT workgroups per CU the grid is sized for
-    int ntt_wpc_fwd = 4;             // the same for the forward passes (no register prefetch)
+    int ntt_wpc = 3;                 // resident workgroups per CU of the prefetching inverse rows pass
+    int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
     bool ntt_onepass = false;        // single-launch NTT with the intermediate kept in L2 (ntt_kernels.h)
     int onepass_wpc = 3;             // workgroups per CU of the single-launch NTT
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),

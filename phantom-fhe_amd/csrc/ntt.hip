@@ -66,7 +66,7 @@ void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES, c.ntt_wpc)), dim3(G::COL_THREADS), 0, s, b2,
+    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES, c.ntt_wpc_fwd)), dim3(G::COL_THREADS), 0, s, b2,
                        t);
 }
 

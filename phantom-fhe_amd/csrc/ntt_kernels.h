@@ -742,41 +742,38 @@ __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
     for (int e = 0; e < SB::E; e++) st_stream(&data[(size_t)(F + SB::T * e) * G::N2 + c], ar.store(x[e]));
 }
 
+// Like the forward columns pass: no register prefetch (124 VGPRs, 4 waves
+// per SIMD) and the tile's twiddle factors staged in LDS, requested before its
+// residues (config-2 inverse 41.0-41.2 -> 39.4 us; with the prefetch at 3
+// waves, the staging alone had cost 3 us).
 template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) ntt_inv_cols(NttBatch b, NttTables t) {
+__global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) __attribute__((amdgpu_waves_per_eu(4, 8)))
+ntt_inv_cols(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     __shared__ double lds[G::COL_LDS];
+    __shared__ ulonglong2 twl[G::N1];
     const uint32_t total = b.M * b.L * G::COL_TILES;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
-    uint32_t cur = next_tile(b, G::COL_TILES, blockIdx.x, total);
-    uint64_t raw[SB::E];
-    if (cur < total) {
-        const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, cur), b.src, b.sstride);
+    for (uint32_t cur = next_tile(b, G::COL_TILES, blockIdx.x, total); cur < total;
+         cur = next_tile(b, G::COL_TILES, cur + gridDim.x, total)) {
+        const TileRef r = decode_tile(b, G::COL_TILES, cur);
+        const uint32_t prow = b.map.row(r.l);
+        TwStage<G::N1, G::COL_THREADS> st;
+        st.load([&](uint32_t i) { return t.itw[(size_t)prow * G::N + i]; });
+        uint64_t raw[SB::E];
+        const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[(size_t)(F * SB::E + e) * G::N2 + c]);
-    }
-    while (cur < total) {
-        const uint32_t nxt = next_tile(b, G::COL_TILES, cur + gridDim.x, total);
-        const TileRef r = decode_tile(b, G::COL_TILES, cur);
-        uint64_t nraw[SB::E];
-        if (nxt < total) {
-            const uint64_t *s = cols_src<S1, S2>(b, decode_tile(b, G::COL_TILES, nxt), b.src, b.sstride);
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[(size_t)(F * SB::E + e) * G::N2 + c]);
-        }
-        const uint32_t prow = b.map.row(r.l);
+        st.store(twl);
+        __syncthreads();
         const uint64_t q = t.mod[prow];
-        const ulonglong2 *itw = t.itw + (size_t)prow * G::N;
         const ulonglong2 *scale = b.scale ? b.scale + r.l : nullptr;
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_cols_tile<ArithF64, S1, S2>(raw, itw, t.ninv[prow], scale, r, q, lds, olimb);
+            inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, lds, olimb);
         else
-            inv_cols_tile<ArithInt, S1, S2>(raw, itw, t.ninv[prow], scale, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
-#pragma unroll
-        for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
-        cur = nxt;
+            inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
         __syncthreads();
     }
 }
