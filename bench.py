@@ -73,6 +73,38 @@ def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def ntt_limb_sweep(torch, P, dev, gen, steps):
+    """Forward and inverse NTT time (HIP events, 10 rotating batches) for 2 polys
+    x L limbs of 50-bit primes at N = 2^16, over L around the config-2 batch.
+    Both passes process 16 tiles per limb on 4 x #CU resident workgroups, so the
+    sweep shows what a batch whose tile count exceeds the resident workgroups by
+    a little pays for its second round."""
+    mods = P.create_coeff_modulus(N, [50] * 48 + [60])
+    ctx = P.NativeContext(N, mods, 1)
+    stream = torch.cuda.current_stream()
+    h = stream.cuda_stream
+    rows = []
+    for L in (28, 30, 32, 33, 34, 35, 36, 40, 48):
+        bs = [uniform(torch, (POLYS, L, N), mods, dev, gen) for _ in range(10)]
+        us = []
+        for fn in (ctx.ntt_forward, ctx.ntt_inverse):
+            for i in range(20):
+                fn(bs[i % 10], POLYS, L, 0, h)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for i in range(steps):
+                fn(bs[i % 10], POLYS, L, 0, h)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us.append(e0.elapsed_time(e1) / steps * 1000)
+        rows.append({"limbs": POLYS * L, "tiles_per_pass": POLYS * L * 16, "forward_us": round(us[0], 2),
+                     "inverse_us": round(us[1], 2)})
+        log(f"bench: sweep {POLYS * L} limbs: forward {us[0]:.2f} us, inverse {us[1]:.2f} us")
+        del bs
+    return rows
+
+
 def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
     """multiply_and_relin + rescale on fresh chain-index-1 ciphertexts; returns ms per op."""
     bits = [60] + [50] * (nq - 1) + [60] * alpha
@@ -288,9 +320,10 @@ def main():
     ap.add_argument("--no-hmult", action="store_true")
     ap.add_argument("--no-bsgs", action="store_true")
     ap.add_argument("--no-boot", action="store_true")
-    ap.add_argument("--mode", choices=["full", "ntt", "copy", "hmult", "hmult35", "bsgs", "bootstrap"],
+    ap.add_argument("--mode", choices=["full", "ntt", "ntt-sweep", "copy", "hmult", "hmult35", "bsgs", "bootstrap"],
                     default="full",
-                    help="ntt: only the NTT timing (for rocprofv3 kernel traces); copy: torch copies of the "
+                    help="ntt: only the NTT timing (for rocprofv3 kernel traces); ntt-sweep: forward and inverse "
+                         "NTT time for 56 to 96 limbs; copy: torch copies of the "
                          "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
                          "config-3 HMult + relin + rescale; hmult35: only the L=35 variant; bsgs: only the "
                          "config-4 matrix-vector product; bootstrap: only the config-5 bootstrap")
@@ -321,6 +354,10 @@ def main():
         del batches
         r = time_bootstrap(torch, max(2, args.steps // 40), 1)
         log(f"bench: bootstrap mode, config 5: {r}")
+        return
+    if args.mode == "ntt-sweep":
+        del batches
+        print(json.dumps({"ntt_limb_sweep": ntt_limb_sweep(torch, P, dev, gen, args.steps)}))
         return
     if args.mode == "hmult":
         del batches
