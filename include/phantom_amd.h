@@ -72,6 +72,15 @@ void pfa_context_destroy(pfa_context *ctx);
 /* Copies the minimal primitive 2N-th root of every prime (|QP| values). */
 int pfa_context_roots(const pfa_context *ctx, uint64_t *out);
 
+/* cudaStreamSynchronize under PHANTOM_CHECK_CUDA (include/cuda_wrapper.cuh:19-43),
+ * plus the errors kernels of this context recorded on the device: waits for
+ * `stream`, then returns PFA_ERR_RUNTIME if a single-launch NTT (opt-in with
+ * PFA_NTT_FLOW=1, batches of 8+ limbs at N = 2^16) recorded that it did not
+ * transform every tile.  Every later NTT launch of the context reports such a
+ * record too, once its kernel has run.  The reference's kernels record no
+ * errors. */
+int pfa_synchronize(const pfa_context *ctx, void *stream);
+
 /* ------------------------------------------------------------------ NTT */
 
 /* nwt_2d_radix8_forward_inplace[_batched] (include/ntt.cuh:173, :184;
@@ -82,6 +91,19 @@ int pfa_ntt_forward(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L,
 /* nwt_2d_radix8_backward_inplace (include/ntt.cuh:216; src/ntt/intt_2d.cu:769-813),
  * batched over M polys like the forward. */
 int pfa_ntt_inverse(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L, size_t start, void *stream);
+
+/* No reference counterpart (a query for tests and tools): *out = 1 if an NTT of
+ * M polys x L limbs on this context runs as the single launch whose
+ * intermediate stays in one XCD's L2 (opted into with PFA_NTT_FLOW=1 at context
+ * creation, N = 2^16, M L >= 8, the device deals workgroups to 8 XCDs
+ * round-robin), 0 if it runs as two launches. */
+int pfa_ntt_single_launch(const pfa_context *ctx, size_t M, size_t L, int *out);
+
+/* No reference counterpart (a measurement aid): copies n uint64 words (n even)
+ * from src to dst with nontemporal 16-byte loads and stores, on `workgroups`
+ * workgroups of 256 threads (0: one per 16 KiB), the achievable one-read
+ * one-write bandwidth against which the NTT is measured. */
+int pfa_stream_copy(uint64_t *dst, const uint64_t *src, size_t n, size_t workgroups, void *stream);
 
 /* --------------------------------------------------- RNS / key switching */
 

@@ -234,14 +234,23 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     for (auto &e : c.stage_ev) PFA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
-    // Single-launch NTT (N = 2^16): needs the round-robin workgroup-to-XCD
-    // dealing of a full-chip MI355X partition, checked here by a probe kernel.
-    // PFA_NTT_ONEPASS=0 selects the two-launch path.
-    if (const char *w = std::getenv("PFA_ONEPASS_WPC")) c.onepass_wpc = std::max(1, std::atoi(w));
+    // Single-launch NTT (N = 2^16, opt-in with PFA_NTT_FLOW=1): built for the
+    // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition,
+    // checked here by a probe kernel.  The other variables tune it (workgroups
+    // per CU, look-ahead window, smallest batch, wait bound).
+    if (const char *w = std::getenv("PFA_FLOW_WPC")) c.flow_wpc = std::max(1, std::atoi(w));
+    if (const char *w = std::getenv("PFA_FLOW_WINDOW"))
+        c.flow_window = (uint32_t)std::min(32, std::max(1, std::atoi(w)));
+    if (const char *w = std::getenv("PFA_FLOW_MIN_JOBS")) c.flow_min_jobs = (uint32_t)std::max(1, std::atoi(w));
+    if (const char *w = std::getenv("PFA_FLOW_WAIT_TICKS")) c.flow_wait_ticks = (uint32_t)std::max(0, std::atoi(w));
+    PFA_HIP(hipHostMalloc((void **)&c.flow_err_host, 64, hipHostMallocMapped));
+    *c.flow_err_host = 0;
+    PFA_HIP(hipHostGetDevicePointer((void **)&c.flow_err_host_dev, c.flow_err_host, 0));
+    c.flow_err_dev = c.upload(std::vector<uint32_t>(16, 0u));
     {
-        const char *f = std::getenv("PFA_NTT_ONEPASS");
+        const char *f = std::getenv("PFA_NTT_FLOW");
         const bool want = f ? std::atoi(f) != 0 : false;
-        c.ntt_onepass = want && c.N == 65536 && c.n_cu * c.onepass_wpc >= 128 && xcd_round_robin(c);
+        c.ntt_flow = want && c.N == 65536 && xcd_round_robin(c);
     }
 
     const uint64_t *Qm = moduli, *Pm = moduli + c.Q;
@@ -348,7 +357,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     }
 }
 
-static Arena &arena_for(const Ctx &c, hipStream_t s) {
+Arena &arena_for(const Ctx &c, hipStream_t s) {
     std::lock_guard<std::mutex> lock(c.arena_mu);
     Arena *&a = c.arenas[{std::this_thread::get_id(), s}];
     if (!a) a = new Arena();
@@ -405,8 +414,10 @@ static void destroy(Ctx *c) {
     for (auto &e : c->stage_ev)
         if (e) (void)hipEventDestroy(e);
     if (c->stage) (void)hipHostFree(c->stage);
+    if (c->flow_err_host) (void)hipHostFree(c->flow_err_host);
     for (auto &kv : c->arenas) {
         for (auto &ch : kv.second->chunks) (void)hipFree(ch.base);
+        if (kv.second->flow) (void)hipFree(kv.second->flow);
         delete kv.second;
     }
     for (void *p : c->allocations) (void)hipFree(p);
@@ -417,6 +428,25 @@ static void destroy(Ctx *c) {
 Ctx *ctx_of(const pfa_context *c) {
     if (!c) fail(PFA_ERR_INVALID_ARGUMENT, "null context");
     return (Ctx *)c;
+}
+
+void check_device_errors(const Ctx &c) {
+    if (!c.flow_err_host) return;
+    volatile uint32_t *h = c.flow_err_host;
+    if (*h == 0) return;
+    *h = 0;
+    uint32_t bits = 0;
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(c.device);
+    (void)hipMemcpy(&bits, c.flow_err_dev, sizeof(bits), hipMemcpyDeviceToHost);
+    (void)hipMemset(c.flow_err_dev, 0, sizeof(bits));
+    (void)hipSetDevice(prev);
+    std::string why;
+    if (bits & 1u) why += " a bounded wait expired;";
+    if (bits & 2u) why += " the launch ended with tiles not transformed;";
+    fail(PFA_ERR_RUNTIME, "single-launch NTT error:" + why +
+                              " its output and everything computed from it are invalid");
 }
 
 }  // namespace pfa
@@ -461,6 +491,14 @@ int pfa_context_create(uint64_t poly_degree, const uint64_t *moduli, size_t size
 }
 
 void pfa_context_destroy(pfa_context *ctx) { destroy((Ctx *)ctx); }
+
+int pfa_synchronize(const pfa_context *ctx, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        PFA_HIP(hipStreamSynchronize(as_stream(stream)));
+        check_device_errors(c);
+    });
+}
 
 int pfa_context_roots(const pfa_context *ctx, uint64_t *out) {
     return guarded([&] {

@@ -96,6 +96,11 @@ struct Arena {
         size_t cap, top;
     };
     std::vector<Chunk> chunks;
+    // control blocks of the single-launch NTT on this stream (two, used in
+    // turn; see FlowCtl in ntt_kernels.h), allocated on first use
+    uint32_t *flow = nullptr;
+    uint32_t flow_parity = 0;
+    uint32_t flow_dirty[2] = {0, 0};  // jobs the last launch on each block used
 };
 
 struct Ctx {
@@ -117,8 +122,17 @@ struct Ctx {
     int n_cu = 256;                  // compute units of the device
     int ntt_wpc = 3;                 // resident workgroups per CU of the prefetching inverse rows pass
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
-    bool ntt_onepass = false;        // single-launch NTT with the intermediate kept in L2 (ntt_kernels.h)
-    int onepass_wpc = 3;             // workgroups per CU of the single-launch NTT
+    // single-launch NTT (ntt_kernels.h, opt-in): needs a device that deals
+    // workgroups to 8 XCDs round-robin; used for batches of at least
+    // flow_min_jobs limbs at N = 2^16
+    bool ntt_flow = false;
+    int flow_wpc = 2;                // workgroups per CU
+    uint32_t flow_window = 2;        // jobs ahead of the second-pass front
+    uint32_t flow_min_jobs = 8;
+    uint32_t flow_wait_ticks = 10000000;  // 100 ms at the 100 MHz s_memrealtime clock
+    uint32_t *flow_err_dev = nullptr;      // device error word of the single-launch NTT
+    uint32_t *flow_err_host = nullptr;     // mapped pinned word the kernel sets on error
+    uint32_t *flow_err_host_dev = nullptr; // its device address
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
     // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
     ulonglong2 *moddown_scale = nullptr;
@@ -171,6 +185,13 @@ T *Ctx::upload(const std::vector<T> &v) {
 }
 
 Ctx *ctx_of(const pfa_context *c);
+// Throws PFA_ERR_RUNTIME (and clears the record) if a kernel of this context
+// recorded an error on the device since the last check.  Kernels record it in
+// mapped host memory, so the check sees it once the kernel has run.
+void check_device_errors(const Ctx &c);
+// The calling thread's workspace for stream s (its single-launch NTT control
+// blocks live there).
+Arena &arena_for(const Ctx &c, hipStream_t s);
 void encoder_init(Ctx &c);
 
 // RAII scope over the calling thread's workspace for stream s: alloc() hands
@@ -210,8 +231,9 @@ struct NttLaunch {
 };
 void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s);
 void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s);
-// True when the device deals workgroups to 8 XCDs round-robin (workgroup w on
-// XCD w mod 8), which the single-launch NTT relies on; runs a probe kernel.
+// True when the device deals a launch's workgroups to 8 XCDs round-robin
+// (workgroup w on XCD (w + r) mod 8 for some r), which the single-launch NTT is
+// built for; runs a probe kernel.
 bool xcd_round_robin(const Ctx &c);
 
 // Fused key-switching / rescale pipelines (fused_ks.hip).

@@ -1,5 +1,7 @@
 // NTT launchers and the raw-limb NTT entry points of the C ABI.
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "internal.h"
@@ -88,24 +90,46 @@ void check_launch(const Ctx &c, const NttLaunch &a) {
 
 }  // namespace
 
-// Single-launch transform (N = 2^16 only; see ntt_kernels.h).
+// Single-launch transform (N = 2^16; see ntt_kernels.h).  Takes the next of
+// the two control blocks of the calling thread's workspace for stream s.
 template <bool FWD>
-void onepass(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
-    constexpr uint32_t T = OnePassGeo<8, 8>::T;
+void flow(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     const uint32_t jobs = b.M * b.L;
-    const uint32_t words = jobs * (T + 1) + 1;
-    Scratch sc(c, s);
-    uint32_t *ctl = sc.alloc<uint32_t>(words);
-    hipLaunchKernelGGL(k_zero_u32, dim3(std::min<uint32_t>((words + 255) / 256, 1024)), dim3(256), 0, s, ctl, words);
-    const OnePass o{ctl, ctl + (size_t)jobs * T, ctl + (size_t)jobs * (T + 1)};
-    // a whole number of job slots (8 XCDs x T workgroups) per launch
-    const uint32_t per = kXcds * T;
-    const uint32_t grid = std::max<uint32_t>(per, ((uint32_t)c.n_cu * (uint32_t)c.onepass_wpc) / per * per);
-    if (FWD)
-        hipLaunchKernelGGL((ntt_fwd_1p<8, 8>), dim3(grid), dim3(256), 0, s, b, t, o);
-    else
-        hipLaunchKernelGGL((ntt_inv_1p<8, 8>), dim3(grid), dim3(256), 0, s, b, t, o);
+    Arena &a = arena_for(c, s);
+    if (!a.flow) {
+        PFA_HIP(hipMalloc((void **)&a.flow, 2 * (size_t)kFlowBlockWords * sizeof(uint32_t)));
+        PFA_HIP(hipMemsetAsync(a.flow, 0, 2 * (size_t)kFlowBlockWords * sizeof(uint32_t), s));
+    }
+    const uint32_t p = a.flow_parity;
+    FlowCtl f;
+    f.blk = a.flow + (size_t)p * kFlowBlockWords;
+    f.other = a.flow + (size_t)(1 - p) * kFlowBlockWords;
+    f.other_jobs = a.flow_dirty[1 - p];
+    f.window = c.flow_window;
+    f.wait_ticks = c.flow_wait_ticks;
+    f.dev_err = c.flow_err_dev;
+    f.host_err = c.flow_err_host_dev;
+    const uint32_t grid = (uint32_t)c.n_cu * (uint32_t)c.flow_wpc / kXcds * kXcds;
+    if (FWD) {
+        if (c.flow_wpc >= 4)
+            hipLaunchKernelGGL((ntt_fwd_flow<8, 8, 4>), dim3(grid), dim3(256), 0, s, b, t, f);
+        else
+            hipLaunchKernelGGL((ntt_fwd_flow<8, 8, 3>), dim3(grid), dim3(256), 0, s, b, t, f);
+    } else {
+        if (c.flow_wpc >= 4)
+            hipLaunchKernelGGL((ntt_inv_flow<8, 8, 4>), dim3(grid), dim3(256), 0, s, b, t, f);
+        else
+            hipLaunchKernelGGL((ntt_inv_flow<8, 8, 3>), dim3(grid), dim3(256), 0, s, b, t, f);
+    }
     PFA_HIP(hipGetLastError());
+    a.flow_parity = 1 - p;
+    a.flow_dirty[p] = jobs;
+    a.flow_dirty[1 - p] = 0;
+}
+
+bool use_flow(const Ctx &c, const NttBatch &b) {
+    const uint32_t jobs = b.M * b.L;
+    return c.ntt_flow && c.logN == 16 && jobs >= c.flow_min_jobs && jobs <= kFlowMaxJobs;
 }
 
 #define PFA_NTT_DISPATCH(FN)                                                 \
@@ -125,8 +149,9 @@ void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    if (c.ntt_onepass) {
-        onepass<true>(c, b, t, s);
+    check_device_errors(c);
+    if (use_flow(c, b)) {
+        flow<true>(c, b, t, s);
         return;
     }
     PFA_NTT_DISPATCH(fwd);
@@ -137,12 +162,41 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    if (c.ntt_onepass) {
-        onepass<false>(c, b, t, s);
+    check_device_errors(c);
+    if (use_flow(c, b)) {
+        flow<false>(c, b, t, s);
         return;
     }
     PFA_NTT_DISPATCH(inv);
     PFA_HIP(hipGetLastError());
+}
+
+// Streaming copy of n 16-byte words, each thread moving U words per round with
+// nontemporal loads and stores: the achievable-bandwidth reference for the
+// NTT's one-read-one-write traffic.
+template <int U>
+__global__ void __launch_bounds__(256) k_stream_copy(ulonglong2 *__restrict__ dst, const ulonglong2 *__restrict__ src,
+                                                     uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256 * U;
+    for (uint64_t base = (uint64_t)blockIdx.x * 256 * U + threadIdx.x; base < n; base += stride) {
+        ulonglong2 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + (uint64_t)u * 256;
+            if (i < n) {
+                v[u].x = __builtin_nontemporal_load(&src[i].x);
+                v[u].y = __builtin_nontemporal_load(&src[i].y);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + (uint64_t)u * 256;
+            if (i < n) {
+                __builtin_nontemporal_store(v[u].x, &dst[i].x);
+                __builtin_nontemporal_store(v[u].y, &dst[i].y);
+            }
+        }
+    }
 }
 
 bool xcd_round_robin(const Ctx &c) {
@@ -155,8 +209,17 @@ bool xcd_round_robin(const Ctx &c) {
     if (e == hipSuccess) e = hipMemcpy(h.data(), d, G * sizeof(uint32_t), hipMemcpyDeviceToHost);
     (void)hipFree(d);
     PFA_HIP(e);
+    // round-robin from the XCD of workgroup 0, which depends on earlier dispatches
+    const bool debug = std::getenv("PFA_FLOW_DEBUG") != nullptr;
+    const uint32_t r = h[0];
     for (uint32_t i = 0; i < G; i++)
-        if (h[i] != i % kXcds) return false;
+        if (h[i] != (i + r) % kXcds) {
+            if (debug)
+                std::fprintf(stderr, "pfa: workgroup %u ran on XCD %u, not %u: single-launch NTT disabled\n", i,
+                             h[i], (i + r) % kXcds);
+            return false;
+        }
+    if (debug) std::fprintf(stderr, "pfa: workgroups are dealt to %u XCDs round-robin (from XCD %u)\n", kXcds, r);
     return true;
 }
 
@@ -173,6 +236,31 @@ int pfa_ntt_forward(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L,
         NttLaunch a{inout, inout, 0, 0, (uint32_t)M, (uint32_t)L};
         a.start = (uint32_t)start;
         ntt_forward(c, a, as_stream(stream));
+    });
+}
+
+int pfa_stream_copy(uint64_t *dst, const uint64_t *src, size_t n, size_t workgroups, void *stream) {
+    return guarded([&] {
+        require(dst && src, "null data pointer");
+        require(n % 2 == 0, "copy length must be a multiple of 2 words");
+        const uint64_t n2 = n / 2;
+        if (n2 == 0) return;
+        const uint64_t need = (n2 + 256 * 4 - 1) / (256 * 4);
+        const uint64_t grid = workgroups ? std::min<uint64_t>(workgroups, need) : need;
+        hipLaunchKernelGGL(k_stream_copy<4>, dim3((uint32_t)grid), dim3(256), 0, as_stream(stream),
+                           (ulonglong2 *)dst, (const ulonglong2 *)src, n2);
+        PFA_HIP(hipGetLastError());
+    });
+}
+
+int pfa_ntt_single_launch(const pfa_context *ctx, size_t M, size_t L, int *out) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(out != nullptr, "null argument");
+        NttBatch b{};
+        b.M = (uint32_t)M;
+        b.L = (uint32_t)L;
+        *out = M * L <= kFlowMaxJobs && use_flow(c, b) ? 1 : 0;
     });
 }
 

@@ -780,267 +780,333 @@ ntt_inv_cols(NttBatch b, NttTables t) {
 
 }  // namespace pfa
 
+
 namespace pfa {
 
-// ================================================================ single pass
-// One launch runs both passes of every limb, and a limb's intermediate never
-// leaves the L2 of the XCD that owns the limb: each first-pass tile rewrites
-// only its own tile of the output limb, and the second pass reads the limb back
-// from that L2.  HBM sees one read of the input and one write of the output.
+// ================================================================ single launch
+// One launch runs both passes of every limb of the batch, and a limb's
+// intermediate never leaves the L2 of the XCD that transforms it: HBM sees one
+// read of the input and one write of the output instead of two of each.
 //
-// Ownership: limb-job j (tile order: j = l M + m) belongs to XCD j mod 8.
-// Workgroups are dealt to the XCDs round-robin (workgroup w runs on XCD w mod 8,
-// checked once per context by a probe kernel before this path is enabled), so
-// workgroup w is local workgroup u = w / 8 of XCD x = w mod 8.  With U = grid / 8
-// local workgroups and T tiles per pass, an XCD works on S = U / T jobs at a
-// time: local workgroup u takes first-pass tile u mod T of the XCD's jobs
-// u / T, u / T + S, ..., and after each the second-pass tile u mod T.
+// Jobs (j = l M + m) belong to XCD j mod 8.  Every workgroup reads the id of
+// the XCD it runs on (hardware register) and serves only that XCD's jobs, so a
+// job's two passes always share one L2 whatever the dispatch order.  (The
+// device deals a launch's workgroups to the 8 XCDs round-robin, starting at an
+// XCD that depends on earlier dispatches, so a grid that is a multiple of 8
+// gives every XCD the same number of workgroups.)  Work is handed out
+// dynamically per XCD:
+//   - first-pass tiles by a ticket counter in job order, at most `window` jobs
+//     ahead of the oldest job whose second pass is not fully handed out (the
+//     front), which bounds the limbs held in L2;
+//   - second-pass tiles of a job once all its first-pass tiles are finished,
+//     by a per-job claim counter.
+// A workgroup waits only when no tile can be handed to it; then every
+// first-pass tile of the jobs in the window is held by a running workgroup,
+// which finishes it without waiting, so every wait ends (no co-residency or
+// cooperative launch is assumed).  A wait is still bounded in time: on expiry
+// the workgroup records the error (device word and a mapped host word) and
+// leaves, and the kernel ends.  The last workgroup to leave checks that every
+// tile of the batch was transformed (a device-wide count) and records an error
+// otherwise, so missing work can never pass silently.
 //
-// No co-residency is assumed.  A first-pass tile is run only after claiming it
-// (agent-scope exchange on its flag), by its owner or by any workgroup of the
-// XCD that waits for the job; a workgroup waits only while every first-pass
-// tile of its job is claimed, i.e. held by running workgroups, which finish
-// them without waiting for anything.
+// Visibility inside an XCD: a first-pass tile's stores are complete in L2
+// (s_waitcnt vmcnt(0)) before its job's finished count is raised; a workgroup
+// that starts a second-pass tile invalidates its CU's L1 (buffer_inv sc0) and
+// reads the limb from the XCD's L2.
 //
-// Visibility within the XCD: a first-pass tile's stores are acknowledged by L2
-// (s_waitcnt 0) before the job's count is raised with an atomic add (atomics
-// execute in L2); a workgroup that reads the full count invalidates its CU's L1
-// (buffer_inv sc0) before it loads the limb, so it reads the XCD's L2.  Every
-// wait is bounded: on expiry bit 0 of the flag word is set and the kernel
-// still ends.
-struct OnePass {
-    uint32_t *claim;  // [jobs][T] first-pass tile claims, zero at launch
-    uint32_t *done;   // [jobs] finished first-pass tiles, zero at launch
-    uint32_t *flags;  // [1] bit 0: a wait expired
-};
-
+// Control words live in two blocks per (context, thread, stream): a launch
+// uses one (all zero at launch) and zeroes the part of the other that the
+// previous launch used, for the next launch.
 constexpr uint32_t kXcds = 8;
-constexpr uint32_t kSpinLimit = 1u << 16;   // polls of one wait (each an agent-scope load after s_sleep 2)
-constexpr uint32_t kStealEvery = 64;         // polls between scans for unclaimed first-pass tiles
+constexpr uint32_t kFlowXcdWords = 64;   // per XCD: first-pass ticket at +0, front at +32 (own 128-B lines)
+// after the XCD words, one 128-B line whose first 8 bytes count, for the whole
+// launch, (workgroups that left) << 32 | (tiles transformed)
+constexpr uint32_t kFlowHeadWords = kXcds * kFlowXcdWords + 32;
+constexpr uint32_t kFlowJobWords = 16;   // per job: finished first-pass tiles at +0, second-pass claims at +1
+constexpr uint32_t kFlowMaxJobs = 4096;
+constexpr uint32_t kFlowBlockWords = kFlowHeadWords + kFlowMaxJobs * kFlowJobWords;
+constexpr uint32_t kFlowMaxWindow = 32;
+// error bits
+constexpr uint32_t kFlowErrWait = 1u;        // a wait expired
+constexpr uint32_t kFlowErrIncomplete = 2u;  // the launch ended with tiles not transformed
+
+struct FlowCtl {
+    uint32_t *blk;         // this launch's control block (zero at launch)
+    uint32_t *other;       // the other block: its first other_jobs jobs are zeroed here
+    uint32_t other_jobs;
+    uint32_t window;       // 1 .. kFlowMaxWindow
+    uint32_t wait_ticks;   // bound of one wait, s_memrealtime ticks (100 MHz)
+    uint32_t *dev_err;     // device error word (bits above), or-ed
+    uint32_t *host_err;    // mapped pinned host word, written on error only
+};
 
 template <int S1, int S2>
-struct OnePassGeo {
+struct FlowGeo {
     using G = Geo<S1, S2>;
-    static constexpr bool OK = G::COL_THREADS == 256 && G::ROW_THREADS == 256 && G::COL_LDS == G::ROW_LDS &&
-                               G::COL_TILES == G::ROW_TILES;
+    static constexpr bool OK = G::COL_THREADS == 256 && G::ROW_THREADS == 256 && G::COL_TILES == G::ROW_TILES;
     static constexpr uint32_t T = G::COL_TILES;
+    static constexpr int LDS = G::COL_LDS > G::ROW_LDS ? G::COL_LDS : G::ROW_LDS;
+    static constexpr int TWL = G::N1 > RowStage<S1, S2>::N ? G::N1 : RowStage<S1, S2>::N;
 };
 
-// Polls are read-modify-writes (fetch_or 0): on gfx950 atomic RMWs execute in
-// the XCD's L2, where the counters live, while an agent-scope atomic load is
-// issued past L2 and costs a round trip to memory per poll.
-__device__ __forceinline__ uint32_t ld_agent(uint32_t *p) {
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xfu;
+}
+
+// Reads of control words are read-modify-writes: they execute in the XCD's L2
+// where the words live, and never hit a stale L1 line.
+__device__ __forceinline__ uint32_t flow_rd(uint32_t *p) {
     return __hip_atomic_fetch_or(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool try_claim(uint32_t *p) {
-    return __hip_atomic_exchange(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
+__device__ __forceinline__ uint32_t flow_add(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Next first-pass tile this workgroup runs for `job` (< T), T + 1 once the job's
-// first pass is complete, or T to keep waiting.  `own` is the workgroup's own
-// tile on its first call for the job, T afterwards.  Uniform across the
-// workgroup (decided by thread 0, shared through LDS).
+__device__ __forceinline__ void flow_error(const FlowCtl &c, uint32_t bits) {
+    __hip_atomic_fetch_or(c.dev_err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(c.host_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+constexpr uint32_t kFlowExit = 0xffffffffu, kFlowWait = 0xfffffffeu, kFlowPass2 = 0x80000000u;
+
+// Next command of a workgroup, decided by wave 0 (every lane of it calls this):
+// a first-pass tile k (local job k / T, tile k mod T), kFlowPass2 | k for a
+// second-pass tile, kFlowWait or kFlowExit.  Lane i looks at job front + i.
 template <uint32_t T>
-__device__ __forceinline__ uint32_t onepass_next(const OnePass &c, uint32_t job, uint32_t own, uint32_t spins,
-                                                 uint32_t *s_pick, uint32_t *s_free) {
-    uint32_t *cl = c.claim + (size_t)job * T;
-    if (threadIdx.x == 0) {
-        uint32_t pick = T;
-        if (own < T && try_claim(cl + own)) pick = own;
-        if (pick == T && ld_agent(c.done + job) >= T) pick = T + 1;
-        *s_pick = pick;
+__device__ __forceinline__ uint32_t flow_decide(const FlowCtl &c, uint32_t x, uint32_t nj, uint32_t *next1,
+                                                uint32_t *front, uint32_t *jobw) {
+    const uint32_t lane = threadIdx.x;
+    uint32_t f = lane == 0 ? flow_rd(front) : 0u;
+    f = __builtin_amdgcn_readfirstlane(f);
+    if (f >= nj) return kFlowExit;
+    const uint32_t lj = f + lane;
+    const bool act = lane < c.window && lj < nj;
+    uint32_t *jw = jobw + (size_t)(x + kXcds * lj) * kFlowJobWords;
+    uint32_t done = 0, claimed = T;
+    if (act) {
+        done = flow_rd(jw);
+        claimed = flow_rd(jw + 1);
     }
-    __syncthreads();
-    uint32_t pick = *s_pick;
-    if (pick == T && spins % kStealEvery == kStealEvery - 1) {
-        // look for first-pass tiles nobody has claimed (their owner is not running)
-        if (threadIdx.x < T) s_free[threadIdx.x] = ld_agent(cl + threadIdx.x) == 0u;
-        __syncthreads();
-        if (threadIdx.x == 0)
-            for (uint32_t i = 0; i < T; i++)
-                if (s_free[i] && try_claim(cl + i)) {
-                    *s_pick = i;
-                    break;
-                }
-        __syncthreads();
-        pick = *s_pick;
+    // advance the front past leading jobs whose second pass is fully handed out
+    // (a failed exchange means another workgroup moved it; either is fine)
+    const uint64_t full = __ballot(act && claimed >= T);
+    const uint32_t adv = (uint32_t)__builtin_ctzll(~full);
+    if (adv > 0 && lane == 0) {
+        uint32_t expect = f;
+        __hip_atomic_compare_exchange_strong(front, &expect, f + adv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
     }
-    __syncthreads();
-    return pick;
+    if (f + adv >= nj) return kFlowExit;
+    uint64_t ready = __ballot(act && done >= T && claimed < T);
+    while (ready) {
+        const uint32_t i = (uint32_t)__builtin_ctzll(ready);
+        ready &= ready - 1;
+        uint32_t k = 0;
+        if (lane == 0) k = flow_add(jobw + (size_t)(x + kXcds * (f + i)) * kFlowJobWords + 1, 1u);
+        k = __builtin_amdgcn_readfirstlane(k);
+        if (k < T) return kFlowPass2 | ((f + i) * T + k);
+    }
+    uint32_t k1 = kFlowWait;
+    if (lane == 0) {
+        const uint32_t n1 = nj * T;
+        uint32_t k = flow_rd(next1);
+        if (k < n1 && k / T < f + c.window) {
+            k = flow_add(next1, 1u);
+            if (k < n1) k1 = k;
+        }
+    }
+    return __builtin_amdgcn_readfirstlane(k1);
 }
 
-__device__ __forceinline__ void onepass_publish(uint32_t *done) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void onepass_expired(uint32_t *flags) {
-    if (threadIdx.x == 0) __hip_atomic_fetch_or(flags, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The two passes of one job for the single-pass kernels; FWD selects the
-// forward (columns then rows) or inverse (rows then columns) transform.
+// Tiles of one job for the single-launch kernel.  FWD: columns pass then rows
+// pass; inverse: rows pass then columns pass.  twl: LDS for the tile's staged
+// twiddle factors, lds: the transpose buffer.
 template <bool FWD, int S1, int S2>
-struct OnePassJob {
+struct FlowJob {
     using G = Geo<S1, S2>;
     using S1B = Sub<S1>;
     using S2B = Sub<S2>;
-    static constexpr uint32_t T = OnePassGeo<S1, S2>::T;
+    using RS = RowStage<S1, S2>;
     const NttBatch &b;
     const NttTables &t;
     uint32_t m, l, prow;
     uint64_t q;
     uint64_t *limb;
 
-    __device__ OnePassJob(const NttBatch &b_, const NttTables &t_, uint32_t job) : b(b_), t(t_) {
+    __device__ FlowJob(const NttBatch &b_, const NttTables &t_, uint32_t job) : b(b_), t(t_) {
         m = job % b.M;
         l = job / b.M;
         prow = b.map.row(l);
         q = t.mod[prow];
         limb = b.dst + m * b.dstride + (size_t)l * G::N;
     }
-    // first-pass tile `tile`: reads the source, leaves the intermediate in the
-    // tile's own part of the output limb (plain stores: the lines stay in L2)
-    __device__ void first(uint32_t tile, double *lds) const {
+
+    // first-pass tile: source -> the tile's part of the output limb in the
+    // intermediate form, with plain stores so the lines stay in L2
+    __device__ void first(uint32_t tile, double *lds, ulonglong2 *twl) const {
         const TileRef r{m, l, tile};
         if (FWD) {
             const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+            TwStage<G::N1, G::COL_THREADS> st;
+            st.load([&](uint32_t i) { return t.tw[(size_t)prow * G::N + i]; });
             const uint64_t *s = cols_src<S1, S2>(b, r, b.src, b.sstride);
             uint64_t raw[S1B::E];
 #pragma unroll
             for (int e = 0; e < S1B::E; e++) raw[e] = ld_stream(&s[(size_t)(F + S1B::T * e) * G::N2 + c]);
+            st.store(twl);
+            __syncthreads();
             if (q < kF64PrimeBound)
-                fwd_cols_tile<ArithF64, S1, S2, false>(raw, t.tw + (size_t)prow * G::N, r, q, lds, limb);
+                fwd_cols_tile<ArithF64, S1, S2, false>(raw, twl, r, q, lds, limb);
             else
-                fwd_cols_tile<ArithInt, S1, S2, false>(raw, t.tw + (size_t)prow * G::N, r, q,
-                                                       reinterpret_cast<uint64_t *>(lds), limb);
+                fwd_cols_tile<ArithInt, S1, S2, false>(raw, twl, r, q, reinterpret_cast<uint64_t *>(lds), limb);
         } else {
-            const uint32_t F = threadIdx.x % S2B::T;
+            const uint32_t F = threadIdx.x % S2B::T, rr = threadIdx.x / S2B::T;
+            RS stage;
+            stage.load(t, prow, tile, false);
             const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
             uint64_t raw[S2B::E];
 #pragma unroll
             for (int e = 0; e < S2B::E; e++) raw[e] = ld_stream(&s[F + S2B::T * e]);
+            stage.st.store(twl);
+            __syncthreads();
+            const TileTw w = RS::view(twl, t.itw + (size_t)prow * G::N, rr);
             if (q < kF64PrimeBound)
-                inv_rows_tile<ArithF64, S1, S2, G::N1, false>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, false), r, q, lds, limb);
+                inv_rows_tile<ArithF64, S1, S2, G::ROWS, false>(raw, w, r, q, lds, limb);
             else
-                inv_rows_tile<ArithInt, S1, S2, G::N1, false>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, false), r, q,
-                                                              reinterpret_cast<uint64_t *>(lds), limb);
+                inv_rows_tile<ArithInt, S1, S2, G::ROWS, false>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds),
+                                                                limb);
         }
     }
-    // second-pass tile `tile` of the output limb, after the job's first pass
-    __device__ void second(uint32_t tile, double *lds) const {
+
+    // second-pass tile of the output limb, after all first-pass tiles of the job
+    __device__ void second(uint32_t tile, double *lds, ulonglong2 *twl) const {
         asm volatile("buffer_inv sc0" ::: "memory");
         const TileRef r{m, l, tile};
         if (FWD) {
-            const uint32_t F = threadIdx.x % S2B::T;
+            const uint32_t F = threadIdx.x % S2B::T, rr = threadIdx.x / S2B::T;
+            RS stage;
+            stage.load(t, prow, tile, true);
             const uint64_t *s = rows_ptr<S1, S2>(b, r, b.dst, b.dstride);
             uint64_t raw[S2B::E];
 #pragma unroll
             for (int e = 0; e < S2B::E; e++) raw[e] = s[F + S2B::T * e];
+            stage.st.store(twl);
+            __syncthreads();
+            const TileTw w = RS::view(twl, t.tw + (size_t)prow * G::N, rr);
             if (q < kF64PrimeBound)
-                fwd_rows_tile<ArithF64, S1, S2, G::N1>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, true), r, q, lds, limb);
+                fwd_rows_tile<ArithF64, S1, S2, G::ROWS>(raw, w, r, q, lds, limb);
             else
-                fwd_rows_tile<ArithInt, S1, S2, G::N1>(raw, global_tw<S1, S2>(t, prow, tile * G::ROWS + threadIdx.x / S2B::T, true), r, q,
-                                                       reinterpret_cast<uint64_t *>(lds), limb);
+                fwd_rows_tile<ArithInt, S1, S2, G::ROWS>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), limb);
         } else {
             const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
+            TwStage<G::N1, G::COL_THREADS> st;
+            st.load([&](uint32_t i) { return t.itw[(size_t)prow * G::N + i]; });
             const uint64_t *s = cols_src<S1, S2>(b, r, b.dst, b.dstride);
             uint64_t raw[S1B::E];
 #pragma unroll
             for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F * S1B::E + e) * G::N2 + c];
+            st.store(twl);
+            __syncthreads();
+            const ulonglong2 *scale = b.scale ? b.scale + l : nullptr;
             if (q < kF64PrimeBound)
-                inv_cols_tile<ArithF64, S1, S2>(raw, t.itw + (size_t)prow * G::N, t.ninv[prow], b.scale ? b.scale + l : nullptr, r, q, lds, limb);
+                inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, lds, limb);
             else
-                inv_cols_tile<ArithInt, S1, S2>(raw, t.itw + (size_t)prow * G::N, t.ninv[prow], b.scale ? b.scale + l : nullptr, r, q,
+                inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scale, r, q,
                                                 reinterpret_cast<uint64_t *>(lds), limb);
         }
-        __syncthreads();
     }
 };
 
-// Claims and runs first-pass tiles of `job` (its own tile `own` first, when
-// given) until the job's first pass is complete; false if a wait expired.
 template <bool FWD, int S1, int S2>
-__device__ bool onepass_complete(const OnePassJob<FWD, S1, S2> &J, const OnePass &ctl, uint32_t job, uint32_t own,
-                                 bool wait, double *lds, uint32_t *s_pick, uint32_t *s_free) {
-    constexpr uint32_t T = OnePassGeo<S1, S2>::T;
-    for (uint32_t spins = 0;; own = T) {
-        const uint32_t pick = onepass_next<T>(ctl, job, own, spins, s_pick, s_free);
-        if (pick == T + 1) return true;
-        if (pick < T) {
-            J.first(pick, lds);
-            onepass_publish(ctl.done + job);
-            if (!wait) return true;
+__device__ __forceinline__ void flow_run(const NttBatch &b, const NttTables &t, const FlowCtl &c) {
+    using FG = FlowGeo<S1, S2>;
+    constexpr uint32_t T = FG::T;
+    __shared__ double lds[FG::LDS];
+    __shared__ ulonglong2 twl[FG::TWL];
+    __shared__ uint32_t s_cmd;
+    {
+        const uint32_t words = kFlowHeadWords + c.other_jobs * kFlowJobWords;
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
+            c.other[i] = 0u;
+    }
+    const uint32_t x = xcc_id() & (kXcds - 1);
+    const uint32_t J = b.M * b.L;
+    const uint32_t nj = J > x ? (J - x + kXcds - 1) / kXcds : 0u;
+    uint32_t *next1 = c.blk + x * kFlowXcdWords, *front = next1 + 32;
+    uint32_t *jobw = c.blk + kFlowHeadWords;
+    uint64_t wait_from = 0;
+    bool waiting = false;
+    uint32_t tiles = 0;  // tiles this workgroup transformed (or skipped as excluded)
+    for (;;) {
+        if (threadIdx.x < 64) {
+            uint32_t cmd = flow_decide<T>(c, x, nj, next1, front, jobw);
+            if (threadIdx.x == 0) {
+                if (cmd == kFlowWait) {
+                    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+                    if (!waiting) {
+                        waiting = true;
+                        wait_from = now;
+                    } else if (now - wait_from > c.wait_ticks) {
+                        flow_error(c, kFlowErrWait);
+                        cmd = kFlowExit;
+                    }
+                } else {
+                    waiting = false;
+                }
+                s_cmd = cmd;
+            }
+        }
+        __syncthreads();
+        const uint32_t cmd = s_cmd;
+        __syncthreads();
+        if (cmd == kFlowExit) break;
+        if (cmd == kFlowWait) {
+            __builtin_amdgcn_s_sleep(2);
             continue;
         }
-        if (!wait) return true;
-        if (++spins > kSpinLimit) return false;
-        __builtin_amdgcn_s_sleep(2);
+        const uint32_t k = cmd & ~kFlowPass2;
+        const uint32_t job = x + kXcds * (k / T);
+        const FlowJob<FWD, S1, S2> fj(b, t, job);
+        const bool skip = b.excluded(fj.m, fj.l);
+        if (cmd & kFlowPass2) {
+            if (!skip) fj.second(k % T, lds, twl);
+        } else {
+            if (!skip) fj.first(k % T, lds, twl);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (threadIdx.x == 0) flow_add(jobw + (size_t)job * kFlowJobWords, 1u);
+        }
+        ++tiles;
+        __syncthreads();
     }
-}
-
-// Lag-one schedule of a local workgroup: first pass of job i + 1 before the
-// second pass of job i, so the wait for job i's first pass is usually over.
-template <bool FWD, int S1, int S2>
-__device__ void onepass_run(const NttBatch &b, const NttTables &t, const OnePass &ctl, double *lds, uint32_t *s_pick,
-                            uint32_t *s_free) {
-    constexpr uint32_t T = OnePassGeo<S1, S2>::T;
-    const uint32_t x = blockIdx.x % kXcds, u = blockIdx.x / kXcds;
-    const uint32_t S = (gridDim.x / kXcds) / T, slot = u / T, tau = u % T;
-    const uint32_t jobs = b.M * b.L;
-    const uint32_t nx = jobs > x ? (jobs - x + kXcds - 1) / kXcds : 0;
-    if (slot >= S) return;
-    uint32_t prev = 0xffffffffu;  // job whose second pass is pending
-    for (uint32_t kx = slot;; kx += S) {
-        uint32_t job = 0xffffffffu;
-        if (kx < nx) {
-            job = x + kXcds * kx;
-            if (b.excluded(job % b.M, job / b.M)) job = 0xffffffffu;
-        }
-        if (job != 0xffffffffu) {
-            const OnePassJob<FWD, S1, S2> J(b, t, job);
-            onepass_complete<FWD, S1, S2>(J, ctl, job, tau, false, lds, s_pick, s_free);
-        }
-        if (prev != 0xffffffffu) {
-            const OnePassJob<FWD, S1, S2> P(b, t, prev);
-            if (onepass_complete<FWD, S1, S2>(P, ctl, prev, T, true, lds, s_pick, s_free))
-                P.second(tau, lds);
-            else
-                onepass_expired(ctl.flags);
-        }
-        prev = job;
-        if (kx >= nx && prev == 0xffffffffu) break;
-    }
-}
-
-template <int S1, int S2>
-__global__ void __launch_bounds__(256) ntt_fwd_1p(NttBatch b, NttTables t, OnePass ctl) {
-    static_assert(OnePassGeo<S1, S2>::OK, "single-pass NTT needs matching 256-thread passes");
-    __shared__ double lds[Geo<S1, S2>::COL_LDS];
-    __shared__ uint32_t s_pick, s_free[OnePassGeo<S1, S2>::T];
-    onepass_run<true, S1, S2>(b, t, ctl, lds, &s_pick, s_free);
-}
-
-template <int S1, int S2>
-__global__ void __launch_bounds__(256) ntt_inv_1p(NttBatch b, NttTables t, OnePass ctl) {
-    static_assert(OnePassGeo<S1, S2>::OK, "single-pass NTT needs matching 256-thread passes");
-    __shared__ double lds[Geo<S1, S2>::COL_LDS];
-    __shared__ uint32_t s_pick, s_free[OnePassGeo<S1, S2>::T];
-    onepass_run<false, S1, S2>(b, t, ctl, lds, &s_pick, s_free);
-}
-
-// Records XCD ids by workgroup (the probe that enables the single-pass path).
-static __global__ void k_xcc_probe(uint32_t *out) {
     if (threadIdx.x == 0) {
-        uint32_t v;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-        out[blockIdx.x] = v & 0xfu;
+        uint64_t *fin = reinterpret_cast<uint64_t *>(c.blk + kXcds * kFlowXcdWords);
+        const uint64_t old = __hip_atomic_fetch_add(fin, (1ull << 32) | tiles, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(old >> 32) == gridDim.x - 1 && (uint32_t)old + tiles != 2u * T * J)
+            flow_error(c, kFlowErrIncomplete);
     }
 }
 
-static __global__ void k_zero_u32(uint32_t *p, uint32_t n) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+template <int S1, int S2, int W>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, 8)))
+ntt_fwd_flow(NttBatch b, NttTables t, FlowCtl c) {
+    static_assert(FlowGeo<S1, S2>::OK, "single-launch NTT needs matching 256-thread passes");
+    flow_run<true, S1, S2>(b, t, c);
+}
+
+template <int S1, int S2, int W>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, 8)))
+ntt_inv_flow(NttBatch b, NttTables t, FlowCtl c) {
+    static_assert(FlowGeo<S1, S2>::OK, "single-launch NTT needs matching 256-thread passes");
+    flow_run<false, S1, S2>(b, t, c);
+}
+
+// Records XCD ids by workgroup (the probe that enables the single-launch path).
+static __global__ void k_xcc_probe(uint32_t *out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
 }  // namespace pfa

@@ -31,6 +31,9 @@ SIGNATURES = {
     "pfa_context_create": (_i32, [_u64, _u64p, _sz, _sz, _i32, C.POINTER(_vp)]),
     "pfa_context_destroy": (None, [_vp]),
     "pfa_context_roots": (_i32, [_vp, _u64p]),
+    "pfa_synchronize": (_i32, [_vp, _vp]),
+    "pfa_ntt_single_launch": (_i32, [_vp, _sz, _sz, C.POINTER(C.c_int)]),
+    "pfa_stream_copy": (_i32, [_vp, _vp, _sz, _sz, _vp]),
     "pfa_ntt_forward": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp]),
     "pfa_ntt_inverse": (_i32, [_vp, _vp, _sz, _sz, _sz, _vp]),
     "pfa_modup": (_i32, [_vp, _sz, _vp, _vp, _vp]),
@@ -138,6 +141,14 @@ def stream_of(t=None):
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def stream_copy(dst, src, workgroups: int = 0, stream=None):
+    """Streaming copy of a uint64 tensor into another of the same size (the
+    achievable-bandwidth reference of the NTT's measurement)."""
+    if dst.numel() != src.numel():
+        raise ValueError("copy between tensors of different sizes")
+    call("pfa_stream_copy", ptr(dst), ptr(src), src.numel(), workgroups, stream or stream_of(src))
+
+
 def create_coeff_modulus(poly_degree: int, bit_sizes) -> list[int]:
     bits = (C.c_int * len(bit_sizes))(*bit_sizes)
     out = (C.c_uint64 * len(bit_sizes))()
@@ -202,6 +213,22 @@ class NativeContext:
 
     def ntt_inverse(self, data, M: int, L: int, start: int = 0, stream=None):
         call("pfa_ntt_inverse", self._h, ptr(data), M, L, start, stream or stream_of(data))
+
+    def ntt_single_launch(self, M: int, L: int) -> bool:
+        """True if an NTT of M x L limbs runs as one launch (intermediate in L2)."""
+        out = C.c_int(0)
+        call("pfa_ntt_single_launch", self._h, M, L, C.byref(out))
+        return bool(out.value)
+
+    def synchronize(self, stream=None):
+        """Waits for `stream` (default: torch's current stream on the context's
+        device) and raises RuntimeError if a kernel of this context recorded an
+        error on the device (a single-launch NTT that did not finish)."""
+        if stream is None:
+            import torch
+
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+        call("pfa_synchronize", self._h, stream)
 
     def modup(self, chain_index, c2, out, stream=None):
         call("pfa_modup", self._h, chain_index, ptr(c2), ptr(out), stream or stream_of(c2))

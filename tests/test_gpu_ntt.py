@@ -83,29 +83,70 @@ def test_ntt_config2_full_size(dev):
     assert np.array_equal(to_host(d), x)
 
 
-def test_ntt_single_launch_variant(dev, monkeypatch):
-    """The opt-in single-launch NTT (PFA_NTT_ONEPASS=1, read at context creation;
-    N = 2^16 on a device that deals workgroups to 8 XCDs round-robin) against
-    the oracle, both arithmetic policies, batches whose job count is not a
-    multiple of the XCD count, and a single limb."""
+def test_ntt_single_launch(dev, monkeypatch):
+    """The single-launch NTT (opt-in with PFA_NTT_FLOW=1 at N = 2^16 for batches
+    of 8+ limbs on a device that deals workgroups to 8 XCDs round-robin) against the oracle:
+    both arithmetic policies in one batch, job counts that are and are not
+    multiples of the XCD count, the smallest batch that takes it, and repeated
+    launches (its control blocks alternate between calls)."""
     import pfa_native as P
 
-    monkeypatch.setenv("PFA_NTT_ONEPASS", "1")
     N = 1 << 16
-    bits = [50, 60, 45, 50, 60, 50, 49]
+    bits = [50, 60, 45, 50, 60, 50, 49, 58, 50, 60, 50]
     mods = O.create_coeff_modulus(N, bits + [60])
+    monkeypatch.setenv("PFA_NTT_FLOW", "1")
     ctx = P.NativeContext(N, mods, 1)
+    if not ctx.ntt_single_launch(2, 11):
+        pytest.skip("this device does not deal workgroups to 8 XCDs round-robin; the two-launch NTT runs")
+    assert not ctx.ntt_single_launch(1, 7)
     orc = O.Oracle(N, mods, 1)
     rng = np.random.default_rng(11)
-    for M, L in [(2, 7), (3, 5), (1, 1)]:
+    for M, L in [(2, 11), (3, 5), (1, 8), (4, 9), (2, 11)]:
+        assert ctx.ntt_single_launch(M, L)
         x = uniform_limbs(rng, (M, L, N), mods)
         d = to_dev(x, dev)
         ctx.ntt_forward(d, M, L, 0)
         got = to_host(d)
-        assert np.array_equal(got, orc.ntt_fwd(x, threads=8)), first_mismatch(got, orc.ntt_fwd(x, threads=8))
+        want = orc.ntt_fwd(x, threads=8)
+        assert np.array_equal(got, want), (M, L, first_mismatch(got, want))
         ctx.ntt_inverse(d, M, L, 0)
         back = to_host(d)
-        assert np.array_equal(back, x), first_mismatch(back, x)
+        assert np.array_equal(back, x), (M, L, first_mismatch(back, x))
+    ctx.synchronize()
+
+
+def test_ntt_single_launch_expired_wait_is_an_error(dev, monkeypatch):
+    """A single-launch NTT whose bounded wait gives up reports PFA_ERR_RUNTIME
+    at the next synchronizing call instead of returning wrong residues.  The
+    condition is forced from the host: a look-ahead window of one job makes most
+    workgroups wait, and a wait bound of 0 ticks makes every such wait expire at
+    its second poll; every workgroup then leaves and the kernel ends normally."""
+    import pfa_native as P
+
+    N = 1 << 16
+    mods = O.create_coeff_modulus(N, [50] * 35 + [60])
+    monkeypatch.setenv("PFA_NTT_FLOW", "1")
+    monkeypatch.setenv("PFA_FLOW_WAIT_TICKS", "0")
+    monkeypatch.setenv("PFA_FLOW_WINDOW", "1")
+    ctx = P.NativeContext(N, mods, 1)
+    if not ctx.ntt_single_launch(2, 35):
+        pytest.skip("this device does not deal workgroups to 8 XCDs round-robin; the two-launch NTT runs")
+    rng = np.random.default_rng(12)
+    d = to_dev(uniform_limbs(rng, (2, 35, N), mods), dev)
+    ctx.ntt_forward(d, 2, 35, 0)
+    with pytest.raises(RuntimeError, match="single-launch NTT"):
+        ctx.synchronize()
+    # the record is cleared once reported
+    ctx.synchronize()
+    monkeypatch.delenv("PFA_FLOW_WAIT_TICKS")
+    monkeypatch.delenv("PFA_FLOW_WINDOW")
+    ok = P.NativeContext(N, mods, 1)
+    x = uniform_limbs(rng, (2, 9, N), mods)
+    d = to_dev(x, dev)
+    ok.ntt_forward(d, 2, 9, 0)
+    ok.ntt_inverse(d, 2, 9, 0)
+    ok.synchronize()
+    assert np.array_equal(to_host(d), x)
 
 
 @pytest.mark.parametrize("logn,M,L", [(12, 2, 26), (16, 2, 25), (13, 4, 12)])
