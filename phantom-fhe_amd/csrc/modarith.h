@@ -217,6 +217,19 @@ __device__ __forceinline__ uint64_t wave_uniform(uint64_t v) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Loads of read-only tables at a wave-uniform index, issued as scalar loads
+// (constant address space): counted by lgkmcnt, so a kernel that has
+// prefetched its next tile's residues can read them without waiting for the
+// prefetch (vector loads complete in issue order).
+__device__ __forceinline__ uint64_t ld_const(const uint64_t *p) {
+    return *(const __attribute__((address_space(4))) uint64_t *)p;
+}
+__device__ __forceinline__ ulonglong2 ld_const(const ulonglong2 *p) {
+    const uint64_t *w = reinterpret_cast<const uint64_t *>(p);
+    return ulonglong2{ld_const(w), ld_const(w + 1)};
+}
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
 __device__ __forceinline__ uint32_t brv(uint32_t x, uint32_t bits) { return __builtin_bitreverse32(x) >> (32 - bits); }
 
 // Galois permutation of NTT slots (include/galois.cuh:98-113):

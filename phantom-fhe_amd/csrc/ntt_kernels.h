@@ -711,12 +711,12 @@ ntt_inv_rows_staged(NttBatch b, NttTables t) {
     }
 }
 
-// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and optional scale
-// (scale: the pair for this limb, or null).
+// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and, when scaled,
+// the limb's scale pair.
 template <class A, int S1, int S2>
 __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const ulonglong2 *itw,
-                                              ulonglong2 ninv, const ulonglong2 *scale, const TileRef &r, uint64_t q,
-                                              typename A::T *lds, uint64_t *olimb) {
+                                              ulonglong2 ninv, bool scaled, ulonglong2 scale, const TileRef &r,
+                                              uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     using T = typename A::T;
@@ -733,10 +733,9 @@ __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lds[(F + SB::T * e) * kColStride + c];
     inv_round_b<A, S1, true>(x, ar, itw, 1, ninv);
-    if (scale) {
-        const ulonglong2 s = *scale;
+    if (scaled) {
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) ar.mul(x[e], s);
+        for (int e = 0; e < SB::E; e++) ar.mul(x[e], scale);
     }
 #pragma unroll
     for (int e = 0; e < SB::E; e++) st_stream(&data[(size_t)(F + SB::T * e) * G::N2 + c], ar.store(x[e]));
@@ -768,18 +767,19 @@ ntt_inv_cols(NttBatch b, NttTables t) {
         st.store(twl);
         __syncthreads();
         const uint64_t q = t.mod[prow];
-        const ulonglong2 *scale = b.scale ? b.scale + r.l : nullptr;
+        const bool scaled = b.scale != nullptr;
+        const ulonglong2 sc = scaled ? b.scale[r.l] : ulonglong2{0, 0};
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, lds, olimb);
+            inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q, lds, olimb);
         else
-            inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
+            inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q,
+                                            reinterpret_cast<uint64_t *>(lds), olimb);
         __syncthreads();
     }
 }
 
 }  // namespace pfa
-
 
 namespace pfa {
 
@@ -1009,11 +1009,12 @@ struct FlowJob {
             for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F * S1B::E + e) * G::N2 + c];
             st.store(twl);
             __syncthreads();
-            const ulonglong2 *scale = b.scale ? b.scale + l : nullptr;
+            const bool scaled = b.scale != nullptr;
+            const ulonglong2 sc = scaled ? b.scale[l] : ulonglong2{0, 0};
             if (q < kF64PrimeBound)
-                inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scale, r, q, lds, limb);
+                inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q, lds, limb);
             else
-                inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scale, r, q,
+                inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q,
                                                 reinterpret_cast<uint64_t *>(lds), limb);
         }
     }
