@@ -296,8 +296,23 @@ def cpu_baseline(mods, seconds, threads=1):
             break
     return {"value": round(limbs / el, 2), "unit": "limbs/s", "cores": threads, "kind": "port",
             "sample": f"{limbs // (POLYS * LIMBS)} forward NTTs of the 2x35-limb N=2^16 batch "
-                      f"({limbs} limbs, {el:.1f} s) by oracle/ckks_oracle.c (radix-2, Shoup), "
-                      f"{threads} thread{'s' if threads > 1 else ''}"}
+                      f"({limbs} limbs, {el:.1f} s) by oracle/ckks_oracle.c (radix-2 Cooley-Tukey with "
+                      f"precomputed Shoup twiddle pairs), {threads} thread{'s' if threads > 1 else ''}",
+            "cpu": cpu_model(), "build": O.build_info()}
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
 
 
 def host_threads():

@@ -205,40 +205,59 @@ void orc_ntt_tables(uint64_t N, uint64_t q, uint64_t *tw, uint64_t *tw_shoup, ui
 }
 
 /* Forward negacyclic NTT, radix-2 Cooley-Tukey in the order of
- * inplace_fnwt_radix2 (src/ntt/ntt_1d.cu:17-76): stage m uses tw[m + i]. */
-void orc_ntt_fwd_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *tw) {
+ * inplace_fnwt_radix2 (src/ntt/ntt_1d.cu:17-76): stage m uses tw[m + i], with
+ * its precomputed Shoup quotient tws[m + i] (the reference's tables carry the
+ * same pairs, include/ntt.cuh:34-129).  Butterflies are Harvey's lazy form, as
+ * the reference's (include/butterfly.cuh:17-76): operands stay in [0, 4q)
+ * between stages (q < 2^62) and one correction at the end makes them
+ * canonical, so the output equals the textbook transform's. */
+void orc_ntt_fwd_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *tw, const uint64_t *tws) {
+    const uint64_t q2 = 2 * q;
     for (uint64_t m = 1, t = N >> 1; m < N; m <<= 1, t >>= 1) {
         for (uint64_t i = 0; i < m; i++) {
-            uint64_t w = tw[m + i], ws = orc_shoup(w, q);
-            uint64_t *x = a + 2 * i * t, *y = x + t;
+            const uint64_t w = tw[m + i], ws = tws[m + i];
+            uint64_t *restrict x = a + 2 * i * t, *restrict y = x + t;
             for (uint64_t j = 0; j < t; j++) {
-                uint64_t u = x[j], v = mul_shoup(y[j], w, ws, q);
-                x[j] = add_mod(u, v, q);
-                y[j] = sub_mod(u, v, q);
+                uint64_t u = x[j];
+                u = u >= q2 ? u - q2 : u;                                   /* [0, 2q) */
+                const uint64_t v = y[j] * w - (uint64_t)(((u128)y[j] * ws) >> 64) * q; /* [0, 2q) */
+                x[j] = u + v;
+                y[j] = u - v + q2;
             }
         }
+    }
+    for (uint64_t j = 0; j < N; j++) {
+        uint64_t u = a[j];
+        u = u >= q2 ? u - q2 : u;
+        a[j] = u >= q ? u - q : u;
     }
 }
 
 /* Inverse, Gentleman-Sande in the order of inplace_inwt_radix2
  * (src/ntt/ntt_1d.cu:180-240): stage m uses itw[m + i]; in the last stage the
  * sum half is scaled by N^-1 and the difference half gets N^-1 through the
- * folded itw[1]. */
-void orc_ntt_inv_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *itw, uint64_t ninv) {
-    uint64_t ninv_s = orc_shoup(ninv, q);
+ * folded itw[1].  Lazy as the reference's (include/butterfly.cuh:78-134):
+ * operands in [0, 2q) between stages, canonical at the end. */
+void orc_ntt_inv_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *itw, const uint64_t *itws,
+                      uint64_t ninv) {
+    const uint64_t q2 = 2 * q, ninv_s = orc_shoup(ninv, q);
     for (uint64_t m = N >> 1, t = 1; m >= 1; m >>= 1, t <<= 1) {
         for (uint64_t i = 0; i < m; i++) {
-            uint64_t w = itw[m + i], ws = orc_shoup(w, q);
-            uint64_t *x = a + 2 * i * t, *y = x + t;
+            const uint64_t w = itw[m + i], ws = itws[m + i];
+            uint64_t *restrict x = a + 2 * i * t, *restrict y = x + t;
             for (uint64_t j = 0; j < t; j++) {
-                uint64_t u = x[j], v = y[j];
-                uint64_t s = add_mod(u, v, q);
-                x[j] = (m == 1) ? mul_shoup(s, ninv, ninv_s, q) : s;
-                y[j] = mul_shoup(sub_mod(u, v, q), w, ws, q);
+                const uint64_t u = x[j], v = y[j];
+                uint64_t s = u + v;
+                s = s >= q2 ? s - q2 : s;                                    /* [0, 2q) */
+                const uint64_t d = u - v + q2;                               /* [0, 4q) */
+                if (m == 1) s = s * ninv - (uint64_t)(((u128)s * ninv_s) >> 64) * q;
+                x[j] = s;
+                y[j] = d * w - (uint64_t)(((u128)d * ws) >> 64) * q;         /* [0, 2q) */
             }
         }
         if (m == 1) break;
     }
+    for (uint64_t j = 0; j < N; j++) a[j] = a[j] >= q ? a[j] - q : a[j];
 }
 
 void orc_ntt_naive_limb(const uint64_t *a, uint64_t *out, uint64_t N, uint64_t q, uint64_t psi) {
@@ -307,6 +326,18 @@ void orc_ctx_destroy(orc_ctx *c) {
 }
 
 size_t orc_ctx_size_QP(const orc_ctx *c) { return c->size_QP; }
+
+#ifndef ORC_BUILD_FLAGS
+#define ORC_BUILD_FLAGS "unknown flags"
+#endif
+/* Compiler and flags this library was built with (reported beside CPU timings). */
+const char *orc_build_info(void) {
+#ifdef __VERSION__
+    return "cc " __VERSION__ ", " ORC_BUILD_FLAGS;
+#else
+    return ORC_BUILD_FLAGS;
+#endif
+}
 uint64_t orc_ctx_root(const orc_ctx *c, size_t i) { return c->roots[i]; }
 
 const uint64_t *orc_ctx_table(const orc_ctx *c, size_t i, int which) {
@@ -322,11 +353,11 @@ const uint64_t *orc_ctx_table(const orc_ctx *c, size_t i, int which) {
 }
 
 static void fwd_limb(const orc_ctx *c, uint64_t *a, size_t tidx) {
-    orc_ntt_fwd_limb(a, c->N, c->moduli[tidx], c->tw + tidx * c->N);
+    orc_ntt_fwd_limb(a, c->N, c->moduli[tidx], c->tw + tidx * c->N, c->tws + tidx * c->N);
 }
 
 static void inv_limb(const orc_ctx *c, uint64_t *a, size_t tidx) {
-    orc_ntt_inv_limb(a, c->N, c->moduli[tidx], c->itw + tidx * c->N, c->ninv[tidx]);
+    orc_ntt_inv_limb(a, c->N, c->moduli[tidx], c->itw + tidx * c->N, c->itws + tidx * c->N, c->ninv[tidx]);
 }
 
 void orc_ntt_fwd(const orc_ctx *c, uint64_t *data, size_t M, size_t L, size_t start, int threads) {

@@ -47,8 +47,9 @@ void orc_ntt_tables(uint64_t N, uint64_t q, uint64_t *tw, uint64_t *tw_shoup,
                     uint64_t *itw, uint64_t *itw_shoup, uint64_t *ninv, uint64_t *ninv_shoup);
 
 /* ---- single-limb transforms ---- */
-void orc_ntt_fwd_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *tw);
-void orc_ntt_inv_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *itw, uint64_t ninv);
+void orc_ntt_fwd_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *tw, const uint64_t *tws);
+void orc_ntt_inv_limb(uint64_t *a, uint64_t N, uint64_t q, const uint64_t *itw, const uint64_t *itws,
+                      uint64_t ninv);
 /* O(N^2) closed form: out[i] = sum_j a_j psi^((2 brv(i)+1) j) */
 void orc_ntt_naive_limb(const uint64_t *a, uint64_t *out, uint64_t N, uint64_t q, uint64_t psi);
 
@@ -57,6 +58,7 @@ typedef struct orc_ctx orc_ctx;
 orc_ctx *orc_ctx_create(uint64_t N, const uint64_t *moduli, size_t size_QP, size_t size_P);
 void orc_ctx_destroy(orc_ctx *ctx);
 size_t orc_ctx_size_QP(const orc_ctx *ctx);
+const char *orc_build_info(void);
 const uint64_t *orc_ctx_table(const orc_ctx *ctx, size_t prime_idx, int which);
 uint64_t orc_ctx_root(const orc_ctx *ctx, size_t prime_idx);
 

@@ -34,8 +34,8 @@ def _load():
         "orc_invmod": (u64, [u64, u64]),
         "orc_shoup": (u64, [u64, u64]),
         "orc_ntt_tables": (None, [u64, u64, _u64p, _u64p, _u64p, _u64p, _u64p, _u64p]),
-        "orc_ntt_fwd_limb": (None, [_u64p, u64, u64, _u64p]),
-        "orc_ntt_inv_limb": (None, [_u64p, u64, u64, _u64p, u64]),
+        "orc_ntt_fwd_limb": (None, [_u64p, u64, u64, _u64p, _u64p]),
+        "orc_ntt_inv_limb": (None, [_u64p, u64, u64, _u64p, _u64p, u64]),
         "orc_ntt_naive_limb": (None, [_u64p, _u64p, u64, u64, u64]),
         "orc_ctx_create": (vp, [u64, _u64p, sz, sz]),
         "orc_ctx_destroy": (None, [vp]),
@@ -60,6 +60,7 @@ def _load():
         "orc_hoisting": (i32, [vp, sz, _u64p, _u32p, sz, C.POINTER(_u64p), sz, _u64p, i32]),
         "orc_kswitch_key": (None, [vp, _u64p, _u64p, _u64p, _u64p, _u64p]),
         "orc_mul_poly": (None, [vp, sz, sz, _u64p, _u64p, _u64p]),
+        "orc_build_info": (C.c_char_p, []),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -85,6 +86,11 @@ def _p(a: np.ndarray):
 
 def u64(a) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
+
+
+def build_info() -> str:
+    """Compiler and flags the oracle library was built with."""
+    return lib().orc_build_info().decode()
 
 
 def threads_default() -> int:
