@@ -1,0 +1,125 @@
+"""The benchmark configurations at their full sizes (
+plus the metric's "L=35" HMult), so that no benchmarked workload is checked
+only by bench.py.
+
+* L = 35 HMult + relinearize + rescale (N = 2^16, chain {60, 50 x 34, 60},
+  alpha = 1, dnum = 35): multiply_and_relin, rescale and the fused call are
+  bit-exact against the oracle's multiply_and_relin_inplace
+  (src/evaluate.cu:1061-1104) followed by rescale_to_next (src/rns.cu:1128-1184).
+* Config 4, the BSGS matrix-vector product at N = 2^16 (4096 x 4096 matrix
+  uniform in [-1/64, 1/64], baby 64 / giant 64, L = 20, scale 2^40): decode
+  within 1e-5 of numpy's W x.  The reference's own check of this product is a
+  decode tolerance (python/llm_project/blocks/bsgs_test.py:77); its residues are
+  pinned bit-exactly at N = 2^12 in test_gpu_bsgs.py.
+* Config 5, bootstrapping at N = 2^16 (2^15 slots uniform in [-1, 1], |Q| = 30
+  with 6 special primes, dnum = 5, sparse secret h = 192): at least 15 bits of
+  refreshed precision (the reference's acceptance bound is 1e-3, about 10 bits,
+  test/ckks_engine_test.cu:182-188), and the refreshed ciphertext takes a
+  further multiplication.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from gpu_util import empty, first_mismatch, to_dev, to_host
+from test_gpu_keyswitch import Setup
+
+pytestmark = pytest.mark.gpu
+
+
+def test_hmult_L35_alpha1_full_size(dev):
+    """The metric's HMult shape: fresh chain-index-1 ciphertexts, 35 digits."""
+    st = Setup(16, 35, 1, seed=35)
+    assert st.orc.beta(1) == 35 and st.orc.dnum == 35
+    a, b = st.ct(1), st.ct(1)
+    key = st.key()
+    da, db, dk = to_dev(a, dev), to_dev(b, dev), to_dev(key, dev)
+    want = st.orc.multiply_and_relin(1, a, b, key, threads=16)
+    out = empty((2, 35, st.N), dev)
+    st.ctx.multiply_and_relin(1, da, db, dk, out)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    want_r = st.orc.rescale(1, want, threads=16)
+    res = empty((2, 34, st.N), dev)
+    st.ctx.rescale(1, out, res)
+    got = to_host(res)
+    assert np.array_equal(got, want_r), first_mismatch(got, want_r)
+    fused = empty((2, 34, st.N), dev)
+    st.ctx.multiply_relin_rescale(1, da, db, dk, fused)
+    got = to_host(fused)
+    assert np.array_equal(got, want_r), first_mismatch(got, want_r)
+
+
+def test_bsgs_config4_full_size(dev):
+    import torch
+
+    import pyPhantom as ph
+
+    N, d_pad, M = 1 << 16, 4096, 64
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, [60] + [40] * 19 + [60] * 4))
+    p.set_special_modulus_size(4)
+    p.set_galois_elts(ph.get_elts_from_steps(ph.bsgs_required_steps(M), N))
+    ctx = ph.context(p)
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192, seed=41)
+    glk = sk.create_galois_keys(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(4)
+    W = rng.uniform(-1 / 64, 1 / 64, (d_pad, d_pad))
+    xv = rng.uniform(-1, 1, d_pad)
+    scale = 2.0 ** 40
+    diags = ph.pre_encode_bsgs_diagonals(ctx, enc, W.ravel(), d_pad, d_pad, d_pad, M, scale)
+    x = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, np.tile(xv, enc.slot_count() // d_pad), scale),
+                             seed=42)
+    y = ph.bsgs_matmul_preencoded(ctx, glk, x, diags)
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, y)))
+    want = np.tile(W @ xv, enc.slot_count() // d_pad)
+    err = float(np.max(np.abs(got - want)))
+    print(f"config 4 BSGS: max |err| {err:.3e}")
+    assert y.chain_index() == x.chain_index() + 1
+    assert err < 1e-5
+    del diags, glk
+    torch.cuda.empty_cache()
+
+
+@pytest.fixture(scope="module")
+def boot16(dev):
+    import pyPhantom as ph
+
+    N = 1 << 16
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, ph.bootstrap_coeff_bits()))
+    p.set_special_modulus_size(6)
+    p.set_galois_elts(ph.bootstrap_required_galois_elts(16))
+    ctx = ph.context(p)
+    assert ctx.size_Q == 30 and ctx.size_P == 6
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192, seed=51)
+    enc = ph.ckks_encoder(ctx)
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=52)
+    yield ph, ctx, sk, enc, bk
+    import torch
+
+    del bk
+    torch.cuda.empty_cache()
+
+
+def test_bootstrap_config5_full_size(boot16):
+    ph, ctx, sk, enc, bk = boot16
+    n = enc.slot_count()
+    assert n == 1 << 15
+    z = np.random.default_rng(5).uniform(-1, 1, n)
+    scale = 2.0 ** 40
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, scale, ctx.size_Q), seed=53)
+    out = ph.bootstrap(ctx, enc, ct, bk, scale)
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, out)))
+    err = float(np.max(np.abs(got - z)))
+    bits = -math.log2(err)
+    print(f"config 5 bootstrap: max |err| {err:.3e} ({bits:.2f} bits), chain index {out.chain_index()}")
+    assert bits >= 15
+    # a further multiplication on the refreshed ciphertext decodes to z^2
+    sq = ph.rescale_to_next(ctx, ph.multiply_and_relin(ctx, out, out, bk.rlk))
+    got2 = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, sq)))
+    assert np.max(np.abs(got2 - z * z)) < 1e-4
