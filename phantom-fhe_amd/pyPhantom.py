@@ -397,8 +397,11 @@ class relin_key(_ksk):
 
 
 class galois_key:
-    def __init__(self):
-        self.keys = {}  # Galois element -> key tensor, in the context's galois_elts order
+    def __init__(self, elts=None):
+        self.keys = {}  # Galois element -> key tensor
+        # the context's galois_elts: the reference keeps one key slot per
+        # element in this order (PhantomGaloisKey::relin_keys_)
+        self.elts = list(elts) if elts is not None else None
 
     def get(self, elt):
         k = self.keys.get(elt)
@@ -408,14 +411,20 @@ class galois_key:
 
     def save(self, stream):
         """PhantomGaloisKey::save (include/secretkey.h:290-302): the key count,
-        then one relin-key record per Galois element in the context's order."""
+        then one relin-key record per Galois element in the context's order.
+        As in the reference, an element without a generated key (a set made by
+        create_galois_keys_per_level for some elements only) is an error."""
+        if not self.keys:
+            raise ValueError("PhantomGaloisKey has not been generated")
+        elts = self.elts if self.elts is not None else list(self.keys)
+        missing = [e for e in elts if e not in self.keys]
+        if missing:
+            raise ValueError(f"PhantomRelinKey has not been generated (no key for Galois element {missing[0]})")
         f, own = _opened(stream, "wb")
         try:
-            if not self.keys:
-                raise ValueError("PhantomGaloisKey has not been generated")
-            f.write(_COUNT.pack(len(self.keys)))
-            for k in self.keys.values():
-                _save_ksk(f, k)
+            f.write(_COUNT.pack(len(elts)))
+            for e in elts:
+                _save_ksk(f, self.keys[e])
         finally:
             if own:
                 f.close()
@@ -429,6 +438,7 @@ class galois_key:
             if n != len(ctx.galois_elts):
                 raise ValueError(f"file holds {n} Galois keys, the context has {len(ctx.galois_elts)} elements")
             self.keys = {e: _load_ksk(f, ctx.dev) for e in ctx.galois_elts}
+            self.elts = list(ctx.galois_elts)
         finally:
             if own:
                 f.close()
@@ -609,7 +619,7 @@ class secret_key:
         """Keys for every element in params.galois_elts (src/secretkey.cu:642-682)."""
         self._require()
         rng = _rng(seed)
-        g = galois_key()
+        g = galois_key(ctx.galois_elts)
         for elt in ctx.galois_elts:
             g.keys[elt] = self._galois_key_for(ctx, elt, rng)
         return g
@@ -624,7 +634,7 @@ class secret_key:
         if len(indices) != len(targets):
             raise ValueError("create_galois_keys_per_level: indices and target_chain_indices must have the same length")
         rng = _rng(seed)
-        g = galois_key()
+        g = galois_key(ctx.galois_elts)
         for idx, tci in zip(indices, targets):
             elt = self._elt_at(ctx, idx, "create_galois_keys_per_level")
             g.keys[elt] = self._galois_key_for(ctx, elt, rng, self._level_digits(ctx, tci))
@@ -832,6 +842,48 @@ def multiply_and_relin(ctx: context, a: ciphertext, b: ciphertext, rlk: relin_ke
     out = ctx._empty(2, L, ctx.N)
     ctx.native.multiply_and_relin(a.chain_index(), a.data, b.data, rlk.data, out)
     return a._like(out, scale=a.scale() * b.scale())
+
+
+def _ntt_check(ctx: context, inout, coeff_modulus_size: int, start_modulus_idx: int, batch: int):
+    t = _torch()
+    if not isinstance(inout, t.Tensor) or inout.dtype != t.uint64 or inout.device.type != "cuda":
+        raise ValueError("ntt: inout must be a torch.uint64 tensor on the context's device")
+    if not inout.is_contiguous():
+        raise ValueError("ntt: inout must be contiguous")
+    if batch < 1 or coeff_modulus_size < 1:
+        raise ValueError("ntt: empty batch")
+    if inout.numel() != batch * coeff_modulus_size * ctx.N:
+        raise ValueError(f"ntt: inout holds {inout.numel()} residues, expected batch x coeff_modulus_size x N = "
+                         f"{batch * coeff_modulus_size * ctx.N}")
+    if start_modulus_idx < 0 or start_modulus_idx + coeff_modulus_size > len(ctx.moduli):
+        raise ValueError("ntt: limb range exceeds the context's primes")
+
+
+def ntt_forward(ctx: context, inout, coeff_modulus_size: int, start_modulus_idx: int = 0, batch: int = 1,
+                stream=None) -> None:
+    """nwt_2d_radix8_forward_inplace[_batched] (include/ntt.cuh:173, :184): in
+    place, `batch` polys x coeff_modulus_size limbs (limb-major, N residues
+    each, a contiguous torch.uint64 device tensor); limb l uses the table row of
+    prime start_modulus_idx + l.  Output in the reference's bit-reversed NTT
+    order.  stream: a hipStream_t handle (default torch's current stream).  The
+    reference exposes no NTT to Python; this follows the C++ signature."""
+    _ntt_check(ctx, inout, coeff_modulus_size, start_modulus_idx, batch)
+    ctx.native.ntt_forward(inout, batch, coeff_modulus_size, start_modulus_idx, stream)
+
+
+def ntt_inverse(ctx: context, inout, coeff_modulus_size: int, start_modulus_idx: int = 0, batch: int = 1,
+                stream=None) -> None:
+    """nwt_2d_radix8_backward_inplace (include/ntt.cuh:216), batched like
+    ntt_forward: the exact inverse, canonical residues."""
+    _ntt_check(ctx, inout, coeff_modulus_size, start_modulus_idx, batch)
+    ctx.native.ntt_inverse(inout, batch, coeff_modulus_size, start_modulus_idx, stream)
+
+
+def synchronize(ctx: context, stream=None) -> None:
+    """Waits for the context's work on `stream` (default torch's current
+    stream) and raises RuntimeError if a kernel recorded an error on the device
+    (pfa_synchronize)."""
+    ctx.native.synchronize(stream)
 
 
 def rescale_to_next(ctx: context, ct: ciphertext) -> ciphertext:
@@ -1589,9 +1641,18 @@ def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secr
     bootstrap_required_galois_elts.  The ModRaise runs under a transient
     sparse secret of weight sparse_hamming_weight (|I| < K = 28 holds up to a
     few hundred); the rotation and relinearization keys are the dense
-    secret's.  eval_mod_levels, user_scale and split_scale_down are
-    accepted for the reference's signature (EvalMod here always takes 10
-    levels)."""
+    secret's.  EvalMod here always takes BOOT_EVALMOD_LEVELS levels at the
+    ciphertext's own scale, so eval_mod_levels, user_scale and
+    split_scale_down must keep their defaults (or name that same layout): a
+    reference caller that relies on another layout gets NotImplementedError
+    instead of a silently different chain."""
+    if eval_mod_levels not in (0, BOOT_EVALMOD_LEVELS):
+        raise NotImplementedError(f"eval_mod_levels={eval_mod_levels}: this build's EvalMod takes "
+                                  f"{BOOT_EVALMOD_LEVELS} levels")
+    if user_scale != 0.0:
+        raise NotImplementedError("user_scale: this build bootstraps at the ciphertext's own scale")
+    if split_scale_down:
+        raise NotImplementedError("split_scale_down is not implemented by this build")
     ctx, enc = context, encoder
     log_n = ctx.N.bit_length() - 1
     stages = list(stages_per_layer or _default_stages(log_n))
@@ -1605,7 +1666,7 @@ def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secr
     bk = bootstrap_key()
     bk.small = _small_bootstrap_key(ctx, dense_sk, sparse_hamming_weight, rng)[0]
     bk.rlk = dense_sk.gen_relinkey(ctx, seed=rng)
-    bk.glk = galois_key()
+    bk.glk = galois_key(ctx.galois_elts)
     for elt in bootstrap_required_galois_elts(log_n, stages):
         bk.glk.keys[elt] = dense_sk._galois_key_for(ctx, elt, rng)
     bk.c2s = build_c2s_diagonals(log_n, stages)
@@ -1816,8 +1877,11 @@ def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: boots
     """bootstrap (src/bootstrap.cu:1703-1951): a ciphertext at scale user_scale,
     at any level (it is brought to the bottom of the chain first) -> the same
     message at chain index 1 + 2 * (transform layers) + 10, at a scale within a
-    few parts in 10^12 of user_scale (the exact value is carried)."""
+    few parts in 10^12 of user_scale (the exact value is carried).
+    split_scale_down is not implemented (NotImplementedError when set)."""
     ctx = context
+    if split_scale_down:
+        raise NotImplementedError("split_scale_down is not implemented by this build")
     if ct.size() != 2:
         raise ValueError("bootstrap expects a size-2 ciphertext")
     if abs(ct.scale() - user_scale) > 1e-6 * user_scale:

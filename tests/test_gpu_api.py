@@ -248,6 +248,31 @@ def test_galois_keys_per_level(dev):
         sk.create_one_galois_key(ctx, 2)
     with pytest.raises(ValueError):
         sk.create_one_galois_key(ctx, 0, ctx.size_Q + 1)
+    # save writes one key per element in the context's order, whatever order
+    # the indices were given in (PhantomGaloisKey::relin_keys_), so a load
+    # gives every element its own key back
+    import io
+
+    perm = sk.create_galois_keys_per_level(ctx, [1, 0], [0, 3])
+    buf = io.BytesIO()
+    perm.save(buf)
+    back = ph.galois_key().load(io.BytesIO(buf.getvalue()), ctx)
+    for e in ctx.galois_elts:
+        assert torch_equal(back.keys[e], perm.keys[e])
+    r = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ph.rotate(ctx, ct3, 1, back))))
+    assert np.max(np.abs(r - np.roll(v, -1))) < TOL
+    r = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, ph.rotate(ctx, ct1, 2, back))))
+    assert np.max(np.abs(r - np.roll(v, -2))) < TOL
+    # a set without a key for every element cannot be saved, as in the
+    # reference (PhantomRelinKey::save of a key never generated)
+    with pytest.raises(ValueError):
+        sk.create_galois_keys_per_level(ctx, [1], [0]).save(io.BytesIO())
+
+
+def torch_equal(a, b):
+    import torch
+
+    return a.shape == b.shape and bool(torch.equal(a, b))
 
 
 def test_device_helpers(dev):
@@ -411,3 +436,37 @@ def test_library_loaded_before_torch(dev):
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-2000:]
     assert float(r.stdout.split()[-1]) < 1e-6
+
+
+@pytest.mark.parametrize("logN,batch,L,start", [(16, 2, 35, 0), (13, 1, 3, 1), (12, 3, 4, 2)])
+def test_pyphantom_ntt_entry_points(dev, logN, batch, L, start):
+    """pyPhantom.ntt_forward / ntt_inverse (the C++ nwt_2d_radix8_forward_inplace
+    [_batched] / nwt_2d_radix8_backward_inplace signatures, include/ntt.cuh:173,
+    :184, :216) against the oracle, including a start offset into the table and
+    the config-2 batch; then the argument errors."""
+    N = 1 << logN
+    bits = [50] * 35 + [60] if logN == 16 else [60, 50, 55, 60, 49, 60]
+    ph, ctx = make_ctx(logN, bits, 1)
+    orc = O.Oracle(N, ctx.moduli, 1)
+    rng = np.random.default_rng(logN + L)
+    x = uniform_limbs(rng, (batch, L, N), ctx.moduli[start:start + L])
+    d = to_dev(x, dev)
+    ph.ntt_forward(ctx, d, L, start, batch)
+    ph.synchronize(ctx)
+    got, want = to_host(d), orc.ntt_fwd(x, start=start, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    ph.ntt_inverse(ctx, d, L, start, batch)
+    back = to_host(d)
+    assert np.array_equal(back, x), first_mismatch(back, x)
+    with pytest.raises(ValueError):  # size does not match batch x L x N
+        ph.ntt_forward(ctx, d, L + 1, start, batch)
+    with pytest.raises(ValueError):  # limbs beyond the context's primes
+        ph.ntt_forward(ctx, empty((batch, len(ctx.moduli), N), dev), len(ctx.moduli), 1, batch)
+    with pytest.raises(ValueError):  # not a uint64 tensor
+        ph.ntt_forward(ctx, d.view(torch_int64()), L, start, batch)
+
+
+def torch_int64():
+    import torch
+
+    return torch.int64

@@ -142,3 +142,19 @@ def test_mod_raise_api_keeps_message(boot12):
     low = ph.mod_switch_to(ctx, raised, ctx.size_Q)
     got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, low)))
     assert np.max(np.abs(got - z)) < 1e-6
+
+
+def test_bootstrap_options_not_implemented(boot12):
+    """The reference's EvalMod layout options that this build does not
+    implement are refused, not ignored (python/src/binding.cu:320-336)."""
+    ph, ctx, sk, enc, bk = boot12
+    with pytest.raises(NotImplementedError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, eval_mod_levels=9)
+    with pytest.raises(NotImplementedError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, user_scale=2.0 ** 40)
+    with pytest.raises(NotImplementedError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, split_scale_down=True)
+    z = np.zeros(enc.slot_count())
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, 2.0 ** 40, ctx.size_Q), seed=1)
+    with pytest.raises(NotImplementedError):
+        ph.bootstrap(ctx, enc, ct, bk, 2.0 ** 40, split_scale_down=True)
