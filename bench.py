@@ -73,6 +73,28 @@ def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def time_copy(torch, P, batches, steps, warmup):
+    """The hand-written streaming copy (pfa_stream_copy: 16-byte nontemporal
+    loads and stores) of the same 2 x 35-limb batches, rotating sources and
+    destinations: the achievable one-read-one-write rate the NTT's 73.4 MB per
+    transform is measured against.  Returns microseconds per copy (HIP events)."""
+    stream = torch.cuda.current_stream()
+    h = stream.cuda_stream
+    dsts = [torch.empty_like(b) for b in batches]
+    n = len(batches)
+    for i in range(warmup):
+        P.stream_copy(dsts[(i + 3) % n], batches[i % n], 0, h)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        P.stream_copy(dsts[(i + 3) % n], batches[i % n], 0, h)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del dsts
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
 def ntt_limb_sweep(torch, P, dev, gen, steps):
     """Forward and inverse NTT time (HIP events, 10 rotating batches) for 2 polys
     x L limbs of 50-bit primes at N = 2^16, over L around the config-2 batch.
@@ -338,7 +360,7 @@ def main():
     ap.add_argument("--mode", choices=["full", "ntt", "ntt-sweep", "copy", "hmult", "hmult35", "bsgs", "bootstrap"],
                     default="full",
                     help="ntt: only the NTT timing (for rocprofv3 kernel traces); ntt-sweep: forward and inverse "
-                         "NTT time for 56 to 96 limbs; copy: torch copies of the "
+                         "NTT time for 56 to 96 limbs; copy: the hand-written streaming copy of the "
                          "same 35 MiB batches (the plain-copy calibration of FETCH_SIZE / WRITE_SIZE); hmult: only "
                          "config-3 HMult + relin + rescale; hmult35: only the L=35 variant; bsgs: only the "
                          "config-4 matrix-vector product; bootstrap: only the config-5 bootstrap")
@@ -385,17 +407,17 @@ def main():
         log(f"bench: hmult35 mode, L=35: {r}")
         return
     if args.mode == "copy":
-        dst = torch.empty_like(batches[0])
-        for i in range(args.steps):
-            dst.copy_(batches[i % n_batches])
-        torch.cuda.synchronize()
-        log(f"bench: {args.steps} copies of {POLYS * LIMBS * LIMB_BYTES} bytes done")
+        us = time_copy(torch, P, batches, args.steps, args.warmup)
+        log(f"bench: {args.steps} streaming copies of {POLYS * LIMBS * LIMB_BYTES} bytes, {us:.2f} us each "
+            f"({NTT_BYTES / (us * 1e-6) / 1e9:.0f} GB/s)")
         return
     log(f"bench: config 2 forward NTT, {args.steps} steps, {args.warmup} warmup, {n_batches} rotating batches")
     wall, ev_ms = time_ntt(torch, ctx, batches, args.steps, args.warmup)
     log(f"bench: forward done, {ev_ms * 1e3:.1f} us/launch")
     _, ev_inv_ms = time_ntt(torch, ctx, batches, args.steps, args.warmup, inverse=True)
     log(f"bench: inverse done, {ev_inv_ms * 1e3:.1f} us/launch")
+    copy_us = time_copy(torch, P, batches, args.steps, args.warmup)
+    log(f"bench: streaming copy of the batch {copy_us:.1f} us")
     limbs = POLYS * LIMBS
     value = limbs * args.steps / wall
     achieved = NTT_BYTES / (ev_ms * 1e-3) / 1e9
@@ -457,6 +479,9 @@ def main():
         "cpu_baseline_all_threads": cpu_all,
         "ntt_inverse_limbs_per_s": round(limbs / (ev_inv_ms * 1e-3), 1),
         "ntt_forward_us": round(ev_ms * 1e3, 2),
+        "copy_ceiling": {"us": round(copy_us, 2), "GB_per_s": round(NTT_BYTES / (copy_us * 1e-6) / 1e9, 1),
+                         "what": "pfa_stream_copy of the same 2x35-limb batch (73.4 MB moved), the achievable "
+                                 "one-read-one-write time of a forward NTT"},
         "ntt_inverse_us": round(ev_inv_ms * 1e3, 2),
         "hmult_relin_rescale": hm,
         "bsgs_matvec_config4": bsgs,

@@ -234,6 +234,11 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     for (auto &e : c.stage_ev) PFA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
+    // The key-switch inner product splits the items left over after whole
+    // rounds of its resident workgroups by digit range; PFA_WS_SLOTS sets the
+    // resident count it assumes (tests use it to split small shapes).
+    if (const char *w = std::getenv("PFA_WS_SLOTS")) c.ws_slots = (uint32_t)std::max(0, std::atoi(w));
+    if (const char *w = std::getenv("PFA_WS_MAX_CHUNKS")) c.ws_max_chunks = (uint32_t)std::max(0, std::atoi(w));
     // Single-launch NTT (N = 2^16, opt-in with PFA_NTT_FLOW=1): built for the
     // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition,
     // checked here by a probe kernel.  The other variables tune it (workgroups
@@ -243,10 +248,10 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         c.flow_window = (uint32_t)std::min(32, std::max(1, std::atoi(w)));
     if (const char *w = std::getenv("PFA_FLOW_MIN_JOBS")) c.flow_min_jobs = (uint32_t)std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_FLOW_WAIT_TICKS")) c.flow_wait_ticks = (uint32_t)std::max(0, std::atoi(w));
-    PFA_HIP(hipHostMalloc((void **)&c.flow_err_host, 64, hipHostMallocMapped));
-    *c.flow_err_host = 0;
-    PFA_HIP(hipHostGetDevicePointer((void **)&c.flow_err_host_dev, c.flow_err_host, 0));
-    c.flow_err_dev = c.upload(std::vector<uint32_t>(16, 0u));
+    PFA_HIP(hipHostMalloc((void **)&c.err_host, 64, hipHostMallocMapped));
+    *c.err_host = 0;
+    PFA_HIP(hipHostGetDevicePointer((void **)&c.err_host_dev, c.err_host, 0));
+    c.err_dev = c.upload(std::vector<uint32_t>(16, 0u));
     {
         const char *f = std::getenv("PFA_NTT_FLOW");
         const bool want = f ? std::atoi(f) != 0 : false;
@@ -414,10 +419,11 @@ static void destroy(Ctx *c) {
     for (auto &e : c->stage_ev)
         if (e) (void)hipEventDestroy(e);
     if (c->stage) (void)hipHostFree(c->stage);
-    if (c->flow_err_host) (void)hipHostFree(c->flow_err_host);
+    if (c->err_host) (void)hipHostFree(c->err_host);
     for (auto &kv : c->arenas) {
         for (auto &ch : kv.second->chunks) (void)hipFree(ch.base);
         if (kv.second->flow) (void)hipFree(kv.second->flow);
+        if (kv.second->ws_counter) (void)hipFree(kv.second->ws_counter);
         delete kv.second;
     }
     for (void *p : c->allocations) (void)hipFree(p);
@@ -431,22 +437,23 @@ Ctx *ctx_of(const pfa_context *c) {
 }
 
 void check_device_errors(const Ctx &c) {
-    if (!c.flow_err_host) return;
-    volatile uint32_t *h = c.flow_err_host;
+    if (!c.err_host) return;
+    volatile uint32_t *h = c.err_host;
     if (*h == 0) return;
     *h = 0;
     uint32_t bits = 0;
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(c.device);
-    (void)hipMemcpy(&bits, c.flow_err_dev, sizeof(bits), hipMemcpyDeviceToHost);
-    (void)hipMemset(c.flow_err_dev, 0, sizeof(bits));
+    (void)hipMemcpy(&bits, c.err_dev, sizeof(bits), hipMemcpyDeviceToHost);
+    (void)hipMemset(c.err_dev, 0, sizeof(bits));
     (void)hipSetDevice(prev);
     std::string why;
-    if (bits & 1u) why += " a bounded wait expired;";
-    if (bits & 2u) why += " the launch ended with tiles not transformed;";
-    fail(PFA_ERR_RUNTIME, "single-launch NTT error:" + why +
-                              " its output and everything computed from it are invalid");
+    if (bits & 1u) why += " a single-launch NTT's bounded wait expired;";
+    if (bits & 2u) why += " a single-launch NTT ended with tiles not transformed;";
+    if (bits & 4u) why += " the digit chunks of one key-switch inner-product item ran on different XCDs;";
+    fail(PFA_ERR_RUNTIME, "device error:" + why + " the outputs of the kernels involved and everything computed "
+                                                  "from them are invalid");
 }
 
 }  // namespace pfa

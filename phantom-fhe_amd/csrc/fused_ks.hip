@@ -37,6 +37,8 @@
 // the true quotient); the sum is reduced whenever the next product could take
 // it past 7 x 0.875 q, which keeps every partial sum below 2^53.  Targets q >= 2^50 use integer
 // Shoup products, each in [0, 2q), summed with a conditional subtraction.
+#include <algorithm>
+
 #include "internal.h"
 #include "ntt_kernels.h"
 
@@ -228,6 +230,15 @@ struct InnerRows {
     uint32_t fold_r = ~0u;
     const uint64_t *fold_base0 = nullptr, *fold_base1 = nullptr;
     const ulonglong2 *fold_f = nullptr;
+    // Items from `full` on are split by digit range (see k_inner_ws): rem
+    // items of kch chunks each; chunk c of item full + j writes its canonical
+    // sums to partial + (j kch + c) 2 ROWS N2, and the last chunk of the item to
+    // arrive (counter[j]) adds them and writes the output.
+    uint32_t full = ~0u;
+    uint32_t rem = 0, kch = 1;
+    uint64_t *partial = nullptr;
+    uint32_t *counter = nullptr;
+    uint32_t *dev_err = nullptr, *host_err = nullptr;
 };
 
 // Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
@@ -278,7 +289,7 @@ struct WsGeo {
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
                                              uint32_t prow, uint32_t k1, uint32_t rr, const ulonglong2 *tws,
-                                             typename A::T *b0, typename A::T *b1) {
+                                             typename A::T *b0, typename A::T *b1, uint32_t db, uint32_t de) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
     using SB = Sub<S2>;
@@ -288,19 +299,19 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
     uint64_t nraw[SB::E];
     bool nown;
     {
-        const uint64_t *s = inner_src(a, 0, r, rowoff, G::N, nown);
+        const uint64_t *s = inner_src(a, db, r, rowoff, G::N, nown);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
     }
-    for (uint32_t b = 0; b < a.beta; b++) {
-        T *buf = (b & 1u) ? b1 : b0;
+    for (uint32_t b = db; b < de; b++) {
+        T *buf = ((b - db) & 1u) ? b1 : b0;
         const bool own = nown;
         T x[SB::E];
         // A
 #pragma unroll
         for (int e = 0; e < SB::E; e++) x[e] = own ? ar.load(nraw[e]) : ar.load_mid(nraw[e]);
         {
-            const uint64_t *s = inner_src(a, b + 1 < a.beta ? b + 1 : b, r, rowoff, G::N, nown);
+            const uint64_t *s = inner_src(a, b + 1 < de ? b + 1 : b, r, rowoff, G::N, nown);
 #pragma unroll
             for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[SB::T * e]);
         }
@@ -344,7 +355,7 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
         }
         __syncthreads();
     }
-    // step beta: the accumulate waves consume the last digit
+    // the last step: the accumulate waves consume the last digit
     __syncthreads();
     __syncthreads();
     __syncthreads();
@@ -365,17 +376,35 @@ __device__ __forceinline__ void ws_mac(const A &ar, typename A::T &acc, typename
     }
 }
 
+// Output limb r, element e of this thread's row: the canonical sums v0, v1, or
+// with the fold (see InnerRows) base_k + v_k [P^-1]_q.
+__device__ __forceinline__ void ws_out(const InnerRows &a, uint32_t r, size_t rowoff, uint32_t N, uint32_t off,
+                                       uint64_t q, uint64_t v0, uint64_t v1) {
+    uint64_t *o0 = a.cx + (size_t)r * N + rowoff;
+    uint64_t *o1 = o0 + (size_t)a.QlP * N;
+    if (r == a.fold_r) {
+        const ulonglong2 f = *a.fold_f;
+        v0 = add_mod(shoup(v0, f.x, f.y, q), a.fold_base0[(size_t)r * N + rowoff + off], q);
+        v1 = add_mod(shoup(v1, f.x, f.y, q), a.fold_base1[(size_t)r * N + rowoff + off], q);
+    }
+    st_stream(&o0[off], v0);
+    st_stream(&o1[off], v1);
+}
+
+// Accumulates digits db .. de-1; with part null the item is whole and its
+// output is written, else the canonical sums go to part ([2][ROWS][N2]).
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, uint32_t r, uint32_t prow,
-                                              uint32_t k1, const typename A::T *b0, const typename A::T *b1) {
+                                              uint32_t k1, const typename A::T *b0, const typename A::T *b1,
+                                              uint32_t db, uint32_t de, uint64_t *part) {
     using G = Geo<S1, S2>;
+    using W = WsGeo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
-    const uint32_t F = (threadIdx.x % WsGeo<S1, S2>::HALF) % SB::T;
+    const uint32_t F = (threadIdx.x % W::HALF) % SB::T, rr = (threadIdx.x % W::HALF) / SB::T;
     const size_t rowoff = (size_t)k1 * G::N2 + F;
     const size_t keyrow = (size_t)prow * G::N + rowoff;
     const uint64_t QPN = (uint64_t)a.QP * G::N;
-    // key limb k of digit d at this thread's positions
     // limb i = 2 d + k of the key (digit d, output k) at this thread's positions
     auto key_at = [&](uint32_t i) { return a.key + (size_t)i * QPN + keyrow; };
     ulonglong2 rt = a.ratio[prow];
@@ -387,7 +416,7 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
 #pragma unroll
     for (int e = 0; e < SB::E; e++) acc0[e] = acc1[e] = 0;
     {
-        const uint64_t *k = key_at(0);
+        const uint64_t *k = key_at(2 * db);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
     }
@@ -395,14 +424,16 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
     __syncthreads();
     __syncthreads();
     __syncthreads();
-    // Output k of digit b - 1 is accumulated in phase B (k = 0) or C (k = 1) of
-    // step b.  One set of key registers: right after a limb is consumed, the
-    // next one (output 1 of the same digit, or output 0 of the next digit) is
-    // loaded, a phase ahead of its use.  Key limbs use plain loads (unlike the
-    // streamed residues): a key is reused call after call (relinearization,
-    // a rotation step repeated), and plain loads measured 5% faster here.
-    for (uint32_t b = 1; b <= a.beta; b++) {
-        const T *buf = ((b - 1) & 1u) ? b1 : b0;
+    // Step s consumes digit d = db + s - 1: output k of it is accumulated in
+    // phase B (k = 0) or C (k = 1).  One set of key registers: right after a
+    // limb is consumed, the next one (output 1 of the same digit, or output 0
+    // of the next digit) is loaded, a phase ahead of its use.  Key limbs use
+    // plain loads (unlike the streamed residues): a key is reused call after
+    // call (relinearization, a rotation step repeated), and plain loads
+    // measured 5% faster here.
+    for (uint32_t st = 1; st <= de - db; st++) {
+        const uint32_t d = db + st - 1;
+        const T *buf = ((st - 1) & 1u) ? b1 : b0;
         // A
         __syncthreads();
         // B
@@ -414,7 +445,7 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
         // keep the refill after the products so it can reuse their key registers
         __builtin_amdgcn_sched_barrier(0);
         {
-            const uint64_t *k = key_at(2 * b - 1);
+            const uint64_t *k = key_at(2 * d + 1);
 #pragma unroll
             for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
         }
@@ -428,12 +459,12 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
         __builtin_amdgcn_sched_barrier(0);
         {
             // after the last digit: reload the limb just consumed (still in L2)
-            const uint64_t *k = key_at(b < a.beta ? 2 * b : 2 * b - 1);
+            const uint64_t *k = key_at(d + 1 < de ? 2 * d + 2 : 2 * d + 1);
 #pragma unroll
             for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
         }
         if constexpr (A::kF64) {
-            if (!(b & 1u)) {
+            if (!(st & 1u)) {
 #pragma unroll
                 for (int e = 0; e < SB::E; e++) {
                     ar.reduce(acc0[e]);
@@ -443,74 +474,158 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
         }
         __syncthreads();
     }
-    uint64_t *o0 = a.cx + (size_t)r * G::N + rowoff;
-    uint64_t *o1 = o0 + (size_t)a.QlP * G::N;
-    // fold (see InnerRows): e_k = base_k + cx_k [P^-1]_q, the NTT-form limb whose
-    // INTT, less the base conversion of the P limbs times P^-1, is the
-    // coefficient form of the ModDown output's last limb
-    const bool fold = r == a.fold_r;
-    ulonglong2 f{0, 0};
-    const uint64_t *fb0 = a.fold_base0 + (size_t)r * G::N + rowoff;
-    const uint64_t *fb1 = a.fold_base1 + (size_t)r * G::N + rowoff;
-    if (fold) f = *a.fold_f;
+    if (part) {
+        // a digit chunk: plain stores, so the sums stay in the XCD's L2 for the
+        // chunk that adds them
+        uint64_t *p0 = part + (size_t)rr * G::N2 + F, *p1 = p0 + (size_t)W::ROWS * G::N2;
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) {
+            p0[SB::T * e] = ar.store(acc0[e]);
+            p1[SB::T * e] = ar.store(acc1[e]);
+        }
+        return;
+    }
     const uint64_t q = (uint64_t)ar.q;
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) {
-        uint64_t v0 = ar.store(acc0[e]), v1 = ar.store(acc1[e]);
-        if (fold) {
-            v0 = add_mod(shoup(v0, f.x, f.y, q), fb0[SB::T * e], q);
-            v1 = add_mod(shoup(v1, f.x, f.y, q), fb1[SB::T * e], q);
-        }
-        st_stream(&o0[SB::T * e], v0);
-        st_stream(&o1[SB::T * e], v1);
-    }
+    for (int e = 0; e < SB::E; e++) ws_out(a, r, rowoff, G::N, SB::T * e, q, ar.store(acc0[e]), ar.store(acc1[e]));
 }
 
+// One work item (target limb r of member mi, a tile of ROWS rows) over digits
+// db .. de-1.
 template <int S1, int S2>
-__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a0, NttTables t) {
+__device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t, uint32_t w0, uint32_t db,
+                                        uint32_t de, uint64_t *part, double *lds, ulonglong2 *tws) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
-    __shared__ double lds[W::LDS + 2 * W::TW];
-    ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + W::LDS);
     const bool transform = threadIdx.x < W::HALF;
     const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
     const uint32_t per = a0.QlP * W::TILES;
-    const uint32_t total = a0.batch * per;
-    for (uint32_t w0 = blockIdx.x; w0 < total; w0 += gridDim.x) {
-        const uint32_t mi = w0 / per, w = w0 % per;
-        InnerRows a = a0;
-        a.inter += mi * a0.inter_bstride;
-        a.c2 += mi * a0.c2_bstride;
-        a.cx += mi * a0.cx_bstride;
-        const uint32_t r = w / W::TILES, tile = w % W::TILES;
-        const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
-        const uint64_t q = wave_uniform(t.mod[prow]);
-        const uint32_t k1 = tile * W::ROWS + rr;
-        if (q < kF64PrimeBound) {
-            double *b0 = lds + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
-            if (transform) {
-                // this item's rows' base factors rb[g][tile ROWS + i] and the small table
-                const ulonglong2 *rb = t.rb_fw + (size_t)prow * S2 * G::N1 + tile * W::ROWS;
-                const ulonglong2 *small = t.small_fw + (size_t)prow * kSmall;
-                for (uint32_t i = threadIdx.x; i < (uint32_t)W::TW; i += W::HALF)
-                    tws[i] = i < (uint32_t)W::TW_RB ? rb[(i / W::ROWS) * G::N1 + i % W::ROWS] : small[i - W::TW_RB];
-            }
-            __syncthreads();
-            if (transform)
-                ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, b0, b1);
-            else
-                ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, k1, b0, b1);
-        } else {
-            uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
-            if (transform)
-                ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, b0, b1);
-            else
-                ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, k1, b0, b1);
+    const uint32_t mi = w0 / per, w = w0 % per;
+    InnerRows a = a0;
+    a.inter += mi * a0.inter_bstride;
+    a.c2 += mi * a0.c2_bstride;
+    a.cx += mi * a0.cx_bstride;
+    const uint32_t r = w / W::TILES, tile = w % W::TILES;
+    const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
+    const uint64_t q = wave_uniform(t.mod[prow]);
+    const uint32_t k1 = tile * W::ROWS + rr;
+    if (q < kF64PrimeBound) {
+        double *b0 = lds + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
+        if (transform) {
+            // this item's rows' base factors rb[g][tile ROWS + i] and the small table
+            const ulonglong2 *rb = t.rb_fw + (size_t)prow * S2 * G::N1 + tile * W::ROWS;
+            const ulonglong2 *small = t.small_fw + (size_t)prow * kSmall;
+            for (uint32_t i = threadIdx.x; i < (uint32_t)W::TW; i += W::HALF)
+                tws[i] = i < (uint32_t)W::TW_RB ? rb[(i / W::ROWS) * G::N1 + i % W::ROWS] : small[i - W::TW_RB];
         }
         __syncthreads();
+        if (transform)
+            ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, b0, b1, db, de);
+        else
+            ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, k1, b0, b1, db, de, part);
+    } else {
+        uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
+        if (transform)
+            ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, b0, b1, db, de);
+        else
+            ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, k1, b0, b1, db, de, part);
     }
 }
 
+// The last chunk of split item w0 to finish adds the kch partial sums
+// (canonical, in this XCD's L2) and writes the output.
+template <int S1, int S2>
+__device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables &t, uint32_t w0,
+                                           const uint64_t *parts) {
+    using G = Geo<S1, S2>;
+    using W = WsGeo<S1, S2>;
+    using SB = Sub<S2>;
+    const uint32_t F = (threadIdx.x % W::HALF) % SB::T, rr = (threadIdx.x % W::HALF) / SB::T;
+    const uint32_t per = a0.QlP * W::TILES;
+    const uint32_t mi = w0 / per, w = w0 % per;
+    InnerRows a = a0;
+    a.cx += mi * a0.cx_bstride;
+    const uint32_t r = w / W::TILES, tile = w % W::TILES;
+    const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
+    const uint64_t q = wave_uniform(t.mod[prow]);
+    const size_t rowoff = (size_t)(tile * W::ROWS + rr) * G::N2 + F;
+    constexpr size_t PS = (size_t)2 * W::ROWS * G::N2;  // one chunk's sums
+    const uint64_t *p = parts + (size_t)rr * G::N2 + F;
+    uint64_t v0[SB::E], v1[SB::E];
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) v0[e] = v1[e] = 0;
+    // one chunk at a time, its 2 E loads in flight together
+    for (uint32_t c = 0; c < a.kch; c++) {
+        uint64_t l0[SB::E], l1[SB::E];
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) {
+            l0[e] = p[c * PS + SB::T * e];
+            l1[e] = p[c * PS + (size_t)W::ROWS * G::N2 + SB::T * e];
+        }
+#pragma unroll
+        for (int e = 0; e < SB::E; e++) {
+            v0[e] = add_mod(v0[e], l0[e], q);
+            v1[e] = add_mod(v1[e], l1[e], q);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) ws_out(a, r, rowoff, G::N, SB::T * e, q, v0[e], v1[e]);
+}
+
+// Items 0 .. full-1 are processed whole, by workgroup w0 mod grid.  When the
+// item count is not a multiple of the resident workgroups, the rem items left
+// over would run as a second round on a mostly idle chip; they are split into
+// kch digit chunks instead, which fill one short round: workgroup g takes
+// chunk (u mod kch) of item full + (u / kch) 8 + (g mod 8), u = g / 8.  The
+// chunks of an item thus run on workgroups congruent mod 8, i.e. on one XCD
+// (a launch's workgroups are dealt to the 8 XCDs round-robin), so their
+// partial sums meet in that XCD's L2; nothing waits for anything.  Each chunk
+// marks its XCD in the item's counter, and the last to arrive records an error
+// if they differ.
+template <int S1, int S2>
+__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a0, NttTables t) {
+    using W = WsGeo<S1, S2>;
+    __shared__ double lds[W::LDS + 2 * W::TW];
+    __shared__ uint32_t s_last;
+    ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + W::LDS);
+    const uint32_t total = a0.batch * a0.QlP * W::TILES;
+    const uint32_t full = a0.full < total ? a0.full : total;
+    for (uint32_t w0 = blockIdx.x; w0 < full; w0 += gridDim.x) {
+        ws_item<S1, S2>(a0, t, w0, 0, a0.beta, nullptr, lds, tws);
+        __syncthreads();
+    }
+    if (a0.rem == 0) return;
+    const uint32_t u = blockIdx.x / kXcds, c = u % a0.kch;
+    const uint32_t j = (u / a0.kch) * kXcds + blockIdx.x % kXcds;
+    if (j >= a0.rem) return;
+    constexpr size_t PS = (size_t)2 * W::ROWS * Geo<S1, S2>::N2;
+    const uint64_t *parts = a0.partial + (size_t)j * a0.kch * PS;
+    ws_item<S1, S2>(a0, t, full + j, c * a0.beta / a0.kch, (c + 1) * a0.beta / a0.kch,
+                    a0.partial + ((size_t)j * a0.kch + c) * PS, lds, tws);
+    // the chunk's sums are in L2 before its arrival is counted
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t mine = 1u << (8 + (xcc_id() & (kXcds - 1)));
+        uint32_t *cnt = a0.counter + j;
+        __hip_atomic_fetch_or(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = (old & 0xffu) == a0.kch - 1;
+        if (last) {
+            if (((old | mine) & ~0xffu) != mine) {
+                __hip_atomic_fetch_or(a0.dev_err, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a0.host_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
+        }
+        s_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last && threadIdx.x >= W::HALF) {
+        asm volatile("buffer_inv sc0" ::: "memory");  // the other chunks' sums: read L2, not this CU's L1
+        ws_combine<S1, S2>(a0, t, full + j, parts);
+    }
+}
 
 // ------------------------------------------------------------ epilogue rows
 // out[m][j] = (base[m][j] if given) + (c[m][j] - NTT(D[m][j])) f_j   (mod q_j)
@@ -664,11 +779,49 @@ void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
     PFA_HIP(hipGetLastError());
 }
 
+// largest number of split items one launch may have (arrival counters per workspace)
+constexpr uint32_t kWsMaxSplit = 4096;
+
 template <int S1, int S2>
-void launch_inner(const Ctx &c, const InnerRows &a, hipStream_t s) {
+void launch_inner(const Ctx &c, InnerRows a, hipStream_t s) {
+    using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
-    hipLaunchKernelGGL((k_inner_ws<S1, S2>), dim3(fgrid(c, a.batch * a.QlP * W::TILES, 4)), dim3(W::THREADS), 0, s, a,
-                       tables_of(c));
+    static const int occ = [] {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *)k_inner_ws<S1, S2>, W::THREADS, 0) !=
+            hipSuccess)
+            n = 1;
+        return n > 0 ? n : 1;
+    }();
+    const uint32_t items = a.batch * a.QlP * W::TILES;
+    const uint32_t P = c.ws_slots ? c.ws_slots : (uint32_t)c.n_cu * (uint32_t)occ;  // resident workgroups
+    uint32_t grid = items;
+    a.full = items;
+    a.rem = 0;
+    a.kch = 1;
+    Scratch sc(c, s);
+    if (items > P) {
+        grid = P;
+        const uint32_t rem = items % P;
+        const uint32_t per_x = (rem + kXcds - 1) / kXcds;  // split items per XCD class
+        const uint32_t kmax = std::min<uint32_t>(a.beta, c.ws_max_chunks ? c.ws_max_chunks : a.beta);
+        const uint32_t kch = rem && P % kXcds == 0 ? std::min<uint32_t>(kmax, (P / kXcds) / per_x) : 0;
+        if (kch >= 2 && rem <= kWsMaxSplit) {
+            Arena &ar = arena_for(c, s);
+            if (!ar.ws_counter) {
+                PFA_HIP(hipMalloc((void **)&ar.ws_counter, kWsMaxSplit * sizeof(uint32_t)));
+                PFA_HIP(hipMemsetAsync(ar.ws_counter, 0, kWsMaxSplit * sizeof(uint32_t), s));
+            }
+            a.full = items - rem;
+            a.rem = rem;
+            a.kch = kch;
+            a.partial = sc.alloc((size_t)rem * kch * 2 * W::ROWS * G::N2);
+            a.counter = ar.ws_counter;
+            a.dev_err = c.err_dev;
+            a.host_err = c.err_host_dev;
+        }
+    }
+    hipLaunchKernelGGL((k_inner_ws<S1, S2>), dim3(grid), dim3(W::THREADS), 0, s, a, tables_of(c));
     PFA_HIP(hipGetLastError());
 }
 

@@ -101,6 +101,9 @@ struct Arena {
     uint32_t *flow = nullptr;
     uint32_t flow_parity = 0;
     uint32_t flow_dirty[2] = {0, 0};  // jobs the last launch on each block used
+    // arrival counters of the inner product's split items (k_inner_ws), zero
+    // between launches (the last arrival clears its counter)
+    uint32_t *ws_counter = nullptr;
 };
 
 struct Ctx {
@@ -122,6 +125,8 @@ struct Ctx {
     int n_cu = 256;                  // compute units of the device
     int ntt_wpc = 3;                 // resident workgroups per CU of the prefetching inverse rows pass
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
+    uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)
+    uint32_t ws_max_chunks = 0;      // most digit chunks of a split inner-product item (0: beta)
     // single-launch NTT (ntt_kernels.h, opt-in): needs a device that deals
     // workgroups to 8 XCDs round-robin; used for batches of at least
     // flow_min_jobs limbs at N = 2^16
@@ -130,9 +135,14 @@ struct Ctx {
     uint32_t flow_window = 2;        // jobs ahead of the second-pass front
     uint32_t flow_min_jobs = 8;
     uint32_t flow_wait_ticks = 10000000;  // 100 ms at the 100 MHz s_memrealtime clock
-    uint32_t *flow_err_dev = nullptr;      // device error word of the single-launch NTT
-    uint32_t *flow_err_host = nullptr;     // mapped pinned word the kernel sets on error
-    uint32_t *flow_err_host_dev = nullptr; // its device address
+    // Errors kernels record while they run (bits or-ed into err_dev; any
+    // error also sets the mapped pinned word err_host): 1 a single-launch NTT's
+    // bounded wait expired, 2 a single-launch NTT ended with tiles not
+    // transformed, 4 the digit chunks of one inner-product item ran on
+    // different XCDs.  Reported by check_device_errors.
+    uint32_t *err_dev = nullptr;
+    uint32_t *err_host = nullptr;
+    uint32_t *err_host_dev = nullptr;  // err_host's device address
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
     // matrix [P/p_j]_{q_i} ([P][Q]), [P^-1]_{q_i} Shoup pairs ([Q])
     ulonglong2 *moddown_scale = nullptr;

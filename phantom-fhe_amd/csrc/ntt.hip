@@ -107,8 +107,8 @@ void flow(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     f.other_jobs = a.flow_dirty[1 - p];
     f.window = c.flow_window;
     f.wait_ticks = c.flow_wait_ticks;
-    f.dev_err = c.flow_err_dev;
-    f.host_err = c.flow_err_host_dev;
+    f.dev_err = c.err_dev;
+    f.host_err = c.err_host_dev;
     const uint32_t grid = (uint32_t)c.n_cu * (uint32_t)c.flow_wpc / kXcds * kXcds;
     if (FWD) {
         if (c.flow_wpc >= 4)

@@ -24,6 +24,7 @@ from __future__ import annotations
 import enum
 import itertools
 import struct
+import threading
 
 import numpy as np
 
@@ -151,6 +152,28 @@ class context:
         # device constants made on first use (monomials, constant plaintexts):
         # each upload would otherwise be one more host-to-device copy per call
         self._const_cache = {}
+        self._const_lock = threading.Lock()
+
+    def _cached_const(self, key, make):
+        """The device constant `key`, made by make() once per context on the
+        calling thread's current stream.  An event recorded after it is made
+        orders every later use: a stream that first reads it waits for that
+        event once (a device-side wait, the host does not block)."""
+        t = _torch()
+        stream = t.cuda.current_stream(self.device)
+        with self._const_lock:
+            hit = self._const_cache.get(key)
+            if hit is None:
+                data = make()
+                ev = t.cuda.Event()
+                ev.record(stream)
+                hit = (data, ev, {stream.cuda_stream})
+                self._const_cache[key] = hit
+            data, ev, ready = hit
+            if stream.cuda_stream not in ready:
+                stream.wait_event(ev)
+                ready.add(stream.cuda_stream)
+        return data
 
     def total_parm_size(self) -> int:
         return self.size_Q + 1
@@ -1531,19 +1554,16 @@ def _const_plain(ctx: context, value: complex, scale: float, chain: int) -> plai
     pt._chain_index, pt._scale = chain, float(scale)
     re = int(round(value.real * scale))
     im = int(round(value.imag * scale))
-    key = ("const", re, im, L)
-    data = ctx._const_cache.get(key)
-    if data is None:
+    def make():
         if im == 0:
             r = np.array([re % q for q in ctx.moduli[:L]], dtype=np.uint64)
-            data = _to_dev(r, ctx.dev).view(L, 1).expand(L, ctx.N).contiguous()
-        else:
-            c = np.zeros(ctx.N, dtype=np.int64)
-            c[0] = re
-            c[ctx.N // 2] = im
-            data = ctx._ntt(ctx._signed_to_rns(c, L), L)
-        ctx._const_cache[key] = data
-    pt.data = data
+            return _to_dev(r, ctx.dev).view(L, 1).expand(L, ctx.N).contiguous()
+        c = np.zeros(ctx.N, dtype=np.int64)
+        c[0] = re
+        c[ctx.N // 2] = im
+        return ctx._ntt(ctx._signed_to_rns(c, L), L)
+
+    pt.data = ctx._cached_const(("const", re, im, L), make)
     return pt
 
 
@@ -1860,12 +1880,13 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
 def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
     """ct * (sign i): the plaintext polynomial times sign X^(N/2), exact."""
     L = ctx.size_Ql(ct.chain_index())
-    mono = ctx._const_cache.get(("times_i", sign, L))
-    if mono is None:
+
+    def make():
         c = np.zeros(ctx.N, dtype=np.int64)
         c[ctx.N // 2] = sign
-        mono = ctx._ntt(ctx._signed_to_rns(c, L), L)
-        ctx._const_cache[("times_i", sign, L)] = mono
+        return ctx._ntt(ctx._signed_to_rns(c, L), L)
+
+    mono = ctx._cached_const(("times_i", sign, L), make)
     out = ctx._empty(*ct.data.shape)
     for k in range(ct.size()):
         ctx.native.poly_mul(ct.data[k], mono, out[k], L)

@@ -373,3 +373,29 @@ def test_top_level_of_uneven_chain_rejected(dev):
         st.ctx.keyswitch(1, to_dev(ct, dev), to_dev(ct[1], dev), to_dev(key, dev))
     with pytest.raises(ValueError):
         st.orc.keyswitch(1, ct, ct[1], key)
+
+
+@pytest.mark.parametrize("slots", [64, 48, 40, 16])
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 9, 3, 1), (12, 20, 1, 1), (13, 12, 4, 1)])
+def test_inner_product_split_items(dev, monkeypatch, slots, logN, nq, alpha, chain):
+    """The inner product splits the items left over after whole rounds of its
+    resident workgroups into digit chunks whose partial sums the last chunk
+    adds (k_inner_ws).  PFA_WS_SLOTS shrinks the assumed resident count so small
+    shapes split with several chunk counts; the fused and two-call HMult and the
+    key switch stay bit-exact against the oracle, and no placement error is
+    recorded."""
+    monkeypatch.setenv("PFA_WS_SLOTS", str(slots))
+    st = Setup(logN, nq, alpha, seed=slots + logN)
+    Ql = st.orc.size_Ql(chain)
+    a, b = st.ct(chain), st.ct(chain)
+    key = st.key()
+    want = st.orc.multiply_and_relin(chain, a, b, key, threads=8)
+    out = empty((2, Ql, st.N), dev)
+    st.ctx.multiply_and_relin(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    fused = empty((2, Ql - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), fused)
+    got, want_r = to_host(fused), st.orc.rescale(chain, want, threads=8)
+    assert np.array_equal(got, want_r), first_mismatch(got, want_r)
+    st.ctx.synchronize()
