@@ -146,6 +146,18 @@ int pfa_relinearize(const pfa_context *ctx, size_t chain_index, const uint64_t *
 int pfa_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *in, size_t size, uint64_t *out,
                 void *stream);
 
+/* No counterpart in the reference: pfa_rescale for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops or
+ * harnesses that forbid hipMalloc).  Same residues as pfa_rescale; allocates
+ * nothing: the base conversion's intermediate is formed in `out`, and the last
+ * limb's coefficients go to a static per-device scratch array of 4 MiB
+ * (size x N <= 524288 residues: 8 polys at N = 2^16; larger calls return
+ * PFA_ERR_INVALID_ARGUMENT).  `in` and `out` must not overlap.  Calls that
+ * overlap in time on one device share that scratch and race; calls on one
+ * stream are ordered.  The single-launch NTT is never used here. */
+int pfa_rescale_noalloc(const pfa_context *ctx, size_t chain_index, const uint64_t *in, size_t size, uint64_t *out,
+                        void *stream);
+
 /* multiply_and_relin_inplace then rescale_to_next_inplace (src/evaluate.cu:1061-1104,
  * :1582-1602) as one call: out [2][|Ql|-1][N] = rescale(multiply_and_relin(a, b)),
  * bit-identical to pfa_multiply_and_relin followed by pfa_rescale.  The ModDown

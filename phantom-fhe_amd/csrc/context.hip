@@ -486,6 +486,7 @@ int pfa_context_create(uint64_t poly_degree, const uint64_t *moduli, size_t size
         PFA_HIP(hipSetDevice(device));
         try {
             build(*c, poly_degree, moduli, size_QP, special_size);
+            noalloc_init(device);
         } catch (...) {
             (void)hipSetDevice(prev);
             throw;

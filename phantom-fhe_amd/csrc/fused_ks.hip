@@ -983,14 +983,20 @@ void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M,
 
 // in [size][L][N] -> out [size][L-1][N]: floor division by the last prime
 void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s) {
-    const Level &lv = c.level(chain);
-    const uint32_t L = lv.Ql;
+    const uint32_t L = c.level(chain).Ql;
     Scratch sc(c, s);
     uint64_t *last = sc.alloc((size_t)size * c.N);
     uint64_t *inter = sc.alloc((size_t)size * (L - 1) * c.N);
+    fused_rescale_with(c, chain, in, size, out, last, inter, s, true);
+}
+
+void fused_rescale_with(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out,
+                        uint64_t *last, uint64_t *inter, hipStream_t s, bool allow_flow) {
+    const Level &lv = c.level(chain);
+    const uint32_t L = lv.Ql;
     NttLaunch inv{in + (size_t)(L - 1) * c.N, last, (uint64_t)L * c.N, (uint64_t)c.N, size, 1};
     inv.start = L - 1;
-    ntt_inverse(c, inv, s);
+    ntt_inverse(c, inv, s, allow_flow);
     BconvCols b{};
     b.in = last;
     b.out = inter;

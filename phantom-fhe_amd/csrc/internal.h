@@ -239,8 +239,10 @@ struct NttLaunch {
     uint32_t ex_lo = 0, ex_step = 0, ex_len = 0, ex_cap = 0;
     const ulonglong2 *scale = nullptr;
 };
-void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s);
-void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s);
+// allow_flow false keeps the transform on the two-launch path, which needs no
+// workspace (the single-launch path takes control blocks from it)
+void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow = true);
+void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow = true);
 // True when the device deals a launch's workgroups to 8 XCDs round-robin
 // (workgroup w on XCD (w + r) mod 8 for some r), which the single-launch NTT is
 // built for; runs a probe kernel.
@@ -268,5 +270,14 @@ void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M,
                    const uint64_t *base0, const uint64_t *base1, hipStream_t s, uint64_t base_stride = 0);
 // in [size][Ql][N] -> out [size][Ql-1][N]: floor division by the level's last prime.
 void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out, hipStream_t s);
+// The same with the caller's buffers for the last limb's coefficients (last,
+// size N) and the base conversion's intermediate (inter, size (Ql - 1) N; may
+// be out itself: the epilogue rewrites each tile of it in place); allocates
+// nothing when allow_flow is false.
+void fused_rescale_with(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out,
+                        uint64_t *last, uint64_t *inter, hipStream_t s, bool allow_flow);
+// Allocation-free entry points (noalloc.hip): takes the address of this
+// device's static scratch array; called once per device, with it current.
+void noalloc_init(int device);
 
 }  // namespace pfa

@@ -145,12 +145,12 @@ bool use_flow(const Ctx &c, const NttBatch &b) {
     default: fail(PFA_ERR_INVALID_ARGUMENT, "unsupported poly_modulus_degree"); \
     }
 
-void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
     check_device_errors(c);
-    if (use_flow(c, b)) {
+    if (allow_flow && use_flow(c, b)) {
         flow<true>(c, b, t, s);
         return;
     }
@@ -158,12 +158,12 @@ void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     PFA_HIP(hipGetLastError());
 }
 
-void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
     check_device_errors(c);
-    if (use_flow(c, b)) {
+    if (allow_flow && use_flow(c, b)) {
         flow<false>(c, b, t, s);
         return;
     }

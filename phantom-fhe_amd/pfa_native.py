@@ -44,6 +44,7 @@ SIGNATURES = {
     "pfa_multiply_and_relin": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
     "pfa_relinearize": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
     "pfa_rescale": (_i32, [_vp, _sz, _vp, _sz, _vp, _vp]),
+    "pfa_rescale_noalloc": (_i32, [_vp, _sz, _vp, _sz, _vp, _vp]),
     "pfa_multiply_relin_rescale": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
     "pfa_relinearize_rescale": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
     "pfa_galois_elt_from_step": (_i32, [_i32, _u64, C.POINTER(C.c_uint32)]),
@@ -265,6 +266,11 @@ class NativeContext:
 
     def rescale(self, chain_index, ct, out, stream=None):
         call("pfa_rescale", self._h, chain_index, ptr(ct), ct.shape[0], ptr(out), stream or stream_of(ct))
+
+    def rescale_noalloc(self, chain_index, ct, out, stream=None):
+        """pfa_rescale_noalloc: the same residues as rescale, with no device
+        allocation (a static per-device scratch; see include/phantom_amd.h)."""
+        call("pfa_rescale_noalloc", self._h, chain_index, ptr(ct), ct.shape[0], ptr(out), stream or stream_of(ct))
 
     def apply_galois_ntt(self, elt, src, dst, L, stream=None):
         call("pfa_apply_galois_ntt", self._h, elt, ptr(src), ptr(dst), L, stream or stream_of(src))
