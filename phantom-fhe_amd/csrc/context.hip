@@ -184,7 +184,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     // itw[1] *= N^-1.
     // rows-pass geometry of the NTT kernels: N = N1 * N2 with S1 = min(8, logN / 2)
     const uint32_t S1 = c.logN / 2 > 8 ? 8 : c.logN / 2, S2 = c.logN - S1, N1 = 1u << S1;
-    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP), sfw(QP * 256), sinv(QP * 256),
+    std::vector<ulonglong2> tw(QP * N), itw(QP * N), ninv(QP), ratio(QP), mont(QP), sfw(QP * 256), sinv(QP * 256),
         rbf((size_t)QP * S2 * N1), rbi((size_t)QP * S2 * N1);
     c.roots.resize(QP);
     for (size_t r = 0; r < QP; ++r) {
@@ -219,9 +219,16 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         ninv[r] = ntt_pair(ni, q);
         u128 rt = (~(u128)0) / q;  // floor((2^128 - 1) / q) == floor(2^128 / q) for non powers of two
         ratio[r] = ulonglong2{(uint64_t)rt, (uint64_t)(rt >> 64)};
+        // Montgomery constants (R = 2^64): -q^-1 mod R (Newton's iteration doubles
+        // the correct low bits from the 3 of q^-1 = q mod 8) and R^2 mod q
+        uint64_t qi = q;
+        for (int it = 0; it < 5; ++it) qi *= 2 - q * qi;
+        const u128 r1 = ((~(u128)0) % q + 1) % q;  // 2^128 mod q
+        mont[r] = ulonglong2{(uint64_t)0 - qi, (uint64_t)r1};
     }
     c.mod = c.upload(c.moduli);
     c.ratio = c.upload(ratio);
+    c.mont = c.upload(mont);
     c.tw = c.upload(tw);
     c.itw = c.upload(itw);
     c.ninv = c.upload(ninv);

@@ -219,7 +219,7 @@ struct InnerRows {
     const uint64_t *c2;     // [Ql][N] NTT form: the digit's own limbs
     const uint64_t *key;    // [dnum][2][QP][N]
     uint64_t *cx;           // [2][QlP][N]
-    const ulonglong2 *ratio;
+    const ulonglong2 *mont;  // [QP] Montgomery constants (-q^-1 mod 2^64, 2^128 mod q)
     uint32_t Ql, QlP, alpha, beta, Q, QP;
     // independent key switches with the same key: member i adds i * the stride
     uint32_t batch = 1;
@@ -255,19 +255,20 @@ __device__ __forceinline__ const uint64_t *inner_src(const InnerRows &a, uint32_
 // buffers while the second half (the accumulate waves) multiplies digit b-1's
 // transformed tile, read from the other buffer, by its key limbs.  The roles
 // keep disjoint register state (transform: the tile and the next digit's
-// prefetched tile; accumulate: the two accumulators and the key limbs), so the
-// key traffic overlaps the transforms of the other waves.  Both roles run
-// beta + 1 steps of three workgroup barriers each, in the same order:
-//   A  transform: round a of digit b (or its own limb of c2) -> buffer b%2
-//   B  transform: round b;   accumulate: output 0 of digit b-1 from buffer (b-1)%2
-//   C  transform: final layout -> buffer b%2;   accumulate: output 1 of digit b-1
+// prefetched tile; accumulate: the accumulators and the next digit's key
+// limbs), so the key traffic overlaps the transforms of the other waves.
+// A row's threads are all in one wave, so the rows pass exchanges data within
+// each wave only (wave_lds_sync) and the roles meet at one workgroup barrier
+// per digit, the hand-off of the buffers; between two barriers both roles work.
+// With two accumulate waves or more, each takes one output (0 or 1) of the
+// whole tile, AE elements per thread, in the order the key is laid out.
 //
 // Two properties keep the prefetches a full step ahead:
 // * Global loads complete in issue order (one vmcnt counter), so a load issued
 //   after a prefetch cannot be waited for without waiting for the prefetch.
 //   The FP64 rows-pass twiddle factors therefore come from LDS: the item's
 //   rows' base factors and the small table are staged there once per item.
-//   The Barrett ratio is loaded before the first key limbs.
+//   The Montgomery constants are loaded before the first key limbs.
 // * Every prefetch is unconditional (the step after the last one reloads the
 //   rows it has just consumed, which are still in L2), so the prefetched
 //   registers are never merged with their previous values at the loop head,
@@ -283,8 +284,22 @@ struct WsGeo {
     static constexpr int TW_RB = S2 * ROWS;                   // staged base factors [S2][ROWS]
     static constexpr int TW_SMALL = 1 << (S2 - 1);            // staged small table entries
     static constexpr int TW = TW_RB + TW_SMALL;               // ulonglong2 entries after the buffers
+    // accumulate role: outputs per thread, threads per output, elements per thread and output
+    static constexpr int NO = HALF >= 128 ? 1 : 2;
+    static constexpr int TPO = NO == 1 ? HALF / 2 : HALF;
+    static constexpr int AE = ROWS * G::N2 / TPO;
     static_assert(HALF % 64 == 0, "each role must be whole wavefronts");
+    static_assert(TPO % 64 == 0 && ROWS * G::N2 % TPO == 0, "each output must be whole wavefronts");
 };
+
+// Orders this wave's LDS accesses around an exchange between its lanes: a
+// wave's LDS operations execute in issue order, so the exchange needs no
+// workgroup barrier, only that the compiler keep the accesses in order.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
@@ -307,7 +322,6 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
         T *buf = ((b - db) & 1u) ? b1 : b0;
         const bool own = nown;
         T x[SB::E];
-        // A
 #pragma unroll
         for (int e = 0; e < SB::E; e++) x[e] = own ? ar.load(nraw[e]) : ar.load_mid(nraw[e]);
         {
@@ -329,12 +343,9 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
             }
 #pragma unroll
             for (int e = 0; e < SB::E; e++) ar.reduce(x[e]);
-        }
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
-        __syncthreads();
-        // B
-        if (!own) {
+            for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
+            wave_lds_sync();
 #pragma unroll
             for (int e = 0; e < SB::E; e++) x[e] = buf[rpad(F * SB::E + e)];
             if constexpr (A::kF64) {
@@ -346,130 +357,121 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
                 asm volatile("" : "+v"(kr), "+s"(pr));
                 fwd_round_b<A, S2>(x, ar, t.tw + (size_t)pr * G::N, G::N1 + kr, F);
             }
-        }
-        __syncthreads();
-        // C
-        if (!own) {
+            wave_lds_sync();
 #pragma unroll
             for (int e = 0; e < SB::E; e++) buf[rpad(F * SB::E + e)] = x[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) buf[rpad(F + SB::T * e)] = x[e];
         }
-        __syncthreads();
+        __syncthreads();  // buffer (b - db) % 2 to the accumulate waves
     }
-    // the last step: the accumulate waves consume the last digit
-    __syncthreads();
-    __syncthreads();
-    __syncthreads();
+    __syncthreads();  // the accumulate waves consume the last digit
 }
 
 // Product of digit d's transformed element x (lazy) with key limb value w,
 // accumulated into acc: FP64 policy exact products (acc reduced every second
-// digit), integer policy Barrett products summed modulo q.
+// digit); integer policy Montgomery products x w 2^-64, each in [0, 2q), summed
+// in [0, 2q) (ws_sum turns the sum back into sum x w mod q).
 template <class A>
-__device__ __forceinline__ void ws_mac(const A &ar, typename A::T &acc, typename A::T x, uint64_t w, ulonglong2 rt) {
+__device__ __forceinline__ void ws_mac(const A &ar, typename A::T &acc, typename A::T x, uint64_t w, ulonglong2 mt) {
     if constexpr (A::kF64) {
         ar.reduce(x);
         const double wd = ar.load(w);
         acc += ar.mulw(x, wd, wd * ar.qinv);
     } else {
-        U128 p{x * w, mulhi64(x, w)};
-        acc = add_mod(acc, barrett128(p, ar.q, rt.x, rt.y), ar.q);
+        acc = csub(acc + mont_mul(x, w, ar.q, mt.x), ar.q2);
     }
 }
 
-// Output limb r, element e of this thread's row: the canonical sums v0, v1, or
-// with the fold (see InnerRows) base_k + v_k [P^-1]_q.
-__device__ __forceinline__ void ws_out(const InnerRows &a, uint32_t r, size_t rowoff, uint32_t N, uint32_t off,
-                                       uint64_t q, uint64_t v0, uint64_t v1) {
-    uint64_t *o0 = a.cx + (size_t)r * N + rowoff;
-    uint64_t *o1 = o0 + (size_t)a.QlP * N;
+// The canonical residue of an accumulated sum.
+template <class A>
+__device__ __forceinline__ uint64_t ws_sum(const A &ar, typename A::T acc, ulonglong2 mt) {
+    if constexpr (A::kF64)
+        return ar.store(acc);
+    else
+        return ar.store(mont_mul(acc, mt.y, ar.q, mt.x));  // (sum 2^-64) 2^128 2^-64
+}
+
+// Output k of limb r at offset off (within the limb): the canonical sum v, or
+// with the fold (see InnerRows) base_k + v [P^-1]_q.
+__device__ __forceinline__ void ws_out(const InnerRows &a, uint32_t k, uint32_t r, size_t off, uint32_t N,
+                                       uint64_t q, uint64_t v) {
     if (r == a.fold_r) {
         const ulonglong2 f = *a.fold_f;
-        v0 = add_mod(shoup(v0, f.x, f.y, q), a.fold_base0[(size_t)r * N + rowoff + off], q);
-        v1 = add_mod(shoup(v1, f.x, f.y, q), a.fold_base1[(size_t)r * N + rowoff + off], q);
+        v = add_mod(shoup(v, f.x, f.y, q), (k ? a.fold_base1 : a.fold_base0)[(size_t)r * N + off], q);
     }
-    st_stream(&o0[off], v0);
-    st_stream(&o1[off], v1);
+    st_stream(a.cx + ((size_t)k * a.QlP + r) * N + off, v);
 }
 
-// Accumulates digits db .. de-1; with part null the item is whole and its
-// output is written, else the canonical sums go to part ([2][ROWS][N2]).
+// Accumulates digits db .. de-1 of the tile (B0 / B1: the two tile buffers);
+// with part null the item is whole and its output is written, else the
+// canonical sums go to part ([2][ROWS][N2]).
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, uint32_t r, uint32_t prow,
-                                              uint32_t k1, const typename A::T *b0, const typename A::T *b1,
+                                              uint32_t tile, const typename A::T *B0, const typename A::T *B1,
                                               uint32_t db, uint32_t de, uint64_t *part) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
-    using SB = Sub<S2>;
     using T = typename A::T;
-    const uint32_t F = (threadIdx.x % W::HALF) % SB::T, rr = (threadIdx.x % W::HALF) / SB::T;
-    const size_t rowoff = (size_t)k1 * G::N2 + F;
-    const size_t keyrow = (size_t)prow * G::N + rowoff;
+    constexpr int NO = W::NO, AE = W::AE, TPO = W::TPO;
+    const uint32_t u = threadIdx.x - W::HALF;
+    const uint32_t lane = u % TPO, kf = NO == 1 ? u / TPO : 0;  // kf: this thread's output when NO == 1
+    const size_t tbase = (size_t)tile * W::ROWS * G::N2 + lane;  // element offset within a limb
+    const size_t keyrow = (size_t)prow * G::N + tbase;
     const uint64_t QPN = (uint64_t)a.QP * G::N;
     // limb i = 2 d + k of the key (digit d, output k) at this thread's positions
     auto key_at = [&](uint32_t i) { return a.key + (size_t)i * QPN + keyrow; };
-    ulonglong2 rt = a.ratio[prow];
-    rt.x = wave_uniform(rt.x);
-    rt.y = wave_uniform(rt.y);
+    ulonglong2 mt = a.mont[prow];
+    mt.x = wave_uniform(mt.x);
+    mt.y = wave_uniform(mt.y);
     __builtin_amdgcn_sched_barrier(0);
-    T acc0[SB::E], acc1[SB::E];
-    uint64_t kw[SB::E];
+    T acc[NO][AE];
+    uint64_t kw[NO][AE];
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) acc0[e] = acc1[e] = 0;
-    {
-        const uint64_t *k = key_at(2 * db);
+    for (int o = 0; o < NO; o++) {
+        const uint64_t *k = key_at(2 * db + (NO == 1 ? kf : o));
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
+        for (int i = 0; i < AE; i++) {
+            acc[o][i] = 0;
+            kw[o][i] = k[(size_t)TPO * i];
+        }
     }
-    // step 0: the transform waves fill buffer 0
-    __syncthreads();
-    __syncthreads();
-    __syncthreads();
-    // Step s consumes digit d = db + s - 1: output k of it is accumulated in
-    // phase B (k = 0) or C (k = 1).  One set of key registers: right after a
-    // limb is consumed, the next one (output 1 of the same digit, or output 0
-    // of the next digit) is loaded, a phase ahead of its use.  Key limbs use
-    // plain loads (unlike the streamed residues): a key is reused call after
-    // call (relinearization, a rotation step repeated), and plain loads
-    // measured 5% faster here.
+    __syncthreads();  // step 0: the transform waves fill buffer 0
+    // Step s consumes digit d = db + s - 1; its key limbs were requested a whole
+    // step earlier.  Key limbs use plain loads (unlike the streamed residues): a
+    // key is reused call after call (relinearization, a rotation step repeated).
     for (uint32_t st = 1; st <= de - db; st++) {
         const uint32_t d = db + st - 1;
-        const T *buf = ((st - 1) & 1u) ? b1 : b0;
-        // A
-        __syncthreads();
-        // B
+        const T *buf = ((st - 1) & 1u) ? B1 : B0;
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) {
-            ws_mac(ar, acc0[e], buf[rpad(F + SB::T * e)], kw[e], rt);
-            if constexpr (!A::kF64) __builtin_amdgcn_sched_barrier(0);  // one Barrett product at a time
+        for (int i = 0; i < AE; i++) {
+            const uint32_t p = lane + (uint32_t)TPO * i;
+            const T x = buf[(p / G::N2) * G::ROW_PITCH + rpad(p % G::N2)];
+#pragma unroll
+            for (int o = 0; o < NO; o++) {
+                ws_mac(ar, acc[o][i], x, kw[o][i], mt);
+                if constexpr (!A::kF64) __builtin_amdgcn_sched_barrier(0);  // one integer product at a time
+            }
         }
         // keep the refill after the products so it can reuse their key registers
         __builtin_amdgcn_sched_barrier(0);
         {
-            const uint64_t *k = key_at(2 * d + 1);
+            // after the last digit: reload the limbs just consumed (still in L2)
+            const uint32_t dn = d + 1 < de ? d + 1 : d;
 #pragma unroll
-            for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
-        }
-        __syncthreads();
-        // C
+            for (int o = 0; o < NO; o++) {
+                const uint64_t *k = key_at(2 * dn + (NO == 1 ? kf : o));
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) {
-            ws_mac(ar, acc1[e], buf[rpad(F + SB::T * e)], kw[e], rt);
-            if constexpr (!A::kF64) __builtin_amdgcn_sched_barrier(0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            // after the last digit: reload the limb just consumed (still in L2)
-            const uint64_t *k = key_at(d + 1 < de ? 2 * d + 2 : 2 * d + 1);
-#pragma unroll
-            for (int e = 0; e < SB::E; e++) kw[e] = k[SB::T * e];
+                for (int i = 0; i < AE; i++) kw[o][i] = k[(size_t)TPO * i];
+            }
         }
         if constexpr (A::kF64) {
             if (!(st & 1u)) {
 #pragma unroll
-                for (int e = 0; e < SB::E; e++) {
-                    ar.reduce(acc0[e]);
-                    ar.reduce(acc1[e]);
-                }
+                for (int o = 0; o < NO; o++)
+#pragma unroll
+                    for (int i = 0; i < AE; i++) ar.reduce(acc[o][i]);
             }
         }
         __syncthreads();
@@ -477,17 +479,20 @@ __device__ __forceinline__ void ws_accumulate(const InnerRows &a, const A &ar, u
     if (part) {
         // a digit chunk: plain stores, so the sums stay in the XCD's L2 for the
         // chunk that adds them
-        uint64_t *p0 = part + (size_t)rr * G::N2 + F, *p1 = p0 + (size_t)W::ROWS * G::N2;
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) {
-            p0[SB::T * e] = ar.store(acc0[e]);
-            p1[SB::T * e] = ar.store(acc1[e]);
+        for (int o = 0; o < NO; o++) {
+            uint64_t *pk = part + (size_t)(NO == 1 ? kf : o) * W::ROWS * G::N2 + lane;
+#pragma unroll
+            for (int i = 0; i < AE; i++) pk[(size_t)TPO * i] = ws_sum(ar, acc[o][i], mt);
         }
         return;
     }
     const uint64_t q = (uint64_t)ar.q;
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) ws_out(a, r, rowoff, G::N, SB::T * e, q, ar.store(acc0[e]), ar.store(acc1[e]));
+    for (int o = 0; o < NO; o++)
+#pragma unroll
+        for (int i = 0; i < AE; i++)
+            ws_out(a, NO == 1 ? kf : o, r, tbase + (size_t)TPO * i, G::N, q, ws_sum(ar, acc[o][i], mt));
 }
 
 // One work item (target limb r of member mi, a tile of ROWS rows) over digits
@@ -522,13 +527,15 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
         if (transform)
             ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, b0, b1, db, de);
         else
-            ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, k1, b0, b1, db, de, part);
+            ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, tile, lds, lds + W::ROWS * G::ROW_PITCH, db, de,
+                                             part);
     } else {
         uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
         if (transform)
             ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, b0, b1, db, de);
         else
-            ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, k1, b0, b1, db, de, part);
+            ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, tile, reinterpret_cast<uint64_t *>(lds),
+                                             reinterpret_cast<uint64_t *>(lds) + W::ROWS * G::ROW_PITCH, db, de, part);
     }
 }
 
@@ -569,7 +576,10 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
         }
     }
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) ws_out(a, r, rowoff, G::N, SB::T * e, q, v0[e], v1[e]);
+    for (int e = 0; e < SB::E; e++) {
+        ws_out(a, 0, r, rowoff + SB::T * e, G::N, q, v0[e]);
+        ws_out(a, 1, r, rowoff + SB::T * e, G::N, q, v1[e]);
+    }
 }
 
 // Items 0 .. full-1 are processed whole, by workgroup w0 mod grid.  When the
@@ -582,8 +592,19 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
 // partial sums meet in that XCD's L2; nothing waits for anything.  Each chunk
 // marks its XCD in the item's counter, and the last to arrive records an error
 // if they differ.
+//
+// At N = 2^16 the kernel is compiled for 3 waves per SIMD (168 VGPRs): the
+// integer-policy accumulate path would take 176, and the values the compiler
+// then spills are loop invariants reloaded once per item (measured: L = 35
+// inner product 540 -> 520 us against 2 waves per SIMD).
 template <int S1, int S2>
-__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) k_inner_ws(InnerRows a0, NttTables t) {
+struct WsWaves {
+    static constexpr int MIN = S1 == 8 && S2 == 8 ? 3 : 1;
+};
+
+template <int S1, int S2>
+__global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) __attribute__((amdgpu_waves_per_eu(WsWaves<S1, S2>::MIN, 8)))
+k_inner_ws(InnerRows a0, NttTables t) {
     using W = WsGeo<S1, S2>;
     __shared__ double lds[W::LDS + 2 * W::TW];
     __shared__ uint32_t s_last;
@@ -883,7 +904,7 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.in_bstride = LN;
     b.out_bstride = IN;
     PFA_FUSED_DISPATCH(launch_bconv, b);
-    InnerRows r{inter, c2, key, cx, c.ratio, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
+    InnerRows r{inter, c2, key, cx, c.mont, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
     r.batch = batch;
     r.inter_bstride = IN;
     r.c2_bstride = c2_stride;

@@ -115,6 +115,7 @@ struct Ctx {
     // device, all primes (rows of the QP table)
     uint64_t *mod = nullptr;        // [QP]
     ulonglong2 *ratio = nullptr;    // [QP] floor(2^128 / q) as (lo, hi)
+    ulonglong2 *mont = nullptr;     // [QP] Montgomery constants (-q^-1 mod 2^64, 2^128 mod q)
     ulonglong2 *tw = nullptr;       // [QP][N]
     ulonglong2 *itw = nullptr;      // [QP][N]
     ulonglong2 *ninv = nullptr;     // [QP] NTT-policy pairs of N^-1

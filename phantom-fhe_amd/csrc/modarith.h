@@ -90,6 +90,15 @@ __device__ __forceinline__ uint64_t barrett128(U128 x, uint64_t q, uint64_t r0, 
     return csub(r, q);
 }
 
+// Montgomery product x y 2^-64 mod q, in [0, 2q), for x y < q 2^64 (e.g. x < 4q,
+// y < q with q < 2^62); qn = -q^-1 mod 2^64.  With m = lo(x y) qn, x y + m q is
+// a multiple of 2^64 whose low word sums to 0 or 2^64 (lo(x y) != 0).
+__device__ __forceinline__ uint64_t mont_mul(uint64_t x, uint64_t y, uint64_t q, uint64_t qn) {
+    const uint64_t lo = x * y, hi = mulhi64(x, y);
+    const uint64_t m = lo * qn;
+    return hi + mulhi64(m, q) + (lo != 0 ? 1 : 0);
+}
+
 // ----------------------------------------------------------------------------
 // NTT arithmetic policies.  Twiddle table entries are 16-byte pairs whose
 // meaning depends on the prime's policy:
