@@ -235,38 +235,47 @@ def time_bsgs(torch, steps, warmup):
             "giant": d_pad // M}
 
 
-def time_bootstrap(torch, steps, warmup):
+def time_bootstrap(torch, steps, warmup, evalmod="cheb63"):
     """benchmark config 5 through the pyPhantom API: N = 2^16, the 2^15 slots
-    uniform in [-1, 1] (seeded), scale 2^40, chain bootstrap_coeff_bits()
-    (|Q| = 30: q0 60 | 13 x 40 | SlotToCoeff 3 x 50 | EvalMod 10 x 60 |
-    CoeffToSlot 3 x 60, then 6 special primes of 60 bits, dnum = 5), sparse
-    ternary secret h = 192 with the ModRaise under an h = 192 encapsulation
-    secret.  Times whole bootstraps (the ciphertext enters at the bottom of
-    the chain) with the keys and diagonals resident; reports the refreshed
-    precision -log2(max |decrypted - input|)."""
+    uniform in [-1, 1] (seeded), scale 2^40, sparse ternary secret h = 192
+    with the ModRaise under an h = 192 encapsulation secret, |Q| = 30 and 6
+    special primes (dnum = 5).  evalmod "cheb63": this build's pipeline on
+    bootstrap_coeff_bits() (q0 60 | 13 x 40 | SlotToCoeff 3 x 50 | EvalMod
+    10 x 60 | CoeffToSlot 3 x 60, special 60), the ciphertext entering at the
+    bottom of the chain.  evalmod "k28_r3": the reference's pipeline
+    (EvalRound with evalmod_k28_r3) on the reference engine's chain
+    ckks_engine_coeff_bits() (q_msg 58 | 14 x 40 | 3 x 58 | 9 x 58 | 3 x 29,
+    special 58), entering one level above the bottom, SlotToCoeff at user
+    scale 2^40.  Times whole bootstraps with the keys and diagonals resident;
+    reports the refreshed precision -log2(max |decrypted - input|)."""
     import math
 
     import numpy as np
 
     import pyPhantom as ph
 
+    ref = evalmod == "k28_r3"
+    bits = ph.ckks_engine_coeff_bits() if ref else ph.bootstrap_coeff_bits()
     p = ph.params(ph.scheme_type.ckks)
     p.set_poly_modulus_degree(N)
-    p.set_coeff_modulus(ph.create_coeff_modulus(N, ph.bootstrap_coeff_bits()))
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, bits))
     p.set_special_modulus_size(6)
     p.set_galois_elts(ph.bootstrap_required_galois_elts(16))
     ctx = ph.context(p)
     ph.set_seed(5)
     sk = ph.secret_key(ctx).generate_sparse(ctx, 192)
     enc = ph.ckks_encoder(ctx)
+    scale = 2.0 ** 40
     t0 = time.perf_counter()
-    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192)
+    if ref:
+        bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, eval_mod_levels=9, user_scale=scale)
+    else:
+        bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, evalmod="cheb63")
     torch.cuda.synchronize()
     t_key = time.perf_counter() - t0
     rng = np.random.default_rng(5)
     z = rng.uniform(-1, 1, enc.slot_count())
-    scale = 2.0 ** 40
-    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, scale, ctx.size_Q))
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, scale, ctx.size_Q - (1 if ref else 0)))
     for _ in range(warmup):
         out = ph.bootstrap(ctx, enc, ct, bk, scale)
     torch.cuda.synchronize()
@@ -281,10 +290,15 @@ def time_bootstrap(torch, steps, warmup):
     ms = e0.elapsed_time(e1) / steps
     got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, out)))
     err = float(np.max(np.abs(got - z)))
-    return {"ms": round(ms, 2), "wall_ms": round(wall_ms, 2), "precision_bits": round(-math.log2(err), 2),
-            "max_abs_err": err, "keygen_s": round(t_key, 1), "galois_keys": len(bk.glk.keys),
-            "levels_left": ctx.size_Ql(out.chain_index()) - 1,
-            "chain": "q0 60 | 13 x 40 | 3 x 50 | 10 x 60 | 3 x 60 + 6 x 60 special", "secret_h": 192}
+    chain = ("q_msg 58 | 14 x 40 | 3 x 58 | 9 x 58 | 3 x 29 + 6 x 58 special" if ref
+             else "q0 60 | 13 x 40 | 3 x 50 | 10 x 60 | 3 x 60 + 6 x 60 special")
+    r = {"ms": round(ms, 2), "wall_ms": round(wall_ms, 2), "precision_bits": round(-math.log2(err), 2),
+         "max_abs_err": err, "keygen_s": round(t_key, 1), "galois_keys": len(bk.glk.keys),
+         "levels_left": ctx.size_Ql(out.chain_index()) - 1, "evalmod": evalmod,
+         "evalmod_levels": bk.eval_mod_levels, "chain": chain, "secret_h": 192}
+    del bk
+    torch.cuda.empty_cache()
+    return r
 
 
 def measured_traffic():
@@ -391,6 +405,8 @@ def main():
         del batches
         r = time_bootstrap(torch, max(2, args.steps // 40), 1)
         log(f"bench: bootstrap mode, config 5: {r}")
+        r = time_bootstrap(torch, max(2, args.steps // 40), 1, "k28_r3")
+        log(f"bench: bootstrap mode, config 5 EvalRound: {r}")
         return
     if args.mode == "ntt-sweep":
         del batches
@@ -442,10 +458,12 @@ def main():
         log(f"bench: bsgs config4 {bsgs['ms']} ms, max abs err {bsgs['max_abs_err']:.2e}")
         torch.cuda.empty_cache()
 
-    boot = None
+    boot = boot_ref = None
     if not args.no_boot:
         boot = time_bootstrap(torch, 3, 1)
         log(f"bench: bootstrap config5 {boot['ms']} ms, {boot['precision_bits']} bits")
+        boot_ref = time_bootstrap(torch, 3, 1, "k28_r3")
+        log(f"bench: bootstrap config5 EvalRound {boot_ref['ms']} ms, {boot_ref['precision_bits']} bits")
         torch.cuda.empty_cache()
 
     cpu = cpu_all = None
@@ -486,6 +504,7 @@ def main():
         "hmult_relin_rescale": hm,
         "bsgs_matvec_config4": bsgs,
         "bootstrap_config5": boot,
+        "bootstrap_config5_evalround": boot_ref,
     }
     print(json.dumps(line), flush=True)
 

@@ -1368,22 +1368,24 @@ def bsgs_apply_giants_with_babies_complex(context: context, galois_key: galois_k
 # ---------------------------------------------------------------- bootstrapping
 # CKKS bootstrapping with the API of include/bootstrap.h / python/src/binding.cu
 # (create_bootstrap_key, bootstrap, bootstrap_required_galois_elts,
-# build_c2s_diagonals, ...), on the chain layout
-#     [q0 | user levels | SlotToCoeff x 3 | EvalMod x 10 | CoeffToSlot x 3] + special
-# (bootstrap_coeff_bits).  The pipeline follows the reference's order
-# (src/bootstrap.cu:1703-1800): ModRaise, CoeffToSlot, conjugate split into
-# real and imaginary tracks, the modular reduction on both, recombination,
-# SlotToCoeff.  The reduction is EvalMod (sin(2 pi x) / (2 pi) ~ x - round(x)
-# through a Chebyshev approximation of cos(2 pi (x - 1/4) / 2^r) and r
-# double-angle steps) where the reference runs the lapis EvalRound tables
-# (src/evalmod.cu); the secret is used as generated (sparse, so |I| < K), where
-# the reference switches to a sparse secret around ModRaise.  Parity is the
-# reference's own acceptance test: decoded slots within 1e-3
+# build_c2s_diagonals, ...).  Two pipelines share ModRaise (under a transient
+# sparse secret, so |I| < K), CoeffToSlot, the conjugate split into real and
+# imaginary tracks, recombination and SlotToCoeff:
+#   * "k28_r3" -- the reference's (src/bootstrap.cu:1703-1951) on its engine's
+#     chain (ckks_engine_coeff_bits): the message scaled up to q_msg, EvalRound
+#     K x - evalmod_k28_r3(x) on both tracks, then the raised ciphertext minus
+#     SlotToCoeff of the rounding part, with the reference's scale-down options;
+#   * "cheb63" -- this build's, on bootstrap_coeff_bits(): the message lifted to
+#     q0 / 2^12 only, EvalMod as sin(2 pi x) through a degree-63 Chebyshev
+#     approximation of cos(2 pi (x - 1/4) / 2^r) and r double-angle steps, and
+#     SlotToCoeff of the sine times 1 / (2 pi).
+# Parity is the reference's own acceptance test: decoded slots within 1e-3
 # (test/ckks_engine_test.cu:182).
 #
-# Scales are tracked exactly: diagonal plaintexts are encoded at the prime the
-# following rescale drops, and every constant at the scale that makes the sum
-# it joins line up, so no addition ever mixes scales.
+# In the "cheb63" pipeline scales are tracked exactly: diagonal plaintexts are
+# encoded at the prime the following rescale drops, and every constant at the
+# scale that makes the sum it joins line up, so no addition ever mixes scales.
+# The reference's EvalMod snaps scales instead, and its pipeline does the same.
 
 BOOT_K = 28            # |x| bound of EvalMod's input (|I| < K for the sparse secret)
 BOOT_R = 3             # double-angle steps
@@ -1400,14 +1402,32 @@ BOOT_LT_LEVELS = 3
 
 
 def bootstrap_coeff_bits(user_levels: int = 13, q0_bits: int = 60, user_bits: int = 40, s2c_bits: int = 50,
-                         evalmod_bits: int = 60, c2s_bits: int = 60, special: int = 6, special_bits: int = 60):
-    """Prime sizes of a bootstrappable chain, bottom to top, then the special
-    primes: q0 | user levels | SlotToCoeff x 3 | EvalMod x 10 | CoeffToSlot x 3.
-    CoeffToSlot's diagonals are encoded at the scale of the prime its rescale
-    drops and act on slots of size ~sum |I| (hundreds to thousands), so its
-    primes are the widest; SlotToCoeff acts on the small refreshed message."""
-    return ([q0_bits] + [user_bits] * user_levels + [s2c_bits] * BOOT_LT_LEVELS + [evalmod_bits] * BOOT_EVALMOD_LEVELS
+                         evalmod_bits: int = 60, c2s_bits: int = 60, special: int = 6, special_bits: int = 60,
+                         eval_mod_levels: int = BOOT_EVALMOD_LEVELS):
+    """Prime sizes of a bootstrappable chain for this build's EvalMod
+    (create_bootstrap_key(..., evalmod="cheb63")), bottom to top, then the
+    special primes: q0 | user levels | SlotToCoeff x 3 | EvalMod x 10 |
+    CoeffToSlot x 3.  CoeffToSlot's diagonals are encoded at the scale of the
+    prime its rescale drops and act on slots of size ~sum |I| (hundreds to
+    thousands), so its primes are the widest; SlotToCoeff acts on the small
+    refreshed message."""
+    return ([q0_bits] + [user_bits] * user_levels + [s2c_bits] * BOOT_LT_LEVELS + [evalmod_bits] * eval_mod_levels
             + [c2s_bits] * BOOT_LT_LEVELS + [special_bits] * special)
+
+
+def ckks_engine_coeff_bits(num_scale_levels: int = 14, num_special_primes: int = 6) -> list:
+    """The reference engine's bootstrappable chain (src/ckks_engine.cu:117-126,
+    its default CKKSEngineConfig: 14 scale levels, 6 special primes, |Q| = 30,
+    dnum = 5), bottom to top, then the special primes:
+        q_msg 58 | scale 40 x num_scale_levels | SlotToCoeff 58 x 3 |
+        EvalRound 58 x 9 | CoeffToSlot 29 x 3 | special 58 x num_special_primes.
+    The chain of create_bootstrap_key(..., eval_mod_levels=9) (evalmod "k28_r3")."""
+    if num_scale_levels < 2 or num_special_primes < 1:
+        raise ValueError("need at least 2 scale levels and 1 special prime")
+    if (16 + num_scale_levels) % num_special_primes:
+        raise ValueError("size_Q must be divisible by num_special_primes")
+    return ([58] + [40] * num_scale_levels + [58] * BOOT_LT_LEVELS + [58] * 9 + [29] * BOOT_LT_LEVELS
+            + [58] * num_special_primes)
 
 
 def _brv_index(x: int, bits: int) -> int:
@@ -1617,6 +1637,15 @@ class bootstrap_key:
         self.s2c_pts = []
         self.cheb = None
         self.K, self.r = BOOT_K, BOOT_R
+        # "k28_r3": the reference's pipeline (EvalRound with evalmod_k28_r3,
+        # then saved - SlotToCoeff(round)); "cheb63": this build's EvalMod
+        # (sin(2 pi x) by a degree-63 Chebyshev fit, SlotToCoeff of the sine)
+        self.evalmod = "cheb63"
+        self.eval_mod_levels = BOOT_EVALMOD_LEVELS
+        self.user_scale = 0.0
+        self.split_scale_down = False
+        self.s2c_start = 0   # chain index of SlotToCoeff's first layer
+        self.c2s_boost, self.s2c_boost = BOOT_C2S_BOOST, BOOT_S2C_BOOST
 
 
 class _LayerPlan:
@@ -1628,13 +1657,15 @@ class _LayerPlan:
         self.babies, self.giants, self.grid, self.scale, self.zero = babies, giants, grid, scale, zero
 
 
-def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1) -> _LayerPlan:
+def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1,
+                  encode_scale: float = 0.0) -> _LayerPlan:
     """Layer i's diagonals, each pre-rotated by minus its giant step, encoded
-    at `chain` with the scale of the prime the following rescale drops,
-    divided by scale_div (a power of two, so the scale stays exact)."""
+    at `chain` with the scale of the prime the following rescale drops (or
+    encode_scale when given), divided by scale_div (a power of two, so the
+    scale stays exact)."""
     n1, groups, span = lt.baby_giant(i)
     L = ctx.size_Ql(chain)
-    scale = float(ctx.moduli[L - 1]) / scale_div
+    scale = (float(encode_scale) if encode_scale > 0 else float(ctx.moduli[L - 1])) / scale_div
     babies = sorted({b for terms in groups.values() for b, _ in terms})
     giants = sorted(groups)
     zero = None
@@ -1653,37 +1684,58 @@ def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, 
     return _LayerPlan(babies, giants, grid, scale, zero)
 
 
+BOOT_EVALMODS = ("k28_r3", "cheb63")
+
+
 def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secret_key,
                          sparse_hamming_weight: int = 128, eval_mod_levels: int = 0, user_scale: float = 0.0,
-                         split_scale_down: bool = False, stages_per_layer=None, seed=None) -> bootstrap_key:
-    """create_bootstrap_key (src/bootstrap.cu:895-960, python/src/binding.cu:320-327).
-    The context must use the bootstrap_coeff_bits layout and carry
-    bootstrap_required_galois_elts.  The ModRaise runs under a transient
-    sparse secret of weight sparse_hamming_weight (|I| < K = 28 holds up to a
-    few hundred); the rotation and relinearization keys are the dense
-    secret's.  EvalMod here always takes BOOT_EVALMOD_LEVELS levels at the
-    ciphertext's own scale, so eval_mod_levels, user_scale and
-    split_scale_down must keep their defaults (or name that same layout): a
-    reference caller that relies on another layout gets NotImplementedError
-    instead of a silently different chain."""
-    if eval_mod_levels not in (0, BOOT_EVALMOD_LEVELS):
-        raise NotImplementedError(f"eval_mod_levels={eval_mod_levels}: this build's EvalMod takes "
-                                  f"{BOOT_EVALMOD_LEVELS} levels")
-    if user_scale != 0.0:
-        raise NotImplementedError("user_scale: this build bootstraps at the ciphertext's own scale")
-    if split_scale_down:
-        raise NotImplementedError("split_scale_down is not implemented by this build")
+                         split_scale_down: bool = False, stages_per_layer=None, seed=None,
+                         evalmod: str = "k28_r3") -> bootstrap_key:
+    """create_bootstrap_key (src/bootstrap.cu:895-980, python/src/binding.cu:320-327).
+    The context must carry bootstrap_required_galois_elts.  The ModRaise runs
+    under a transient sparse secret of weight sparse_hamming_weight; the
+    rotation and relinearization keys are the dense secret's.
+
+    evalmod "k28_r3" (default) is the reference's pipeline: CoeffToSlot on
+    chains 1 .. 3 (normalized by 1 / (2 K), K = 28, when eval_mod_levels > 0,
+    by 1 otherwise), SlotToCoeff from chain 4 + eval_mod_levels with its last
+    layer encoded at user_scale when user_scale > 0 and not split_scale_down.
+    eval_mod_levels = 0 is the reference's round-trip key (CoeffToSlot straight
+    into SlotToCoeff; bootstrap() then refuses it, as the reference does); a
+    full bootstrap needs at least 9 (evalmod_k28_r3), the chain of
+    ckks_engine_coeff_bits.
+
+    evalmod "cheb63" is this build's pipeline (bootstrap_coeff_bits chain):
+    EvalMod by a degree-63 Chebyshev fit over 10 levels; eval_mod_levels must
+    be 0 or 10, user_scale 0 and split_scale_down false (it returns the
+    message at the input scale)."""
+    if evalmod not in BOOT_EVALMODS:
+        raise ValueError(f"evalmod must be one of {BOOT_EVALMODS}")
+    if eval_mod_levels < 0:
+        raise ValueError("eval_mod_levels must be >= 0")
+    if evalmod == "cheb63":
+        if eval_mod_levels not in (0, BOOT_EVALMOD_LEVELS):
+            raise ValueError(f"evalmod 'cheb63' takes {BOOT_EVALMOD_LEVELS} levels")
+        if user_scale != 0.0 or split_scale_down:
+            raise ValueError("evalmod 'cheb63' bootstraps at the ciphertext's own scale "
+                             "(user_scale and split_scale_down do not apply)")
+        eval_mod_levels = BOOT_EVALMOD_LEVELS
+    if user_scale < 0.0:
+        raise ValueError("user_scale must be >= 0")
     ctx, enc = context, encoder
     log_n = ctx.N.bit_length() - 1
     stages = list(stages_per_layer or _default_stages(log_n))
-    need = 2 * len(stages) + BOOT_EVALMOD_LEVELS + 1
+    nl = len(stages)
+    need = 2 * nl + eval_mod_levels + 1
     if ctx.size_Q < need:
-        raise ValueError(f"bootstrapping needs at least {need} primes (bootstrap_coeff_bits)")
+        raise ValueError(f"bootstrapping needs at least {need} primes")
     missing = [e for e in bootstrap_required_galois_elts(log_n, stages) if e not in ctx.galois_elts]
     if missing:
         raise ValueError("the context's galois_elts lack bootstrap_required_galois_elts")
     rng = _rng(seed)
     bk = bootstrap_key()
+    bk.evalmod, bk.eval_mod_levels = evalmod, eval_mod_levels
+    bk.user_scale, bk.split_scale_down = float(user_scale), bool(split_scale_down)
     bk.small = _small_bootstrap_key(ctx, dense_sk, sparse_hamming_weight, rng)[0]
     bk.rlk = dense_sk.gen_relinkey(ctx, seed=rng)
     bk.glk = galois_key(ctx.galois_elts)
@@ -1691,18 +1743,28 @@ def create_bootstrap_key(context: context, encoder: ckks_encoder, dense_sk: secr
         bk.glk.keys[elt] = dense_sk._galois_key_for(ctx, elt, rng)
     bk.c2s = build_c2s_diagonals(log_n, stages)
     bk.s2c = build_s2c_diagonals(log_n, stages)
-    nl = len(stages)
-    # CoeffToSlot at chains 1 .. nl, with 1 / (2K) in its last layer;
-    # SlotToCoeff starts after EvalMod, with 1 / (2 pi) in its first layer.  The
-    # last layer of each takes the 2^BOOT_LT_BOOST the input carries back out.
-    bk.c2s_pts = [_encode_layer(ctx, enc, bk.c2s, i, 1 + i, 1 / (2 * BOOT_K) if i == nl - 1 else 1.0,
-                                1 << BOOT_C2S_BOOST if i == nl - 1 else 1)
+    # The transforms run 2^boost above their output scale (an exact integer
+    # multiple taken back out in their last layer's diagonals).  On narrow
+    # CoeffToSlot primes (the reference engine's 29-bit ones) the diagonals'
+    # rounding dominates instead, so no boost there.
+    c2s_prime_bits = ctx.moduli[ctx.size_Ql(1) - 1].bit_length()
+    bk.c2s_boost = BOOT_C2S_BOOST if c2s_prime_bits > 40 else 0
+    bk.s2c_boost = BOOT_S2C_BOOST
+    # CoeffToSlot at chains 1 .. nl with 1 / (2K) in its last layer (1 for the
+    # round-trip key); SlotToCoeff after EvalMod, with 1 / (2 pi) in its first
+    # layer for this build's sine (the reference's EvalRound needs none)
+    c2s_norm = 1 / (2 * BOOT_K) if eval_mod_levels > 0 else 1.0
+    bk.c2s_pts = [_encode_layer(ctx, enc, bk.c2s, i, 1 + i, c2s_norm if i == nl - 1 else 1.0,
+                                1 << bk.c2s_boost if i == nl - 1 else 1)
                   for i in range(nl)]
-    s2c0 = 1 + nl + BOOT_EVALMOD_LEVELS
-    bk.s2c_pts = [_encode_layer(ctx, enc, bk.s2c, i, s2c0 + i, 1 / (2 * np.pi) if i == 0 else 1.0,
-                                1 << BOOT_S2C_BOOST if i == nl - 1 else 1)
+    bk.s2c_start = 1 + nl + eval_mod_levels
+    s2c_first = 1 / (2 * np.pi) if evalmod == "cheb63" else 1.0
+    last_scale = bk.user_scale if (evalmod == "k28_r3" and not bk.split_scale_down) else 0.0
+    bk.s2c_pts = [_encode_layer(ctx, enc, bk.s2c, i, bk.s2c_start + i, s2c_first if i == 0 else 1.0,
+                                1 << bk.s2c_boost if i == nl - 1 else 1, last_scale if i == nl - 1 else 0.0)
                   for i in range(nl)]
-    bk.cheb = evalmod_chebyshev(BOOT_K, BOOT_R, BOOT_DEG)
+    if evalmod == "cheb63":
+        bk.cheb = evalmod_chebyshev(BOOT_K, BOOT_R, BOOT_DEG)
     return bk
 
 
@@ -1751,14 +1813,16 @@ def _transform(ctx, ct, lt, pts, glk, boost, last_rescale=True):
 
 def apply_c2s_inplace(context: context, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     """CoeffToSlot (src/bootstrap.cu apply_c2s_inplace): slots -> the packed
-    coefficients in bit-reversed order, times 1 / (2K), at ct's scale."""
-    return _transform(context, ct, bk.c2s, bk.c2s_pts, bk.glk, BOOT_C2S_BOOST)
+    coefficients in bit-reversed order, times 1 / (2K) (1 for a round-trip
+    key), at ct's scale."""
+    return _transform(context, ct, bk.c2s, bk.c2s_pts, bk.glk, bk.c2s_boost)
 
 
 def apply_s2c_inplace(context: context, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     """SlotToCoeff (src/bootstrap.cu apply_s2c_inplace): the inverse layout
-    change, times 1 / (2 pi), at ct's scale."""
-    return _transform(context, ct, bk.s2c, bk.s2c_pts, bk.glk, BOOT_S2C_BOOST)
+    change (times 1 / (2 pi) for the "cheb63" key), at ct's scale, or at
+    user_scale when the key bakes it into the last layer."""
+    return _transform(context, ct, bk.s2c, bk.s2c_pts, bk.glk, bk.s2c_boost)
 
 
 def mod_raise_inplace(context: context, ct: ciphertext, bk) -> ciphertext:
@@ -1877,6 +1941,293 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     return y
 
 
+# ---------------------------------------------------------------- the reference's EvalMod
+# evalmod_k7_r3 / evalmod_k16_r3 / evalmod_k28_r3 / evalmod_k28_r4
+# (include/evalmod.h, src/evalmod.cu): sin(2 pi K x) / (2 pi) for x in
+# [-1, 1] as a Chebyshev-basis polynomial for (2 pi)^(-1/2^R) cos(2 pi K x / 2^R
+# - pi / 2^(R+1)) followed by R double-angle steps y <- 2 y^2 - (2 pi)^(-2^(j-R)).
+# The operation order is the reference's: the Chebyshev basis by T_2n = 2 T_n^2
+# - 1 and T_(a+b) = 2 T_a T_b - T_(a-b) with the same level alignment, weighted
+# sums with one deferred rescale, the same Paterson-Stockmeyer factorings, and
+# the scale of every rescaled result set back to the input's ("snapped": the
+# dropped prime is taken to equal the scale).  A weighted sum of ciphertexts by
+# constants is one pfa_ct_lincomb with the integer weights round(c scale) -- the
+# residues of the reference's multiply_plain-by-constant then add sequence.
+#
+# The coefficient tables define the polynomials and are kept equal to the
+# reference's (src/evalmod.cu:25-47 K = 7, :57-77 K = 16, :90-120 K = 28).
+
+_K7_LOW = (-5.92365525763352552e-03, -1.05915002790352347e-01, 1.81872438169629558e-01,
+           -7.96115559593863209e-02, 6.18237166588616383e-01, 9.97204899504430670e-02,
+           -2.85567102345358925e-01, -3.02985739088491718e-02, 5.23393518416412837e-02)
+_K7_HIGH = (0.0, 3.49656797384041707e-03, -5.21322493828673197e-03, -2.75767647883437550e-04,
+            3.34517473917776004e-04, 1.47041114332627232e-05, -1.50752826718614230e-05,
+            -5.67939380614890243e-07)
+# degree 31, K = 16: entry 0 of each the constant, 1 .. 7 those of T_1 .. T_7
+_K16_Q_HIGH = (1.40933240904887619e-05, 1.50639230276274228e-06, -1.94594040092296340e-06,
+               -9.53210705782742233e-08, 1.13318833226784231e-07, 5.12709912705527410e-09,
+               -5.64857600334760771e-09, -2.37565221374504097e-10)
+_K16_Q_LOW = (3.59519354992413262e-02, 6.20731655651990660e-03, -1.25289184971230146e-02,
+              -9.32191173092421330e-04, 1.64251931763363971e-03, 1.07868728320514593e-04,
+              -1.68130129335233066e-04, -1.07079565087396969e-05)
+_K16_R_HIGH = (-1.03480520058724892e-01, 9.00051357854676909e-02, -8.54845145538975948e-01,
+               -1.80792080525974813e-01, 7.33614949409451600e-01, 9.95683206882135990e-02,
+               -2.78190804126826174e-01, -3.64211934038645019e-02)
+_K16_R_LOW = (1.22772867008426184e-01, -2.97084681220240107e-02, 4.22982423883966452e-01,
+              -7.97287003613950523e-02, -1.10422768440682217e-02, 1.05502625978328088e-01,
+              7.22752525999589279e-01, 2.62006578429296658e-02)
+# degree 49, K = 28: coefficient 0 the constant, 1 .. 7 those of T_1 .. T_7
+_K28_AUX = (-0.4674215360340989, -0.24807246365084598, -0.03360736343811264, 0.10485552200765141,
+            0.012171628025753911, -0.031034212401993305, -0.003985828764410408, 0.0)
+_K28_QUOT = ((-0.7500012154934053, 4.148627473785995e-06, 2.707983311367457e-07, -4.324538856989888e-07,
+              -2.648274421485692e-08, 3.9515438249932484e-08, 2.4720260690299275e-09, 0.0),
+             (-6.511205244110998e-09, -7.076428529570776e-10, 1.0183620860162692e-09, 0.0, 0.0, 0.0, 0.0, 4.0),
+             (0.007868944223231958, 0.0014193060148561195, -0.003081157124604844, -0.00025275745577540515,
+              0.0005030348400875631, 3.734766164626263e-05, -7.780382338014487e-05, 1.0))
+_K28_REM = ((-1.1324455480972702, -0.8116709016985189, -0.20294197180913795, 0.5290215620326779,
+             -0.32084902738708476, 0.43458317383580536, -0.06303880005650665, 0.0),
+            (0.23316927298939902, 0.12938749185636858, -0.3042902283756468, -0.008967445477730096,
+             -0.6955791340472846, -0.07562064123442451, 1.2510854562849574, 2.0),
+            (0.1429148264191405, 0.4544397978460022, -0.8401926425765848, -0.4292803758141986,
+             -1.495563076527614, 0.3580084476476745, 1.7971594278092713, 1.0))
+
+EVALMOD_K = {"k7_r3": 7, "k16_r3": 16, "k28_r3": 28, "k28_r4": 28}
+EVALMOD_R = {"k7_r3": 3, "k16_r3": 3, "k28_r3": 3, "k28_r4": 4}
+# levels consumed: basis (3) + the variant's products, then R double angles
+EVALMOD_LEVELS = {"k7_r3": 8, "k16_r3": 9, "k28_r3": 9, "k28_r4": 10}
+
+
+class _EvalModOps:
+    """The reference's EvalMod operations on ciphertexts (or, for the float64
+    model of the same polynomial, on arrays of slot values: ctx None)."""
+
+    def __init__(self, ctx, rk, target_scale: float):
+        self.ctx, self.rk, self.s = ctx, rk, float(target_scale)
+
+    def _chain(self, a):
+        return a.chain_index() if self.ctx else 0
+
+    def to(self, a, chain):  # align_to: drop to the deeper level
+        if self.ctx and a.chain_index() < chain:
+            return mod_switch_to(self.ctx, a, chain)
+        return a
+
+    def align(self, a, b):  # align_pair
+        c = max(self._chain(a), self._chain(b))
+        return self.to(a, c), self.to(b, c)
+
+    def lincomb(self, terms, bias: float = 0.0):
+        """sum c_i a_i + bias over ciphertexts at one level and scale; the
+        weights c_i are small integers (2, 1, -1) and bias a real constant."""
+        if not self.ctx:
+            return sum(c * a for a, c in terms) + bias
+        a0 = terms[0][0]
+        chain = a0.chain_index()
+        for a, _ in terms:
+            if a.chain_index() != chain or abs(a.scale() - a0.scale()) > 1e-9 * a0.scale():
+                raise ValueError("EvalMod operands differ in level or scale")
+        L = self.ctx.size_Ql(chain)
+        out = self.ctx._empty(2, L, self.ctx.N)
+        b = int(round(bias * a0.scale())) if bias else None
+        self.ctx.native.ct_lincomb(L, [a.data for a, _ in terms], [c for _, c in terms], out, b)
+        return a0._like(out)
+
+    def mul(self, a, b):  # multiply_and_relin, rescale_to_next, snap
+        if not self.ctx:
+            return a * b
+        r = multiply_and_relin_rescale(self.ctx, a, b, self.rk)
+        r.set_scale(self.s)
+        return r
+
+    def square_minus(self, a, scalar: float):  # 2 (a^2 + scalar): the reference adds, then doubles
+        sq = self.mul(a, a)
+        if not self.ctx:
+            return 2 * (sq + scalar)
+        L = self.ctx.size_Ql(sq.chain_index())
+        out = self.ctx._empty(2, L, self.ctx.N)
+        self.ctx.native.ct_lincomb(L, [sq.data], [2], out, 2 * int(round(scalar * sq.scale())))
+        return sq._like(out)
+
+    def weighted_sum(self, basis, coeffs):
+        """weighted_sum_chebyshev: coeffs[0] + sum_(i >= 1) coeffs[i] basis[i-1],
+        the products at the basis scale squared, one rescale, snap, then the
+        constant (src/evalmod.cu:266-319)."""
+        terms = [(basis[i - 1], coeffs[i]) for i in range(1, len(coeffs)) if abs(coeffs[i]) >= 1e-50]
+        if not terms:
+            raise ValueError("weighted_sum_chebyshev: all coefficients zero")
+        if not self.ctx:
+            acc = sum(c * t for t, c in terms)
+            return acc + coeffs[0] if abs(coeffs[0]) >= 1e-50 else acc
+        bs = basis[0].scale()
+        chain = basis[0].chain_index()
+        L = self.ctx.size_Ql(chain)
+        for t, _ in terms:
+            if t.chain_index() != chain:
+                raise ValueError("weighted_sum_chebyshev: basis levels differ")
+        out = self.ctx._empty(2, L, self.ctx.N)
+        ws = [int(round(c * bs)) for _, c in terms]
+        self.ctx.native.ct_lincomb(L, [t.data for t, _ in terms], ws, out)
+        acc = rescale_to_next(self.ctx, basis[0]._like(out, scale=bs * bs))
+        acc.set_scale(self.s)
+        if abs(coeffs[0]) >= 1e-50:
+            acc = self.lincomb([(acc, 1)], coeffs[0])
+        return acc
+
+
+def _chebyshev_basis(ops: _EvalModOps, ct, max_power: int) -> list:
+    """build_chebyshev_basis (src/evalmod.cu:206-264): T_1 .. T_max_power, the
+    lower powers aligned to each power of two and to the last."""
+    T = {1: ct}
+    for n in range(2, max_power + 1):
+        if n & (n - 1) == 0:
+            T[n] = ops.square_minus(T[n >> 1], -0.5)
+        else:
+            hp2 = 1 << (n.bit_length() - 1)
+            a, b = ops.align(T[hp2], T[n - hp2])
+            prod = ops.lincomb([(ops.mul(a, b), 2)])
+            prod, sp = ops.align(prod, T[2 * hp2 - n])
+            T[n] = ops.lincomb([(prod, 1), (sp, -1)])
+        if n & (n - 1) == 0 or n == max_power:
+            point = n >> 1 if n & (n - 1) == 0 else 1 << (n.bit_length() - 1)
+            target = ops._chain(T[n])
+            for p in range(point, 0, -1):
+                if p in T:
+                    T[p] = ops.to(T[p], target)
+    return [T[i] for i in range(1, max_power + 1)]
+
+
+def _sine_k7(ops: _EvalModOps, ct):
+    """sine_chebyshev_k7 (src/evalmod.cu:404-433): low + 2 T_8 high."""
+    baby = _chebyshev_basis(ops, ct, 8)
+    low = ops.weighted_sum(baby, _K7_LOW)
+    high = ops.weighted_sum(baby[:7], _K7_HIGH)
+    t8, high = ops.align(baby[7], high)
+    prod = ops.lincomb([(ops.mul(t8, high), 2)])
+    prod, low = ops.align(prod, low)
+    return ops.lincomb([(prod, 1), (low, 1)])
+
+
+def _sine_deg31(ops: _EvalModOps, ct, q_high, q_low, r_high, r_low):
+    """sine_chebyshev_deg31 (src/evalmod.cu:343-402): T_16 (T_8 Q_high + Q_low)
+    + T_8 R_high + R_low, the inner sums weighted_sum(T_1 .. T_7) of 8-entry
+    tables (entry 0 the constant, as weighted_sum_chebyshev reads them)."""
+    baby = _chebyshev_basis(ops, ct, 8)
+    t16 = ops.square_minus(baby[7], -0.5)
+    seven = baby[:7]
+    qh, ql, rh, rl = (ops.weighted_sum(seven, c) for c in (q_high, q_low, r_high, r_low))
+
+    def fma8(hi, lo):
+        t8, hi = ops.align(baby[7], hi)
+        p = ops.mul(t8, hi)
+        p, lo = ops.align(p, lo)
+        return ops.lincomb([(p, 1), (lo, 1)])
+
+    Q, R = fma8(qh, ql), fma8(rh, rl)
+    t16, Q = ops.align(t16, Q)
+    p = ops.mul(t16, Q)
+    p, R = ops.align(p, R)
+    return ops.lincomb([(p, 1), (R, 1)])
+
+
+def _sine_k28(ops: _EvalModOps, ct):
+    """sine_chebyshev_k28 (src/evalmod.cu:464-586): baby T_1 .. T_7, giants
+    T_14, T_28 and T_49 = 2 T_28 T_21 - T_7 with T_21 = 2 T_14 T_7 - T_7, then
+    (ws_aux + T_28)((T_14 + Q_0) Q_1 + Q_2) + (T_14 + R_0) R_1 + R_2 - T_49."""
+    baby = _chebyshev_basis(ops, ct, 7)
+    t7 = baby[6]
+    t14 = ops.square_minus(t7, -0.5)
+    t28 = ops.square_minus(t14, -0.5)
+    aux = ops.weighted_sum(baby, _K28_AUX)
+    qs = [ops.weighted_sum(baby, c) for c in _K28_QUOT]
+    rs = [ops.weighted_sum(baby, c) for c in _K28_REM]
+    a, b = ops.align(t14, t7)
+    t21 = ops.lincomb([(ops.mul(a, b), 2)])
+    t21 = ops.lincomb([(t21, 1), (ops.to(t7, ops._chain(t21)), -1)])
+    a, b = ops.align(t28, t21)
+    t49 = ops.lincomb([(ops.mul(a, b), 2)])
+    t49 = ops.lincomb([(t49, 1), (ops.to(t7, ops._chain(t49)), -1)])
+    aux, t28a = ops.align(aux, t28)
+    aux = ops.lincomb([(aux, 1), (t28a, 1)])
+
+    def ps(c):
+        p = ops.mul(ops.lincomb([(t14, 1), (c[0], 1)]), c[1])
+        return ops.lincomb([(p, 1), (ops.to(c[2], ops._chain(p)), 1)])
+
+    quotient, remainder = ps(qs), ps(rs)
+    res = ops.mul(aux, quotient)
+    res = ops.lincomb([(res, 1), (ops.to(remainder, ops._chain(res)), 1)])
+    return ops.lincomb([(res, 1), (ops.to(t49, ops._chain(res)), -1)])
+
+
+def _double_angle(ops: _EvalModOps, ct, R: int):
+    """apply_double_angle (src/evalmod.cu:592-605): y <- 2 y^2 - (2 pi)^(-2^(j-R)),
+    j = 1 .. R (the reference squares, rescales, doubles, then adds)."""
+    for j in range(1, R + 1):
+        scalar = -(2 * np.pi) ** (-(2.0 ** (j - R)))
+        sq = ops.mul(ct, ct)
+        if not ops.ctx:
+            ct = 2 * sq + scalar
+            continue
+        L = ops.ctx.size_Ql(sq.chain_index())
+        out = ops.ctx._empty(2, L, ops.ctx.N)
+        ops.ctx.native.ct_lincomb(L, [sq.data], [2], out, int(round(scalar * sq.scale())))
+        ct = sq._like(out)
+    return ct
+
+
+def _sine(ops: _EvalModOps, ct, variant: str):
+    if variant == "k7_r3":
+        return _sine_k7(ops, ct)
+    if variant == "k16_r3":
+        return _sine_deg31(ops, ct, _K16_Q_HIGH, _K16_Q_LOW, _K16_R_HIGH, _K16_R_LOW)
+    if variant in ("k28_r3", "k28_r4"):
+        return _sine_k28(ops, ct)
+    raise ValueError(f"unknown EvalMod variant {variant!r}")
+
+
+def _evalmod(context: context, ct: ciphertext, relin_keys: relin_key, variant: str) -> ciphertext:
+    if ct.size() != 2:
+        raise ValueError("EvalMod expects a size-2 ciphertext")
+    need = EVALMOD_LEVELS[variant]
+    if context.size_Ql(ct.chain_index()) <= need:
+        raise ValueError(f"EvalMod {variant} consumes {need} levels: the ciphertext has too few primes left")
+    ops = _EvalModOps(context, relin_keys, ct.scale())
+    return _double_angle(ops, _sine(ops, ct, variant), EVALMOD_R[variant])
+
+
+def evalmod_model(x, variant: str = "k28_r3"):
+    """The polynomial an EvalMod variant evaluates, applied to the real array x
+    in float64 with the same operation sequence (no encryption, no rounding
+    of the constants): the value the decrypted EvalMod output approximates,
+    itself an approximation of sin(2 pi K x) / (2 pi) on [-1, 1]."""
+    ops = _EvalModOps(None, None, 1.0)
+    x = np.asarray(x, dtype=np.float64)
+    return _double_angle(ops, _sine(ops, x, variant), EVALMOD_R[variant])
+
+
+def evalmod_k7_r3(context: context, encoder: ckks_encoder, ct: ciphertext, relin_keys: relin_key) -> ciphertext:
+    """evalmod_k7_r3 (include/evalmod.h:29): degree 15, 3 double angles, 8 levels."""
+    return _evalmod(context, ct, relin_keys, "k7_r3")
+
+
+def evalmod_k16_r3(context: context, encoder: ckks_encoder, ct: ciphertext, relin_keys: relin_key) -> ciphertext:
+    """evalmod_k16_r3 (include/evalmod.h:36): degree 31, 3 double angles, 9 levels."""
+    return _evalmod(context, ct, relin_keys, "k16_r3")
+
+
+def evalmod_k28_r3(context: context, encoder: ckks_encoder, ct: ciphertext, relin_keys: relin_key) -> ciphertext:
+    """evalmod_k28_r3 (include/evalmod.h:45): degree 49, 3 double angles, 9 levels."""
+    return _evalmod(context, ct, relin_keys, "k28_r3")
+
+
+def evalmod_k28_r4(context: context, encoder: ckks_encoder, ct: ciphertext, relin_keys: relin_key) -> ciphertext:
+    """evalmod_k28_r4 (include/evalmod.h:55): the K = 28 polynomial with a fourth
+    double angle, 10 levels.  As in the reference, the polynomial is tuned for
+    three steps, so the result is not sin(2 pi 28 x) / (2 pi) (the reference's
+    own test leaves this variant disabled, test/evalmod_test.cu:236-243)."""
+    return _evalmod(context, ct, relin_keys, "k28_r4")
+
+
 def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
     """ct * (sign i): the plaintext polynomial times sign X^(N/2), exact."""
     L = ctx.size_Ql(ct.chain_index())
@@ -1893,18 +2244,140 @@ def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
     return ct._like(out)
 
 
+def _times_int(ctx, ct: ciphertext, k: int) -> ciphertext:
+    """ct times the integer k (|k| < 2^63), residue by residue; scale unchanged
+    (the reference's multiply_uint_scalars_per_tower)."""
+    L = ctx.size_Ql(ct.chain_index())
+    out = ctx._empty(*ct.data.shape)
+    ctx.native.ct_lincomb(L, [ct.data], [int(k)], out)
+    return ct._like(out)
+
+
+def _scale_up_for_bootstrap(ctx, ct: ciphertext, current_scale: float) -> ciphertext:
+    """scale_up_for_bootstrap (src/bootstrap.cu:1435-1510): a ciphertext one
+    level above the bottom ([q_msg, q_scale]; fresher ones are switched down
+    first) times c0 = round(q_msg q_scale / current_scale), rescaled: scale
+    q_msg at the bottom.  At the bottom already: nothing if the scale is q_msg,
+    else times round(q_msg / current_scale)."""
+    from fractions import Fraction
+
+    bottom = ctx.size_Q
+    q_msg = ctx.moduli[0]
+    cs = Fraction(current_scale)
+    if ct.chain_index() == bottom:
+        if abs(current_scale / q_msg - 1.0) < 1e-6:
+            ct.set_scale(float(q_msg))
+            return ct
+        c0 = round(Fraction(q_msg) / cs)
+        if c0 == 0:
+            raise ValueError("scale_up_for_bootstrap: at bottom but ratio q_msg/current_scale rounds to 0")
+        out = _times_int(ctx, ct, c0)
+        out.set_scale(current_scale * c0)
+        return out
+    if ct.chain_index() < bottom - 1:
+        ct = mod_switch_to(ctx, ct, bottom - 1)
+    c0 = round(Fraction(q_msg * ctx.moduli[1]) / cs)
+    if not 0 < c0 < (1 << 63):
+        raise ValueError("scale_up_for_bootstrap: scale ratio out of range")
+    out = _times_int(ctx, ct, c0)
+    out.set_scale(current_scale * c0)
+    out = rescale_to_next(ctx, out)
+    out.set_scale(float(q_msg))
+    return out
+
+
+def _eval_round(ctx, ct: ciphertext, rk: relin_key) -> ciphertext:
+    """eval_round_k28_r3 (src/bootstrap.cu:1661-1680): K ct - evalmod_k28_r3(ct),
+    ~ the integer part, K = 28."""
+    kct = _times_int(ctx, ct, 28)
+    em = _evalmod(ctx, ct, rk, "k28_r3")
+    kct = mod_switch_to(ctx, kct, em.chain_index())
+    kct.set_scale(em.scale())
+    return sub(ctx, kct, em)
+
+
+def _bootstrap_evalround(ctx, ct: ciphertext, bk: bootstrap_key, user_scale: float,
+                         split_scale_down: bool) -> ciphertext:
+    """The reference's bootstrap (src/bootstrap.cu:1703-1951) on this build's
+    transforms: scale-up to q_msg, ModRaise (saved), CoeffToSlot, conjugate
+    split, EvalRound on both tracks, recombination, SlotToCoeff (the rounding
+    part qi), then saved brought to qi's level and exact scale by one integer
+    multiply and rescale, minus qi; with split_scale_down the small result is
+    then brought to user_scale by one more integer multiply and rescale."""
+    from fractions import Fraction
+
+    if bk.eval_mod_levels < EVALMOD_LEVELS["k28_r3"]:
+        raise RuntimeError("bootstrap: ct deeper than S2C start — eval_mod_levels mismatch")
+    if split_scale_down != bk.split_scale_down:
+        raise ValueError("split_scale_down differs from the bootstrap key's")
+    if user_scale <= 0.0:
+        raise ValueError("user_scale must be > 0")
+    q_msg = ctx.moduli[0]
+    ct = _scale_up_for_bootstrap(ctx, ct, user_scale)
+    saved = mod_raise_inplace(ctx, ct, bk.small)
+    saved.set_scale(float(q_msg))
+    # CoeffToSlot; its last rescale waits until the conjugate split is done
+    u = _transform(ctx, saved, bk.c2s, bk.c2s_pts, bk.glk, bk.c2s_boost, last_rescale=False)
+    conj = apply_galois(ctx, u, 2 * ctx.N - 1, bk.glk)
+    real = rescale_to_next(ctx, add(ctx, u, conj))
+    imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))
+    real = _eval_round(ctx, real, bk.rlk)
+    imag = _times_i(ctx, _eval_round(ctx, imag, bk.rlk), 1)
+    c = max(real.chain_index(), imag.chain_index())
+    real, imag = mod_switch_to(ctx, real, c), mod_switch_to(ctx, imag, c)
+    imag.set_scale(real.scale())
+    out = add(ctx, real, imag)
+    if out.chain_index() > bk.s2c_start:
+        raise RuntimeError("bootstrap: ct deeper than S2C start — eval_mod_levels mismatch")
+    out = mod_switch_to(ctx, out, bk.s2c_start)
+    out.set_scale(float(ctx.moduli[ctx.size_Ql(bk.s2c_start) - 1]))
+    out = _transform(ctx, out, bk.s2c, bk.s2c_pts, bk.glk, bk.s2c_boost)
+    qi_chain = out.chain_index()
+    if abs(out.scale() - saved.scale()) > 0.5:
+        saved = mod_switch_to(ctx, saved, qi_chain - 1)
+        q_back = ctx.moduli[ctx.size_Ql(qi_chain - 1) - 1]
+        D = round(Fraction(out.scale()) * q_back / q_msg)
+        if not 0 < D < (1 << 63):
+            raise ValueError("bootstrap: scale alignment factor out of range")
+        saved = _times_int(ctx, saved, D)
+        saved.set_scale(saved.scale() * D)
+        saved = rescale_to_next(ctx, saved)
+    saved = mod_switch_to(ctx, saved, qi_chain)
+    saved.set_scale(out.scale())
+    res = sub(ctx, saved, out)
+    if split_scale_down:
+        q_drop = ctx.moduli[ctx.size_Ql(qi_chain) - 1]
+        D2 = round(Fraction(q_drop) * Fraction(user_scale) / Fraction(res.scale()))
+        if not 0 < D2 < (1 << 63):
+            raise ValueError("bootstrap: scale-down factor out of range")
+        res = _times_int(ctx, res, D2)
+        res.set_scale(res.scale() * D2)
+        res = rescale_to_next(ctx, res)
+        res.set_scale(float(user_scale))
+    return res
+
+
 def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: bootstrap_key, user_scale: float,
               split_scale_down: bool = False) -> ciphertext:
-    """bootstrap (src/bootstrap.cu:1703-1951): a ciphertext at scale user_scale,
-    at any level (it is brought to the bottom of the chain first) -> the same
-    message at chain index 1 + 2 * (transform layers) + 10, at a scale within a
-    few parts in 10^12 of user_scale (the exact value is carried).
-    split_scale_down is not implemented (NotImplementedError when set)."""
-    ctx = context
-    if split_scale_down:
-        raise NotImplementedError("split_scale_down is not implemented by this build")
+    """bootstrap (src/bootstrap.cu:1703-1951, python/src/binding.cu:329-336).
+
+    With a "k28_r3" key: the reference's pipeline (_bootstrap_evalround); the
+    result is at chain 4 + eval_mod_levels + 3 (one more with
+    split_scale_down) at scale user_scale (the key's baked SlotToCoeff scale,
+    or the split's last step).  split_scale_down must match the key's.
+
+    With a "cheb63" key: a ciphertext at scale user_scale, at any level (it is
+    brought to the bottom of the chain first) -> the same message at chain
+    index 1 + 2 * (transform layers) + 10, at a scale within a few parts in
+    10^12 of user_scale (the exact value is carried); split_scale_down must be
+    false."""
     if ct.size() != 2:
         raise ValueError("bootstrap expects a size-2 ciphertext")
+    if bk.evalmod == "k28_r3":
+        return _bootstrap_evalround(context, ct, bk, user_scale, split_scale_down)
+    ctx = context
+    if split_scale_down:
+        raise ValueError("split_scale_down applies to the 'k28_r3' pipeline only")
     if abs(ct.scale() - user_scale) > 1e-6 * user_scale:
         raise ValueError("ciphertext scale differs from user_scale")
     q0 = ctx.moduli[0]
@@ -1921,7 +2394,7 @@ def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: boots
     raised.set_scale(float(q0))  # slots now read coefficients / q0 = I + m scale / q0
     # CoeffToSlot; its last rescale waits until the conjugate split is done,
     # so the conjugation's key-switching noise lands at the larger scale too
-    u = _transform(ctx, raised, bk.c2s, bk.c2s_pts, bk.glk, BOOT_C2S_BOOST, last_rescale=False)
+    u = _transform(ctx, raised, bk.c2s, bk.c2s_pts, bk.glk, bk.c2s_boost, last_rescale=False)
     conj = apply_galois(ctx, u, 2 * ctx.N - 1, bk.glk)
     real = rescale_to_next(ctx, add(ctx, u, conj))                     # Re(x) / K
     imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))  # Im(x) / K

@@ -129,3 +129,62 @@ def test_oracle_mod_raise_centres():
         q = mods[l]
         want = [(v - q0 if v >= q0 >> 1 else v) % q for v in coef]
         assert [int(v) for v in got[0, l]] == want
+
+
+@pytest.mark.parametrize("variant,bound", [("k7_r3", 1e-5), ("k16_r3", 2e-9), ("k28_r3", 1e-9)])
+def test_reference_evalmod_polynomials(variant, bound):
+    """The reference's EvalMod polynomials (src/evalmod.cu tables, PS
+    factorings and double angles), evaluated in float64 by the same operation
+    sequence pyPhantom runs on ciphertexts, approximate sin(2 pi K x) / (2 pi)
+    on [-1, 1] to the precision the reference states for them (K = 7 ~17 bits
+    observed 6e-6, K = 16 and K = 28 30+ bits; test/evalmod_test.cu:209-216).
+    A wrong table entry, basis recurrence or factoring step breaks this by
+    orders of magnitude."""
+    K = ph.EVALMOD_K[variant]
+    x = np.linspace(-1.0, 1.0, 200001)
+    err = np.abs(ph.evalmod_model(x, variant) - np.sin(2 * np.pi * K * x) / (2 * np.pi))
+    assert err.max() < bound, err.max()
+
+
+def test_reference_evalmod_k28_r4_is_not_the_sine():
+    """evalmod_k28_r4 runs the K = 28 polynomial tuned for three double angles
+    through four; the reference documents the result as off by ~0.1 and keeps
+    the variant out of its test (test/evalmod_test.cu:236-243).  The model
+    shows the same."""
+    x = np.linspace(-1.0, 1.0, 20001)
+    err = np.abs(ph.evalmod_model(x, "k28_r4") - np.sin(2 * np.pi * 28 * x) / (2 * np.pi))
+    assert err.max() > 0.1
+
+
+def test_evalmod_levels_match_the_reference():
+    """Levels consumed (include/evalmod.h): K = 7 eight, K = 16 and K = 28 nine,
+    K = 28 R = 4 ten -- the depth of the evaluation graph, counted here by
+    running the model on integers that count rescales."""
+    class Depth:
+        def __init__(self, d):
+            self.d = d
+
+        def __mul__(self, o):
+            return Depth(max(self.d, o.d) + 1) if isinstance(o, Depth) else self
+
+        __rmul__ = __mul__
+
+        def __add__(self, o):
+            return Depth(max(self.d, o.d)) if isinstance(o, Depth) else self
+
+        __radd__ = __add__
+
+        def __sub__(self, o):
+            return self + o
+
+        def __neg__(self):
+            return self
+
+    class Ops(ph._EvalModOps):
+        def weighted_sum(self, basis, coeffs):
+            return Depth(max(b.d for b in basis) + 1)
+
+    for v, levels in ph.EVALMOD_LEVELS.items():
+        ops = Ops(None, None, 1.0)
+        out = ph._double_angle(ops, ph._sine(ops, Depth(0), v), ph.EVALMOD_R[v])
+        assert out.d == levels, (v, out.d)

@@ -97,7 +97,7 @@ def boot_setup(logN, user_levels, special, seed=4):
     ctx = ph.context(p)
     sk = ph.secret_key(ctx, seed=seed)
     enc = ph.ckks_encoder(ctx)
-    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=seed + 1)
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=seed + 1, evalmod="cheb63")
     return ph, ctx, sk, enc, bk
 
 
@@ -144,17 +144,18 @@ def test_mod_raise_api_keeps_message(boot12):
     assert np.max(np.abs(got - z)) < 1e-6
 
 
-def test_bootstrap_options_not_implemented(boot12):
-    """The reference's EvalMod layout options that this build does not
-    implement are refused, not ignored (python/src/binding.cu:320-336)."""
+def test_bootstrap_cheb63_options(boot12):
+    """This build's EvalMod pipeline takes its own level count and returns the
+    message at the input scale: the reference's layout options are refused
+    for it, not ignored (python/src/binding.cu:320-336)."""
     ph, ctx, sk, enc, bk = boot12
-    with pytest.raises(NotImplementedError):
-        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, eval_mod_levels=9)
-    with pytest.raises(NotImplementedError):
-        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, user_scale=2.0 ** 40)
-    with pytest.raises(NotImplementedError):
-        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, split_scale_down=True)
+    with pytest.raises(ValueError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, eval_mod_levels=9, evalmod="cheb63")
+    with pytest.raises(ValueError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, user_scale=2.0 ** 40, evalmod="cheb63")
+    with pytest.raises(ValueError):
+        ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, split_scale_down=True, evalmod="cheb63")
     z = np.zeros(enc.slot_count())
     ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, 2.0 ** 40, ctx.size_Q), seed=1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):
         ph.bootstrap(ctx, enc, ct, bk, 2.0 ** 40, split_scale_down=True)

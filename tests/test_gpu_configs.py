@@ -98,7 +98,7 @@ def boot16(dev):
     assert ctx.size_Q == 30 and ctx.size_P == 6
     sk = ph.secret_key(ctx).generate_sparse(ctx, 192, seed=51)
     enc = ph.ckks_encoder(ctx)
-    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=52)
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, seed=52, evalmod="cheb63")
     yield ph, ctx, sk, enc, bk
     import torch
 
@@ -123,3 +123,49 @@ def test_bootstrap_config5_full_size(boot16):
     sq = ph.rescale_to_next(ctx, ph.multiply_and_relin(ctx, out, out, bk.rlk))
     got2 = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, sq)))
     assert np.max(np.abs(got2 - z * z)) < 1e-4
+
+
+@pytest.fixture(scope="module")
+def engine16(dev):
+    import pyPhantom as ph
+
+    N = 1 << 16
+    p = ph.params(ph.scheme_type.ckks)
+    p.set_poly_modulus_degree(N)
+    p.set_coeff_modulus(ph.create_coeff_modulus(N, ph.ckks_engine_coeff_bits()))
+    p.set_special_modulus_size(6)
+    p.set_galois_elts(ph.bootstrap_required_galois_elts(16))
+    ctx = ph.context(p)
+    assert ctx.size_Q == 30 and ctx.size_P == 6
+    sk = ph.secret_key(ctx).generate_sparse(ctx, 192, seed=81)
+    enc = ph.ckks_encoder(ctx)
+    bk = ph.create_bootstrap_key(ctx, enc, sk, sparse_hamming_weight=192, eval_mod_levels=9,
+                                 user_scale=2.0 ** 40, seed=82)
+    yield ph, ctx, sk, enc, bk
+    import torch
+
+    del bk
+    torch.cuda.empty_cache()
+
+
+def test_bootstrap_config5_evalround(engine16):
+    """Config 5 through the reference's pipeline: the engine's chain
+    (q_msg 58 | 14 x 40 | 3 x 58 | 9 x 58 | 3 x 29 + 6 x 58 special, |Q| = 30,
+    dnum = 5), EvalRound with evalmod_k28_r3, SlotToCoeff at user scale 2^40,
+    the ciphertext entering one level above the bottom as the engine
+    hands it over; the reference's bar is 1e-3 (test/ckks_engine_test.cu:182)."""
+    ph, ctx, sk, enc, bk = engine16
+    n = enc.slot_count()
+    z = np.random.default_rng(5).uniform(-1, 1, n)
+    scale = 2.0 ** 40
+    ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, scale, ctx.size_Q - 1), seed=83)
+    out = ph.bootstrap(ctx, enc, ct, bk, scale)
+    assert out.chain_index() == 16 and abs(out.scale() / scale - 1) < 1e-9
+    got = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, out)))
+    err = float(np.max(np.abs(got - z)))
+    bits = -math.log2(err)
+    print(f"config 5 EvalRound bootstrap: max |err| {err:.3e} ({bits:.2f} bits)")
+    assert err < 1e-3
+    sq = ph.rescale_to_next(ctx, ph.multiply_and_relin(ctx, out, out, bk.rlk))
+    got2 = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, sq)))
+    assert np.max(np.abs(got2 - z * z)) < 4e-3
