@@ -284,6 +284,13 @@ struct WsGeo {
     static constexpr int TW_RB = S2 * ROWS;                   // staged base factors [S2][ROWS]
     static constexpr int TW_SMALL = 1 << (S2 - 1);            // staged small table entries
     static constexpr int TW = TW_RB + TW_SMALL;               // ulonglong2 entries after the buffers
+    // FP64 policy: the item's rows' twiddle values, one row of 2^S2 - 1 per
+    // tile row (doubles after the staged entries), built once per item; up to
+    // N2 = 256, where the table (16 KiB) still leaves 3 workgroups per CU
+    static constexpr bool USE_TAB = S2 <= 8;
+    static constexpr int TAB_ROW = G::N2 - 1;
+    static constexpr int TAB = USE_TAB ? ROWS * TAB_ROW : 0;
+    static_assert(!USE_TAB || 2 * TW <= ROWS * G::ROW_PITCH, "staged entries must fit in one tile buffer");
     // accumulate role: outputs per thread, threads per output, elements per thread and output
     static constexpr int NO = HALF >= 128 ? 1 : 2;
     static constexpr int TPO = NO == 1 ? HALF / 2 : HALF;
@@ -304,7 +311,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <class A, int S1, int S2>
 __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables &t, const A &ar, uint32_t r,
                                              uint32_t prow, uint32_t k1, uint32_t rr, const ulonglong2 *tws,
-                                             typename A::T *b0, typename A::T *b1, uint32_t db, uint32_t de) {
+                                             const double *tab, typename A::T *b0, typename A::T *b1, uint32_t db,
+                                             uint32_t de) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
     using SB = Sub<S2>;
@@ -332,7 +340,11 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
         if (!own) {
             // the twiddle addresses are made opaque per digit: left loop-invariant,
             // the compiler would hold every twiddle live across the digit loop
-            if constexpr (A::kF64) {
+            if constexpr (A::kF64 && W::USE_TAB) {
+                uint32_t kr = rr;
+                asm volatile("" : "+v"(kr));
+                fwd_round_a_tab<S2>(x, ar, tab + kr * W::TAB_ROW);
+            } else if constexpr (A::kF64) {
                 uint32_t kr = rr;
                 asm volatile("" : "+v"(kr));
                 fwd_round_a_derived<S2, W::ROWS>(x, ar, tws, tws + W::TW_RB, kr);
@@ -348,7 +360,11 @@ __device__ __forceinline__ void ws_transform(const InnerRows &a, const NttTables
             wave_lds_sync();
 #pragma unroll
             for (int e = 0; e < SB::E; e++) x[e] = buf[rpad(F * SB::E + e)];
-            if constexpr (A::kF64) {
+            if constexpr (A::kF64 && W::USE_TAB) {
+                uint32_t kr = rr;
+                asm volatile("" : "+v"(kr));
+                fwd_round_b_tab<S2>(x, ar, tab + kr * W::TAB_ROW, F);
+            } else if constexpr (A::kF64) {
                 uint32_t kr = rr;
                 asm volatile("" : "+v"(kr));
                 fwd_round_b_derived<S2, W::ROWS>(x, ar, tws, tws + W::TW_RB, kr, F);
@@ -502,6 +518,7 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
                                         uint32_t de, uint64_t *part, double *lds, ulonglong2 *tws) {
     using G = Geo<S1, S2>;
     using W = WsGeo<S1, S2>;
+    double *tab = lds + W::LDS;
     const bool transform = threadIdx.x < W::HALF;
     const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
     const uint32_t per = a0.QlP * W::TILES;
@@ -524,15 +541,22 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
                 tws[i] = i < (uint32_t)W::TW_RB ? rb[(i / W::ROWS) * G::N1 + i % W::ROWS] : small[i - W::TW_RB];
         }
         __syncthreads();
+        // the rows' twiddle values once per item (they do not depend on the
+        // digit): each digit's rows pass then reads them instead of deriving
+        // them, which shortens the transform role, the longer of the two
+        if constexpr (W::USE_TAB) {
+            build_row_tab<S2, W::ROWS>(tab, ArithF64(q), tws, tws + W::TW_RB, threadIdx.x, W::THREADS);
+            __syncthreads();
+        }
         if (transform)
-            ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, b0, b1, db, de);
+            ws_transform<ArithF64, S1, S2>(a, t, ArithF64(q), r, prow, k1, rr, tws, tab, b0, b1, db, de);
         else
             ws_accumulate<ArithF64, S1, S2>(a, ArithF64(q), r, prow, tile, lds, lds + W::ROWS * G::ROW_PITCH, db, de,
                                              part);
     } else {
         uint64_t *b0 = reinterpret_cast<uint64_t *>(lds) + rr * G::ROW_PITCH, *b1 = b0 + W::ROWS * G::ROW_PITCH;
         if (transform)
-            ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, b0, b1, db, de);
+            ws_transform<ArithInt, S1, S2>(a, t, ArithInt(q), r, prow, k1, rr, tws, tab, b0, b1, db, de);
         else
             ws_accumulate<ArithInt, S1, S2>(a, ArithInt(q), r, prow, tile, reinterpret_cast<uint64_t *>(lds),
                                              reinterpret_cast<uint64_t *>(lds) + W::ROWS * G::ROW_PITCH, db, de, part);
@@ -606,9 +630,11 @@ template <int S1, int S2>
 __global__ void __launch_bounds__((WsGeo<S1, S2>::THREADS)) __attribute__((amdgpu_waves_per_eu(WsWaves<S1, S2>::MIN, 8)))
 k_inner_ws(InnerRows a0, NttTables t) {
     using W = WsGeo<S1, S2>;
-    __shared__ double lds[W::LDS + 2 * W::TW];
+    // with the table, the staged entries (needed only to build it) live in
+    // the second tile buffer, which the first digit leaves unused
+    __shared__ double lds[W::LDS + (W::USE_TAB ? 0 : 2 * W::TW) + W::TAB];
     __shared__ uint32_t s_last;
-    ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + W::LDS);
+    ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + (W::USE_TAB ? W::ROWS * Geo<S1, S2>::ROW_PITCH : W::LDS));
     const uint32_t total = a0.batch * a0.QlP * W::TILES;
     const uint32_t full = a0.full < total ? a0.full : total;
     for (uint32_t w0 = blockIdx.x; w0 < full; w0 += gridDim.x) {

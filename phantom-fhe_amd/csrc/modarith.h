@@ -208,8 +208,12 @@ struct ArithF64 {
     // w = base w * s w with |w| <= (1 + 1/16) q, and wq = w / q to within half
     // an ulp (one FMA correction step), which keeps the butterfly bound above
     // (growth B -> B + 1 + B/8 per stage, four stages from B = 1 reach 6.4 < 8).
-    __device__ __forceinline__ ulonglong2 twmul(ulonglong2 base, ulonglong2 s) const {
-        const double w = mulw(as_f(base.x), as_f(s.x), as_f(s.y));
+    __device__ __forceinline__ ulonglong2 twmul(ulonglong2 base, ulonglong2 s) const { return pair_of(twval(base, s)); }
+    // the twiddle value of twmul alone, and the pair twmul forms from it
+    __device__ __forceinline__ double twval(ulonglong2 base, ulonglong2 s) const {
+        return mulw(as_f(base.x), as_f(s.x), as_f(s.y));
+    }
+    __device__ __forceinline__ ulonglong2 pair_of(double w) const {
         double wq = w * qinv;
         const double e = __fma_rn(-wq, q, w);
         wq = __fma_rn(e, qinv, wq);

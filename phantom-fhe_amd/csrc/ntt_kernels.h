@@ -203,6 +203,61 @@ __device__ __forceinline__ void fwd_round_b_derived(double (&x)[Sub<S>::E], cons
     }
 }
 
+// Forward rounds with the twiddle values read from a per-row table instead of
+// derived: tab[(2^g - 1) + j] holds the value rows_tw derives for stage g,
+// index j < 2^g (2^S - 1 entries per row; see build_row_tab); the pair is
+// completed by pair_of, so the butterflies see the derived twiddles exactly.
+template <int S>
+__device__ __forceinline__ void fwd_round_a_tab(double (&x)[Sub<S>::E], const ArithF64 &ar, const double *tab) {
+    constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
+#pragma unroll
+    for (int g = 0; g < LE; g++) {
+        const int d = E >> (g + 1);
+        ulonglong2 w[1 << (LE - 1)];
+#pragma unroll
+        for (int i = 0; i < (1 << g); i++) w[i] = ar.pair_of(tab[(1 << g) - 1 + i]);
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            if (e & d) continue;
+            ar.ct(x[e], x[e + d], w[e >> (LE - g)]);
+        }
+    }
+}
+
+template <int S>
+__device__ __forceinline__ void fwd_round_b_tab(double (&x)[Sub<S>::E], const ArithF64 &ar, const double *tab,
+                                                uint32_t F) {
+    constexpr int LE = Sub<S>::LE, E = Sub<S>::E;
+#pragma unroll
+    for (int g = LE; g < S; g++) {
+        const int d = 1 << (S - 1 - g);
+        const uint32_t jb = F << (LE - S + g);
+        ulonglong2 w[1 << (LE - 1)];
+#pragma unroll
+        for (int i = 0; i < (1 << (g + LE - S)); i++) w[i] = ar.pair_of(tab[(1 << g) - 1 + jb + i]);
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            if (e & d) continue;
+            ar.ct(x[e], x[e + d], w[e >> (S - g)]);
+        }
+    }
+}
+
+// Fills tab[row][(2^g - 1) + j] (rows of 2^S - 1 doubles) for rows 0 .. R-1 of
+// a tile with the twiddle values rows_tw derives from the staged base factors
+// rb[g * R + row] and small table, threads `tid` of `nthreads` sharing the work.
+template <int S, int R>
+__device__ __forceinline__ void build_row_tab(double *tab, const ArithF64 &ar, const ulonglong2 *rb,
+                                              const ulonglong2 *small, uint32_t tid, uint32_t nthreads) {
+    constexpr uint32_t PER = (1u << S) - 1;
+    for (uint32_t e = tid; e < R * PER; e += nthreads) {
+        const uint32_t row = e / PER, idx = e % PER;
+        const uint32_t g = 31 - __builtin_clz(idx + 1), j = idx + 1 - (1u << g);
+        const ulonglong2 B = rb[g * R + row];
+        tab[e] = j == 0 ? ArithF64::as_f(B.x) : ar.twval(B, small[j]);
+    }
+}
+
 // inverse, stages g = S-1 .. LE on u = F' E + e
 template <int S, int N1>
 __device__ __forceinline__ void inv_round_a_derived(double (&x)[Sub<S>::E], const ArithF64 &ar,
