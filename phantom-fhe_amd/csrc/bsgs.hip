@@ -102,6 +102,53 @@ __device__ __forceinline__ Pair MacArgs::span(uint32_t d, uint32_t j, uint32_t t
     return Pair{(lo & 0xffffffffull) | ((uint64_t)(hi & 0xffu) << 32), (lo >> 32) | ((uint64_t)(hi >> 8) << 32)};
 }
 
+// giants per accumulation work item
+constexpr uint32_t kGB = 8;
+
+// Where an item's plaintext spans come from (uniform per item: a limb is
+// packed or not, the set tiled or a pointer list).
+enum SpanSrc { kSrcList = 0, kSrcTiled = 1, kSrcPacked = 2 };
+
+// The kGB plaintext spans one baby step of an item multiplies (giants g0 ..
+// g0 + kGB - 1; past the set's last giant, a repeat of the block's first,
+// whose products are never stored).  All loads are issued before any value is
+// used and none sits under a branch, so each wave keeps kGB loads in flight:
+// with one load waited for at a time, an item reads 640 B per wave round trip
+// and the accumulation ran at 2.8 TB/s.
+template <int SRC>
+__device__ __forceinline__ void load_spans(const MacArgs &a, uint32_t g0, uint32_t K, uint32_t b, uint32_t j,
+                                           uint32_t tile, Pair (&xv)[kGB]) {
+    if constexpr (SRC == kSrcList) {
+#pragma unroll
+        for (uint32_t k = 0; k < kGB; k++) xv[k] = a.span((g0 + (k < K ? k : 0)) * a.M + b, j, tile);
+    } else {
+        const size_t base = (size_t)tile * ((size_t)a.G * a.M) * kSpan + kPer * threadIdx.x;
+        const uint8_t *r = a.tiled + a.lay.off[j];
+        if constexpr (SRC == kSrcTiled) {
+#pragma unroll
+            for (uint32_t k = 0; k < kGB; k++) {
+                const size_t d = (size_t)(g0 + (k < K ? k : 0)) * a.M + b;
+                xv[k] = ld_pair_stream(reinterpret_cast<const uint64_t *>(r) + base + d * kSpan);
+            }
+        } else {
+            const uint64_t *lo = reinterpret_cast<const uint64_t *>(r);
+            const uint16_t *hi = reinterpret_cast<const uint16_t *>(r + (size_t)a.G * a.M * a.N * 4);
+            uint64_t l[kGB];
+            uint32_t h[kGB];
+#pragma unroll
+            for (uint32_t k = 0; k < kGB; k++) {
+                const size_t i = base + (size_t)((g0 + (k < K ? k : 0)) * a.M + b) * kSpan;
+                l[k] = __builtin_nontemporal_load(lo + i / 2);
+                h[k] = __builtin_nontemporal_load(hi + i / 2);
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kGB; k++)
+                xv[k] = Pair{(l[k] & 0xffffffffull) | ((uint64_t)(h[k] & 0xffu) << 32),
+                             (l[k] >> 32) | ((uint64_t)(h[k] >> 8) << 32)};
+        }
+    }
+}
+
 // A work item is (limb j, kSpan consecutive residues, block of up to kGB
 // giants).  Baby b's residues are loaded once per item (kPer adjacent ones per
 // thread and poly) and multiplied into every giant of the block, so the
@@ -115,7 +162,90 @@ __device__ __forceinline__ Pair MacArgs::span(uint32_t d, uint32_t j, uint32_t t
 // FP64 policy: each product is within 0.875 q (|x y / q| < q < 2^50), so four
 // of them on top of a reduced sum stay below 4 q < 2^53; integer policy: each
 // product reduced (Barrett) and summed modulo q.
-constexpr uint32_t kGB = 8;
+template <int SRC, bool F64>
+__device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t tile, uint32_t g0, uint32_t K,
+                                         uint64_t q, const ulonglong2 *ratio) {
+    const size_t off0 = (size_t)j * a.N + tile * kSpan + kPer * threadIdx.x;
+    const size_t off1 = off0 + (size_t)a.Ql * a.N;
+    if constexpr (F64) {
+        const ArithF64 ar(q);
+        double acc0[kGB][kPer], acc1[kGB][kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+            for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0.0;
+        for (uint32_t b = 0; b < a.M; b++) {
+            const uint64_t *c = a.baby(b);
+            const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
+            Pair xv[kGB];
+            load_spans<SRC>(a, g0, K, b, j, tile, xv);
+            double y0[kPer], y1[kPer], y0q[kPer], y1q[kPer];
+#pragma unroll
+            for (int e = 0; e < kPer; e++) {
+                y0[e] = ar.load(c0[e]);
+                y1[e] = ar.load(c1[e]);
+                y0q[e] = y0[e] * ar.qinv;
+                y1q[e] = y1[e] * ar.qinv;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    const double x = ar.load(xv[k][e]);
+                    acc0[k][e] += ar.mulw(x, y0[e], y0q[e]);
+                    acc1[k][e] += ar.mulw(x, y1[e], y1q[e]);
+                }
+            if ((b & 3u) == 3u) {
+#pragma unroll
+                for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                    for (int e = 0; e < kPer; e++) {
+                        ar.reduce(acc0[k][e]);
+                        ar.reduce(acc1[k][e]);
+                    }
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kGB; k++) {
+            if (k < K) {
+                uint64_t *o = a.out[g0 + k];
+                st_pair_stream(o + off0, Pair{ar.store(acc0[k][0]), ar.store(acc0[k][1])});
+                st_pair_stream(o + off1, Pair{ar.store(acc1[k][0]), ar.store(acc1[k][1])});
+            }
+        }
+    } else {
+        ulonglong2 r = ratio[j];
+        r.x = wave_uniform(r.x);
+        r.y = wave_uniform(r.y);
+        uint64_t acc0[kGB][kPer], acc1[kGB][kPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+            for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0;
+        for (uint32_t b = 0; b < a.M; b++) {
+            const uint64_t *c = a.baby(b);
+            const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
+            Pair xv[kGB];
+            load_spans<SRC>(a, g0, K, b, j, tile, xv);
+#pragma unroll
+            for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    const uint64_t x = xv[k][e];
+                    acc0[k][e] = add_mod(acc0[k][e], barrett128(U128{x * c0[e], mulhi64(x, c0[e])}, q, r.x, r.y), q);
+                    acc1[k][e] = add_mod(acc1[k][e], barrett128(U128{x * c1[e], mulhi64(x, c1[e])}, q, r.x, r.y), q);
+                }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kGB; k++) {
+            if (k < K) {
+                uint64_t *o = a.out[g0 + k];
+                st_pair_stream(o + off0, Pair{acc0[k][0], acc0[k][1]});
+                st_pair_stream(o + off1, Pair{acc1[k][0], acc1[k][1]});
+            }
+        }
+    }
+}
 
 __global__ void __launch_bounds__(kThreads)
 k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
@@ -128,98 +258,25 @@ k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
         if (!grouped_item(w, groups, GB, grp, gb)) continue;
         gb += a.gb_begin;
         const uint32_t j = grp / T, tile = grp % T;
-        const size_t off0 = (size_t)j * a.N + tile * kSpan + kPer * threadIdx.x;
-        const size_t off1 = off0 + (size_t)a.Ql * a.N;
         const uint64_t q = wave_uniform(mod[j]);
         const uint32_t g0 = gb * kGB;
         const uint32_t K = a.G - g0 < kGB ? a.G - g0 : kGB;  // giants in this block
-        if (q < kF64PrimeBound) {
-            const ArithF64 ar(q);
-            double acc0[kGB][kPer], acc1[kGB][kPer];
-#pragma unroll
-            for (uint32_t k = 0; k < kGB; k++)
-#pragma unroll
-                for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0.0;
-            for (uint32_t b = 0; b < a.M; b++) {
-                const uint64_t *c = a.baby(b);
-                double y0[kPer], y1[kPer], y0q[kPer], y1q[kPer];
-                const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
-#pragma unroll
-                for (int e = 0; e < kPer; e++) {
-                    y0[e] = ar.load(c0[e]);
-                    y1[e] = ar.load(c1[e]);
-                    y0q[e] = y0[e] * ar.qinv;
-                    y1q[e] = y1[e] * ar.qinv;
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < kGB; k++) {
-                    if (k < K) {
-                        const Pair xv = a.span((g0 + k) * a.M + b, j, tile);
-#pragma unroll
-                        for (int e = 0; e < kPer; e++) {
-                            const double x = ar.load(xv[e]);
-                            acc0[k][e] += ar.mulw(x, y0[e], y0q[e]);
-                            acc1[k][e] += ar.mulw(x, y1[e], y1q[e]);
-                        }
-                    }
-                }
-                if ((b & 3u) == 3u) {
-#pragma unroll
-                    for (uint32_t k = 0; k < kGB; k++)
-#pragma unroll
-                        for (int e = 0; e < kPer; e++) {
-                            ar.reduce(acc0[k][e]);
-                            ar.reduce(acc1[k][e]);
-                        }
-                }
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < kGB; k++) {
-                if (k < K) {
-                    uint64_t *o = a.out[g0 + k];
-                    st_pair_stream(o + off0, Pair{ar.store(acc0[k][0]), ar.store(acc0[k][1])});
-                    st_pair_stream(o + off1, Pair{ar.store(acc1[k][0]), ar.store(acc1[k][1])});
-                }
-            }
+        const bool f64 = q < kF64PrimeBound;
+        if (!a.tiled) {
+            if (f64)
+                mac_item<kSrcList, true>(a, j, tile, g0, K, q, ratio);
+            else
+                mac_item<kSrcList, false>(a, j, tile, g0, K, q, ratio);
+        } else if ((a.lay.packed >> j) & 1u) {
+            if (f64)
+                mac_item<kSrcPacked, true>(a, j, tile, g0, K, q, ratio);
+            else
+                mac_item<kSrcPacked, false>(a, j, tile, g0, K, q, ratio);
         } else {
-            ulonglong2 r = ratio[j];
-            r.x = wave_uniform(r.x);
-            r.y = wave_uniform(r.y);
-            uint64_t acc0[kGB][kPer], acc1[kGB][kPer];
-#pragma unroll
-            for (uint32_t k = 0; k < kGB; k++)
-#pragma unroll
-                for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0;
-            for (uint32_t b = 0; b < a.M; b++) {
-                const uint64_t *c = a.baby(b);
-                uint64_t y0[kPer], y1[kPer];
-                const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
-#pragma unroll
-                for (int e = 0; e < kPer; e++) {
-                    y0[e] = c0[e];
-                    y1[e] = c1[e];
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < kGB; k++) {
-                    if (k < K) {
-                        const Pair xv = a.span((g0 + k) * a.M + b, j, tile);
-#pragma unroll
-                        for (int e = 0; e < kPer; e++) {
-                            const uint64_t x = xv[e];
-                            acc0[k][e] = add_mod(acc0[k][e], barrett128(U128{x * y0[e], mulhi64(x, y0[e])}, q, r.x, r.y), q);
-                            acc1[k][e] = add_mod(acc1[k][e], barrett128(U128{x * y1[e], mulhi64(x, y1[e])}, q, r.x, r.y), q);
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < kGB; k++) {
-                if (k < K) {
-                    uint64_t *o = a.out[g0 + k];
-                    st_pair_stream(o + off0, Pair{acc0[k][0], acc0[k][1]});
-                    st_pair_stream(o + off1, Pair{acc1[k][0], acc1[k][1]});
-                }
-            }
+            if (f64)
+                mac_item<kSrcTiled, true>(a, j, tile, g0, K, q, ratio);
+            else
+                mac_item<kSrcTiled, false>(a, j, tile, g0, K, q, ratio);
         }
     }
 }
