@@ -725,47 +725,56 @@ __device__ __forceinline__ void epi_item(const EpiRows &a, const NttTables &t, c
     if (bp) bp += (size_t)(m >> 1) * a.base_stride + (size_t)j * G::N + rowoff;
     const ulonglong2 f = a.f[j];
     uint64_t *op = a.out + lo;
-    if (a.f1) {
-        const ulonglong2 f1 = a.f1[j];
+    // The c and base values of a group of EG elements are requested before the
+    // group's first store: the output may alias the base, so loads interleaved
+    // with the stores would each be waited for in turn (one load in flight per
+    // wave).  Each thread reads and writes only its own positions, so this is
+    // safe; groups of 8 keep the registers those values take in bounds.
+    constexpr int EG = SB::E < 8 ? SB::E : 8;
+    const ulonglong2 f1 = a.f1 ? a.f1[j] : ulonglong2{0, 0};
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) {
+    for (int e0 = 0; e0 < SB::E; e0 += EG) {
+        uint64_t cv[EG], bv[EG];
+#pragma unroll
+        for (int i = 0; i < EG; i++) cv[i] = ld_stream(&cp[SB::T * (e0 + i)]);
+#pragma unroll
+        for (int i = 0; i < EG; i++) bv[i] = bp ? ld_stream(&bp[SB::T * (e0 + i)]) : 0;
+#pragma unroll
+        for (int i = 0; i < EG; i++) {
+            const int e = e0 + i;
             uint64_t v;
-            if constexpr (A::kF64) {
+            if (a.f1) {
+                if constexpr (A::kF64) {
+                    ar.reduce(x[e]);
+                    double d = ar.load(cv[i]);
+                    ar.mul(d, f1);
+                    d += ar.load(bv[i]) - x[e];
+                    ar.mul(d, f);
+                    v = ar.store(d);
+                } else {
+                    const uint64_t cf = shoup(cv[i], f1.x, f1.y, ar.q);
+                    const uint64_t d = sub_mod(add_mod(cf, bv[i], ar.q), ar.store(x[e]), ar.q);
+                    v = shoup(d, f.x, f.y, ar.q);
+                }
+            } else if constexpr (A::kF64) {
                 ar.reduce(x[e]);
-                double d = ar.load(ld_stream(&cp[SB::T * e]));
-                ar.mul(d, f1);
-                d += ar.load(ld_stream(&bp[SB::T * e])) - x[e];
+                double d = ar.load(cv[i]) - x[e];
                 ar.mul(d, f);
                 v = ar.store(d);
+                if (bp) v = add_mod(v, bv[i], (uint64_t)ar.q);
             } else {
-                const uint64_t cf = shoup(ld_stream(&cp[SB::T * e]), f1.x, f1.y, ar.q);
-                const uint64_t d = sub_mod(add_mod(cf, ld_stream(&bp[SB::T * e]), ar.q), ar.store(x[e]), ar.q);
+                const uint64_t d = sub_mod(cv[i], ar.store(x[e]), ar.q);
                 v = shoup(d, f.x, f.y, ar.q);
+                if (bp) v = add_mod(v, bv[i], ar.q);
             }
             st_stream(&op[SB::T * e], v);
         }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < SB::E; e++) {
-        uint64_t v;
-        if constexpr (A::kF64) {
-            ar.reduce(x[e]);
-            double d = ar.load(ld_stream(&cp[SB::T * e])) - x[e];
-            ar.mul(d, f);
-            v = ar.store(d);
-            if (bp) v = add_mod(v, ld_stream(&bp[SB::T * e]), (uint64_t)ar.q);
-        } else {
-            const uint64_t d = sub_mod(ld_stream(&cp[SB::T * e]), ar.store(x[e]), ar.q);
-            v = shoup(d, f.x, f.y, ar.q);
-            if (bp) v = add_mod(v, ld_stream(&bp[SB::T * e]), ar.q);
-        }
-        st_stream(&op[SB::T * e], v);
     }
 }
 
 template <int S1, int S2>
-__global__ void __launch_bounds__((FGeo<S1, S2>::THREADS)) k_epi_rows(EpiRows a, NttTables t) {
+__global__ void __launch_bounds__((FGeo<S1, S2>::THREADS))
+k_epi_rows(EpiRows a, NttTables t) {
     using G = Geo<S1, S2>;
     using FG = FGeo<S1, S2>;
     __shared__ double lds[FG::LDS];
