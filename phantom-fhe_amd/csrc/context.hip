@@ -9,6 +9,7 @@
 #include <mutex>
 
 #include "internal.h"
+#include "modarith.h"
 
 namespace pfa {
 
@@ -246,6 +247,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     // resident count it assumes (tests use it to split small shapes).
     if (const char *w = std::getenv("PFA_WS_SLOTS")) c.ws_slots = (uint32_t)std::max(0, std::atoi(w));
     if (const char *w = std::getenv("PFA_WS_MAX_CHUNKS")) c.ws_max_chunks = (uint32_t)std::max(0, std::atoi(w));
+    if (const char *w = std::getenv("PFA_WS_NO_ORDER")) c.ws_no_order = std::atoi(w) != 0;
     // Single-launch NTT (N = 2^16, opt-in with PFA_NTT_FLOW=1): built for the
     // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition,
     // checked here by a probe kernel.  The other variables tune it (workgroups
@@ -365,6 +367,13 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             }
             lv.mdr_scale = c.upload(ms);
             lv.mdr_glast = c.upload(gl);
+        }
+        {
+            std::vector<uint32_t> order, tail;
+            for (uint32_t r = 0; r < QlP; ++r)
+                (moduli[c.qlp_row(Ql, r)] < kF64PrimeBound ? order : tail).push_back(r);
+            order.insert(order.end(), tail.begin(), tail.end());
+            lv.ws_order = c.upload(order);
         }
     }
 }

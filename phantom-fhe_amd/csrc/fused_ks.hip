@@ -239,7 +239,13 @@ struct InnerRows {
     uint64_t *partial = nullptr;
     uint32_t *counter = nullptr;
     uint32_t *dev_err = nullptr, *host_err = nullptr;
+    // target of item group i: order[i] (null: i).  Items of integer-policy
+    // targets take ~1.5-2.25x as long as FP64 ones; ordered last, they are the
+    // first to be split when items are left over after whole rounds.
+    const uint32_t *order = nullptr;
 };
+
+__device__ __forceinline__ uint32_t ws_target(const InnerRows &a, uint32_t i) { return a.order ? a.order[i] : i; }
 
 // Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
 // (already in NTT form) or the columns-pass output to transform.
@@ -527,7 +533,7 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
     a.inter += mi * a0.inter_bstride;
     a.c2 += mi * a0.c2_bstride;
     a.cx += mi * a0.cx_bstride;
-    const uint32_t r = w / W::TILES, tile = w % W::TILES;
+    const uint32_t r = ws_target(a, w / W::TILES), tile = w % W::TILES;
     const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
     const uint64_t q = wave_uniform(t.mod[prow]);
     const uint32_t k1 = tile * W::ROWS + rr;
@@ -576,7 +582,7 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
     const uint32_t mi = w0 / per, w = w0 % per;
     InnerRows a = a0;
     a.cx += mi * a0.cx_bstride;
-    const uint32_t r = w / W::TILES, tile = w % W::TILES;
+    const uint32_t r = ws_target(a, w / W::TILES), tile = w % W::TILES;
     const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
     const uint64_t q = wave_uniform(t.mod[prow]);
     const size_t rowoff = (size_t)(tile * W::ROWS + rr) * G::N2 + F;
@@ -944,6 +950,7 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.inter_bstride = IN;
     r.c2_bstride = c2_stride;
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
+    if (batch == 1 && !c.ws_no_order) r.order = lv.ws_order;
     if (fold) {
         require(batch == 1 && fold->base0 && fold->base1 && Ql >= 2, "bad ModDown + rescale fold");
         r.fold_r = Ql - 1;

@@ -83,6 +83,9 @@ struct Level {
     // [p_i^-1]_{q_l} for i < alpha (plain residues)
     ulonglong2 *mdr_scale = nullptr;
     uint64_t *mdr_glast = nullptr;
+    // key-switch inner product: the QlP targets with the FP64-policy primes
+    // first (in order), then the integer-policy ones
+    uint32_t *ws_order = nullptr;
 };
 
 // Device workspace of one (host thread, stream): chunks grown on demand and
@@ -128,6 +131,7 @@ struct Ctx {
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
     uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)
     uint32_t ws_max_chunks = 0;      // most digit chunks of a split inner-product item (0: beta)
+    bool ws_no_order = false;        // inner product in plain target order (PFA_WS_NO_ORDER)
     // single-launch NTT (ntt_kernels.h, opt-in): needs a device that deals
     // workgroups to 8 XCDs round-robin; used for batches of at least
     // flow_min_jobs limbs at N = 2^16
