@@ -30,10 +30,13 @@ struct PtrList {
     P *const *table;
     P *base;
     uint64_t stride;  // elements
-    __device__ __forceinline__ P *operator[](size_t i) const { return table ? table[i] : base + i * stride; }
+    // entry i (a wave-uniform index): table entries are read with scalar
+    // loads, which do not queue behind the vector loads in flight
+    __device__ __forceinline__ P *operator[](size_t i) const {
+        return table ? reinterpret_cast<P *>(ld_const(reinterpret_cast<const uint64_t *>(table + i)))
+                     : base + i * stride;
+    }
 };
-
-constexpr uint32_t kInlineBabies = 64;
 
 // Residues per span of the tiled plaintext layout (and per accumulation work item).
 constexpr uint32_t kSpan = 512;
@@ -81,13 +84,10 @@ struct MacArgs {
     const uint8_t *tiled;        // or the same set in the tiled layout (pfa_bsgs_tile_plaintexts)
     TiledLayout lay;
     PtrList<uint64_t> out;       // [G] ciphertexts, [2][Ql][N] each
-    const uint64_t *const *baby_table;          // [M] ciphertexts [2][Ql][N], when M > kInlineBabies
-    const uint64_t *baby_inline[kInlineBabies];  // the same, by value, when M <= kInlineBabies
+    PtrList<const uint64_t> babies;  // [M] ciphertexts, [2][Ql][N] each
     uint32_t M, G, Ql, N;
     uint32_t gb_begin, gb_end;  // giant blocks [gb_begin, gb_end) of kGB giants this launch covers
-    __device__ __forceinline__ const uint64_t *baby(uint32_t b) const {
-        return baby_table ? baby_table[b] : baby_inline[b];
-    }
+    __device__ __forceinline__ const uint64_t *baby(uint32_t b) const { return babies[b]; }
     // this thread's kPer residues of span `tile` of limb j of plaintext d
     __device__ __forceinline__ Pair span(uint32_t d, uint32_t j, uint32_t tile) const;
 };
@@ -149,6 +149,17 @@ __device__ __forceinline__ void load_spans(const MacArgs &a, uint32_t g0, uint32
     }
 }
 
+// One baby step's loads: the kGB plaintext spans and baby b's residues of both polys.
+template <int SRC>
+__device__ __forceinline__ void load_step(const MacArgs &a, uint32_t g0, uint32_t K, uint32_t b, uint32_t j,
+                                          uint32_t tile, size_t off0, size_t off1, Pair (&xv)[kGB], Pair &c0,
+                                          Pair &c1) {
+    const uint64_t *c = a.baby(b);
+    c0 = ld_pair(c + off0);
+    c1 = ld_pair(c + off1);
+    load_spans<SRC>(a, g0, K, b, j, tile, xv);
+}
+
 // A work item is (limb j, kSpan consecutive residues, block of up to kGB
 // giants).  Baby b's residues are loaded once per item (kPer adjacent ones per
 // thread and poly) and multiplied into every giant of the block, so the
@@ -174,11 +185,8 @@ __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t 
         for (uint32_t k = 0; k < kGB; k++)
 #pragma unroll
             for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0.0;
-        for (uint32_t b = 0; b < a.M; b++) {
-            const uint64_t *c = a.baby(b);
-            const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
-            Pair xv[kGB];
-            load_spans<SRC>(a, g0, K, b, j, tile, xv);
+        // baby step b: the kGB spans times baby b's residues of both polys
+        auto step = [&](const Pair (&xv)[kGB], Pair c0, Pair c1, uint32_t b) {
             double y0[kPer], y1[kPer], y0q[kPer], y1q[kPer];
 #pragma unroll
             for (int e = 0; e < kPer; e++) {
@@ -204,6 +212,21 @@ __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t 
                         ar.reduce(acc1[k][e]);
                     }
             }
+        };
+        // Two register sets: the next step's loads are requested before this
+        // step's products, so they are in flight while it computes.  Indices
+        // past the last step repeat it (no load under a branch).
+        Pair xa[kGB], xb[kGB], a0, a1, b0, b1;
+        load_step<SRC>(a, g0, K, 0, j, tile, off0, off1, xa, a0, a1);
+        for (uint32_t b = 0; b < a.M; b += 2) {
+            load_step<SRC>(a, g0, K, b + 1 < a.M ? b + 1 : b, j, tile, off0, off1, xb, b0, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            step(xa, a0, a1, b);
+            __builtin_amdgcn_sched_barrier(0);
+            load_step<SRC>(a, g0, K, b + 2 < a.M ? b + 2 : a.M - 1, j, tile, off0, off1, xa, a0, a1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 1 < a.M) step(xb, b0, b1, b + 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (uint32_t k = 0; k < kGB; k++) {
@@ -247,7 +270,7 @@ __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t 
     }
 }
 
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
 k_bsgs_mac(MacArgs a, const uint64_t *mod, const ulonglong2 *ratio) {
     const uint32_t T = a.N / kSpan;               // spans per limb
     const uint32_t GB = a.gb_end - a.gb_begin;    // giant blocks of this launch
@@ -407,12 +430,12 @@ MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, c
         upload_async(c, t, out, G * sizeof(void *), s);
         a.out = PtrList<uint64_t>{t, nullptr, 0};
     }
-    if (M <= kInlineBabies) {
-        for (size_t i = 0; i < M; i++) a.baby_inline[i] = babies[i];
+    if (progression((const void *const *)babies, M, st)) {
+        a.babies = PtrList<const uint64_t>{nullptr, babies[0], st};
     } else {
         const uint64_t **t = sc.alloc<const uint64_t *>(M);
         upload_async(c, t, babies, M * sizeof(void *), s);
-        a.baby_table = t;
+        a.babies = PtrList<const uint64_t>{t, nullptr, 0};
     }
     return a;
 }
