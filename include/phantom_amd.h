@@ -167,6 +167,23 @@ int pfa_rescale_noalloc(const pfa_context *ctx, size_t chain_index, const uint64
 int pfa_multiply_relin_rescale(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
                                const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream);
 
+/* multiply_and_relin_inplace (src/evaluate.cu:1061-1104) over `count`
+ * independent pairs with one relinearization key, in one set of launches:
+ * a, b, out [count][2][|Ql|][N]; member i's residues equal pfa_multiply_and_relin
+ * of a[i], b[i].  out may equal a or b but not overlap them otherwise. */
+int pfa_multiply_and_relin_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *a,
+                                 const uint64_t *b, const uint64_t *rlk, size_t key_dnum, uint64_t *out,
+                                 void *stream);
+
+/* pfa_multiply_relin_rescale (multiply_and_relin_inplace then
+ * rescale_to_next_inplace, src/evaluate.cu:1061-1104, :1582-1602) over `count`
+ * independent pairs with one key: a, b [count][2][|Ql|][N] -> out
+ * [count][2][|Ql|-1][N], member i equal to pfa_multiply_relin_rescale of a[i],
+ * b[i].  out must not overlap a or b; |Ql| >= 2. */
+int pfa_multiply_relin_rescale_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *a,
+                                     const uint64_t *b, const uint64_t *rlk, size_t key_dnum, uint64_t *out,
+                                     void *stream);
+
 /* relinearize_inplace then rescale_to_next_inplace (src/evaluate.cu:1342-1374,
  * :1582-1602) as one call: ct3 [3][|Ql|][N] -> out [2][|Ql|-1][N], bit-identical to
  * pfa_relinearize followed by pfa_rescale.  out must not alias ct3. */

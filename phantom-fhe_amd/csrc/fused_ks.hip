@@ -229,6 +229,7 @@ struct InnerRows {
     // fold_f = [P^-1]_q as an integer Shoup pair; ~0u = no folding
     uint32_t fold_r = ~0u;
     const uint64_t *fold_base0 = nullptr, *fold_base1 = nullptr;
+    uint64_t fold_bstride = 0;  // member i's bases at + i fold_bstride
     const ulonglong2 *fold_f = nullptr;
     // Items from `full` on are split by digit range (see k_inner_ws): rem
     // items of kch chunks each; chunk c of item full + j writes its canonical
@@ -533,6 +534,13 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
     a.inter += mi * a0.inter_bstride;
     a.c2 += mi * a0.c2_bstride;
     a.cx += mi * a0.cx_bstride;
+    {
+        // member mi's fold bases (stride 0 without a batched fold); the offset
+        // is made explicitly wave-uniform for the compiler
+        const uint64_t fo = wave_uniform((uint64_t)mi * a0.fold_bstride);
+        a.fold_base0 += fo;
+        a.fold_base1 += fo;
+    }
     const uint32_t r = ws_target(a, w / W::TILES), tile = w % W::TILES;
     const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
     const uint64_t q = wave_uniform(t.mod[prow]);
@@ -582,6 +590,13 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
     const uint32_t mi = w0 / per, w = w0 % per;
     InnerRows a = a0;
     a.cx += mi * a0.cx_bstride;
+    {
+        // member mi's fold bases (stride 0 without a batched fold); the offset
+        // is made explicitly wave-uniform for the compiler
+        const uint64_t fo = wave_uniform((uint64_t)mi * a0.fold_bstride);
+        a.fold_base0 += fo;
+        a.fold_base1 += fo;
+    }
     const uint32_t r = ws_target(a, w / W::TILES), tile = w % W::TILES;
     const uint32_t prow = r < a.Ql ? r : a.Q + (r - a.Ql);
     const uint64_t q = wave_uniform(t.mod[prow]);
@@ -952,10 +967,11 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
     if (batch == 1 && !c.ws_no_order) r.order = lv.ws_order;
     if (fold) {
-        require(batch == 1 && fold->base0 && fold->base1 && Ql >= 2, "bad ModDown + rescale fold");
+        require(fold->base0 && fold->base1 && Ql >= 2 && (batch == 1 || fold->stride), "bad ModDown + rescale fold");
         r.fold_r = Ql - 1;
         r.fold_base0 = fold->base0;
         r.fold_base1 = fold->base1;
+        r.fold_bstride = fold->stride;
         r.fold_f = c.pinv + (Ql - 1);
     }
     PFA_FUSED_DISPATCH(launch_inner, r);
@@ -969,21 +985,23 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
 // which is ModDown's (cx - NTT(delta)) P^-1 + base followed by the rescale's
 // (c - NTT(t mod q_j)) q_l^-1 with the two NTTs merged by linearity.
 void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, const uint64_t *base0,
-                           const uint64_t *base1, uint64_t *out, hipStream_t s) {
+                           const uint64_t *base1, uint64_t *out, hipStream_t s, uint32_t count,
+                           uint64_t base_stride) {
     const Level &lv = c.level(chain);
-    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha, J = Ql - 1;
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha, J = Ql - 1, M = 2 * count;
     require(Ql >= 2, "cannot rescale at the last level");
+    require(count >= 1 && (count == 1 || base_stride), "bad ModDown + rescale batch");
     Scratch sc(c, s);
-    uint64_t *x = sc.alloc((size_t)2 * (alpha + 1) * c.N);
-    uint64_t *inter = sc.alloc((size_t)2 * J * c.N);
-    NttLaunch inv{cx + (size_t)(Ql - 1) * c.N, x, (uint64_t)QlP * c.N, (uint64_t)(alpha + 1) * c.N, 2, alpha + 1};
+    uint64_t *x = sc.alloc((size_t)M * (alpha + 1) * c.N);
+    uint64_t *inter = sc.alloc((size_t)M * J * c.N);
+    NttLaunch inv{cx + (size_t)(Ql - 1) * c.N, x, (uint64_t)QlP * c.N, (uint64_t)(alpha + 1) * c.N, M, alpha + 1};
     inv.start = Ql - 1;
     inv.split = 1;
     inv.split_base = c.Q;
     inv.scale = lv.mdr_scale;
     ntt_inverse(c, inv, s);
-    hipLaunchKernelGGL(k_mdr_last, dim3((2 * c.N + 255) / 256), dim3(256), 0, s, x, lv.mdr_glast, c.mod, c.ratio,
-                       Ql - 1, alpha, c.N, 2u);
+    hipLaunchKernelGGL(k_mdr_last, dim3((M * c.N + 255) / 256), dim3(256), 0, s, x, lv.mdr_glast, c.mod, c.ratio,
+                       Ql - 1, alpha, c.N, M);
     PFA_HIP(hipGetLastError());
     BconvCols b{};
     b.in = x;
@@ -991,7 +1009,7 @@ void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, con
     b.bc = c.mdr_bc;
     b.in_gstride = (uint64_t)(alpha + 1) * c.N;
     b.out_gstride = (uint64_t)J * c.N;
-    b.groups = 2;
+    b.groups = M;
     b.J = J;
     b.n_in = alpha + 1;
     b.n_in_last = alpha + 1;
@@ -1004,7 +1022,8 @@ void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, con
     b.bc_gstride = 0;
     b.bc_istride = c.Q;
     PFA_FUSED_DISPATCH(launch_bconv, b);
-    EpiRows e{inter, cx, base0, base1, out, lv.rescale_inv_p, (uint64_t)QlP * c.N, 2, J};
+    EpiRows e{inter, cx, base0, base1, out, lv.rescale_inv_p, (uint64_t)QlP * c.N, M, J};
+    e.base_stride = base_stride;
     e.f1 = c.pinv_p;
     PFA_FUSED_DISPATCH(launch_epi, e);
 }

@@ -257,18 +257,23 @@ bool xcd_round_robin(const Ctx &c);
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp then the inner product with key.
 // With batch > 1, member i reads c2 + i c2_stride and writes cx + i cx_stride
 // (default 2 QlP N), all with the same key.
-// With fold (batch 1), limb Ql - 1 of output k is written as
-// fold->base_k[Ql - 1] + cx_k[Ql - 1] [P^-1]: the input fused_moddown_rescale expects.
+// With fold, limb Ql - 1 of output k of member i is written as
+// (fold->base_k + i stride)[Ql - 1] + cx_k[Ql - 1] [P^-1]: the input
+// fused_moddown_rescale expects.
 struct KsFold {
     const uint64_t *base0 = nullptr, *base1 = nullptr;
+    uint64_t stride = 0;
 };
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
                        hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0,
                        const KsFold *fold = nullptr);
 // cx [2][QlP][N] from fused_modup_inner with a fold over base -> out [2][Ql-1][N]
 // = rescale(base + ModDown(cx)), bit-identical to fused_moddown then fused_rescale.
+// With count > 1: cx [count][2][QlP][N], member i's bases at + i base_stride,
+// out [count][2][Ql-1][N].
 void fused_moddown_rescale(const Ctx &c, uint32_t chain, const uint64_t *cx, const uint64_t *base0,
-                           const uint64_t *base1, uint64_t *out, hipStream_t s);
+                           const uint64_t *base1, uint64_t *out, hipStream_t s, uint32_t count = 1,
+                           uint64_t base_stride = 0);
 // cx [M][QlP][N] -> out [M][Ql][N] = base + ModDown(cx): poly 2i + k adds
 // base_k + i base_stride; the bases may alias out's polys or be null.
 void fused_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, uint64_t *out,

@@ -70,12 +70,20 @@ k_from_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t st
 // (primes below 2^50: exact FP64 products; |a b / q| < q < 2^50 keeps
 // fl(a fl(b/q)) within 3/8 of the true quotient, so each product is within
 // 0.875 q and a sum of two stays far below 2^53)
+// Member z = blockIdx.z of a batch reads a, b at + z in_stride and writes
+// d0, d1 at + z d_stride, d2 at + z d2_stride.
 __global__ void __launch_bounds__(kThreads)
 k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint64_t *d2, const uint64_t *mod,
-         const ulonglong2 *ratio, uint32_t Ql, uint32_t N) {
+         const ulonglong2 *ratio, uint32_t Ql, uint32_t N, uint64_t in_stride, uint64_t d_stride,
+         uint64_t d2_stride) {
     const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     const uint64_t q = mod[l];
-    const size_t i = (size_t)l * N + n, LN = (size_t)Ql * N;
+    const size_t LN = (size_t)Ql * N, i = (size_t)l * N + n;
+    a += blockIdx.z * in_stride;
+    b += blockIdx.z * in_stride;
+    d0 += blockIdx.z * d_stride;
+    d1 += blockIdx.z * d_stride;
+    d2 += blockIdx.z * d2_stride;
     const uint64_t a0 = ld_stream(&a[i]), a1 = ld_stream(&a[LN + i]), b0 = ld_stream(&b[i]), b1 = ld_stream(&b[LN + i]);
     if (q < kF64PrimeBound) {
         const ArithF64 ar(q);
@@ -250,40 +258,50 @@ void op_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, ui
     fused_moddown(c, chain, cx, M, out, base.p[0], M > 1 ? base.p[1] : nullptr, s);
 }
 
-// out[k] = base_k + KS(c2)_k for k = 0, 1 (out [2][Ql][N]; bases may alias out or be null)
+// out[k] = base_k + KS(c2)_k for k = 0, 1 (out [2][Ql][N]; bases may alias out or be null).
+// With count > 1, member i switches c2 + i c2_stride into out + i 2 Ql N with
+// bases + i base_stride (the same key).
 void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum, uint64_t *out,
-                  Bases base, hipStream_t s) {
+                  Bases base, hipStream_t s, uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
     Scratch sc(c, s);
-    uint64_t *cx = sc.alloc((size_t)2 * (lv.Ql + c.P) * c.N);
-    fused_modup_inner(c, chain, c2, key, cx, s);
-    fused_moddown(c, chain, cx, 2, out, base.p[0], base.p[1], s);
+    const uint64_t cxs = (uint64_t)2 * (lv.Ql + c.P) * c.N;
+    uint64_t *cx = sc.alloc((size_t)count * cxs);
+    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs);
+    fused_moddown(c, chain, cx, 2 * count, out, base.p[0], base.p[1], s, base_stride);
 }
 
 // out [2][Ql-1][N] = rescale(base + KS(c2)): bit-identical to op_keyswitch
-// followed by op_rescale, without forming the key-switched ciphertext
+// followed by op_rescale, without forming the key-switched ciphertext.  With
+// count > 1, member i: c2 + i c2_stride, bases + i base_stride, out + i 2 (Ql-1) N.
 void op_keyswitch_rescale(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum,
-                          const uint64_t *base0, const uint64_t *base1, uint64_t *out, hipStream_t s) {
+                          const uint64_t *base0, const uint64_t *base1, uint64_t *out, hipStream_t s,
+                          uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
     require(lv.Ql >= 2, "cannot rescale at the last level");
     Scratch sc(c, s);
-    uint64_t *cx = sc.alloc((size_t)2 * (lv.Ql + c.P) * c.N);
-    const KsFold fold{base0, base1};
-    fused_modup_inner(c, chain, c2, key, cx, s, 1, 0, 0, &fold);
-    fused_moddown_rescale(c, chain, cx, base0, base1, out, s);
+    const uint64_t cxs = (uint64_t)2 * (lv.Ql + c.P) * c.N;
+    uint64_t *cx = sc.alloc((size_t)count * cxs);
+    const KsFold fold{base0, base1, base_stride};
+    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs, &fold);
+    fused_moddown_rescale(c, chain, cx, base0, base1, out, s, count, base_stride);
 }
 
+// count independent products: member i reads a, b at + i in_stride and writes
+// d0, d1 at + i d_stride, d2 at + i d2_stride
 void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1,
-               uint64_t *d2, hipStream_t s) {
+               uint64_t *d2, hipStream_t s, uint32_t count = 1, uint64_t in_stride = 0, uint64_t d_stride = 0,
+               uint64_t d2_stride = 0) {
     check_chain(c, chain);
     const uint32_t Ql = c.size_Ql(chain);
-    hipLaunchKernelGGL(k_tensor, grid(c, Ql), dim3(kThreads), 0, s, a, b, d0, d1, d2, c.mod, c.ratio, Ql, c.N);
+    hipLaunchKernelGGL(k_tensor, grid(c, Ql, count), dim3(kThreads), 0, s, a, b, d0, d1, d2, c.mod, c.ratio, Ql, c.N,
+                       in_stride, d_stride, d2_stride);
     PFA_HIP(hipGetLastError());
 }
 
@@ -392,6 +410,49 @@ int pfa_multiply_relin_rescale(const pfa_context *ctx, size_t chain_index, const
         uint64_t *d = sc.alloc(3 * LN);
         op_tensor(c, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s);
         op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s);
+    });
+}
+
+int pfa_multiply_and_relin_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *a,
+                                 const uint64_t *b, const uint64_t *rlk, size_t key_dnum, uint64_t *out,
+                                 void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && b && out && rlk, "null argument");
+        require(count >= 1 && count <= 4096, "count out of range");
+        check_chain(c, chain_index);
+        const hipStream_t s = as_stream(stream);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
+        require(out + count * 2 * LN <= a || out >= a + count * 2 * LN || out == a, "output overlaps an input");
+        require(out + count * 2 * LN <= b || out >= b + count * 2 * LN || out == b, "output overlaps an input");
+        Scratch sc(c, s);
+        uint64_t *c2 = sc.alloc(count * LN);
+        // d0, d1 into out (the key switch adds to them in place), d2 of member i to c2 + i LN
+        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2, s, (uint32_t)count, 2 * LN, 2 * LN, LN);
+        op_keyswitch(c, (uint32_t)chain_index, c2, rlk, key_dnum, out, Bases{{out, out + LN}}, s, (uint32_t)count,
+                     LN, 2 * LN);
+    });
+}
+
+int pfa_multiply_relin_rescale_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *a,
+                                     const uint64_t *b, const uint64_t *rlk, size_t key_dnum, uint64_t *out,
+                                     void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(a && b && out && rlk, "null argument");
+        require(count >= 1 && count <= 4096, "count out of range");
+        check_chain(c, chain_index);
+        require(c.size_Ql((uint32_t)chain_index) >= 2, "cannot rescale at the last level");
+        const hipStream_t s = as_stream(stream);
+        const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N, ON = LN - c.N;
+        require(out + count * 2 * ON <= a || out >= a + count * 2 * LN, "output overlaps an input");
+        require(out + count * 2 * ON <= b || out >= b + count * 2 * LN, "output overlaps an input");
+        Scratch sc(c, s);
+        // member i: d0, d1, d2 at d + i 3 LN
+        uint64_t *d = sc.alloc(count * 3 * LN);
+        op_tensor(c, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s, (uint32_t)count, 2 * LN, 3 * LN, 3 * LN);
+        op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s, (uint32_t)count,
+                             3 * LN, 3 * LN);
     });
 }
 

@@ -47,6 +47,8 @@ SIGNATURES = {
     "pfa_rescale_noalloc": (_i32, [_vp, _sz, _vp, _sz, _vp, _vp]),
     "pfa_multiply_relin_rescale": (_i32, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
     "pfa_relinearize_rescale": (_i32, [_vp, _sz, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_multiply_and_relin_batch": (_i32, [_vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "pfa_multiply_relin_rescale_batch": (_i32, [_vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp]),
     "pfa_galois_elt_from_step": (_i32, [_i32, _u64, C.POINTER(C.c_uint32)]),
     "pfa_apply_galois_ntt": (_i32, [_vp, _u32, _vp, _vp, _sz, _vp]),
     "pfa_apply_galois": (_i32, [_vp, _sz, _vp, _u32, _vp, _sz, _vp]),
@@ -259,6 +261,14 @@ class NativeContext:
     def multiply_relin_rescale(self, chain_index, a, b, rlk, out, stream=None):
         call("pfa_multiply_relin_rescale", self._h, chain_index, ptr(a), ptr(b), ptr(rlk), rlk.shape[0], ptr(out),
              stream or stream_of(a))
+
+    def multiply_and_relin_batch(self, chain_index, count, a, b, rlk, out, stream=None):
+        call("pfa_multiply_and_relin_batch", self._h, chain_index, count, ptr(a), ptr(b), ptr(rlk), rlk.shape[0],
+             ptr(out), stream or stream_of(a))
+
+    def multiply_relin_rescale_batch(self, chain_index, count, a, b, rlk, out, stream=None):
+        call("pfa_multiply_relin_rescale_batch", self._h, chain_index, count, ptr(a), ptr(b), ptr(rlk), rlk.shape[0],
+             ptr(out), stream or stream_of(a))
 
     def relinearize_rescale(self, chain_index, ct3, rlk, out, stream=None):
         call("pfa_relinearize_rescale", self._h, chain_index, ptr(ct3), ptr(rlk), rlk.shape[0], ptr(out),

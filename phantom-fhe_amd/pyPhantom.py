@@ -328,6 +328,10 @@ class ciphertext:
         self._chain_index = 0
         self._scale = 1.0
         self.is_ntt_form = True
+        # > 1: a bundle of that many size-2 ciphertexts at one level and scale,
+        # data [2 members][|Ql|][N], that the evaluator steps in lockstep with
+        # batched native calls (bootstrap's EvalMod tracks)
+        self._members = 1
 
     def chain_index(self) -> int:
         return self._chain_index
@@ -346,6 +350,7 @@ class ciphertext:
         c.data = data
         c._chain_index = self._chain_index if chain is None else chain
         c._scale = self._scale if scale is None else scale
+        c._members = self._members
         return c
 
     def save(self, stream):
@@ -856,14 +861,25 @@ def relinearize(ctx: context, ct: ciphertext, rlk: relin_key) -> ciphertext:
     return ct._like(out)
 
 
-def multiply_and_relin(ctx: context, a: ciphertext, b: ciphertext, rlk: relin_key) -> ciphertext:
-    """src/evaluate.cu:1061-1104."""
-    _check_same(a, b)
-    if a.size() != 2 or b.size() != 2:
+def _bundle_pair(a: ciphertext, b: ciphertext) -> int:
+    """Members of a (bundle) operand pair of a multiplication; checks shapes."""
+    m = a._members
+    if b._members != m or a.size() != 2 * m or b.size() != 2 * m:
         raise ValueError("multiply_and_relin expects size-2 ciphertexts")
+    return m
+
+
+def multiply_and_relin(ctx: context, a: ciphertext, b: ciphertext, rlk: relin_key) -> ciphertext:
+    """src/evaluate.cu:1061-1104 (bundles: every member in one batched call,
+    pfa_multiply_and_relin_batch)."""
+    _check_same(a, b)
+    m = _bundle_pair(a, b)
     L = ctx.size_Ql(a.chain_index())
-    out = ctx._empty(2, L, ctx.N)
-    ctx.native.multiply_and_relin(a.chain_index(), a.data, b.data, rlk.data, out)
+    out = ctx._empty(2 * m, L, ctx.N)
+    if m == 1:
+        ctx.native.multiply_and_relin(a.chain_index(), a.data, b.data, rlk.data, out)
+    else:
+        ctx.native.multiply_and_relin_batch(a.chain_index(), m, a.data, b.data, rlk.data, out)
     return a._like(out, scale=a.scale() * b.scale())
 
 
@@ -925,13 +941,15 @@ def multiply_and_relin_rescale(ctx: context, a: ciphertext, b: ciphertext, rlk: 
     relinearized product at full level is never formed.  The reference has no
     single call for this pair (src/evaluate.cu:1061-1104 then :1582-1602)."""
     _check_same(a, b)
-    if a.size() != 2 or b.size() != 2:
-        raise ValueError("multiply_and_relin expects size-2 ciphertexts")
+    m = _bundle_pair(a, b)
     L = ctx.size_Ql(a.chain_index())
     if L < 2:
         raise ValueError("end of modulus switching chain reached")
-    out = ctx._empty(2, L - 1, ctx.N)
-    ctx.native.multiply_relin_rescale(a.chain_index(), a.data, b.data, rlk.data, out)
+    out = ctx._empty(2 * m, L - 1, ctx.N)
+    if m == 1:
+        ctx.native.multiply_relin_rescale(a.chain_index(), a.data, b.data, rlk.data, out)
+    else:
+        ctx.native.multiply_relin_rescale_batch(a.chain_index(), m, a.data, b.data, rlk.data, out)
     return a._like(out, chain=a.chain_index() + 1, scale=a.scale() * b.scale() / ctx.moduli[L - 1])
 
 
@@ -1880,7 +1898,6 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     at the exact scale S q, followed by one rescale to S: scales never drift
     and no addition mixes them.  T_k = 2 T_a T_b - T_1 and 2 y^2 - 1 are formed
     the same way before their rescale."""
-    nat = ctx.native
     N = ctx.N
     T = {1: ct}
 
@@ -1892,8 +1909,8 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
         for _, k in terms:
             if not -(1 << 63) <= k < (1 << 63):
                 raise ValueError("Chebyshev weight outside int64")
-        out = ctx._empty(2, L, N)
-        nat.ct_lincomb(L, [c.data for c, _ in terms], [k for _, k in terms], out, bias)
+        out = ctx._empty(ct.size(), L, N)
+        _ct_lincomb(ctx, L, [c.data for c, _ in terms], [k for _, k in terms], out, bias, ct._members)
         return ct._like(out, chain=chain, scale=scale)
 
     def product(a, b):
@@ -1997,6 +2014,47 @@ EVALMOD_R = {"k7_r3": 3, "k16_r3": 3, "k28_r3": 3, "k28_r4": 4}
 EVALMOD_LEVELS = {"k7_r3": 8, "k16_r3": 9, "k28_r3": 9, "k28_r4": 10}
 
 
+def _ct_lincomb(ctx, L: int, ins, consts, out, bias, members: int = 1) -> None:
+    """pfa_ct_lincomb on plain ciphertexts or bundles: the bias goes to poly 0
+    of every member (one call per member of a bundle)."""
+    if members == 1:
+        ctx.native.ct_lincomb(L, ins, consts, out, bias)
+        return
+    for m in range(members):
+        sl = slice(2 * m, 2 * m + 2)
+        ctx.native.ct_lincomb(L, [x[sl] for x in ins], consts, out[sl], bias)
+
+
+def _tracks_bundled() -> bool:
+    """bootstrap steps its two EvalMod tracks as one bundle unless
+    PFA_BOOT_BUNDLE=0 (per-track calls, same residues; for A/B measurement)."""
+    import os
+
+    return os.environ.get("PFA_BOOT_BUNDLE", "1") != "0"
+
+
+def _bundle(ctx, cts) -> ciphertext:
+    """Size-2 ciphertexts at one level and scale -> one bundle (their data stacked)."""
+    t = _torch()
+    c0 = cts[0]
+    for c in cts:
+        if c.size() != 2 or c._members != 1 or c.chain_index() != c0.chain_index():
+            raise ValueError("bundle members must be size-2 ciphertexts at one level")
+        _check_scale(c, c0)
+    b = c0._like(t.cat([c.data for c in cts]).contiguous())
+    b._members = len(cts)
+    return b
+
+
+def _unbundle(b: ciphertext) -> list:
+    out = []
+    for m in range(b._members):
+        c = b._like(b.data[2 * m:2 * m + 2].contiguous())
+        c._members = 1
+        out.append(c)
+    return out
+
+
 class _EvalModOps:
     """The reference's EvalMod operations on ciphertexts (or, for the float64
     model of the same polynomial, on arrays of slot values: ctx None)."""
@@ -2027,9 +2085,9 @@ class _EvalModOps:
             if a.chain_index() != chain or abs(a.scale() - a0.scale()) > 1e-9 * a0.scale():
                 raise ValueError("EvalMod operands differ in level or scale")
         L = self.ctx.size_Ql(chain)
-        out = self.ctx._empty(2, L, self.ctx.N)
+        out = self.ctx._empty(*a0.data.shape[:1], L, self.ctx.N)
         b = int(round(bias * a0.scale())) if bias else None
-        self.ctx.native.ct_lincomb(L, [a.data for a, _ in terms], [c for _, c in terms], out, b)
+        _ct_lincomb(self.ctx, L, [a.data for a, _ in terms], [c for _, c in terms], out, b, a0._members)
         return a0._like(out)
 
     def mul(self, a, b):  # multiply_and_relin, rescale_to_next, snap
@@ -2044,8 +2102,8 @@ class _EvalModOps:
         if not self.ctx:
             return 2 * (sq + scalar)
         L = self.ctx.size_Ql(sq.chain_index())
-        out = self.ctx._empty(2, L, self.ctx.N)
-        self.ctx.native.ct_lincomb(L, [sq.data], [2], out, 2 * int(round(scalar * sq.scale())))
+        out = self.ctx._empty(sq.size(), L, self.ctx.N)
+        _ct_lincomb(self.ctx, L, [sq.data], [2], out, 2 * int(round(scalar * sq.scale())), sq._members)
         return sq._like(out)
 
     def weighted_sum(self, basis, coeffs):
@@ -2064,9 +2122,9 @@ class _EvalModOps:
         for t, _ in terms:
             if t.chain_index() != chain:
                 raise ValueError("weighted_sum_chebyshev: basis levels differ")
-        out = self.ctx._empty(2, L, self.ctx.N)
+        out = self.ctx._empty(basis[0].size(), L, self.ctx.N)
         ws = [int(round(c * bs)) for _, c in terms]
-        self.ctx.native.ct_lincomb(L, [t.data for t, _ in terms], ws, out)
+        _ct_lincomb(self.ctx, L, [t.data for t, _ in terms], ws, out, None, basis[0]._members)
         acc = rescale_to_next(self.ctx, basis[0]._like(out, scale=bs * bs))
         acc.set_scale(self.s)
         if abs(coeffs[0]) >= 1e-50:
@@ -2169,8 +2227,8 @@ def _double_angle(ops: _EvalModOps, ct, R: int):
             ct = 2 * sq + scalar
             continue
         L = ops.ctx.size_Ql(sq.chain_index())
-        out = ops.ctx._empty(2, L, ops.ctx.N)
-        ops.ctx.native.ct_lincomb(L, [sq.data], [2], out, int(round(scalar * sq.scale())))
+        out = ops.ctx._empty(sq.size(), L, ops.ctx.N)
+        _ct_lincomb(ops.ctx, L, [sq.data], [2], out, int(round(scalar * sq.scale())), sq._members)
         ct = sq._like(out)
     return ct
 
@@ -2186,7 +2244,7 @@ def _sine(ops: _EvalModOps, ct, variant: str):
 
 
 def _evalmod(context: context, ct: ciphertext, relin_keys: relin_key, variant: str) -> ciphertext:
-    if ct.size() != 2:
+    if ct.size() != 2 * ct._members:
         raise ValueError("EvalMod expects a size-2 ciphertext")
     need = EVALMOD_LEVELS[variant]
     if context.size_Ql(ct.chain_index()) <= need:
@@ -2249,7 +2307,7 @@ def _times_int(ctx, ct: ciphertext, k: int) -> ciphertext:
     (the reference's multiply_uint_scalars_per_tower)."""
     L = ctx.size_Ql(ct.chain_index())
     out = ctx._empty(*ct.data.shape)
-    ctx.native.ct_lincomb(L, [ct.data], [int(k)], out)
+    _ct_lincomb(ctx, L, [ct.data], [int(k)], out, None, ct._members)
     return ct._like(out)
 
 
@@ -2321,8 +2379,12 @@ def _bootstrap_evalround(ctx, ct: ciphertext, bk: bootstrap_key, user_scale: flo
     conj = apply_galois(ctx, u, 2 * ctx.N - 1, bk.glk)
     real = rescale_to_next(ctx, add(ctx, u, conj))
     imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))
-    real = _eval_round(ctx, real, bk.rlk)
-    imag = _times_i(ctx, _eval_round(ctx, imag, bk.rlk), 1)
+    # both tracks through EvalRound in lockstep: one batched call per step
+    if _tracks_bundled():
+        real, imag = _unbundle(_eval_round(ctx, _bundle(ctx, [real, imag]), bk.rlk))
+    else:
+        real, imag = _eval_round(ctx, real, bk.rlk), _eval_round(ctx, imag, bk.rlk)
+    imag = _times_i(ctx, imag, 1)
     c = max(real.chain_index(), imag.chain_index())
     real, imag = mod_switch_to(ctx, real, c), mod_switch_to(ctx, imag, c)
     imag.set_scale(real.scale())
@@ -2398,8 +2460,11 @@ def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: boots
     conj = apply_galois(ctx, u, 2 * ctx.N - 1, bk.glk)
     real = rescale_to_next(ctx, add(ctx, u, conj))                     # Re(x) / K
     imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))  # Im(x) / K
-    real = _eval_mod(ctx, real, bk)
-    imag = _eval_mod(ctx, imag, bk)
+    # both tracks through EvalMod in lockstep: one batched call per step
+    if _tracks_bundled():
+        real, imag = _unbundle(_eval_mod(ctx, _bundle(ctx, [real, imag]), bk))
+    else:
+        real, imag = _eval_mod(ctx, real, bk), _eval_mod(ctx, imag, bk)
     y = add(ctx, real, _times_i(ctx, imag, 1))
     out = apply_s2c_inplace(ctx, y, bk)
     out.set_scale(scale * out.scale() / q0)

@@ -159,3 +159,19 @@ def test_bootstrap_cheb63_options(boot12):
     ct = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, z, 2.0 ** 40, ctx.size_Q), seed=1)
     with pytest.raises(ValueError):
         ph.bootstrap(ctx, enc, ct, bk, 2.0 ** 40, split_scale_down=True)
+
+
+def test_cheb63_evalmod_bundle_matches_tracks(boot12):
+    """This build's EvalMod on a bundle of two ciphertexts (bootstrap's real and
+    imaginary tracks) is bit-identical to EvalMod of each alone."""
+    ph, ctx, sk, enc, bk = boot12
+    rng = np.random.default_rng(9)
+    chain = 5  # past ModRaise, CoeffToSlot's layers and the conjugate split
+    q0 = float(ctx.moduli[0])  # EvalMod's input scale in bootstrap
+    cts = [sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, rng.uniform(-1, 1, enc.slot_count()) / 8,
+                                                              q0, chain), seed=10 + i) for i in range(2)]
+    alone = [ph._eval_mod(ctx, c, bk) for c in cts]
+    both = ph._unbundle(ph._eval_mod(ctx, ph._bundle(ctx, cts), bk))
+    for a, b in zip(alone, both):
+        assert a.chain_index() == b.chain_index() and a.scale() == b.scale()
+        assert bool((a.data == b.data).all())

@@ -154,3 +154,18 @@ def test_bootstrap_key_arguments(engine12):
         ph.create_bootstrap_key(ctx, enc, sk, 128, evalmod="k99")
     with pytest.raises(ValueError):
         ph.create_bootstrap_key(ctx, enc, sk, 128, eval_mod_levels=40)
+
+
+def test_evalmod_bundle_matches_tracks(lapis16):
+    """Bootstrap runs EvalMod on its real and imaginary tracks as one bundle
+    (each step one batched native call): the bundle's members are bit-identical
+    to EvalMod of each ciphertext alone, with the same level and scale."""
+    ph, ctx, sk, rk, enc = lapis16
+    rng = np.random.default_rng(71)
+    cts = [sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, rng.uniform(-0.5, 0.5, enc.slot_count()),
+                                                              2.0 ** 58, 1), seed=72 + i) for i in range(2)]
+    alone = [ph.evalmod_k28_r3(ctx, enc, c, rk) for c in cts]
+    both = ph._unbundle(ph._evalmod(ctx, ph._bundle(ctx, cts), rk, "k28_r3"))
+    for a, b in zip(alone, both):
+        assert a.chain_index() == b.chain_index() and a.scale() == b.scale()
+        assert bool((a.data == b.data).all())

@@ -399,3 +399,50 @@ def test_inner_product_split_items(dev, monkeypatch, slots, logN, nq, alpha, cha
     got, want_r = to_host(fused), st.orc.rescale(chain, want, threads=8)
     assert np.array_equal(got, want_r), first_mismatch(got, want_r)
     st.ctx.synchronize()
+
+
+@pytest.mark.parametrize("slots", [0, 40])
+@pytest.mark.parametrize("logN,nq,alpha,chain,bits", [(12, 9, 3, 1, None), (12, 4, 2, 1, [60] * 6),
+                                                      (13, 6, 3, 2, [60, 50, 50, 50, 60, 50, 60, 60, 60])])
+def test_multiply_batches(dev, monkeypatch, slots, logN, nq, alpha, chain, bits):
+    """pfa_multiply_and_relin_batch and pfa_multiply_relin_rescale_batch over 3
+    pairs: every member bit-exact against the oracle's multiply_and_relin (and
+    rescale) of its pair, with whole and (PFA_WS_SLOTS = 40) split inner-product
+    items, whose split chunks then carry the fold of other members."""
+    if slots:
+        monkeypatch.setenv("PFA_WS_SLOTS", str(slots))
+    st = Setup(logN, nq, alpha, seed=21 + slots, bits=bits)
+    Ql = st.orc.size_Ql(chain)
+    K = 3
+    a = np.stack([st.ct(chain) for _ in range(K)])
+    b = np.stack([st.ct(chain) for _ in range(K)])
+    key = st.key()
+    da, db, dk = to_dev(a, dev), to_dev(b, dev), to_dev(key, dev)
+    want = [st.orc.multiply_and_relin(chain, a[i], b[i], key, threads=8) for i in range(K)]
+    out = empty((K, 2, Ql, st.N), dev)
+    st.ctx.multiply_and_relin_batch(chain, K, da, db, dk, out)
+    got = to_host(out)
+    for i in range(K):
+        assert np.array_equal(got[i], want[i]), (i, first_mismatch(got[i], want[i]))
+    res = empty((K, 2, Ql - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale_batch(chain, K, da, db, dk, res)
+    got = to_host(res)
+    for i in range(K):
+        w = st.orc.rescale(chain, want[i], threads=8)
+        assert np.array_equal(got[i], w), (i, first_mismatch(got[i], w))
+    # in place: out = a
+    st.ctx.multiply_and_relin_batch(chain, K, da, db, dk, da)
+    got = to_host(da)
+    for i in range(K):
+        assert np.array_equal(got[i], want[i]), (i, first_mismatch(got[i], want[i]))
+    st.ctx.synchronize()
+
+
+def test_multiply_batch_errors(dev):
+    st = Setup(12, 4, 2)
+    a = to_dev(np.stack([st.ct(1), st.ct(1)]), dev)
+    key = to_dev(st.key(), dev)
+    with pytest.raises(ValueError):
+        st.ctx.multiply_relin_rescale_batch(1, 2, a, a, key, a)  # output overlaps an input
+    with pytest.raises(ValueError):
+        st.ctx.multiply_and_relin_batch(1, 0, a, a, key, a)  # empty batch
