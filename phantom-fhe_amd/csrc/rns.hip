@@ -539,12 +539,22 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
         Scratch sc(c, s);
         uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
         op_modup(c, chain, ct + LN, mu, s);
-        uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
-        for (size_t e = 0; e < n; ++e) {
-            uint64_t *o = out + e * 2 * LN;
-            op_galois(c, elts[e], ct, o, Ql, s);
-            op_inner(c, chain, mu, keys[e], key_dnum, cx, elts[e], s);
-            op_moddown(c, chain, cx, 2, o, Bases{{o, nullptr}}, s);
+        // each rotation's inner product into its own slot, then one ModDown
+        // over the 2 n polys of up to kHoistGroup rotations (its small INTT and
+        // base-conversion launches are latency-bound, so one launch for the
+        // group costs about what one rotation's did): poly 2e adds sigma_e(c0),
+        // already in out
+        constexpr size_t kHoistGroup = 16;
+        const size_t CX = (size_t)2 * QlP * c.N;
+        uint64_t *cx = sc.alloc(std::min(n, kHoistGroup) * CX);
+        for (size_t e0 = 0; e0 < n; e0 += kHoistGroup) {
+            const size_t m = std::min(kHoistGroup, n - e0);
+            for (size_t e = 0; e < m; ++e) {
+                op_galois(c, elts[e0 + e], ct, out + (e0 + e) * 2 * LN, Ql, s);
+                op_inner(c, chain, mu, keys[e0 + e], key_dnum, cx + e * CX, elts[e0 + e], s);
+            }
+            uint64_t *o = out + e0 * 2 * LN;
+            fused_moddown(c, chain, cx, (uint32_t)(2 * m), o, o, nullptr, s, 2 * LN);
         }
     });
 }
