@@ -302,6 +302,15 @@ int pfa_bsgs_tiled_size(const pfa_context *ctx, size_t chain_index, size_t D, si
 int pfa_bsgs_mac_tiled(const pfa_context *ctx, size_t chain_index, const uint64_t *tiled,
                        const uint64_t *const *babies, size_t M, size_t G, uint64_t *const *out, void *stream);
 
+/* apply_galois_with_ksk (src/evaluate.cu:1607-1656) over `count` ciphertexts,
+ * each with its own Galois element and key, in one set of launches: in, out
+ * [count][2][Ql][N] at chain_index, out[i] = rotate(in[i], elts[i]) with keys[i]
+ * ([key_dnum][2][QP][N]); the same residues as count pfa_apply_galois calls.
+ * out must not overlap in. */
+int pfa_rotate_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *in,
+                     const uint32_t *elts, const uint64_t *const *keys, size_t key_dnum, uint64_t *out,
+                     void *stream);
+
 /* compute_bsgs_babies (src/bsgs.cu:194-214): babies[0] = ct and
  * babies[b] = rotate(babies[b - msb(b)], msb(b)) for 1 <= b < M, each rotation
  * apply_galois_with_ksk (src/evaluate.cu:1607-1656) with the direct key.

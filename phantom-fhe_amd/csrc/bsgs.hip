@@ -350,12 +350,14 @@ k_bsgs_tile(const uint64_t *src, uint8_t *tiled, TiledLayout lay, uint32_t Ql, u
 // (apply_galois_ntt_permutation, src/galois.cu:11-18): ciphertext i of src
 // (stride src_stride) -> ciphertext i of dst (contiguous [B][2][L][N]),
 //   dst[i][k][l][n] = src[i][k][l][pi(n)]  (+ add0[l][n] for k = 0 when add0 is given, B = 1).
+// With elts (a device table), ciphertext i uses its own element elts[i].
 __global__ void __launch_bounds__(kThreads)
 k_galois_ct(const uint64_t *src, uint64_t src_stride, uint64_t *dst, const uint64_t *add0, const uint64_t *mod,
-            uint32_t elt, uint32_t L, uint32_t N, uint32_t logN) {
+            uint32_t elt, const uint32_t *elts, uint32_t L, uint32_t N, uint32_t logN) {
     const uint32_t l = blockIdx.y, k = blockIdx.z & 1u, i = blockIdx.z >> 1, n = blockIdx.x * kThreads + threadIdx.x;
     const size_t row = ((size_t)k * L + l) * N;
-    uint64_t v = src[i * src_stride + row + galois_perm(elt, n, logN)];
+    const uint32_t e = elts ? elts[i] : elt;
+    uint64_t v = src[i * src_stride + row + galois_perm(e, n, logN)];
     if (k == 0 && add0) v = add_mod(v, add0[(size_t)l * N + n], mod[l]);
     st_stream(dst + (size_t)i * 2 * L * N + row + n, v);
 }
@@ -367,18 +369,31 @@ k_galois_ct(const uint64_t *src, uint64_t src_stride, uint64_t *dst, const uint6
 // followed by add_inplace, with the same residues.  src[i] is at
 // src + i src_stride, out is contiguous [B][2][Ql][N] and must not overlap
 // src; add[1] may alias out's poly 1.
+// With elts / keys (host arrays of B entries), ciphertext i is rotated by its
+// own element with its own key (elt, key unused): the same residues as B
+// single rotations.
 void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src_stride, uint32_t B, uint32_t elt,
-                 const uint64_t *key, const uint64_t *add, uint64_t *out, hipStream_t s) {
+                 const uint64_t *key, const uint64_t *add, uint64_t *out, hipStream_t s,
+                 const uint32_t *elts = nullptr, const uint64_t *const *keys = nullptr) {
     const uint32_t Ql = c.size_Ql(chain), QlP = Ql + c.P;
     const uint64_t LN = (uint64_t)Ql * c.N;
     require(B >= 1 && B <= 32767 && (B == 1 || add == nullptr), "bad rotation batch");
+    require((elts == nullptr) == (keys == nullptr), "per-rotation elements and keys go together");
     Scratch sc(c, s);
+    uint32_t *elt_dev = nullptr;
+    const uint64_t **key_dev = nullptr;
+    if (elts) {
+        elt_dev = sc.alloc<uint32_t>(B);
+        upload_async(c, elt_dev, elts, B * sizeof(uint32_t), s);
+        key_dev = sc.alloc<const uint64_t *>(B);
+        upload_async(c, key_dev, keys, B * sizeof(void *), s);
+    }
     uint64_t *t = sc.alloc((size_t)B * 2 * LN);
     hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2 * B), dim3(kThreads), 0, s, src, src_stride, t, add,
-                       c.mod, elt, Ql, c.N, c.logN);
+                       c.mod, elt, elt_dev, Ql, c.N, c.logN);
     PFA_HIP(hipGetLastError());
     uint64_t *cx = sc.alloc((size_t)B * 2 * QlP * c.N);
-    fused_modup_inner(c, chain, t + LN, key, cx, s, B, 2 * LN, (uint64_t)2 * QlP * c.N);
+    fused_modup_inner(c, chain, t + LN, key, cx, s, B, 2 * LN, (uint64_t)2 * QlP * c.N, nullptr, key_dev);
     fused_moddown(c, chain, cx, 2 * B, out, t, add ? add + LN : nullptr, s, 2 * LN);
 }
 
@@ -503,6 +518,26 @@ int pfa_bsgs_tile_plaintexts(const pfa_context *ctx, size_t chain_index, const u
         hipLaunchKernelGGL(k_bsgs_tile, dim3(c.N / kSpan, Ql, (uint32_t)n), dim3(kThreads), 0, as_stream(stream), src,
                            reinterpret_cast<uint8_t *>(tiled), lay, Ql, c.N, (uint32_t)d0, (uint32_t)D);
         PFA_HIP(hipGetLastError());
+    });
+}
+
+int pfa_rotate_batch(const pfa_context *ctx, size_t chain_index, size_t count, const uint64_t *in,
+                     const uint32_t *elts, const uint64_t *const *keys, size_t key_dnum, uint64_t *out,
+                     void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(in && out && elts && keys, "null argument");
+        require(count >= 1 && count <= 4096, "count out of range");
+        if (chain_index < 1 || chain_index > c.Q) fail(PFA_ERR_INVALID_ARGUMENT, "chain index out of range");
+        const uint32_t chain = (uint32_t)chain_index;
+        const size_t ct_elems = (size_t)2 * c.size_Ql(chain) * c.N;
+        require(out + count * ct_elems <= in || out >= in + count * ct_elems, "output overlaps the input");
+        for (size_t i = 0; i < count; i++) {
+            require((elts[i] & 1) && elts[i] < 2 * c.N, "bad Galois element");
+            check_key(c, chain, keys[i], key_dnum);
+        }
+        rotate_into(c, chain, in, ct_elems, (uint32_t)count, 0, nullptr, nullptr, out, as_stream(stream), elts,
+                    keys);
     });
 }
 

@@ -217,7 +217,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
 struct InnerRows {
     const uint64_t *inter;  // [beta][QlP][N] columns-pass output of the base conversion
     const uint64_t *c2;     // [Ql][N] NTT form: the digit's own limbs
-    const uint64_t *key;    // [dnum][2][QP][N]
+    const uint64_t *key;    // [dnum][2][QP][N] (member i: key_table[i] when key_table is set)
     uint64_t *cx;           // [2][QlP][N]
     const ulonglong2 *mont;  // [QP] Montgomery constants (-q^-1 mod 2^64, 2^128 mod q)
     uint32_t Ql, QlP, alpha, beta, Q, QP;
@@ -240,6 +240,7 @@ struct InnerRows {
     uint64_t *partial = nullptr;
     uint32_t *counter = nullptr;
     uint32_t *dev_err = nullptr, *host_err = nullptr;
+    const uint64_t *const *key_table = nullptr;  // per-member keys (device array), or null
     // target of item group i: order[i] (null: i).  Items of integer-policy
     // targets take ~1.5-2.25x as long as FP64 ones; ordered last, they are the
     // first to be split when items are left over after whole rounds.
@@ -534,6 +535,9 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
     a.inter += mi * a0.inter_bstride;
     a.c2 += mi * a0.c2_bstride;
     a.cx += mi * a0.cx_bstride;
+    if (a0.key_table)  // member mi's key, a scalar load (mi is uniform)
+        a.key = reinterpret_cast<const uint64_t *>(
+            wave_uniform(ld_const(reinterpret_cast<const uint64_t *>(a0.key_table + mi))));
     {
         // member mi's fold bases (stride 0 without a batched fold); the offset
         // is made explicitly wave-uniform for the compiler
@@ -928,7 +932,8 @@ void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp and the key-switch inner
 // product against key [dnum][2][QP][N].
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold) {
+                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold,
+                       const uint64_t *const *key_table) {
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
     const uint64_t LN = (uint64_t)Ql * c.N, IN = (uint64_t)lv.beta * QlP * c.N;
@@ -965,6 +970,7 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.inter_bstride = IN;
     r.c2_bstride = c2_stride;
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
+    r.key_table = key_table;
     if (batch == 1 && !c.ws_no_order) r.order = lv.ws_order;
     if (fold) {
         require(fold->base0 && fold->base1 && Ql >= 2 && (batch == 1 || fold->stride), "bad ModDown + rescale fold");

@@ -264,9 +264,10 @@ struct KsFold {
     const uint64_t *base0 = nullptr, *base1 = nullptr;
     uint64_t stride = 0;
 };
+// With key_table (a device array of batch key pointers), member i uses its own key.
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
                        hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0,
-                       const KsFold *fold = nullptr);
+                       const KsFold *fold = nullptr, const uint64_t *const *key_table = nullptr);
 // cx [2][QlP][N] from fused_modup_inner with a fold over base -> out [2][Ql-1][N]
 // = rescale(base + ModDown(cx)), bit-identical to fused_moddown then fused_rescale.
 // With count > 1: cx [count][2][QlP][N], member i's bases at + i base_stride,

@@ -69,6 +69,7 @@ SIGNATURES = {
     "pfa_bsgs_mac_tiled": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, C.POINTER(_vp), _vp]),
     "pfa_bsgs_tiled_size": (_i32, [_vp, _sz, _sz, C.POINTER(_sz)]),
     "pfa_bsgs_babies": (_i32, [_vp, _sz, _vp, _sz, C.POINTER(_vp), _sz, _vp, _vp]),
+    "pfa_rotate_batch": (_i32, [_vp, _sz, _sz, _vp, C.POINTER(C.c_uint32), C.POINTER(_vp), _sz, _vp, _vp]),
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
     "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
     "pfa_mod_raise": (_i32, [_vp, _vp, _sz, _vp, _vp]),
@@ -391,6 +392,16 @@ class NativeContext:
         bp = (C.c_void_p * M)(*[addr(t) for t in babies])
         op = (C.c_void_p * G)(*[addr(t) for t in outs])
         call("pfa_bsgs_mac_tiled", self._h, chain_index, ptr(tiled), bp, M, G, op, stream or stream_of(tiled))
+
+    def rotate_batch(self, chain_index, inp, elts, keys, out, stream=None):
+        """out[i] = rotate(inp[i], elts[i]) with keys[i]; inp, out [count][2][L][N]."""
+        n = len(elts)
+        if len(keys) != n or n == 0:
+            raise ValueError("one key per Galois element, at least one")
+        ep = (C.c_uint32 * n)(*[int(e) for e in elts])
+        kp = (C.c_void_p * n)(*[ptr(k) for k in keys])
+        call("pfa_rotate_batch", self._h, chain_index, n, ptr(inp), ep, kp, keys[0].shape[0], ptr(out),
+             stream or stream_of(inp))
 
     def bsgs_babies(self, chain_index, ct, M, keys, out, stream=None):
         """out[b] = babies[b] for 0 <= b < M (out[0] = ct, then chained

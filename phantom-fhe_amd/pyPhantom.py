@@ -1804,12 +1804,30 @@ def _apply_layer(ctx, ct: ciphertext, lt: _LTLayers, pts, i: int, glk, rescale: 
     parts = ctx._empty(len(plan.giants), 2, L, ctx.N)
     ctx.native.bsgs_mac(ct.chain_index(), plan.grid, [rotated[b].data for b in plan.babies],
                         [parts[k] for k in range(len(plan.giants))])
-    acc = None
-    for k, g in enumerate(plan.giants):
-        part = ct._like(parts[k], scale=ct.scale() * plan.scale)
-        if g:
-            part = rotate(ctx, part, _signed_step(g * n1 * unit, lt.n), glk)
-        acc = part if acc is None else add(ctx, acc, part)
+    # the giants' rotations are independent: one batched rotation (each part
+    # its own element and key) when every key is present, then one weighted
+    # sum of all parts (weights 1; the same residues as the pairwise adds)
+    scale = ct.scale() * plan.scale
+    moved = [k for k, g in enumerate(plan.giants) if g]
+    elts = [get_elt_from_step(_signed_step(plan.giants[k] * n1 * unit, lt.n), ctx.N) for k in moved]
+    if moved and all(e in glk.keys for e in elts):
+        rot = ctx._empty(len(moved), 2, L, ctx.N)
+        src = parts[moved[0]:moved[-1] + 1] if moved == list(range(moved[0], moved[-1] + 1)) else \
+            parts[moved].contiguous()
+        ctx.native.rotate_batch(ct.chain_index(), src.contiguous(), elts, [glk.keys[e] for e in elts], rot)
+        terms = [parts[k] for k, g in enumerate(plan.giants) if not g] + [rot[i] for i in range(len(moved))]
+    else:
+        terms = []
+        for k, g in enumerate(plan.giants):
+            part = ct._like(parts[k], scale=scale)
+            terms.append((rotate(ctx, part, _signed_step(g * n1 * unit, lt.n), glk) if g else part).data)
+    acc, i = None, 0
+    while i < len(terms):  # pfa_ct_lincomb takes up to 8 inputs
+        chunk = terms[i:i + 8] if acc is None else [acc.data] + terms[i:i + 7]
+        i += len(chunk) if acc is None else len(chunk) - 1
+        out = ctx._empty(2, L, ctx.N)
+        ctx.native.ct_lincomb(L, chunk, [1] * len(chunk), out)
+        acc = ct._like(out, scale=scale)
     return rescale_to_next(ctx, acc) if rescale else acc
 
 

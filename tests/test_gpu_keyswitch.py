@@ -446,3 +446,25 @@ def test_multiply_batch_errors(dev):
         st.ctx.multiply_relin_rescale_batch(1, 2, a, a, key, a)  # output overlaps an input
     with pytest.raises(ValueError):
         st.ctx.multiply_and_relin_batch(1, 0, a, a, key, a)  # empty batch
+
+
+@pytest.mark.parametrize("slots", [0, 40])
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 6, 2, 1), (12, 5, 1, 2), (13, 6, 3, 1)])
+def test_rotate_batch(dev, monkeypatch, slots, logN, nq, alpha, chain):
+    """pfa_rotate_batch: 3 ciphertexts, each with its own Galois element and
+    key, every member bit-exact against the oracle's apply_galois (whole and
+    split inner-product items)."""
+    import pfa_native as P
+
+    if slots:
+        monkeypatch.setenv("PFA_WS_SLOTS", str(slots))
+    st = Setup(logN, nq, alpha, seed=30 + slots)
+    cts = np.stack([st.ct(chain) for _ in range(3)])
+    keys = [st.key() for _ in range(3)]
+    elts = [P.galois_elt_from_step(s, st.N) for s in (1, -5, 7)]
+    out = empty(cts.shape, dev)
+    st.ctx.rotate_batch(chain, to_dev(cts, dev), elts, [to_dev(k, dev) for k in keys], out)
+    got = to_host(out)
+    for i in range(3):
+        want = st.orc.apply_galois(chain, cts[i], elts[i], keys[i], threads=8)
+        assert np.array_equal(got[i], want), (i, first_mismatch(got[i], want))
