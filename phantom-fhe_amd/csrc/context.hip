@@ -248,6 +248,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     if (const char *w = std::getenv("PFA_WS_SLOTS")) c.ws_slots = (uint32_t)std::max(0, std::atoi(w));
     if (const char *w = std::getenv("PFA_WS_MAX_CHUNKS")) c.ws_max_chunks = (uint32_t)std::max(0, std::atoi(w));
     if (const char *w = std::getenv("PFA_WS_NO_ORDER")) c.ws_no_order = std::atoi(w) != 0;
+    if (const char *w = std::getenv("PFA_WS_MEMBER_MAJOR")) c.ws_member_major = std::atoi(w) != 0;
     // Single-launch NTT (N = 2^16, opt-in with PFA_NTT_FLOW=1): built for the
     // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition,
     // checked here by a probe kernel.  The other variables tune it (workgroups

@@ -241,6 +241,7 @@ struct InnerRows {
     uint32_t *counter = nullptr;
     uint32_t *dev_err = nullptr, *host_err = nullptr;
     const uint64_t *const *key_table = nullptr;  // per-member keys (device array), or null
+    uint32_t member_fast = 0;  // item order: member index fastest (see ws_decode)
     // target of item group i: order[i] (null: i).  Items of integer-policy
     // targets take ~1.5-2.25x as long as FP64 ones; ordered last, they are the
     // first to be split when items are left over after whole rounds.
@@ -248,6 +249,27 @@ struct InnerRows {
 };
 
 __device__ __forceinline__ uint32_t ws_target(const InnerRows &a, uint32_t i) { return a.order ? a.order[i] : i; }
+
+// Item w0 -> (member mi, item w of that member).  With several members the
+// members' items of one (target, tile) read the same key rows (one key for the
+// batch): they are given workgroups congruent mod 8, which run on one XCD
+// (workgroups are dealt to the XCDs round-robin), so the rows come from HBM
+// once and are shared through that XCD's L2 (the grouped order of
+// grouped_item, with the members as the group's items; needs a multiple of 8
+// items per member, else the members only run fastest).
+__device__ __forceinline__ void ws_decode(const InnerRows &a, uint32_t w0, uint32_t tiles, uint32_t &mi,
+                                         uint32_t &w) {
+    const uint32_t per = a.QlP * tiles;
+    if (a.member_fast && per % kXcds == 0) {
+        grouped_item(w0, per, a.batch, w, mi);
+    } else if (a.member_fast) {
+        mi = w0 % a.batch;
+        w = w0 / a.batch;
+    } else {
+        mi = w0 / per;
+        w = w0 % per;
+    }
+}
 
 // Digit b's input for limb r at row offset rowoff: the digit's own limb of c2
 // (already in NTT form) or the columns-pass output to transform.
@@ -529,8 +551,8 @@ __device__ __forceinline__ void ws_item(const InnerRows &a0, const NttTables &t,
     double *tab = lds + W::LDS;
     const bool transform = threadIdx.x < W::HALF;
     const uint32_t rr = (threadIdx.x % W::HALF) / Sub<S2>::T;
-    const uint32_t per = a0.QlP * W::TILES;
-    const uint32_t mi = w0 / per, w = w0 % per;
+    uint32_t mi, w;
+    ws_decode(a0, w0, W::TILES, mi, w);
     InnerRows a = a0;
     a.inter += mi * a0.inter_bstride;
     a.c2 += mi * a0.c2_bstride;
@@ -590,8 +612,8 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
     using W = WsGeo<S1, S2>;
     using SB = Sub<S2>;
     const uint32_t F = (threadIdx.x % W::HALF) % SB::T, rr = (threadIdx.x % W::HALF) / SB::T;
-    const uint32_t per = a0.QlP * W::TILES;
-    const uint32_t mi = w0 / per, w = w0 % per;
+    uint32_t mi, w;
+    ws_decode(a0, w0, W::TILES, mi, w);
     InnerRows a = a0;
     a.cx += mi * a0.cx_bstride;
     {
@@ -971,6 +993,8 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.c2_bstride = c2_stride;
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
     r.key_table = key_table;
+    // one key for all members: interleave them so they share its rows in L2
+    r.member_fast = batch > 1 && !key_table && !c.ws_member_major ? 1u : 0u;
     if (batch == 1 && !c.ws_no_order) r.order = lv.ws_order;
     if (fold) {
         require(fold->base0 && fold->base1 && Ql >= 2 && (batch == 1 || fold->stride), "bad ModDown + rescale fold");

@@ -132,6 +132,7 @@ struct Ctx {
     uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)
     uint32_t ws_max_chunks = 0;      // most digit chunks of a split inner-product item (0: beta)
     bool ws_no_order = false;        // inner product in plain target order (PFA_WS_NO_ORDER)
+    bool ws_member_major = false;    // batched inner product in member-major item order (PFA_WS_MEMBER_MAJOR)
     // single-launch NTT (ntt_kernels.h, opt-in): needs a device that deals
     // workgroups to 8 XCDs round-robin; used for batches of at least
     // flow_min_jobs limbs at N = 2^16
