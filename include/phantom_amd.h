@@ -354,15 +354,18 @@ int pfa_mod_raise(const pfa_context *ctx, const uint64_t *in, size_t size, uint6
 /* Linear combination of ciphertexts with integer constants, the weighted sum
  * of Chebyshev terms before its one rescale (weighted_sum_chebyshev,
  * src/evalmod.cu:277-335):
- *   out[k][l] = sum_t consts[t] ins[t][k][l]  (+ bias on poly 0)  mod q_l
- * for polys k < size and limbs l < L (table rows 0 .. L-1), NTT form.
+ *   out[k][l] = sum_t consts[t] ins[t][k][l]  (+ bias on poly 0 of each ciphertext)  mod q_l
+ * for polys k < size and limbs l < L (table rows 0 .. L-1), NTT form; the
+ * size polys are size / ct_size ciphertexts of ct_size polys each (ct_size =
+ * size for one ciphertext), and the bias goes to polys k with k mod ct_size = 0.
  * ins[t] is [size][in_limbs[t]][N] with in_limbs[t] >= L: a ciphertext at a
  * lower chain index enters as it is (its first L limbs are read).  consts are
  * signed; bias points to a signed 128-bit integer as two words (low, high;
  * two's complement) or is NULL.  n <= 8.  out may be one of the inputs when
  * that input has exactly L limbs. */
-int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, const uint64_t *const *ins, const size_t *in_limbs,
-                   const int64_t *consts, size_t n, const uint64_t *bias, uint64_t *out, void *stream);
+int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, size_t ct_size, const uint64_t *const *ins,
+                   const size_t *in_limbs, const int64_t *consts, size_t n, const uint64_t *bias, uint64_t *out,
+                   void *stream);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,7 @@ struct LincombArgs {
     int64_t k[kMaxTerms];
     uint64_t b_lo, b_hi;  // signed 128-bit bias, two's complement
     uint32_t n, has_bias, L, N;
+    uint32_t ct_size;     // polys per ciphertext: the bias goes to polys k with k mod ct_size = 0
 };
 
 __device__ __forceinline__ uint64_t signed_mod(int64_t v, uint64_t q) {
@@ -61,7 +62,7 @@ k_ct_lincomb(LincombArgs a, uint64_t *out, const uint64_t *mod, const ulonglong2
         w[threadIdx.x] = signed_mod(a.k[threadIdx.x], q);
     } else if (threadIdx.x == kMaxTerms) {
         uint64_t r = 0;
-        if (a.has_bias && k == 0) {
+        if (a.has_bias && k % a.ct_size == 0) {
             const bool neg = (int64_t)a.b_hi < 0;
             U128 m{a.b_lo, a.b_hi};
             if (neg) {  // magnitude of the two's complement value
@@ -107,15 +108,18 @@ int pfa_mod_raise(const pfa_context *ctx, const uint64_t *in, size_t size, uint6
     });
 }
 
-int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, const uint64_t *const *ins, const size_t *in_limbs,
-                   const int64_t *consts, size_t n, const uint64_t *bias, uint64_t *out, void *stream) {
+int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, size_t ct_size, const uint64_t *const *ins,
+                   const size_t *in_limbs, const int64_t *consts, size_t n, const uint64_t *bias, uint64_t *out,
+                   void *stream) {
     return guarded([&] {
         const Ctx &c = *ctx_of(ctx);
         require(out && (n == 0 || (ins && in_limbs && consts)), "null argument");
         require(n <= (size_t)kMaxTerms, "at most 8 terms");
         require(L >= 1 && L <= c.QP, "limb count out of range");
         require(size >= 1 && size <= 65535, "bad ciphertext size");
+        require(ct_size >= 1 && size % ct_size == 0, "size must be a multiple of the ciphertext size");
         LincombArgs a{};
+        a.ct_size = (uint32_t)ct_size;
         for (size_t t = 0; t < n; t++) {
             require(ins[t] != nullptr, "null input");
             require(in_limbs[t] >= L && in_limbs[t] <= c.QP, "input has fewer limbs than the output");

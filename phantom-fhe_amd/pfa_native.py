@@ -73,7 +73,7 @@ SIGNATURES = {
     "pfa_bsgs_giants": (_i32, [_vp, _sz, _vp, _sz, _i32, _vp, _sz, _vp, _vp]),
     "pfa_bsgs_apply_giants": (_i32, [_vp, _sz, _vp, C.POINTER(_vp), _sz, _sz, _vp, _sz, _vp, _vp]),
     "pfa_mod_raise": (_i32, [_vp, _vp, _sz, _vp, _vp]),
-    "pfa_ct_lincomb": (_i32, [_vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "pfa_ct_lincomb": (_i32, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
 }
 
 
@@ -425,10 +425,11 @@ class NativeContext:
              ptr(key) if key is not None else None, key.shape[0] if key is not None else 0, ptr(out),
              stream or stream_of(tiled))
 
-    def ct_lincomb(self, L, ins, consts, out, bias=None, stream=None):
-        """out [size][L][N] = sum_t consts[t] ins[t] (+ bias on poly 0); ins are
-        [size][L_t][N] tensors with L_t >= L; consts Python ints in int64 range,
-        bias a Python int in the signed 128-bit range or None."""
+    def ct_lincomb(self, L, ins, consts, out, bias=None, stream=None, ct_size=None):
+        """out [size][L][N] = sum_t consts[t] ins[t] (+ bias on poly 0 of each
+        ciphertext of ct_size polys, default size); ins are [size][L_t][N]
+        tensors with L_t >= L; consts Python ints in int64 range, bias a Python
+        int in the signed 128-bit range or None."""
         n = len(ins)
         size = out.shape[0]
         for t in ins:
@@ -444,7 +445,8 @@ class NativeContext:
                 raise ValueError("bias out of the signed 128-bit range")
             b &= (1 << 128) - 1
             bp = (C.c_uint64 * 2)(b & 0xFFFFFFFFFFFFFFFF, b >> 64)
-        call("pfa_ct_lincomb", self._h, L, size, ip, il, kc, n, bp, ptr(out), stream or stream_of(out))
+        call("pfa_ct_lincomb", self._h, L, size, ct_size or size, ip, il, kc, n, bp, ptr(out),
+             stream or stream_of(out))
 
     def mod_raise(self, ct_bottom, out, stream=None):
         """ct_bottom [size][1][N] mod q0 -> out [size][|Q|][N], centred lift (NTT form)."""

@@ -2033,14 +2033,9 @@ EVALMOD_LEVELS = {"k7_r3": 8, "k16_r3": 9, "k28_r3": 9, "k28_r4": 10}
 
 
 def _ct_lincomb(ctx, L: int, ins, consts, out, bias, members: int = 1) -> None:
-    """pfa_ct_lincomb on plain ciphertexts or bundles: the bias goes to poly 0
-    of every member (one call per member of a bundle)."""
-    if members == 1:
-        ctx.native.ct_lincomb(L, ins, consts, out, bias)
-        return
-    for m in range(members):
-        sl = slice(2 * m, 2 * m + 2)
-        ctx.native.ct_lincomb(L, [x[sl] for x in ins], consts, out[sl], bias)
+    """pfa_ct_lincomb on plain ciphertexts or bundles (one call; the bias goes
+    to poly 0 of every member)."""
+    ctx.native.ct_lincomb(L, ins, consts, out, bias, ct_size=None if members == 1 else 2)
 
 
 def _tracks_bundled() -> bool:

@@ -67,6 +67,27 @@ def test_ct_lincomb_matches_integers(dev, bias):
             assert got[k, l].tolist() == [a % q for a in acc], (k, l)
 
 
+def test_ct_lincomb_bias_per_ciphertext(dev):
+    """With ct_size = 2 over 4 polys (a bundle of two ciphertexts) the bias
+    goes to polys 0 and 2 only."""
+    import pfa_native as P
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 40, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    rng = np.random.default_rng(6)
+    x = np.stack([np.stack([rng.integers(0, q, N, dtype=np.uint64) for q in mods[:2]]) for _ in range(4)])
+    out = empty((4, 2, N), dev)
+    bias = -(1 << 100) + 3
+    ctx.ct_lincomb(2, [to_dev(x, dev)], [7], out, bias, ct_size=2)
+    got = to_host(out)
+    for k in range(4):
+        for l in range(2):
+            q = mods[l]
+            want = [(7 * v + (bias if k % 2 == 0 else 0)) % q for v in x[k, l].tolist()]
+            assert got[k, l].tolist() == want, (k, l)
+
+
 def test_ct_lincomb_in_place(dev):
     import pfa_native as P
 
