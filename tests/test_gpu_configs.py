@@ -1,4 +1,4 @@
-"""The benchmark configurations at their full sizes (
+"""The benchmark configurations at their full sizes (configs 2-5 of the benchmark,
 plus the metric's "L=35" HMult), so that no benchmarked workload is checked
 only by bench.py.
 
