@@ -423,16 +423,16 @@ struct TwStage {
 
 // Staged entries of a rows-pass tile: rb[g][tile ROWS + i] for g < S2, i < ROWS,
 // then the small table's first 2^(S2-1) entries.
-template <int S1, int S2>
+template <int S1, int S2, int R = Geo<S1, S2>::ROWS>
 struct RowStage {
     using G = Geo<S1, S2>;
-    static constexpr int RB = S2 * G::ROWS;
+    static constexpr int RB = S2 * R;
     static constexpr int N = RB + (1 << (S2 - 1));
-    TwStage<N, G::ROW_THREADS> st;
+    TwStage<N, R * Sub<S2>::T> st;
     __device__ __forceinline__ void load(const NttTables &t, uint32_t prow, uint32_t tile, bool fwd) {
-        const ulonglong2 *rb = (fwd ? t.rb_fw : t.rb_inv) + (size_t)prow * S2 * G::N1 + tile * G::ROWS;
+        const ulonglong2 *rb = (fwd ? t.rb_fw : t.rb_inv) + (size_t)prow * S2 * G::N1 + tile * R;
         const ulonglong2 *small = (fwd ? t.small_fw : t.small_inv) + (size_t)prow * kSmall;
-        st.load([&](uint32_t i) { return i < (uint32_t)RB ? rb[(i / G::ROWS) * G::N1 + i % G::ROWS] : small[i - RB]; });
+        st.load([&](uint32_t i) { return i < (uint32_t)RB ? rb[(i / R) * G::N1 + i % R] : small[i - RB]; });
     }
     // LDS copy -> the tile's twiddle view (full: the prime's global table, for
     // the integer policy)
@@ -586,7 +586,7 @@ __device__ __forceinline__ void fwd_rows_core(typename A::T (&x)[Sub<S2>::E], co
     fwd_rows_core<A, S1, S2, Geo<S1, S2>::N1>(x, ar, global_tw<S1, S2>(t, prow, k1, true), k1, lr);
 }
 
-template <class A, int S1, int S2, int RBS>
+template <class A, int S1, int S2, int RBS, int R = Geo<S1, S2>::ROWS>
 __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
                                               uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
@@ -594,7 +594,7 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     using T = typename A::T;
     const A ar(q);
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    const uint32_t k1 = r.tile * G::ROWS + rr;
+    const uint32_t k1 = r.tile * R + rr;
     uint64_t *rowp = olimb + (size_t)k1 * G::N2;
     T x[SB::E];
 #pragma unroll
@@ -604,27 +604,28 @@ __device__ __forceinline__ void fwd_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     for (int e = 0; e < SB::E; e++) st_stream(&rowp[F + SB::T * e], ar.store(x[e]));
 }
 
-template <int S1, int S2>
+template <int S1, int S2, int R = Geo<S1, S2>::ROWS>
 __device__ __forceinline__ const uint64_t *rows_ptr(const NttBatch &b, const TileRef &r, const uint64_t *base,
                                                     uint64_t stride) {
     using G = Geo<S1, S2>;
     const uint32_t rr = threadIdx.x / Sub<S2>::T;
-    return base + r.m * stride + (size_t)r.l * G::N + (size_t)(r.tile * G::ROWS + rr) * G::N2;
+    return base + r.m * stride + (size_t)r.l * G::N + (size_t)(r.tile * R + rr) * G::N2;
 }
 
-template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) __attribute__((amdgpu_waves_per_eu(4, 8)))
+template <int S1, int S2, int R = Geo<S1, S2>::ROWS>
+__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(4, 8)))
 ntt_fwd_rows(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
-    using RS = RowStage<S1, S2>;
-    __shared__ double lds[G::ROW_LDS];
+    using RS = RowStage<S1, S2, R>;
+    constexpr uint32_t TILES = G::N1 / R;
+    __shared__ double lds[R * G::ROW_PITCH];
     __shared__ ulonglong2 twl[RS::N];
-    const uint32_t total = b.M * b.L * G::ROW_TILES;
+    const uint32_t total = b.M * b.L * TILES;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    for (uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total); cur < total;
-         cur = next_tile(b, G::ROW_TILES, cur + gridDim.x, total)) {
-        const TileRef r = decode_tile(b, G::ROW_TILES, cur);
+    for (uint32_t cur = next_tile(b, TILES, blockIdx.x, total); cur < total;
+         cur = next_tile(b, TILES, cur + gridDim.x, total)) {
+        const TileRef r = decode_tile(b, TILES, cur);
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         // the tile's twiddles are requested before its residues, so both are
@@ -632,7 +633,7 @@ ntt_fwd_rows(NttBatch b, NttTables t) {
         RS stage;
         stage.load(t, prow, r.tile, true);
         uint64_t raw[SB::E];
-        const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
+        const uint64_t *s = rows_ptr<S1, S2, R>(b, r, b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
         stage.st.store(twl);
@@ -640,16 +641,16 @@ ntt_fwd_rows(NttBatch b, NttTables t) {
         const TileTw w = RS::view(twl, t.tw + (size_t)prow * G::N, rr);
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            fwd_rows_tile<ArithF64, S1, S2, G::ROWS>(raw, w, r, q, lds, olimb);
+            fwd_rows_tile<ArithF64, S1, S2, R, R>(raw, w, r, q, lds, olimb);
         else
-            fwd_rows_tile<ArithInt, S1, S2, G::ROWS>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
+            fwd_rows_tile<ArithInt, S1, S2, R, R>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
         __syncthreads();
     }
 }
 
 // ================================================================ inverse
 // Rows pass first: src (canonical) -> dst (intermediate).
-template <class A, int S1, int S2, int RBS, bool NT = true>
+template <class A, int S1, int S2, int RBS, bool NT = true, int R = Geo<S1, S2>::ROWS>
 __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
                                               uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
@@ -657,7 +658,7 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     using T = typename A::T;
     const A ar(q);
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    const uint32_t k1 = r.tile * G::ROWS + rr;
+    const uint32_t k1 = r.tile * R + rr;
     uint64_t *drow = olimb + (size_t)k1 * G::N2;
     T *lr = lds + rr * G::ROW_PITCH;
     T x[SB::E];
@@ -733,25 +734,26 @@ __global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBa
 // Faster on large batches (config-2 inverse 44.5-44.9 -> 41.3 us), slightly
 // slower on the few-limb transforms of a key switch, so ntt_inverse picks it
 // by batch size.
-template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) __attribute__((amdgpu_waves_per_eu(3, 8)))
+template <int S1, int S2, int R = Geo<S1, S2>::ROWS>
+__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(3, 8)))
 ntt_inv_rows_staged(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
-    using RS = RowStage<S1, S2>;
-    __shared__ double lds[G::ROW_LDS];
+    using RS = RowStage<S1, S2, R>;
+    constexpr uint32_t TILES = G::N1 / R;
+    __shared__ double lds[R * G::ROW_PITCH];
     __shared__ ulonglong2 twl[RS::N];
-    const uint32_t total = b.M * b.L * G::ROW_TILES;
+    const uint32_t total = b.M * b.L * TILES;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    for (uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total); cur < total;
-         cur = next_tile(b, G::ROW_TILES, cur + gridDim.x, total)) {
-        const TileRef r = decode_tile(b, G::ROW_TILES, cur);
+    for (uint32_t cur = next_tile(b, TILES, blockIdx.x, total); cur < total;
+         cur = next_tile(b, TILES, cur + gridDim.x, total)) {
+        const TileRef r = decode_tile(b, TILES, cur);
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
         RS stage;
         stage.load(t, prow, r.tile, false);
         uint64_t raw[SB::E];
-        const uint64_t *s = rows_ptr<S1, S2>(b, r, b.src, b.sstride);
+        const uint64_t *s = rows_ptr<S1, S2, R>(b, r, b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
         stage.st.store(twl);
@@ -759,9 +761,9 @@ ntt_inv_rows_staged(NttBatch b, NttTables t) {
         const TileTw w = RS::view(twl, t.itw + (size_t)prow * G::N, rr);
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_rows_tile<ArithF64, S1, S2, G::ROWS>(raw, w, r, q, lds, olimb);
+            inv_rows_tile<ArithF64, S1, S2, R, true, R>(raw, w, r, q, lds, olimb);
         else
-            inv_rows_tile<ArithInt, S1, S2, G::ROWS>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
+            inv_rows_tile<ArithInt, S1, S2, R, true, R>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
         __syncthreads();
     }
 }
