@@ -71,36 +71,79 @@ k_from_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t st
 // fl(a fl(b/q)) within 3/8 of the true quotient, so each product is within
 // 0.875 q and a sum of two stays far below 2^53)
 // Member z = blockIdx.z of a batch reads a, b at + z in_stride and writes
-// d0, d1 at + z d_stride, d2 at + z d2_stride.
+// d0, d1 at + z d_stride, d2 at + z d2_stride.  Each thread takes kTensorE
+// elements in pairs of adjacent ones (16-byte accesses); the prime and its
+// Barrett ratio are scalar loads.
+using u64x2 = unsigned long long __attribute__((ext_vector_type(2)));
+constexpr int kTensorE = 4;  // elements per thread, in 16-byte pairs
+
+__device__ __forceinline__ u64x2 ld_stream2(const uint64_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u64x2 *>(p));
+}
+__device__ __forceinline__ void st_stream2(uint64_t *p, uint64_t x, uint64_t y) {
+    u64x2 v;
+    v.x = x;
+    v.y = y;
+    __builtin_nontemporal_store(v, reinterpret_cast<u64x2 *>(p));
+}
+
 __global__ void __launch_bounds__(kThreads)
 k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint64_t *d2, const uint64_t *mod,
          const ulonglong2 *ratio, uint32_t Ql, uint32_t N, uint64_t in_stride, uint64_t d_stride,
          uint64_t d2_stride) {
-    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
-    const uint64_t q = mod[l];
-    const size_t LN = (size_t)Ql * N, i = (size_t)l * N + n;
+    constexpr int P = kTensorE / 2;
+    const uint32_t l = blockIdx.y;
+    const uint64_t q = ld_const(mod + l);
+    const size_t LN = (size_t)Ql * N, i = (size_t)l * N + (size_t)blockIdx.x * kThreads * kTensorE + threadIdx.x * 2;
     a += blockIdx.z * in_stride;
     b += blockIdx.z * in_stride;
     d0 += blockIdx.z * d_stride;
     d1 += blockIdx.z * d_stride;
     d2 += blockIdx.z * d2_stride;
-    const uint64_t a0 = ld_stream(&a[i]), a1 = ld_stream(&a[LN + i]), b0 = ld_stream(&b[i]), b1 = ld_stream(&b[LN + i]);
+    // pair p of this thread: elements i + 2 kThreads p, +1 (each pair load is one
+    // coalesced 1 KiB row per wave)
+    u64x2 a0[P], a1[P], b0[P], b1[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const size_t j = i + (size_t)2 * kThreads * p;
+        a0[p] = ld_stream2(&a[j]);
+        a1[p] = ld_stream2(&a[LN + j]);
+        b0[p] = ld_stream2(&b[j]);
+        b1[p] = ld_stream2(&b[LN + j]);
+    }
+    uint64_t r0[kTensorE], r1[kTensorE], r2[kTensorE];
     if (q < kF64PrimeBound) {
         const ArithF64 ar(q);
-        const double x0 = ar.load(a0), x1 = ar.load(a1), y0 = ar.load(b0), y1 = ar.load(b1);
-        const double q0 = y0 * ar.qinv, q1 = y1 * ar.qinv;
-        st_stream(&d0[i], ar.store(ar.mulw(x0, y0, q0)));
-        st_stream(&d1[i], ar.store(ar.mulw(x0, y1, q1) + ar.mulw(x1, y0, q0)));
-        st_stream(&d2[i], ar.store(ar.mulw(x1, y1, q1)));
-        return;
+#pragma unroll
+        for (int e = 0; e < kTensorE; e++) {
+            const int p = e / 2, h = e % 2;
+            const double x0 = ar.load(a0[p][h]), x1 = ar.load(a1[p][h]), y0 = ar.load(b0[p][h]),
+                         y1 = ar.load(b1[p][h]);
+            const double q0 = y0 * ar.qinv, q1 = y1 * ar.qinv;
+            r0[e] = ar.store(ar.mulw(x0, y0, q0));
+            r1[e] = ar.store(ar.mulw(x0, y1, q1) + ar.mulw(x1, y0, q0));
+            r2[e] = ar.store(ar.mulw(x1, y1, q1));
+        }
+    } else {
+        const ulonglong2 r = ld_const(ratio + l);
+#pragma unroll
+        for (int e = 0; e < kTensorE; e++) {
+            const int p = e / 2, h = e % 2;
+            U128 m{0, 0};
+            mac(m, a0[p][h], b1[p][h]);
+            mac(m, a1[p][h], b0[p][h]);
+            r0[e] = mulmod_b(a0[p][h], b0[p][h], q, r);
+            r1[e] = barrett128(m, q, r.x, r.y);
+            r2[e] = mulmod_b(a1[p][h], b1[p][h], q, r);
+        }
     }
-    const ulonglong2 r = ratio[l];
-    U128 m{0, 0};
-    mac(m, a0, b1);
-    mac(m, a1, b0);
-    st_stream(&d0[i], mulmod_b(a0, b0, q, r));
-    st_stream(&d1[i], barrett128(m, q, r.x, r.y));
-    st_stream(&d2[i], mulmod_b(a1, b1, q, r));
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const size_t j = i + (size_t)2 * kThreads * p;
+        st_stream2(&d0[j], r0[2 * p], r0[2 * p + 1]);
+        st_stream2(&d1[j], r1[2 * p], r1[2 * p + 1]);
+        st_stream2(&d2[j], r2[2 * p], r2[2 * p + 1]);
+    }
 }
 
 // ModUp base conversion per digit (src/rns_bconv.cu:455-485, :522-528, :530-628):
@@ -300,8 +343,12 @@ void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *
                uint64_t d2_stride = 0) {
     check_chain(c, chain);
     const uint32_t Ql = c.size_Ql(chain);
-    hipLaunchKernelGGL(k_tensor, grid(c, Ql, count), dim3(kThreads), 0, s, a, b, d0, d1, d2, c.mod, c.ratio, Ql, c.N,
-                       in_stride, d_stride, d2_stride);
+    require(c.N % (kThreads * kTensorE) == 0, "poly_modulus_degree too small for the tensor kernel");
+    require(((uintptr_t)a | (uintptr_t)b | (uintptr_t)d0 | (uintptr_t)d1 | (uintptr_t)d2) % 16 == 0 &&
+                (in_stride | d_stride | d2_stride) % 2 == 0,
+            "tensor operands must be 16-byte aligned");
+    hipLaunchKernelGGL(k_tensor, dim3(c.N / (kThreads * kTensorE), Ql, count), dim3(kThreads), 0, s, a, b, d0, d1, d2,
+                       c.mod, c.ratio, Ql, c.N, in_stride, d_stride, d2_stride);
     PFA_HIP(hipGetLastError());
 }
 
