@@ -66,10 +66,22 @@ struct U128 {
     uint64_t lo, hi;
 };
 
+// Full 64 x 64 -> 128-bit product from the four 32 x 32 partial products,
+// each one v_mad_u64_u32 (32 x 32 + 64 -> 64); written out because a * b and
+// __umul64hi(a, b) separately take 3 + 4 multiplies.  No sum overflows:
+// s1, s2 <= (2^32 - 1)^2 + 2^32 - 1 < 2^64 and hi <= (2^32 - 1)^2 + 2 (2^32 - 1).
+__device__ __forceinline__ U128 mul_wide(uint64_t a, uint64_t b) {
+    const uint64_t a0 = (uint32_t)a, a1 = a >> 32, b0 = (uint32_t)b, b1 = b >> 32;
+    const uint64_t p00 = a0 * b0;
+    const uint64_t s1 = a1 * b0 + (p00 >> 32);
+    const uint64_t s2 = a0 * b1 + (uint32_t)s1;
+    return U128{(s2 << 32) | (uint32_t)p00, a1 * b1 + (s1 >> 32) + (s2 >> 32)};
+}
+
 __device__ __forceinline__ void mac(U128 &acc, uint64_t a, uint64_t b) {
-    uint64_t lo = a * b, hi = mulhi64(a, b);
-    acc.lo += lo;
-    acc.hi += hi + (acc.lo < lo ? 1 : 0);
+    const U128 p = mul_wide(a, b);
+    acc.lo += p.lo;
+    acc.hi += p.hi + (acc.lo < p.lo ? 1 : 0);
 }
 
 // x mod q for any 128-bit x, with ratio = floor(2^128 / q) = (r1 : r0).
@@ -94,10 +106,11 @@ __device__ __forceinline__ uint64_t barrett128(U128 x, uint64_t q, uint64_t r0, 
 // y < q with q < 2^62); qn = -q^-1 mod 2^64.  With m = lo(x y) qn, x y + m q is
 // a multiple of 2^64 whose low word sums to 0 or 2^64 (lo(x y) != 0).
 __device__ __forceinline__ uint64_t mont_mul(uint64_t x, uint64_t y, uint64_t q, uint64_t qn) {
-    const uint64_t lo = x * y, hi = mulhi64(x, y);
-    const uint64_t m = lo * qn;
-    return hi + mulhi64(m, q) + (lo != 0 ? 1 : 0);
+    const U128 p = mul_wide(x, y);
+    const uint64_t m = p.lo * qn;
+    return p.hi + mulhi64(m, q) + (p.lo != 0 ? 1 : 0);
 }
+
 
 // ----------------------------------------------------------------------------
 // NTT arithmetic policies.  Twiddle table entries are 16-byte pairs whose
