@@ -980,11 +980,20 @@ def mod_switch_to_next(ctx: context, obj):
 
 
 def mod_switch_to(ctx: context, obj, chain_index: int):
+    """Drops the primes above chain_index's level in one copy (the same limbs
+    as repeated mod_switch_to_next, which copies once per prime)."""
     if chain_index < obj.chain_index():
         raise ValueError("cannot switch to a higher level modulus")
-    while obj.chain_index() < chain_index:
-        obj = mod_switch_to_next(ctx, obj)
-    return obj
+    if chain_index == obj.chain_index():
+        return obj
+    if chain_index > ctx.size_Q:
+        raise ValueError("end of modulus switching chain reached")
+    L = ctx.size_Ql(chain_index)
+    if isinstance(obj, plaintext):
+        pt = plaintext()
+        pt.data, pt._chain_index, pt._scale = obj.data[:L].contiguous(), chain_index, obj.scale()
+        return pt
+    return obj._like(obj.data[:, :L].contiguous(), chain=chain_index)
 
 
 def mod_switch_to_inplace(ctx: context, obj, chain_index: int) -> None:
