@@ -5,6 +5,8 @@
   Python integers in tests/test_bootstrap_math.py.
 * pfa_ct_lincomb (the integer-weighted sums of EvalMod) is bit-exact against
   Python integers.
+* Every CoeffToSlot / SlotToCoeff layer is bit-exact against the oracle
+  running the same rotations, diagonal products, sums and rescale.
 * End to end, the reference's acceptance test is the bar: decoded slots after
   bootstrap within 1e-3 of the input (test/ckks_engine_test.cu:182-188); the
   refreshed ciphertext must also take a further multiplication.
@@ -196,3 +198,65 @@ def test_cheb63_evalmod_bundle_matches_tracks(boot12):
     for a, b in zip(alone, both):
         assert a.chain_index() == b.chain_index() and a.scale() == b.scale()
         assert bool((a.data == b.data).all())
+
+
+def _oracle_layer(orc, ph, N, chain, ct, lt, plan, i, keys):
+    """One transform layer (hoisted baby rotations, the diagonal products, the
+    giant rotations, their sum, the rescale) run operation by operation on the
+    oracle: rotations by apply_galois / hoist_rotations (src/evaluate.cu:1607-1656,
+    :2041-2045), products by mul_poly, sums mod q."""
+    n1, _, _ = lt.baby_giant(i)
+    unit = lt.units[i]
+    qs = orc.moduli[:orc.size_Ql(chain)]
+    rot = {0: ct}
+    moved = [b for b in plan.babies if b]
+    if moved:
+        elts = [ph.get_elt_from_step(b * unit, N) for b in moved]
+        for b, r in zip(moved, orc.hoist_rotations(chain, ct, elts, [keys[e] for e in elts], threads=8)):
+            rot[b] = r
+    M = len(plan.babies)
+    acc = np.zeros_like(ct)
+    for g, step in enumerate(plan.giants):
+        part = np.zeros_like(ct)
+        for bi, b in enumerate(plan.babies):
+            pt = to_host(plan.grid[g * M + bi])
+            for k in range(2):
+                part[k] = _add_mod(part[k], orc.mul_poly(pt, rot[b][k]), qs)
+        if step:
+            e = ph.get_elt_from_step(ph._signed_step(step * n1 * unit, lt.n), N)
+            part = orc.apply_galois(chain, part, e, keys[e], threads=8)
+        acc = _add_mod(acc, part, qs)
+    return orc.rescale(chain, acc, threads=8)
+
+
+def _add_mod(a, b, qs):
+    out = a + b  # residues below 2^61: no uint64 overflow
+    for l, q in enumerate(qs):
+        out[..., l, :] %= np.uint64(q)
+    return out
+
+
+def test_transform_layers_match_oracle(boot12):
+    """Every layer of CoeffToSlot and SlotToCoeff, as bootstrap runs them
+    (_apply_layer: one hoisted ModUp for the babies, pfa_bsgs_mac for the
+    diagonal products, the giants as one batched rotation, one weighted sum,
+    the rescale), has the residues of the oracle running the same operations
+    one by one on the same diagonals.  The inputs are fresh encryptions at the
+    layers' levels (the residue algebra does not depend on the message)."""
+    ph, ctx, sk, enc, bk = boot12
+    orc = O.Oracle(ctx.N, ctx.moduli, ctx.size_P)
+    keys = {e: to_host(k) for e, k in bk.glk.keys.items()}
+    rng = np.random.default_rng(21)
+    cases = [(bk.c2s, bk.c2s_pts, i, 1 + i) for i in range(len(bk.c2s_pts))]
+    cases += [(bk.s2c, bk.s2c_pts, i, bk.s2c_start + i) for i in range(len(bk.s2c_pts))]
+    rotations = 0
+    for n, (lt, pts, i, chain) in enumerate(cases):
+        plan = pts[i]
+        rotations += sum(1 for b in plan.babies if b) + sum(1 for g in plan.giants if g)
+        z = rng.uniform(-1, 1, enc.slot_count()) + 1j * rng.uniform(-1, 1, enc.slot_count())
+        ct = sk.encrypt_symmetric(ctx, enc.encode_complex_vector(ctx, z, 2.0 ** 30, chain), seed=22 + n)
+        got = ph._apply_layer(ctx, ct, lt, pts, i, bk.glk)
+        assert got.chain_index() == chain + 1
+        want = _oracle_layer(orc, ph, ctx.N, chain, to_host(ct.data), lt, plan, i, keys)
+        assert np.array_equal(to_host(got.data), want), (chain, i)
+    assert len(cases) == 6 and rotations >= 12  # babies and giants in both transforms
