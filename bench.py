@@ -53,12 +53,29 @@ def uniform(torch, shape, mods, dev, gen):
     return out.view(torch.uint64)
 
 
+def spin_up(torch, step, ms=40.0, chunk=20, cap=20000):
+    """Runs step(i) untimed until the GPU has been kept busy for about `ms`
+    milliseconds, before a workload's warm-up and timed steps: the MI355X's
+    clocks ramp up under sustained load (measured on the config-2 forward NTT:
+    36.9-37.4 us per transform after 20 warm-up steps, 33.9-34.2 us after 500
+    or 2000, interleaved on one box).  Returns the number of steps run."""
+    torch.cuda.synchronize()
+    t0, n = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < ms and n < cap:
+        for _ in range(chunk):
+            step(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
 def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
     """Returns (wall seconds for `steps` transforms, average ms per transform from
     HIP events recorded on the launch stream around the whole timed region)."""
     stream = torch.cuda.current_stream()
     h = stream.cuda_stream
     fn = ctx.ntt_inverse if inverse else ctx.ntt_forward
+    spin_up(torch, lambda i: fn(batches[i % len(batches)], POLYS, LIMBS, 0, h))
     for i in range(warmup):
         fn(batches[i % len(batches)], POLYS, LIMBS, 0, h)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -82,6 +99,7 @@ def time_copy(torch, P, batches, steps, warmup):
     h = stream.cuda_stream
     dsts = [torch.empty_like(b) for b in batches]
     n = len(batches)
+    spin_up(torch, lambda i: P.stream_copy(dsts[(i + 3) % n], batches[i % n], 0, h))
     for i in range(warmup):
         P.stream_copy(dsts[(i + 3) % n], batches[i % n], 0, h)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -141,9 +159,14 @@ def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
     out = torch.empty((2, nq, N), dtype=torch.uint64, device=dev)
     res = torch.empty((2, nq - 1, N), dtype=torch.uint64, device=dev)
     s = torch.cuda.current_stream().cuda_stream
-    for _ in range(warmup):
+
+    def separate(_):
         ctx.multiply_and_relin(1, a, b, key, out, s)
         ctx.rescale(1, out, res, s)
+
+    spin_up(torch, separate, chunk=4)
+    for i in range(warmup):
+        separate(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
