@@ -45,8 +45,10 @@ uint32_t grid_for(const Ctx &c, uint32_t tiles, int wpc) {
 // tiles of 8 rows for 2048 resident workgroups (8 per CU) instead of 1120 of
 // 16 rows for 1024: the tiles dealt beyond one per workgroup are a smaller
 // share of a CU's work (measured on the 2 x 35-limb batch, five interleaved
-// pairs: rows pass 20.4 -> 19.5 us).  The inverse rows pass measured the same
-// with either height and keeps 16.
+// pairs: rows pass 20.4 -> 19.5 us).  The staged inverse rows pass (batches of
+// 48 limbs or more) measured the same with either height and keeps 16; the
+// prefetching one (the key switch's INTTs, 6 workgroups per CU) takes 8 rows:
+// L = 35 HMult 0.800 / 0.801 -> 0.797 / 0.798 ms, config 3 unchanged.
 template <int S1, int S2>
 constexpr int half_rows() {
     using G = Geo<S1, S2>;
@@ -81,6 +83,10 @@ void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     if (ml >= kInvStagedLimbs)
         hipLaunchKernelGGL((ntt_inv_rows_staged<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, 3)),
                            dim3(G::ROW_THREADS), 0, s, b, t);
+    else if (half_rows<S1, S2>() != G::ROWS && c.ntt_half_rows_inv)
+        hipLaunchKernelGGL((ntt_inv_rows<S1, S2, half_rows<S1, S2>()>),
+                           dim3(grid_for(c, ml * (G::N1 / half_rows<S1, S2>()), c.ntt_wpc * (G::ROWS / half_rows<S1, S2>()))),
+                           dim3(half_rows<S1, S2>() * Sub<S2>::T), 0, s, b, t);
     else
         hipLaunchKernelGGL((ntt_inv_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc)),
                            dim3(G::ROW_THREADS), 0, s, b, t);

@@ -690,37 +690,38 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     }
 }
 
-template <int S1, int S2>
-__global__ void __launch_bounds__((Geo<S1, S2>::ROW_THREADS)) ntt_inv_rows(NttBatch b, NttTables t) {
+template <int S1, int S2, int R = Geo<S1, S2>::ROWS>
+__global__ void __launch_bounds__(R * Sub<S2>::T) ntt_inv_rows(NttBatch b, NttTables t) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
-    __shared__ double lds[G::ROW_LDS];
-    const uint32_t total = b.M * b.L * G::ROW_TILES;
+    constexpr uint32_t TILES = G::N1 / R;
+    __shared__ double lds[R * G::ROW_PITCH];
+    const uint32_t total = b.M * b.L * TILES;
     const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
-    uint32_t cur = next_tile(b, G::ROW_TILES, blockIdx.x, total);
+    uint32_t cur = next_tile(b, TILES, blockIdx.x, total);
     uint64_t raw[SB::E];
     if (cur < total) {
-        const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, cur), b.src, b.sstride);
+        const uint64_t *s = rows_ptr<S1, S2, R>(b, decode_tile(b, TILES, cur), b.src, b.sstride);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = ld_stream(&s[F + SB::T * e]);
     }
     while (cur < total) {
-        const uint32_t nxt = next_tile(b, G::ROW_TILES, cur + gridDim.x, total);
-        const TileRef r = decode_tile(b, G::ROW_TILES, cur);
+        const uint32_t nxt = next_tile(b, TILES, cur + gridDim.x, total);
+        const TileRef r = decode_tile(b, TILES, cur);
         uint64_t nraw[SB::E];
         if (nxt < total) {
-            const uint64_t *s = rows_ptr<S1, S2>(b, decode_tile(b, G::ROW_TILES, nxt), b.src, b.sstride);
+            const uint64_t *s = rows_ptr<S1, S2, R>(b, decode_tile(b, TILES, nxt), b.src, b.sstride);
 #pragma unroll
             for (int e = 0; e < SB::E; e++) nraw[e] = ld_stream(&s[F + SB::T * e]);
         }
         const uint32_t prow = b.map.row(r.l);
         const uint64_t q = t.mod[prow];
-        const TileTw w = global_tw<S1, S2>(t, prow, r.tile * G::ROWS + rr, false);
+        const TileTw w = global_tw<S1, S2>(t, prow, r.tile * R + rr, false);
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_rows_tile<ArithF64, S1, S2, G::N1>(raw, w, r, q, lds, olimb);
+            inv_rows_tile<ArithF64, S1, S2, G::N1, true, R>(raw, w, r, q, lds, olimb);
         else
-            inv_rows_tile<ArithInt, S1, S2, G::N1>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
+            inv_rows_tile<ArithInt, S1, S2, G::N1, true, R>(raw, w, r, q, reinterpret_cast<uint64_t *>(lds), olimb);
 #pragma unroll
         for (int e = 0; e < SB::E; e++) raw[e] = nraw[e];
         cur = nxt;
