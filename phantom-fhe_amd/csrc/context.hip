@@ -154,6 +154,15 @@ static void create_coeff_modulus(uint64_t N, const int *bits, size_t count, uint
 // ---------------------------------------------------------------- context
 static uint64_t two32_mod(uint64_t q) { return (uint64_t)(((u128)1 << 32) % q); }
 
+// Second factor pair of a base-conversion entry m for target q: FP64 policy,
+// the pair of m 2^32 mod q (the high half of a wide input); integer policy,
+// m 2^64 mod q (the factor of the Montgomery-accumulated conversion).
+static ulonglong2 bconv_pair1(uint64_t m, uint64_t q) {
+    if (q < kF64PrimeBound) return ntt_pair(mulmod(m, two32_mod(q), q), q);
+    const uint64_t r64 = (uint64_t)((((u128)1 << 64) - 1) % q + 1) % q;  // 2^64 mod q
+    return ulonglong2{mulmod(m, r64, q), 0};
+}
+
 static uint64_t prod_mod(const uint64_t *m, size_t n, size_t skip, uint64_t p) {
     uint64_t r = 1 % p;
     for (size_t k = 0; k < n; ++k)
@@ -227,6 +236,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
         const u128 r1 = ((~(u128)0) % q + 1) % q;  // 2^128 mod q
         mont[r] = ulonglong2{(uint64_t)0 - qi, (uint64_t)r1};
     }
+    c.max_modulus = *std::max_element(c.moduli.begin(), c.moduli.end());
     c.mod = c.upload(c.moduli);
     c.ratio = c.upload(ratio);
     c.mont = c.upload(mont);
@@ -243,6 +253,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_HALF_ROWS")) c.ntt_half_rows = std::atoi(w);
+    if (const char *w = std::getenv("PFA_BCONV_MONT")) c.bconv_mont = std::atoi(w);
     if (const char *w = std::getenv("PFA_NTT_HALF_ROWS_INV")) c.ntt_half_rows_inv = std::atoi(w);
     // The key-switch inner product splits the items left over after whole
     // rounds of its resident workgroups by digit range; PFA_WS_SLOTS sets the
@@ -286,7 +297,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
                 const uint64_t m = prod_mod(Pm, alpha, j, Qm[i]);
                 mat[(size_t)j * c.Q + i] = m;
                 bc[((size_t)j * c.Q + i) * 2] = ntt_pair(m, Qm[i]);
-                bc[((size_t)j * c.Q + i) * 2 + 1] = ntt_pair(mulmod(m, two32_mod(Qm[i]), Qm[i]), Qm[i]);
+                bc[((size_t)j * c.Q + i) * 2 + 1] = bconv_pair1(m, Qm[i]);
             }
         }
         for (uint32_t i = 0; i < c.Q; ++i) {
@@ -296,14 +307,14 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             pinv_p[i] = ntt_pair(invmod(pm, q), q);
             pq[i] = shoup_pair(pm, q);
             unit[(size_t)i * 2] = ntt_pair(1 % q, q);
-            unit[(size_t)i * 2 + 1] = ntt_pair(two32_mod(q), q);
+            unit[(size_t)i * 2 + 1] = bconv_pair1(1 % q, q);
             mdr[(size_t)i * 2] = unit[(size_t)i * 2];
             mdr[(size_t)i * 2 + 1] = unit[(size_t)i * 2 + 1];
             for (uint32_t j = 0; j < alpha; ++j) {
                 const uint64_t g = invmod(Pm[j] % q, q);
                 const size_t k = ((size_t)(1 + j) * c.Q + i) * 2;
                 mdr[k] = ntt_pair(g, q);
-                mdr[k + 1] = ntt_pair(mulmod(g, two32_mod(q), q), q);
+                mdr[k + 1] = bconv_pair1(g, q);
             }
         }
         for (uint32_t j = 0; j < alpha; ++j) pq[c.Q + j] = ulonglong2{0, 0};
@@ -341,7 +352,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
                     const size_t k = ((size_t)b * alpha + i) * QlP + r;
                     mat[k] = m;
                     bc[k * 2] = ntt_pair(m, p);
-                    bc[k * 2 + 1] = ntt_pair(mulmod(m, two32_mod(p), p), p);
+                    bc[k * 2 + 1] = bconv_pair1(m, p);
                 }
             }
         }

@@ -88,6 +88,11 @@ struct BconvCols {
     // every factor is 1 (ModUp with alpha = 1: Q_b = q_i; the rescale's single
     // input): a lone input below 2^50 is then only reduced, not multiplied
     uint32_t unit = 0;
+    // integer-policy targets with two inputs or more: 128-bit sums of the
+    // inputs times the factors in Montgomery form (pair 1, m 2^64 mod q) and
+    // one Montgomery reduction (the context's constants -q^-1 mod 2^64); set by
+    // the launcher when every input sum stays below 2^64, else null (Shoup)
+    const ulonglong2 *mont = nullptr;
 };
 
 __device__ __forceinline__ uint32_t bconv_in_row(const BconvCols &a, uint32_t row0, uint32_t i) {
@@ -103,7 +108,8 @@ __device__ __forceinline__ const ulonglong2 *bc_of(const BconvCols &a, uint32_t 
 
 template <class A, int S1, int S2>
 __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables &t, const A &ar, uint32_t mi,
-                                             uint32_t g, uint32_t j, uint32_t tile, typename A::T (&x)[Sub<S1>::E]) {
+                                             uint32_t g, uint32_t j, uint32_t tile, uint32_t prow,
+                                             typename A::T (&x)[Sub<S1>::E]) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
     const uint32_t c = threadIdx.x % kCols, F = threadIdx.x / kCols;
@@ -157,6 +163,25 @@ __device__ __forceinline__ void bconv_source(const BconvCols &a, const NttTables
         }
     } else {
         const uint64_t q = ar.q, q2 = ar.q2;
+        if (a.mont && n_in >= 2) {
+            // sum_i t_i (m_i 2^64 mod q) < q sum_i t_i < q 2^64, so one
+            // Montgomery reduction gives sum_i t_i m_i mod q in [0, 2q): 4
+            // multiplies per input and 7 for the reduction, against a
+            // 10-multiply Shoup product per input
+            const uint64_t qn = ld_const(reinterpret_cast<const uint64_t *>(a.mont + prow));
+            U128 acc[SB::E];
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) acc[e] = U128{0, 0};
+            for (uint32_t i = 0; i < n_in; i++) {
+                const uint64_t mm = ld_const(reinterpret_cast<const uint64_t *>(bc_of(a, g, i, j) + 1));
+                const uint64_t *src = base + (size_t)i * G::N;
+#pragma unroll
+                for (int e = 0; e < SB::E; e++) mac(acc[e], src[(size_t)(F + SB::T * e) * G::N2], mm);
+            }
+#pragma unroll
+            for (int e = 0; e < SB::E; e++) x[e] = mont_reduce(acc[e], q, qn);
+            return;
+        }
         uint64_t acc[SB::E];
 #pragma unroll
         for (int e = 0; e < SB::E; e++) acc[e] = 0;
@@ -195,7 +220,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
         if (q < kF64PrimeBound) {
             const ArithF64 ar(q);
             double x[SB::E];
-            bconv_source<ArithF64, S1, S2>(a, t, ar, mi, g, j, tile, x);
+            bconv_source<ArithF64, S1, S2>(a, t, ar, mi, g, j, tile, prow, x);
             st.store(twl);
             __syncthreads();
             fwd_cols_core<ArithF64, S1, S2>(x, ar, twl, lds);
@@ -203,7 +228,7 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
         } else {
             const ArithInt ar(q);
             uint64_t x[SB::E];
-            bconv_source<ArithInt, S1, S2>(a, t, ar, mi, g, j, tile, x);
+            bconv_source<ArithInt, S1, S2>(a, t, ar, mi, g, j, tile, prow, x);
             st.store(twl);
             __syncthreads();
             fwd_cols_core<ArithInt, S1, S2>(x, ar, twl, reinterpret_cast<uint64_t *>(lds));
@@ -874,8 +899,12 @@ uint32_t fgrid(const Ctx &c, uint32_t items, uint32_t wpc) {
 }
 
 template <int S1, int S2>
-void launch_bconv(const Ctx &c, const BconvCols &a, hipStream_t s) {
+void launch_bconv(const Ctx &c, const BconvCols &a0, hipStream_t s) {
     using G = Geo<S1, S2>;
+    BconvCols a = a0;
+    // the Montgomery-accumulated sums need sum_i t_i < 2^64; every input is
+    // below the context's largest prime
+    if (c.bconv_mont && c.max_modulus <= ~0ull / std::max(a.n_in, a.n_in_last)) a.mont = c.mont;
     const uint32_t total = grouped_total(a.batch * a.groups * G::COL_TILES, a.J);
     hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
                        tables_of(c));

@@ -129,6 +129,8 @@ struct Ctx {
     int n_cu = 256;                  // compute units of the device
     int ntt_wpc = 3;                 // resident workgroups per CU of the prefetching inverse rows pass
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
+    uint64_t max_modulus = 0;        // the largest prime of the context
+    int bconv_mont = 1;              // Montgomery-accumulated integer conversions (PFA_BCONV_MONT=0: Shoup)
     int ntt_half_rows_inv = 1;       // the same for the prefetching inverse rows pass (PFA_NTT_HALF_ROWS_INV=0: full)
     int ntt_half_rows = 1;           // forward rows pass on half-height tiles (PFA_NTT_HALF_ROWS=0: full)
     uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)

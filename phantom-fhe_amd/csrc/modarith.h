@@ -102,6 +102,12 @@ __device__ __forceinline__ uint64_t barrett128(U128 x, uint64_t q, uint64_t r0, 
     return csub(r, q);
 }
 
+// Montgomery reduction T 2^-64 mod q, in [0, 2q), of a 128-bit T < q 2^64.
+__device__ __forceinline__ uint64_t mont_reduce(U128 t, uint64_t q, uint64_t qn) {
+    const uint64_t m = t.lo * qn;
+    return t.hi + mulhi64(m, q) + (t.lo != 0 ? 1 : 0);
+}
+
 // Montgomery product x y 2^-64 mod q, in [0, 2q), for x y < q 2^64 (e.g. x < 4q,
 // y < q with q < 2^62); qn = -q^-1 mod 2^64.  With m = lo(x y) qn, x y + m q is
 // a multiple of 2^64 whose low word sums to 0 or 2^64 (lo(x y) != 0).
