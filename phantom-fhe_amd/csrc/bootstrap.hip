@@ -53,11 +53,23 @@ __device__ __forceinline__ uint64_t signed_mod(int64_t v, uint64_t q) {
     return v < 0 && r ? q - r : r;
 }
 
+// Each thread takes two adjacent residues (16-byte accesses) and requests
+// every term's values before the first product: with the term loop rolled, the
+// load of term t + 1 was issued only after term t's value had arrived (one
+// load in flight per thread).
+using u64x2 = unsigned long long __attribute__((ext_vector_type(2)));
+
 __global__ void __launch_bounds__(kThreads)
 k_ct_lincomb(LincombArgs a, uint64_t *out, const uint64_t *mod, const ulonglong2 *ratio) {
     __shared__ uint64_t w[kMaxTerms + 1];
-    const uint32_t l = blockIdx.y, k = blockIdx.z, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t l = blockIdx.y, k = blockIdx.z, n = (blockIdx.x * kThreads + threadIdx.x) * 2;
     const uint64_t q = mod[l];
+    u64x2 v[kMaxTerms];
+#pragma unroll
+    for (int t = 0; t < kMaxTerms; t++)
+        if (t < (int)a.n)
+            v[t] = __builtin_nontemporal_load(
+                reinterpret_cast<const u64x2 *>(a.in[t] + ((size_t)k * a.in_L[t] + l) * a.N + n));
     if (threadIdx.x < a.n) {
         w[threadIdx.x] = signed_mod(a.k[threadIdx.x], q);
     } else if (threadIdx.x == kMaxTerms) {
@@ -75,10 +87,17 @@ k_ct_lincomb(LincombArgs a, uint64_t *out, const uint64_t *mod, const ulonglong2
         w[kMaxTerms] = r;
     }
     __syncthreads();
-    U128 acc{w[kMaxTerms], 0};
-    for (uint32_t t = 0; t < a.n; t++)
-        mac(acc, w[t], ld_stream(a.in[t] + ((size_t)k * a.in_L[t] + l) * a.N + n));
-    st_stream(out + ((size_t)k * a.L + l) * a.N + n, barrett128(acc, q, ratio[l].x, ratio[l].y));
+    U128 acc0{w[kMaxTerms], 0}, acc1{w[kMaxTerms], 0};
+#pragma unroll
+    for (int t = 0; t < kMaxTerms; t++)
+        if (t < (int)a.n) {
+            mac(acc0, w[t], v[t].x);
+            mac(acc1, w[t], v[t].y);
+        }
+    u64x2 r;
+    r.x = barrett128(acc0, q, ratio[l].x, ratio[l].y);
+    r.y = barrett128(acc1, q, ratio[l].x, ratio[l].y);
+    __builtin_nontemporal_store(r, reinterpret_cast<u64x2 *>(out + ((size_t)k * a.L + l) * a.N + n));
 }
 
 }  // namespace
@@ -135,7 +154,9 @@ int pfa_ct_lincomb(const pfa_context *ctx, size_t L, size_t size, size_t ct_size
         }
         a.L = (uint32_t)L;
         a.N = c.N;
-        hipLaunchKernelGGL(k_ct_lincomb, dim3(c.N / kThreads, (uint32_t)L, (uint32_t)size), dim3(kThreads), 0,
+        require((reinterpret_cast<uintptr_t>(out) & 15) == 0, "output must be 16-byte aligned");
+        for (size_t t = 0; t < n; t++) require((reinterpret_cast<uintptr_t>(ins[t]) & 15) == 0, "inputs must be 16-byte aligned");
+        hipLaunchKernelGGL(k_ct_lincomb, dim3(c.N / (2 * kThreads), (uint32_t)L, (uint32_t)size), dim3(kThreads), 0,
                            as_stream(stream), a, out, c.mod, c.ratio);
         PFA_HIP(hipGetLastError());
     });
