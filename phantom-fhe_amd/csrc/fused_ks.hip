@@ -882,9 +882,20 @@ __global__ void k_mdr_last(uint64_t *x, const uint64_t *g, const uint64_t *mod, 
     for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
         const uint32_t m = idx / N, k = idx % N;
         uint64_t *base = x + (size_t)m * (alpha + 1) * N + k;
+        // the limbs' values are requested before the first product, 8 at a time
+        // (a rolled loop waited for each value before requesting the next)
+        const uint64_t x0 = base[0];
         U128 acc{0, 0};
-        for (uint32_t i = 0; i < alpha; i++) mac(acc, base[(size_t)(i + 1) * N], g[i]);
-        base[0] = sub_mod(base[0], barrett128(acc, q, rt.x, rt.y), q);
+        for (uint32_t i0 = 0; i0 < alpha; i0 += 8) {
+            uint64_t v[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++)
+                if (i0 + u < alpha) v[u] = base[(size_t)(i0 + u + 1) * N];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++)
+                if (i0 + u < alpha) mac(acc, v[u], ld_const(g + i0 + u));
+        }
+        base[0] = sub_mod(x0, barrett128(acc, q, rt.x, rt.y), q);
     }
 }
 
