@@ -57,7 +57,6 @@ __device__ __forceinline__ uint64_t signed_mod(int64_t v, uint64_t q) {
 // every term's values before the first product: with the term loop rolled, the
 // load of term t + 1 was issued only after term t's value had arrived (one
 // load in flight per thread).
-using u64x2 = unsigned long long __attribute__((ext_vector_type(2)));
 
 __global__ void __launch_bounds__(kThreads)
 k_ct_lincomb(LincombArgs a, uint64_t *out, const uint64_t *mod, const ulonglong2 *ratio) {

@@ -254,6 +254,7 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_NTT_HALF_ROWS")) c.ntt_half_rows = std::atoi(w);
     if (const char *w = std::getenv("PFA_BCONV_MONT")) c.bconv_mont = std::atoi(w);
+    if (const char *w = std::getenv("PFA_TENSOR_ROWS")) c.tensor_rows = std::atoi(w);
     if (const char *w = std::getenv("PFA_NTT_HALF_ROWS_INV")) c.ntt_half_rows_inv = std::atoi(w);
     // The key-switch inner product splits the items left over after whole
     // rounds of its resident workgroups by digit range; PFA_WS_SLOTS sets the

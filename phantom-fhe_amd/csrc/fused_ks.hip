@@ -899,6 +899,107 @@ __global__ void k_mdr_last(uint64_t *x, const uint64_t *g, const uint64_t *mod, 
     }
 }
 
+// ------------------------------------------------------------ tensor + INTT rows
+// The HMult's tensor product with the first pass of the key switch's INTT(d2)
+// fused in.  One workgroup per (member, limb, tile of R rows); a tile's R N2
+// residues are contiguous in the limb, so the tensor reads and writes them with
+// 16-byte accesses, thread t taking pairs 2t + 2 NT p.  d2 is still written in
+// NTT form (the inner product reads its own-digit limbs from it) and goes
+// through LDS into the inverse rows pass, whose output the inverse columns pass
+// reads: d2 is not read back from HBM and the rows pass needs no launch of its
+// own (the ModUp's INTT over Ql limbs is a fraction of a round of tiles).
+struct TensorRows {
+    const uint64_t *a, *b;
+    uint64_t *d0, *d1, *d2, *mid;
+    const ulonglong2 *ratio;
+    uint32_t Ql, count;
+    uint64_t in_stride, d_stride, d2_stride, mid_stride;
+    const ulonglong2 *itw;  // set per workgroup: the tile's prime's inverse table
+};
+
+template <class A, int S1, int S2, int R>
+__device__ __forceinline__ void tensor_rows_tile(const TensorRows &a, RowStage<S1, S2, R> &stage,
+                                                 ulonglong2 *twl, const TileRef &r, uint64_t q,
+                                                 typename A::T *lds) {
+    using G = Geo<S1, S2>;
+    using RS = RowStage<S1, S2, R>;
+    constexpr uint32_t NT = R * Sub<S2>::T;
+    constexpr int P = Sub<S2>::E / 2, H = P / 2;
+    static_assert(2 * NT * P == R * G::N2 && 2 * H == P, "a tile is NT threads x 2P residues");
+    const A ar(q);
+    ulonglong2 rt{0, 0};
+    if constexpr (!A::kF64) rt = ld_const(a.ratio + r.l);
+    // wave-uniform tile bases and a 32-bit per-thread index: the accesses
+    // address scalar base + vector offset
+    const size_t base = (size_t)r.l * G::N + (size_t)r.tile * R * G::N2;
+    const uint64_t LN = (uint64_t)a.Ql * G::N;
+    const uint64_t *pa0 = a.a + r.m * a.in_stride + base, *pb0 = a.b + r.m * a.in_stride + base;
+    const uint64_t *pa1 = pa0 + LN, *pb1 = pb0 + LN;
+    uint64_t *d0 = a.d0 + r.m * a.d_stride + base, *d1 = a.d1 + r.m * a.d_stride + base;
+    uint64_t *d2 = a.d2 + r.m * a.d2_stride + base;
+    // a window of W pairs in flight: pair k's products are stored as they are
+    // formed and pair k + W is requested in their place (all 4P inputs at once
+    // would need 8P VGPRs of loads alone); tile element i = 2 t + 2 NT p + h is
+    // element i mod N2 of tile row i / N2
+    constexpr int W = H;
+    u64x2 a0[P], a1[P], b0[P], b1[P];
+    const auto request = [&](int p) {
+        const uint32_t j = 2 * threadIdx.x + 2 * NT * p;
+        a0[p] = ld_stream2(pa0 + j);
+        a1[p] = ld_stream2(pa1 + j);
+        b0[p] = ld_stream2(pb0 + j);
+        b1[p] = ld_stream2(pb1 + j);
+    };
+#pragma unroll
+    for (int p = 0; p < W; p++) request(p);
+    // visible to the rounds after the barrier that follows the LDS fill
+    stage.st.store(twl);
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        uint64_t r0[2], r1[2], r2[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            if constexpr (A::kF64)
+                tensor_elem(ar, a0[p][h], a1[p][h], b0[p][h], b1[p][h], r0[h], r1[h], r2[h]);
+            else
+                tensor_elem(q, rt, a0[p][h], a1[p][h], b0[p][h], b1[p][h], r0[h], r1[h], r2[h]);
+        }
+        const uint32_t j = 2 * threadIdx.x + 2 * NT * p;
+        st_stream2(d0 + j, r0[0], r0[1]);
+        st_stream2(d1 + j, r1[0], r1[1]);
+        st_stream2(d2 + j, r2[0], r2[1]);
+        if (p + W < P) request(p + W);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t i = j + h;
+            lds[(i / G::N2) * G::ROW_PITCH + rpad(i % G::N2)] = ar.load(r2[h]);
+        }
+    }
+    __syncthreads();
+    const TileTw w = RS::view(twl, a.itw, threadIdx.x / Sub<S2>::T);
+    inv_rows_lds<A, S1, S2, R, true, R>(w, r, q, lds, a.mid + r.m * a.mid_stride + (size_t)r.l * G::N);
+}
+
+template <int S1, int S2, int R>
+__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(4, 8)))
+k_tensor_rows(TensorRows a, NttTables t) {
+    using G = Geo<S1, S2>;
+    using RS = RowStage<S1, S2, R>;
+    constexpr uint32_t TILES = G::N1 / R;
+    __shared__ double lds[R * G::ROW_PITCH];
+    __shared__ ulonglong2 twl[RS::N];
+    const TileRef r{blockIdx.y, blockIdx.x / TILES, blockIdx.x % TILES};
+    const uint64_t q = ld_const(t.mod + r.l);
+    a.itw = t.itw + (size_t)r.l * G::N;
+    // the tile's twiddle factors are requested before its residues
+    RS stage;
+    stage.load(t, r.l, r.tile, false);
+    if (q < kF64PrimeBound)
+        tensor_rows_tile<ArithF64, S1, S2, R>(a, stage, twl, r, q, lds);
+    else
+        tensor_rows_tile<ArithInt, S1, S2, R>(a, stage, twl, r, q, reinterpret_cast<uint64_t *>(lds));
+}
+
 // ------------------------------------------------------------ launchers
 NttTables tables_of(const Ctx &c) {
     return NttTables{c.mod, c.tw, c.itw, c.ninv, c.small_fw, c.small_inv, c.rb_fw, c.rb_inv};
@@ -920,6 +1021,21 @@ void launch_bconv(const Ctx &c, const BconvCols &a0, hipStream_t s) {
     hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
                        tables_of(c));
     PFA_HIP(hipGetLastError());
+}
+
+// Rows per tile: 8 for rows of 256 (N = 2^15, 2^16: 8 workgroups of 128
+// threads fill a CU), the inverse rows pass's own height otherwise.
+template <int S1, int S2>
+void launch_tensor_rows(const Ctx &c, const TensorRows &a, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    if constexpr (S2 > 8) {
+        fail(PFA_ERR_INVALID_ARGUMENT, "fused tensor rows pass: N above 2^16");
+    } else {
+        constexpr int R = S2 == 8 && G::ROWS == 16 ? 8 : G::ROWS;
+        hipLaunchKernelGGL((k_tensor_rows<S1, S2, R>), dim3(a.Ql * (G::N1 / R), a.count), dim3(R * Sub<S2>::T), 0, s,
+                           a, tables_of(c));
+        PFA_HIP(hipGetLastError());
+    }
 }
 
 // largest number of split items one launch may have (arrival counters per workspace)
@@ -995,16 +1111,22 @@ void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
 // product against key [dnum][2][QP][N].
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
                        hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold,
-                       const uint64_t *const *key_table) {
+                       const uint64_t *const *key_table, const uint64_t *c2_mid) {
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
     const uint64_t LN = (uint64_t)Ql * c.N, IN = (uint64_t)lv.beta * QlP * c.N;
     Scratch sc(c, s);
     uint64_t *tin = sc.alloc((size_t)batch * LN);
     uint64_t *inter = sc.alloc((size_t)batch * IN);
-    NttLaunch inv{c2, tin, c2_stride, LN, batch, Ql};
-    inv.scale = lv.modup_scale;
-    ntt_inverse(c, inv, s);
+    if (c2_mid) {
+        NttLaunch inv{c2_mid, tin, LN, LN, batch, Ql};
+        inv.scale = lv.modup_scale;
+        ntt_inverse_cols(c, inv, s);
+    } else {
+        NttLaunch inv{c2, tin, c2_stride, LN, batch, Ql};
+        inv.scale = lv.modup_scale;
+        ntt_inverse(c, inv, s);
+    }
     BconvCols b{};
     b.in = tin;
     b.out = inter;
@@ -1045,6 +1167,20 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
         r.fold_f = c.pinv + (Ql - 1);
     }
     PFA_FUSED_DISPATCH(launch_inner, r);
+}
+
+void fused_tensor_rows(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0,
+                       uint64_t *d1, uint64_t *d2, uint64_t *mid, hipStream_t s, uint32_t count,
+                       uint64_t in_stride, uint64_t d_stride, uint64_t d2_stride) {
+    const uint32_t Ql = c.level(chain).Ql;
+    require(c.logN <= 16, "fused tensor rows pass: N above 2^16");
+    require(count >= 1 && (count == 1 || (in_stride && d_stride && d2_stride)), "bad tensor batch");
+    require(((uintptr_t)a | (uintptr_t)b | (uintptr_t)d0 | (uintptr_t)d1 | (uintptr_t)d2 | (uintptr_t)mid) % 16 == 0 &&
+                (in_stride | d_stride | d2_stride) % 2 == 0,
+            "tensor operands must be 16-byte aligned");
+    const TensorRows t{a, b, d0, d1, d2, mid, c.ratio, Ql, count, in_stride, d_stride, d2_stride, (uint64_t)Ql * c.N,
+                       nullptr};
+    PFA_FUSED_DISPATCH(launch_tensor_rows, t);
 }
 
 // The rescale of base + ModDown(cx) without forming the ModDown output.  With

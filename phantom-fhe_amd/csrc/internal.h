@@ -131,6 +131,7 @@ struct Ctx {
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
     uint64_t max_modulus = 0;        // the largest prime of the context
     int bconv_mont = 1;              // Montgomery-accumulated integer conversions (PFA_BCONV_MONT=0: Shoup)
+    int tensor_rows = 1;             // HMult tensor with the INTT rows pass fused in (PFA_TENSOR_ROWS=0: apart)
     int ntt_half_rows_inv = 1;       // the same for the prefetching inverse rows pass (PFA_NTT_HALF_ROWS_INV=0: full)
     int ntt_half_rows = 1;           // forward rows pass on half-height tiles (PFA_NTT_HALF_ROWS=0: full)
     uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)
@@ -253,6 +254,9 @@ struct NttLaunch {
 // workspace (the single-launch path takes control blocks from it)
 void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow = true);
 void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flow = true);
+// The inverse's columns pass alone: a.src holds the output of its rows pass
+// (fused_tensor_rows), a.dst receives the canonical coefficients.
+void ntt_inverse_cols(const Ctx &c, const NttLaunch &a, hipStream_t s);
 // True when the device deals a launch's workgroups to 8 XCDs round-robin
 // (workgroup w on XCD (w + r) mod 8 for some r), which the single-launch NTT is
 // built for; runs a probe kernel.
@@ -270,9 +274,20 @@ struct KsFold {
     uint64_t stride = 0;
 };
 // With key_table (a device array of batch key pointers), member i uses its own key.
+// With c2_mid ([batch][Ql][N], from fused_tensor_rows), the ModUp's INTT runs
+// its columns pass only, on c2_mid.
 void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
                        hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0,
-                       const KsFold *fold = nullptr, const uint64_t *const *key_table = nullptr);
+                       const KsFold *fold = nullptr, const uint64_t *const *key_table = nullptr,
+                       const uint64_t *c2_mid = nullptr);
+// The tensor product of count ciphertext pairs (as op_tensor: member i reads
+// a, b at + i in_stride, writes d0, d1 at + i d_stride, d2 at + i d2_stride)
+// with the first pass of the key switch's INTT(d2) fused in: mid [count][Ql][N]
+// receives the inverse rows pass over d2, the input fused_modup_inner takes as
+// c2_mid.  N = 2^10 .. 2^16.
+void fused_tensor_rows(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0,
+                       uint64_t *d1, uint64_t *d2, uint64_t *mid, hipStream_t s, uint32_t count,
+                       uint64_t in_stride, uint64_t d_stride, uint64_t d2_stride);
 // cx [2][QlP][N] from fused_modup_inner with a fold over base -> out [2][Ql-1][N]
 // = rescale(base + ModDown(cx)), bit-identical to fused_moddown then fused_rescale.
 // With count > 1: cx [count][2][QlP][N], member i's bases at + i base_stride,

@@ -273,4 +273,42 @@ __device__ __forceinline__ uint32_t galois_perm(uint32_t elt, uint32_t i, uint32
     return brv(raw, logN);
 }
 
+// Two adjacent residues moved as one 16-byte access, with the streaming hints
+// of ld_stream / st_stream.
+using u64x2 = unsigned long long __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u64x2 ld_stream2(const uint64_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u64x2 *>(p));
+}
+__device__ __forceinline__ void st_stream2(uint64_t *p, uint64_t x, uint64_t y) {
+    u64x2 v;
+    v.x = x;
+    v.y = y;
+    __builtin_nontemporal_store(v, reinterpret_cast<u64x2 *>(p));
+}
+
+// One residue of the degree-2 tensor product (a0 + a1 s)(b0 + b1 s) mod q
+// (tensor_prod_2x2_rns_poly, src/polymath.cu:463-498): d0 = a0 b0,
+// d1 = a0 b1 + a1 b0, d2 = a1 b1, all canonical.  FP64 policy (q < 2^50):
+// |a b / q| < q < 2^50 keeps fl(a fl(b/q)) within 3/8 of the true quotient, so
+// each product is within 0.875 q and a sum of two stays far below 2^53.
+__device__ __forceinline__ void tensor_elem(const ArithF64 &ar, uint64_t a0, uint64_t a1, uint64_t b0, uint64_t b1,
+                                            uint64_t &d0, uint64_t &d1, uint64_t &d2) {
+    const double x0 = ar.load(a0), x1 = ar.load(a1), y0 = ar.load(b0), y1 = ar.load(b1);
+    const double q0 = y0 * ar.qinv, q1 = y1 * ar.qinv;
+    d0 = ar.store(ar.mulw(x0, y0, q0));
+    d1 = ar.store(ar.mulw(x0, y1, q1) + ar.mulw(x1, y0, q0));
+    d2 = ar.store(ar.mulw(x1, y1, q1));
+}
+// Integer policy: Barrett reduction of each 128-bit product or sum of two
+// (r = floor(2^128 / q) as (lo, hi)).
+__device__ __forceinline__ void tensor_elem(uint64_t q, ulonglong2 r, uint64_t a0, uint64_t a1, uint64_t b0,
+                                            uint64_t b1, uint64_t &d0, uint64_t &d1, uint64_t &d2) {
+    U128 m{0, 0};
+    mac(m, a0, b1);
+    mac(m, a1, b0);
+    d0 = barrett128(U128{a0 * b0, mulhi64(a0, b0)}, q, r.x, r.y);
+    d1 = barrett128(m, q, r.x, r.y);
+    d2 = barrett128(U128{a1 * b1, mulhi64(a1, b1)}, q, r.x, r.y);
+}
+
 }  // namespace pfa

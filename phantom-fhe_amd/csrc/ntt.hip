@@ -76,6 +76,14 @@ void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
 // batches of at least this many limbs take the inverse rows pass with staged twiddles
 constexpr uint32_t kInvStagedLimbs = 48;
 
+// the inverse columns pass alone: b.src holds the rows pass's output
+template <int S1, int S2>
+void inv_cols(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, b.M * b.L * G::COL_TILES, c.ntt_wpc_fwd)),
+                       dim3(G::COL_THREADS), 0, s, b, t);
+}
+
 template <int S1, int S2>
 void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
@@ -93,8 +101,7 @@ void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    hipLaunchKernelGGL((ntt_inv_cols<S1, S2>), dim3(grid_for(c, ml * G::COL_TILES, c.ntt_wpc_fwd)), dim3(G::COL_THREADS), 0, s, b2,
-                       t);
+    inv_cols<S1, S2>(c, b2, t, s);
 }
 
 void check_launch(const Ctx &c, const NttLaunch &a) {
@@ -193,6 +200,15 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flo
         return;
     }
     PFA_NTT_DISPATCH(inv);
+    PFA_HIP(hipGetLastError());
+}
+
+void ntt_inverse_cols(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+    check_launch(c, a);
+    const NttBatch b = make_batch(c, a);
+    const NttTables t = tables(c);
+    check_device_errors(c);
+    PFA_NTT_DISPATCH(inv_cols);
     PFA_HIP(hipGetLastError());
 }
 

@@ -650,9 +650,11 @@ ntt_fwd_rows(NttBatch b, NttTables t) {
 
 // ================================================================ inverse
 // Rows pass first: src (canonical) -> dst (intermediate).
+// The pass over a tile whose residues are in LDS already (element k of tile row
+// rr at lds[rr ROW_PITCH + rpad(k)], as A::load gives it), after a barrier.
 template <class A, int S1, int S2, int RBS, bool NT = true, int R = Geo<S1, S2>::ROWS>
-__device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
-                                              uint64_t q, typename A::T *lds, uint64_t *olimb) {
+__device__ __forceinline__ void inv_rows_lds(const TileTw &w, const TileRef &r, uint64_t q, typename A::T *lds,
+                                             uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -662,9 +664,6 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
     uint64_t *drow = olimb + (size_t)k1 * G::N2;
     T *lr = lds + rr * G::ROW_PITCH;
     T x[SB::E];
-#pragma unroll
-    for (int e = 0; e < SB::E; e++) lr[rpad(F + SB::T * e)] = ar.load(raw[e]);
-    __syncthreads();
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
     if constexpr (A::kF64)
@@ -688,6 +687,20 @@ __device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E],
         else
             drow[F + SB::T * e] = ar.store_mid(x[e]);
     }
+}
+
+template <class A, int S1, int S2, int RBS, bool NT = true, int R = Geo<S1, S2>::ROWS>
+__device__ __forceinline__ void inv_rows_tile(const uint64_t (&raw)[Sub<S2>::E], const TileTw &w, const TileRef &r,
+                                              uint64_t q, typename A::T *lds, uint64_t *olimb) {
+    using G = Geo<S1, S2>;
+    using SB = Sub<S2>;
+    const A ar(q);
+    const uint32_t F = threadIdx.x % SB::T, rr = threadIdx.x / SB::T;
+    typename A::T *lr = lds + rr * G::ROW_PITCH;
+#pragma unroll
+    for (int e = 0; e < SB::E; e++) lr[rpad(F + SB::T * e)] = ar.load(raw[e]);
+    __syncthreads();
+    inv_rows_lds<A, S1, S2, RBS, NT, R>(w, r, q, lds, olimb);
 }
 
 template <int S1, int S2, int R = Geo<S1, S2>::ROWS>

@@ -65,27 +65,12 @@ k_from_signed(const int64_t *in, uint64_t *out, const uint64_t *mod, uint32_t st
     out[(size_t)l * N + n] = r;
 }
 
-// tensor_prod_2x2_rns_poly (src/polymath.cu:463-498):
-//   d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1  (mod q_l)
-// (primes below 2^50: exact FP64 products; |a b / q| < q < 2^50 keeps
-// fl(a fl(b/q)) within 3/8 of the true quotient, so each product is within
-// 0.875 q and a sum of two stays far below 2^53)
-// Member z = blockIdx.z of a batch reads a, b at + z in_stride and writes
-// d0, d1 at + z d_stride, d2 at + z d2_stride.  Each thread takes kTensorE
-// elements in pairs of adjacent ones (16-byte accesses); the prime and its
-// Barrett ratio are scalar loads.
-using u64x2 = unsigned long long __attribute__((ext_vector_type(2)));
+// tensor_prod_2x2_rns_poly (src/polymath.cu:463-498), each residue by
+// tensor_elem.  Member z = blockIdx.z of a batch reads a, b at + z in_stride
+// and writes d0, d1 at + z d_stride, d2 at + z d2_stride.  Each thread takes
+// kTensorE elements in pairs of adjacent ones (16-byte accesses); the prime and
+// its Barrett ratio are scalar loads.
 constexpr int kTensorE = 4;  // elements per thread, in 16-byte pairs
-
-__device__ __forceinline__ u64x2 ld_stream2(const uint64_t *p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u64x2 *>(p));
-}
-__device__ __forceinline__ void st_stream2(uint64_t *p, uint64_t x, uint64_t y) {
-    u64x2 v;
-    v.x = x;
-    v.y = y;
-    __builtin_nontemporal_store(v, reinterpret_cast<u64x2 *>(p));
-}
 
 __global__ void __launch_bounds__(kThreads)
 k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint64_t *d2, const uint64_t *mod,
@@ -117,24 +102,14 @@ k_tensor(const uint64_t *a, const uint64_t *b, uint64_t *d0, uint64_t *d1, uint6
 #pragma unroll
         for (int e = 0; e < kTensorE; e++) {
             const int p = e / 2, h = e % 2;
-            const double x0 = ar.load(a0[p][h]), x1 = ar.load(a1[p][h]), y0 = ar.load(b0[p][h]),
-                         y1 = ar.load(b1[p][h]);
-            const double q0 = y0 * ar.qinv, q1 = y1 * ar.qinv;
-            r0[e] = ar.store(ar.mulw(x0, y0, q0));
-            r1[e] = ar.store(ar.mulw(x0, y1, q1) + ar.mulw(x1, y0, q0));
-            r2[e] = ar.store(ar.mulw(x1, y1, q1));
+            tensor_elem(ar, a0[p][h], a1[p][h], b0[p][h], b1[p][h], r0[e], r1[e], r2[e]);
         }
     } else {
         const ulonglong2 r = ld_const(ratio + l);
 #pragma unroll
         for (int e = 0; e < kTensorE; e++) {
             const int p = e / 2, h = e % 2;
-            U128 m{0, 0};
-            mac(m, a0[p][h], b1[p][h]);
-            mac(m, a1[p][h], b0[p][h]);
-            r0[e] = mulmod_b(a0[p][h], b0[p][h], q, r);
-            r1[e] = barrett128(m, q, r.x, r.y);
-            r2[e] = mulmod_b(a1[p][h], b1[p][h], q, r);
+            tensor_elem(q, r, a0[p][h], a1[p][h], b0[p][h], b1[p][h], r0[e], r1[e], r2[e]);
         }
     }
 #pragma unroll
@@ -304,8 +279,10 @@ void op_moddown(const Ctx &c, uint32_t chain, const uint64_t *cx, uint32_t M, ui
 // out[k] = base_k + KS(c2)_k for k = 0, 1 (out [2][Ql][N]; bases may alias out or be null).
 // With count > 1, member i switches c2 + i c2_stride into out + i 2 Ql N with
 // bases + i base_stride (the same key).
+// With c2_mid (from tensor_for_ks), the ModUp's INTT starts from it.
 void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum, uint64_t *out,
-                  Bases base, hipStream_t s, uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0) {
+                  Bases base, hipStream_t s, uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0,
+                  const uint64_t *c2_mid = nullptr) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
@@ -313,7 +290,7 @@ void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64
     Scratch sc(c, s);
     const uint64_t cxs = (uint64_t)2 * (lv.Ql + c.P) * c.N;
     uint64_t *cx = sc.alloc((size_t)count * cxs);
-    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs);
+    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs, nullptr, nullptr, c2_mid);
     fused_moddown(c, chain, cx, 2 * count, out, base.p[0], base.p[1], s, base_stride);
 }
 
@@ -322,7 +299,8 @@ void op_keyswitch(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64
 // count > 1, member i: c2 + i c2_stride, bases + i base_stride, out + i 2 (Ql-1) N.
 void op_keyswitch_rescale(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, size_t dnum,
                           const uint64_t *base0, const uint64_t *base1, uint64_t *out, hipStream_t s,
-                          uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0) {
+                          uint32_t count = 1, uint64_t c2_stride = 0, uint64_t base_stride = 0,
+                          const uint64_t *c2_mid = nullptr) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
@@ -332,7 +310,7 @@ void op_keyswitch_rescale(const Ctx &c, uint32_t chain, const uint64_t *c2, cons
     const uint64_t cxs = (uint64_t)2 * (lv.Ql + c.P) * c.N;
     uint64_t *cx = sc.alloc((size_t)count * cxs);
     const KsFold fold{base0, base1, base_stride};
-    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs, &fold);
+    fused_modup_inner(c, chain, c2, key, cx, s, count, c2_stride, cxs, &fold, nullptr, c2_mid);
     fused_moddown_rescale(c, chain, cx, base0, base1, out, s, count, base_stride);
 }
 
@@ -350,6 +328,24 @@ void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *
     hipLaunchKernelGGL(k_tensor, dim3(c.N / (kThreads * kTensorE), Ql, count), dim3(kThreads), 0, s, a, b, d0, d1, d2,
                        c.mod, c.ratio, Ql, c.N, in_stride, d_stride, d2_stride);
     PFA_HIP(hipGetLastError());
+}
+
+// op_tensor for a product whose d2 is key-switched next: at N <= 2^16 the
+// tensor kernel also runs the first pass of the key switch's INTT(d2) and the
+// returned buffer (count x Ql N, from sc) holds it for op_keyswitch /
+// op_keyswitch_rescale; otherwise (or with PFA_TENSOR_ROWS=0) plain op_tensor
+// and nullptr.
+const uint64_t *tensor_for_ks(const Ctx &c, Scratch &sc, uint32_t chain, const uint64_t *a, const uint64_t *b,
+                              uint64_t *d0, uint64_t *d1, uint64_t *d2, hipStream_t s, uint32_t count = 1,
+                              uint64_t in_stride = 0, uint64_t d_stride = 0, uint64_t d2_stride = 0) {
+    if (!c.tensor_rows || c.logN > 16) {
+        op_tensor(c, chain, a, b, d0, d1, d2, s, count, in_stride, d_stride, d2_stride);
+        return nullptr;
+    }
+    check_chain(c, chain);
+    uint64_t *mid = sc.alloc((size_t)count * c.size_Ql(chain) * c.N);
+    fused_tensor_rows(c, chain, a, b, d0, d1, d2, mid, s, count, in_stride, d_stride, d2_stride);
+    return mid;
 }
 
 void op_galois(const Ctx &c, uint32_t elt, const uint64_t *src, uint64_t *dst, uint32_t L, hipStream_t s) {
@@ -426,8 +422,8 @@ int pfa_multiply_and_relin(const pfa_context *ctx, size_t chain_index, const uin
         const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
         Scratch sc(c, s);
         uint64_t *c2 = sc.alloc(LN);
-        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2, s);
-        op_keyswitch(c, (uint32_t)chain_index, c2, rlk, key_dnum, out, Bases{{out, out + LN}}, s);
+        const uint64_t *mid = tensor_for_ks(c, sc, (uint32_t)chain_index, a, b, out, out + LN, c2, s);
+        op_keyswitch(c, (uint32_t)chain_index, c2, rlk, key_dnum, out, Bases{{out, out + LN}}, s, 1, 0, 0, mid);
     });
 }
 
@@ -455,8 +451,8 @@ int pfa_multiply_relin_rescale(const pfa_context *ctx, size_t chain_index, const
         const size_t LN = (size_t)c.size_Ql((uint32_t)chain_index) * c.N;
         Scratch sc(c, s);
         uint64_t *d = sc.alloc(3 * LN);
-        op_tensor(c, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s);
-        op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s);
+        const uint64_t *mid = tensor_for_ks(c, sc, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s);
+        op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s, 1, 0, 0, mid);
     });
 }
 
@@ -475,9 +471,10 @@ int pfa_multiply_and_relin_batch(const pfa_context *ctx, size_t chain_index, siz
         Scratch sc(c, s);
         uint64_t *c2 = sc.alloc(count * LN);
         // d0, d1 into out (the key switch adds to them in place), d2 of member i to c2 + i LN
-        op_tensor(c, (uint32_t)chain_index, a, b, out, out + LN, c2, s, (uint32_t)count, 2 * LN, 2 * LN, LN);
+        const uint64_t *mid = tensor_for_ks(c, sc, (uint32_t)chain_index, a, b, out, out + LN, c2, s,
+                                            (uint32_t)count, 2 * LN, 2 * LN, LN);
         op_keyswitch(c, (uint32_t)chain_index, c2, rlk, key_dnum, out, Bases{{out, out + LN}}, s, (uint32_t)count,
-                     LN, 2 * LN);
+                     LN, 2 * LN, mid);
     });
 }
 
@@ -497,9 +494,10 @@ int pfa_multiply_relin_rescale_batch(const pfa_context *ctx, size_t chain_index,
         Scratch sc(c, s);
         // member i: d0, d1, d2 at d + i 3 LN
         uint64_t *d = sc.alloc(count * 3 * LN);
-        op_tensor(c, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s, (uint32_t)count, 2 * LN, 3 * LN, 3 * LN);
+        const uint64_t *mid = tensor_for_ks(c, sc, (uint32_t)chain_index, a, b, d, d + LN, d + 2 * LN, s,
+                                            (uint32_t)count, 2 * LN, 3 * LN, 3 * LN);
         op_keyswitch_rescale(c, (uint32_t)chain_index, d + 2 * LN, rlk, key_dnum, d, d + LN, out, s, (uint32_t)count,
-                             3 * LN, 3 * LN);
+                             3 * LN, 3 * LN, mid);
     });
 }
 

@@ -244,6 +244,27 @@ def test_multiply_relin_rescale_config3(dev):
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("logN", [10, 11, 14, 15, 17])
+def test_multiply_tensor_rows_geometries(dev, logN):
+    """The HMult's tensor kernel runs the key switch's first INTT pass over d2
+    at N <= 2^16 (one kernel per row geometry: 32 rows of 4 threads at N = 2^10,
+    2^11, 16 or 8 rows of 16 threads above) and the plain tensor + INTT above:
+    multiply_and_relin and multiply_relin_rescale bit-exact against the oracle
+    at each, with 60-bit primes (integer policy) in Q."""
+    st = Setup(logN, 4, 2, seed=21, bits=[60, 50, 60, 50, 60, 60])
+    chain = 1
+    a, b, key = st.ct(chain), st.ct(chain), st.key()
+    want = st.orc.multiply_and_relin(chain, a, b, key, threads=8)
+    out = empty(a.shape, dev)
+    st.ctx.multiply_and_relin(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), out)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    res = empty((2, a.shape[1] - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), to_dev(key, dev), res)
+    got, want = to_host(res), st.orc.rescale(chain, want, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
 def test_multiply_relin_rescale_errors(dev):
     st = Setup(12, 3, 1)
     key = to_dev(st.key(), dev)
