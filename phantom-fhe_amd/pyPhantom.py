@@ -1915,34 +1915,77 @@ def _cheb_depth(deg: int) -> int:
     return max(_cheb_depth(deg - m) + 1, m.bit_length(), _cheb_depth(m - 1))
 
 
+class _GpuEngine:
+    """The ciphertext operations both EvalMod families are written over, run by
+    the native library: mod_switch_to, a weighted sum with integer weights
+    (pfa_ct_lincomb), multiply_and_relin (with and without the rescale),
+    rescale_to_next and add.  The test suite runs the same EvalMod code over
+    an oracle implementation of these operations and compares residues."""
+
+    def __init__(self, ctx, rlk):
+        self.ctx, self.rlk = ctx, rlk
+
+    def size_Ql(self, chain: int) -> int:
+        return self.ctx.size_Ql(chain)
+
+    def prime(self, i: int) -> int:
+        return self.ctx.moduli[i]
+
+    def to(self, a, chain: int):
+        return mod_switch_to(self.ctx, a, chain)
+
+    def lincomb(self, terms, bias, chain: int, scale: float, like):
+        """sum_t k_t a_t (+ bias on poly 0 of each member) over the first
+        size_Ql(chain) limbs of every input, as a ciphertext like `like` at
+        chain and scale; the k_t are Python ints in int64 range, bias a Python
+        int or None."""
+        L = self.ctx.size_Ql(chain)
+        out = self.ctx._empty(like.size(), L, self.ctx.N)
+        _ct_lincomb(self.ctx, L, [a.data for a, _ in terms], [k for _, k in terms], out, bias, like._members)
+        return like._like(out, chain=chain, scale=scale)
+
+    def mul_relin(self, a, b):
+        return multiply_and_relin(self.ctx, a, b, self.rlk)
+
+    def mul_relin_rescale(self, a, b):
+        return multiply_and_relin_rescale(self.ctx, a, b, self.rlk)
+
+    def rescale(self, a):
+        return rescale_to_next(self.ctx, a)
+
+    def add(self, a, b):
+        return add(self.ctx, a, b)
+
+
 def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
     """cos(2 pi (K t - 1/4) / 2^r) by Chebyshev (Paterson-Stockmeyer splitting at
     powers of two, src/evalmod.cu:196-335 for the pattern), then r double
-    angles: sin(2 pi K t) for t in [-1, 1].
+    angles: sin(2 pi K t) for t in [-1, 1]."""
+    return _eval_mod_cheb(_GpuEngine(ctx, bk.rlk), ct, list(bk.cheb), bk.r)
 
-    Every weighted sum is one pfa_ct_lincomb over the Chebyshev terms at their
-    own levels, with the integer weights round(c_j S q / scale_j) that land it
-    at the exact scale S q, followed by one rescale to S: scales never drift
-    and no addition mixes them.  T_k = 2 T_a T_b - T_1 and 2 y^2 - 1 are formed
-    the same way before their rescale."""
-    N = ctx.N
+
+def _eval_mod_cheb(eng, ct, cheb, r: int):
+    """_eval_mod's operation sequence over an engine (see _GpuEngine).
+
+    Every weighted sum is one lincomb over the Chebyshev terms at their own
+    levels, with the integer weights round(c_j S q / scale_j) that land it at
+    the exact scale S q, followed by one rescale to S: scales never drift and
+    no addition mixes them.  T_k = 2 T_a T_b - T_1 and 2 y^2 - 1 are formed the
+    same way before their rescale."""
     T = {1: ct}
 
     def q_drop(chain):
-        return ctx.moduli[ctx.size_Ql(chain) - 1]
+        return eng.prime(eng.size_Ql(chain) - 1)
 
     def lincomb(terms, bias, chain, scale):
-        L = ctx.size_Ql(chain)
         for _, k in terms:
             if not -(1 << 63) <= k < (1 << 63):
                 raise ValueError("Chebyshev weight outside int64")
-        out = ctx._empty(ct.size(), L, N)
-        _ct_lincomb(ctx, L, [c.data for c, _ in terms], [k for _, k in terms], out, bias, ct._members)
-        return ct._like(out, chain=chain, scale=scale)
+        return eng.lincomb(terms, bias, chain, scale, ct)
 
     def product(a, b):
         c = max(a.chain_index(), b.chain_index())
-        return multiply_and_relin(ctx, mod_switch_to(ctx, a, c), mod_switch_to(ctx, b, c), bk.rlk)
+        return eng.mul_relin(eng.to(a, c), eng.to(b, c))
 
     def cheb_T(k):
         if k in T:
@@ -1954,7 +1997,7 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
             p = product(cheb_T((k + 1) // 2), cheb_T((k - 1) // 2))
             t1 = cheb_T(1)
             pre = lincomb([(p, 2), (t1, -round(p.scale() / t1.scale()))], None, p.chain_index(), p.scale())
-        T[k] = rescale_to_next(ctx, pre)
+        T[k] = eng.rescale(pre)
         return T[k]
 
     def evaluate(c, target_scale, target_chain):
@@ -1968,20 +2011,20 @@ def _eval_mod(ctx, ct: ciphertext, bk: bootstrap_key) -> ciphertext:
                     t = cheb_T(j)
                     terms.append((t, round(c[j] * target_scale * q / t.scale())))
             pre = lincomb(terms, round(c[0] * target_scale * q), chain, target_scale * q)
-            r = rescale_to_next(ctx, pre)
-            r.set_scale(target_scale)
-            return r
+            res = eng.rescale(pre)
+            res.set_scale(target_scale)
+            return res
         m, hi, lo = _cheb_split(c)
-        Tm = mod_switch_to(ctx, cheb_T(m), chain)
+        Tm = eng.to(cheb_T(m), chain)
         hi_ct = evaluate(hi, target_scale * q / Tm.scale(), chain)
-        prod = multiply_and_relin_rescale(ctx, Tm, hi_ct, bk.rlk)
+        prod = eng.mul_relin_rescale(Tm, hi_ct)
         prod.set_scale(target_scale)
-        return add(ctx, prod, evaluate(lo, target_scale, target_chain))
+        return eng.add(prod, evaluate(lo, target_scale, target_chain))
 
-    y = evaluate(list(bk.cheb), ct.scale(), ct.chain_index() + _cheb_depth(len(bk.cheb) - 1))
-    for _ in range(bk.r):
+    y = evaluate(list(cheb), ct.scale(), ct.chain_index() + _cheb_depth(len(cheb) - 1))
+    for _ in range(r):
         p = product(y, y)
-        y = rescale_to_next(ctx, lincomb([(p, 2)], -round(p.scale()), p.chain_index(), p.scale()))
+        y = eng.rescale(lincomb([(p, 2)], -round(p.scale()), p.chain_index(), p.scale()))
     return y
 
 
@@ -2047,14 +2090,6 @@ def _ct_lincomb(ctx, L: int, ins, consts, out, bias, members: int = 1) -> None:
     ctx.native.ct_lincomb(L, ins, consts, out, bias, ct_size=None if members == 1 else 2)
 
 
-def _tracks_bundled() -> bool:
-    """bootstrap steps its two EvalMod tracks as one bundle unless
-    PFA_BOOT_BUNDLE=0 (per-track calls, same residues; for A/B measurement)."""
-    import os
-
-    return os.environ.get("PFA_BOOT_BUNDLE", "1") != "0"
-
-
 def _bundle(ctx, cts) -> ciphertext:
     """Size-2 ciphertexts at one level and scale -> one bundle (their data stacked)."""
     t = _torch()
@@ -2078,18 +2113,19 @@ def _unbundle(b: ciphertext) -> list:
 
 
 class _EvalModOps:
-    """The reference's EvalMod operations on ciphertexts (or, for the float64
-    model of the same polynomial, on arrays of slot values: ctx None)."""
+    """The reference's EvalMod operations on ciphertexts through an engine (see
+    _GpuEngine), or, for the float64 model of the same polynomial, on arrays of
+    slot values (eng None)."""
 
-    def __init__(self, ctx, rk, target_scale: float):
-        self.ctx, self.rk, self.s = ctx, rk, float(target_scale)
+    def __init__(self, eng, target_scale: float):
+        self.eng, self.s = eng, float(target_scale)
 
     def _chain(self, a):
-        return a.chain_index() if self.ctx else 0
+        return a.chain_index() if self.eng else 0
 
     def to(self, a, chain):  # align_to: drop to the deeper level
-        if self.ctx and a.chain_index() < chain:
-            return mod_switch_to(self.ctx, a, chain)
+        if self.eng and a.chain_index() < chain:
+            return self.eng.to(a, chain)
         return a
 
     def align(self, a, b):  # align_pair
@@ -2099,34 +2135,28 @@ class _EvalModOps:
     def lincomb(self, terms, bias: float = 0.0):
         """sum c_i a_i + bias over ciphertexts at one level and scale; the
         weights c_i are small integers (2, 1, -1) and bias a real constant."""
-        if not self.ctx:
+        if not self.eng:
             return sum(c * a for a, c in terms) + bias
         a0 = terms[0][0]
         chain = a0.chain_index()
         for a, _ in terms:
             if a.chain_index() != chain or abs(a.scale() - a0.scale()) > 1e-9 * a0.scale():
                 raise ValueError("EvalMod operands differ in level or scale")
-        L = self.ctx.size_Ql(chain)
-        out = self.ctx._empty(*a0.data.shape[:1], L, self.ctx.N)
         b = int(round(bias * a0.scale())) if bias else None
-        _ct_lincomb(self.ctx, L, [a.data for a, _ in terms], [c for _, c in terms], out, b, a0._members)
-        return a0._like(out)
+        return self.eng.lincomb(terms, b, chain, a0.scale(), a0)
 
     def mul(self, a, b):  # multiply_and_relin, rescale_to_next, snap
-        if not self.ctx:
+        if not self.eng:
             return a * b
-        r = multiply_and_relin_rescale(self.ctx, a, b, self.rk)
+        r = self.eng.mul_relin_rescale(a, b)
         r.set_scale(self.s)
         return r
 
     def square_minus(self, a, scalar: float):  # 2 (a^2 + scalar): the reference adds, then doubles
         sq = self.mul(a, a)
-        if not self.ctx:
+        if not self.eng:
             return 2 * (sq + scalar)
-        L = self.ctx.size_Ql(sq.chain_index())
-        out = self.ctx._empty(sq.size(), L, self.ctx.N)
-        _ct_lincomb(self.ctx, L, [sq.data], [2], out, 2 * int(round(scalar * sq.scale())), sq._members)
-        return sq._like(out)
+        return self.eng.lincomb([(sq, 2)], 2 * int(round(scalar * sq.scale())), sq.chain_index(), sq.scale(), sq)
 
     def weighted_sum(self, basis, coeffs):
         """weighted_sum_chebyshev: coeffs[0] + sum_(i >= 1) coeffs[i] basis[i-1],
@@ -2135,19 +2165,16 @@ class _EvalModOps:
         terms = [(basis[i - 1], coeffs[i]) for i in range(1, len(coeffs)) if abs(coeffs[i]) >= 1e-50]
         if not terms:
             raise ValueError("weighted_sum_chebyshev: all coefficients zero")
-        if not self.ctx:
+        if not self.eng:
             acc = sum(c * t for t, c in terms)
             return acc + coeffs[0] if abs(coeffs[0]) >= 1e-50 else acc
         bs = basis[0].scale()
         chain = basis[0].chain_index()
-        L = self.ctx.size_Ql(chain)
         for t, _ in terms:
             if t.chain_index() != chain:
                 raise ValueError("weighted_sum_chebyshev: basis levels differ")
-        out = self.ctx._empty(basis[0].size(), L, self.ctx.N)
-        ws = [int(round(c * bs)) for _, c in terms]
-        _ct_lincomb(self.ctx, L, [t.data for t, _ in terms], ws, out, None, basis[0]._members)
-        acc = rescale_to_next(self.ctx, basis[0]._like(out, scale=bs * bs))
+        ws = [(t, int(round(c * bs))) for t, c in terms]
+        acc = self.eng.rescale(self.eng.lincomb(ws, None, chain, bs * bs, basis[0]))
         acc.set_scale(self.s)
         if abs(coeffs[0]) >= 1e-50:
             acc = self.lincomb([(acc, 1)], coeffs[0])
@@ -2244,14 +2271,7 @@ def _double_angle(ops: _EvalModOps, ct, R: int):
     j = 1 .. R (the reference squares, rescales, doubles, then adds)."""
     for j in range(1, R + 1):
         scalar = -(2 * np.pi) ** (-(2.0 ** (j - R)))
-        sq = ops.mul(ct, ct)
-        if not ops.ctx:
-            ct = 2 * sq + scalar
-            continue
-        L = ops.ctx.size_Ql(sq.chain_index())
-        out = ops.ctx._empty(sq.size(), L, ops.ctx.N)
-        _ct_lincomb(ops.ctx, L, [sq.data], [2], out, int(round(scalar * sq.scale())), sq._members)
-        ct = sq._like(out)
+        ct = ops.lincomb([(ops.mul(ct, ct), 2)], scalar)
     return ct
 
 
@@ -2271,7 +2291,12 @@ def _evalmod(context: context, ct: ciphertext, relin_keys: relin_key, variant: s
     need = EVALMOD_LEVELS[variant]
     if context.size_Ql(ct.chain_index()) <= need:
         raise ValueError(f"EvalMod {variant} consumes {need} levels: the ciphertext has too few primes left")
-    ops = _EvalModOps(context, relin_keys, ct.scale())
+    return _evalmod_ops(_GpuEngine(context, relin_keys), ct, variant)
+
+
+def _evalmod_ops(eng, ct, variant: str):
+    """An EvalMod variant's operation sequence over an engine (see _GpuEngine)."""
+    ops = _EvalModOps(eng, ct.scale())
     return _double_angle(ops, _sine(ops, ct, variant), EVALMOD_R[variant])
 
 
@@ -2280,7 +2305,7 @@ def evalmod_model(x, variant: str = "k28_r3"):
     in float64 with the same operation sequence (no encryption, no rounding
     of the constants): the value the decrypted EvalMod output approximates,
     itself an approximation of sin(2 pi K x) / (2 pi) on [-1, 1]."""
-    ops = _EvalModOps(None, None, 1.0)
+    ops = _EvalModOps(None, 1.0)
     x = np.asarray(x, dtype=np.float64)
     return _double_angle(ops, _sine(ops, x, variant), EVALMOD_R[variant])
 
@@ -2402,10 +2427,7 @@ def _bootstrap_evalround(ctx, ct: ciphertext, bk: bootstrap_key, user_scale: flo
     real = rescale_to_next(ctx, add(ctx, u, conj))
     imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))
     # both tracks through EvalRound in lockstep: one batched call per step
-    if _tracks_bundled():
-        real, imag = _unbundle(_eval_round(ctx, _bundle(ctx, [real, imag]), bk.rlk))
-    else:
-        real, imag = _eval_round(ctx, real, bk.rlk), _eval_round(ctx, imag, bk.rlk)
+    real, imag = _unbundle(_eval_round(ctx, _bundle(ctx, [real, imag]), bk.rlk))
     imag = _times_i(ctx, imag, 1)
     c = max(real.chain_index(), imag.chain_index())
     real, imag = mod_switch_to(ctx, real, c), mod_switch_to(ctx, imag, c)
@@ -2483,10 +2505,7 @@ def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: boots
     real = rescale_to_next(ctx, add(ctx, u, conj))                     # Re(x) / K
     imag = rescale_to_next(ctx, _times_i(ctx, sub(ctx, u, conj), -1))  # Im(x) / K
     # both tracks through EvalMod in lockstep: one batched call per step
-    if _tracks_bundled():
-        real, imag = _unbundle(_eval_mod(ctx, _bundle(ctx, [real, imag]), bk))
-    else:
-        real, imag = _eval_mod(ctx, real, bk), _eval_mod(ctx, imag, bk)
+    real, imag = _unbundle(_eval_mod(ctx, _bundle(ctx, [real, imag]), bk))
     y = add(ctx, real, _times_i(ctx, imag, 1))
     out = apply_s2c_inplace(ctx, y, bk)
     out.set_scale(scale * out.scale() / q0)

@@ -32,6 +32,14 @@ generator shares no code with oracle/ or with the HIP library:
                 so pi(i) is the slot of psi^(elt (2 brv(i)+1)); elt = 5^step
                 mod 2N, step 0 -> 2N - 1 (include/galois.cuh:16-49, :98-113),
                 checked against sigma(a)(X) = a(X^elt) in the coefficient domain.
+* rotations  -- the reference's two orders.  apply_galois (src/evaluate.cu:
+                1607-1656): c0 <- sigma(c0), c2 <- sigma(c1), then the key switch
+                of c2 (ModUp of the permuted c1).  hoist_rotations (:1929-2082):
+                ModUp of c1 once, then per rotation sigma on every ModUp slab
+                (:2036-2045), inner product, ModDown, c0 + sigma(c0).  hoisting
+                (:1732-1925): the inner products of all rotations summed mod p
+                before one ModDown, plus sum_i sigma_i(c0).  The two orders give
+                different residues for the same rotation (asserted here).
 
 Run:  python tests/golden/make_golden.py   (about a minute; deterministic)
 """
@@ -240,6 +248,55 @@ def galois_perm(elt):
     return [slot[elt * (2 * brv(i) + 1) % (2 * N)] for i in range(N)]
 
 
+def permute(poly_limbs, pm):
+    return [[int(limb[pm[i]]) for i in range(N)] for limb in poly_limbs]
+
+
+def add_limbs(a, b, mods):
+    return [[(u + v) % q for u, v in zip(x, y)] for x, y, q in zip(a, b, mods)]
+
+
+def ksw_out(ch, c0, cx, Ql):
+    """(c0 + ModDown(cx_0), ModDown(cx_1)): keyswitch_inplace on (c0, 0)."""
+    md = [moddown(ch, cx[k], Ql) for k in range(2)]
+    return [add_limbs(c0, md[0], ch.mods[:Ql]), md[1]]
+
+
+def apply_galois_ct(ch, ct, elt, key):
+    Ql = len(ct[0])
+    pm = galois_perm(elt)
+    c0, c1 = permute(ct[0], pm), permute(ct[1], pm)
+    return ksw_out(ch, c0, inner(ch, modup(ch, c1), key, Ql), Ql)
+
+
+def qlp_mods(ch, Ql):
+    return [ch.mods[r] for r in range(Ql)] + [ch.mods[ch.Q + j] for j in range(ch.P)]
+
+
+def hoist_rotations_ct(ch, ct, elts, keys):
+    Ql = len(ct[0])
+    slabs = modup(ch, [[int(v) for v in limb] for limb in ct[1]])
+    out = []
+    for elt, key in zip(elts, keys):
+        pm = galois_perm(elt)
+        rot = [permute(slab, pm) for slab in slabs]
+        out.append(ksw_out(ch, permute(ct[0], pm), inner(ch, rot, key, Ql), Ql))
+    return out
+
+
+def hoisting_ct(ch, ct, elts, keys):
+    Ql = len(ct[0])
+    slabs = modup(ch, [[int(v) for v in limb] for limb in ct[1]])
+    acc0, acc = None, None
+    for elt, key in zip(elts, keys):
+        pm = galois_perm(elt)
+        c0 = permute(ct[0], pm)
+        cx = inner(ch, [permute(slab, pm) for slab in slabs], key, Ql)
+        acc0 = c0 if acc0 is None else add_limbs(acc0, c0, ch.mods[:Ql])
+        acc = cx if acc is None else [add_limbs(acc[k], cx[k], qlp_mods(ch, Ql)) for k in range(2)]
+    return ksw_out(ch, acc0, acc, Ql)
+
+
 def uniform(rng, shape, mods):
     """uint64 residues, limb axis -2 over `mods`."""
     *pre, L, n = shape
@@ -326,6 +383,25 @@ def main():
     g.update(ks_moduli=u64(ks_mods), ks_roots=u64(ch.psi), ks_alpha=np.array(2), ks_a=a_ct, ks_b=b_ct,
              ks_key=key, ks_tensor=tensor, ks_modup=u64(slabs), ks_cx=u64(cx), ks_moddown=u64(md),
              ks_mul_relin=relin, ks_rescale=resc, ks_c2_low=c2_low, ks_modup_low=u64(slabs_low))
+    # --- rotations: apply_galois (permute, then key-switch) against the hoisted
+    # forms (ModUp, then permute the slabs), on fresh random keys per element
+    rot_ct = uniform(rng, (2, Q, N), ks_mods)
+    rot_steps = [1, 0]
+    rot_elts = [elt_from_step(t) for t in rot_steps]
+    rot_keys = np.stack([np.stack([uniform(rng, (2, QP, N), ks_mods) for _ in range(2)]) for _ in rot_elts])
+    ct_int = [[[int(v) for v in limb] for limb in poly] for poly in rot_ct]
+    ag = u64(apply_galois_ct(ch, ct_int, rot_elts[0], rot_keys[0]))
+    hr = u64(hoist_rotations_ct(ch, ct_int, rot_elts, rot_keys))
+    assert not np.array_equal(ag, hr[0]), "the two rotation orders must give different residues"
+    # hoisting at chain index 2 (Ql = 3: a short last digit and the P-row remap)
+    h_ct = uniform(rng, (2, 3, N), ks_mods)
+    h_steps = [1, 2]
+    h_elts = [elt_from_step(t) for t in h_steps]
+    h_keys = np.stack([np.stack([uniform(rng, (2, QP, N), ks_mods) for _ in range(2)]) for _ in h_elts])
+    hs = u64(hoisting_ct(ch, [[[int(v) for v in limb] for limb in poly] for poly in h_ct], h_elts, h_keys))
+    g.update(rot_ct=rot_ct, rot_steps=np.array(rot_steps, dtype=np.int64), rot_elts=u64(rot_elts),
+             rot_keys=rot_keys, rot_apply_galois=ag, rot_hoist_rotations=hr, hoisting_ct=h_ct,
+             hoisting_elts=u64(h_elts), hoisting_keys=h_keys, hoisting_out=hs)
     np.savez(os.path.join(HERE, "golden_n1024.npz"), **g)
     print("wrote", os.path.join(HERE, "golden_n1024.npz"), sorted(g))
 

@@ -185,6 +185,6 @@ def test_evalmod_levels_match_the_reference():
             return Depth(max(b.d for b in basis) + 1)
 
     for v, levels in ph.EVALMOD_LEVELS.items():
-        ops = Ops(None, None, 1.0)
+        ops = Ops(None, 1.0)
         out = ph._double_angle(ops, ph._sine(ops, Depth(0), v), ph.EVALMOD_R[v])
         assert out.d == levels, (v, out.d)

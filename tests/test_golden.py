@@ -73,3 +73,20 @@ def test_golden_catches_a_planted_mistake():
     q = int(g["ks_moduli"][1])
     got[1, 1, 7] = (int(got[1, 1, 7]) + 1) % q
     assert not np.array_equal(got, g["ks_rescale"])
+
+
+def test_rotation_vectors():
+    """apply_galois permutes c1 before the key switch (src/evaluate.cu:1607-1656);
+    hoist_rotations permutes the ModUp slabs (:2036-2045); hoisting sums the
+    rotations' inner products before one ModDown (:1732-1925).  The oracle
+    reproduces each order's vectors, and the two orders' residues differ."""
+    g, orc = _ks_oracle()
+    elts = ints(g["rot_elts"])
+    keys = list(g["rot_keys"])
+    ag = orc.apply_galois(1, g["rot_ct"], elts[0], keys[0])
+    assert np.array_equal(ag, g["rot_apply_galois"])
+    hr = orc.hoist_rotations(1, g["rot_ct"], elts, keys)
+    assert np.array_equal(np.stack(hr), g["rot_hoist_rotations"])
+    assert not np.array_equal(hr[0], ag)
+    hs = orc.hoisting(2, g["hoisting_ct"], ints(g["hoisting_elts"]), list(g["hoisting_keys"]))
+    assert np.array_equal(hs, g["hoisting_out"])

@@ -70,3 +70,26 @@ def test_keyswitch_chain_vectors(dev):
         _eq(to_host(res), g["ks_rescale"], "rescale")
     finally:
         ctx.close()
+
+
+def test_rotation_vectors(dev):
+    """The rotation orders of the reference: apply_galois (permute c1, then
+    key-switch), hoist_rotations (ModUp once, permute the slabs) and hoisting
+    (summed inner products, one ModDown), bit for bit."""
+    g = golden()
+    ctx = P.NativeContext(N, ints(g["ks_moduli"]), int(g["ks_alpha"]))
+    try:
+        elts = ints(g["rot_elts"])
+        keys = [to_dev(k, dev) for k in g["rot_keys"]]
+        d = to_dev(g["rot_ct"], dev)
+        ctx.apply_galois(1, d, elts[0], keys[0])
+        _eq(to_host(d), g["rot_apply_galois"], "apply_galois")
+        out = empty((len(elts), 2, 4, N), dev)
+        ctx.hoist_rotations(1, to_dev(g["rot_ct"], dev), elts, keys, out)
+        _eq(to_host(out), g["rot_hoist_rotations"], "hoist_rotations")
+        hs = empty((2, 3, N), dev)
+        ctx.hoisting(2, to_dev(g["hoisting_ct"], dev), ints(g["hoisting_elts"]),
+                     [to_dev(k, dev) for k in g["hoisting_keys"]], hs)
+        _eq(to_host(hs), g["hoisting_out"], "hoisting")
+    finally:
+        ctx.close()

@@ -503,6 +503,7 @@ def test_rotation_decrypts():
     # hoisted rotation decrypts to the same message (its residues differ: it
     # permutes the ModUp output instead of ModUp-ing the permuted c1)
     hr = o.hoist_rotations(chain, ct, [elt], [glk])[0]
+    assert not np.array_equal(hr, out), "hoisted and plain rotation residues must differ"
     dec_h = (hr[0].astype(object) + hr[1].astype(object) * sQ) % qs
     noise = centered_coeffs(o, ((dec_h - m_rot) % qs).astype(np.uint64), Ql)
     assert max(abs(x) for x in noise) < 2 ** 30
