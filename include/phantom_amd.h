@@ -74,11 +74,19 @@ int pfa_context_roots(const pfa_context *ctx, uint64_t *out);
 
 /* cudaStreamSynchronize under PHANTOM_CHECK_CUDA (include/cuda_wrapper.cuh:19-43),
  * plus the errors kernels of this context recorded on the device: waits for
- * `stream`, then returns PFA_ERR_RUNTIME if a single-launch NTT (opt-in with
- * PFA_NTT_FLOW=1, batches of 8+ limbs at N = 2^16) recorded that it did not
- * transform every tile.  Every later NTT launch of the context reports such a
- * record too, once its kernel has run.  The reference's kernels record no
- * errors. */
+ * `stream`, then returns PFA_ERR_RUNTIME if a kernel recorded one of
+ *   - a single-launch NTT (opt-in with PFA_NTT_FLOW=1, batches of 8+ limbs at
+ *     N = 2^16) whose bounded wait expired or that did not transform every tile;
+ *   - a key-switch inner product (every key switch: relinearize,
+ *     multiply_and_relin, rotations, hoisting, BSGS, bootstrapping) whose split
+ *     item's digit chunks did not all run on one XCD.  Items are split only on
+ *     a device that deals workgroups to its XCDs round-robin (probed when the
+ *     context is created), so this is a consistency check of that probe.
+ * Every later call that takes this context (any entry point with a `ctx`
+ * argument) also returns such a record, before it launches anything, once the
+ * kernel that recorded it has run; the record is cleared once returned.  So
+ * after key switches or single-launch NTTs, call this before trusting their
+ * outputs.  The reference's kernels record no errors. */
 int pfa_synchronize(const pfa_context *ctx, void *stream);
 
 /* ------------------------------------------------------------------ NTT */
@@ -129,11 +137,15 @@ int pfa_keyswitch(const pfa_context *ctx, size_t chain_index, uint64_t *ct, cons
 /* ------------------------------------------------------------ evaluator */
 
 /* bgv_ckks_multiply's tensor (src/evaluate.cu:345-397 -> tensor_prod_2x2_rns_poly,
- * src/polymath.cu:463-498): a, b [2][|Ql|][N] -> out [3][|Ql|][N]. */
+ * src/polymath.cu:463-498): a, b [2][|Ql|][N] -> out [3][|Ql|][N].  a, b and
+ * out must be 16-byte aligned (the kernel moves residue pairs); a misaligned
+ * pointer returns PFA_ERR_INVALID_ARGUMENT.  The same holds for a, b and out of
+ * pfa_multiply_and_relin, pfa_multiply_relin_rescale and their _batch forms. */
 int pfa_tensor(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b, uint64_t *out,
                void *stream);
 
-/* multiply_and_relin_inplace (src/evaluate.cu:1061-1104): out [2][|Ql|][N]. */
+/* multiply_and_relin_inplace (src/evaluate.cu:1061-1104): out [2][|Ql|][N].
+ * a, b, out 16-byte aligned (as pfa_tensor). */
 int pfa_multiply_and_relin(const pfa_context *ctx, size_t chain_index, const uint64_t *a, const uint64_t *b,
                            const uint64_t *rlk, size_t key_dnum, uint64_t *out, void *stream);
 

@@ -250,36 +250,25 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     PFA_HIP(hipDeviceGetAttribute(&c.n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
     PFA_HIP(hipHostMalloc((void **)&c.stage, Ctx::kStageSlots * Ctx::kStageSlotBytes, hipHostMallocDefault));
     for (auto &e : c.stage_ev) PFA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-    if (const char *w = std::getenv("PFA_NTT_WPC")) c.ntt_wpc = std::max(1, std::atoi(w));
-    if (const char *w = std::getenv("PFA_NTT_WPC_FWD")) c.ntt_wpc_fwd = std::max(1, std::atoi(w));
-    if (const char *w = std::getenv("PFA_NTT_HALF_ROWS")) c.ntt_half_rows = std::atoi(w);
-    if (const char *w = std::getenv("PFA_BCONV_MONT")) c.bconv_mont = std::atoi(w);
-    if (const char *w = std::getenv("PFA_TENSOR_ROWS")) c.tensor_rows = std::atoi(w);
-    if (const char *w = std::getenv("PFA_NTT_HALF_ROWS_INV")) c.ntt_half_rows_inv = std::atoi(w);
     // The key-switch inner product splits the items left over after whole
     // rounds of its resident workgroups by digit range; PFA_WS_SLOTS sets the
     // resident count it assumes (tests use it to split small shapes).
     if (const char *w = std::getenv("PFA_WS_SLOTS")) c.ws_slots = (uint32_t)std::max(0, std::atoi(w));
-    if (const char *w = std::getenv("PFA_WS_MAX_CHUNKS")) c.ws_max_chunks = (uint32_t)std::max(0, std::atoi(w));
-    if (const char *w = std::getenv("PFA_WS_NO_ORDER")) c.ws_no_order = std::atoi(w) != 0;
-    if (const char *w = std::getenv("PFA_WS_MEMBER_MAJOR")) c.ws_member_major = std::atoi(w) != 0;
     // Single-launch NTT (N = 2^16, opt-in with PFA_NTT_FLOW=1): built for the
-    // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition,
-    // checked here by a probe kernel.  The other variables tune it (workgroups
-    // per CU, look-ahead window, smallest batch, wait bound).
-    if (const char *w = std::getenv("PFA_FLOW_WPC")) c.flow_wpc = std::max(1, std::atoi(w));
+    // round-robin workgroup-to-XCD dealing of a full-chip MI355X partition.
+    // PFA_FLOW_WINDOW sets its look-ahead window, PFA_FLOW_WAIT_TICKS its wait
+    // bound (tests force an expired wait with it).
     if (const char *w = std::getenv("PFA_FLOW_WINDOW"))
         c.flow_window = (uint32_t)std::min(32, std::max(1, std::atoi(w)));
-    if (const char *w = std::getenv("PFA_FLOW_MIN_JOBS")) c.flow_min_jobs = (uint32_t)std::max(1, std::atoi(w));
     if (const char *w = std::getenv("PFA_FLOW_WAIT_TICKS")) c.flow_wait_ticks = (uint32_t)std::max(0, std::atoi(w));
     PFA_HIP(hipHostMalloc((void **)&c.err_host, 64, hipHostMallocMapped));
     *c.err_host = 0;
     PFA_HIP(hipHostGetDevicePointer((void **)&c.err_host_dev, c.err_host, 0));
-    c.err_dev = c.upload(std::vector<uint32_t>(16, 0u));
+    c.xcd_rr = xcd_round_robin(c);
     {
         const char *f = std::getenv("PFA_NTT_FLOW");
         const bool want = f ? std::atoi(f) != 0 : false;
-        c.ntt_flow = want && c.N == 65536 && xcd_round_robin(c);
+        c.ntt_flow = want && c.N == 65536 && c.xcd_rr;
     }
 
     const uint64_t *Qm = moduli, *Pm = moduli + c.Q;
@@ -464,21 +453,16 @@ static void destroy(Ctx *c) {
 
 Ctx *ctx_of(const pfa_context *c) {
     if (!c) fail(PFA_ERR_INVALID_ARGUMENT, "null context");
+    check_device_errors(*(const Ctx *)c);
     return (Ctx *)c;
 }
 
 void check_device_errors(const Ctx &c) {
     if (!c.err_host) return;
     volatile uint32_t *h = c.err_host;
-    if (*h == 0) return;
+    const uint32_t bits = *h;
+    if (bits == 0) return;
     *h = 0;
-    uint32_t bits = 0;
-    int prev = 0;
-    (void)hipGetDevice(&prev);
-    (void)hipSetDevice(c.device);
-    (void)hipMemcpy(&bits, c.err_dev, sizeof(bits), hipMemcpyDeviceToHost);
-    (void)hipMemset(c.err_dev, 0, sizeof(bits));
-    (void)hipSetDevice(prev);
     std::string why;
     if (bits & 1u) why += " a single-launch NTT's bounded wait expired;";
     if (bits & 2u) why += " a single-launch NTT ended with tiles not transformed;";
@@ -533,7 +517,10 @@ void pfa_context_destroy(pfa_context *ctx) { destroy((Ctx *)ctx); }
 
 int pfa_synchronize(const pfa_context *ctx, void *stream) {
     return guarded([&] {
-        const Ctx &c = *ctx_of(ctx);
+        // checked after the wait only: a record read before it could be
+        // followed by more stores of the same still-running kernel
+        if (!ctx) fail(PFA_ERR_INVALID_ARGUMENT, "null context");
+        const Ctx &c = *(const Ctx *)ctx;
         PFA_HIP(hipStreamSynchronize(as_stream(stream)));
         check_device_errors(c);
     });

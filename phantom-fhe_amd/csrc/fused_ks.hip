@@ -264,7 +264,7 @@ struct InnerRows {
     uint32_t rem = 0, kch = 1;
     uint64_t *partial = nullptr;
     uint32_t *counter = nullptr;
-    uint32_t *dev_err = nullptr, *host_err = nullptr;
+    uint32_t *host_err = nullptr;  // mapped pinned host word: error bit 4 is stored there
     const uint64_t *const *key_table = nullptr;  // per-member keys (device array), or null
     uint32_t member_fast = 0;  // item order: member index fastest (see ws_decode)
     // target of item group i: order[i] (null: i).  Items of integer-policy
@@ -732,8 +732,7 @@ k_inner_ws(InnerRows a0, NttTables t) {
         const bool last = (old & 0xffu) == a0.kch - 1;
         if (last) {
             if (((old | mine) & ~0xffu) != mine) {
-                __hip_atomic_fetch_or(a0.dev_err, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(a0.host_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(a0.host_err, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
             __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
         }
@@ -1016,7 +1015,7 @@ void launch_bconv(const Ctx &c, const BconvCols &a0, hipStream_t s) {
     BconvCols a = a0;
     // the Montgomery-accumulated sums need sum_i t_i < 2^64; every input is
     // below the context's largest prime
-    if (c.bconv_mont && c.max_modulus <= ~0ull / std::max(a.n_in, a.n_in_last)) a.mont = c.mont;
+    if (c.max_modulus <= ~0ull / std::max(a.n_in, a.n_in_last)) a.mont = c.mont;
     const uint32_t total = grouped_total(a.batch * a.groups * G::COL_TILES, a.J);
     hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
                        tables_of(c));
@@ -1063,8 +1062,10 @@ void launch_inner(const Ctx &c, InnerRows a, hipStream_t s) {
         grid = P;
         const uint32_t rem = items % P;
         const uint32_t per_x = (rem + kXcds - 1) / kXcds;  // split items per XCD class
-        const uint32_t kmax = std::min<uint32_t>(a.beta, c.ws_max_chunks ? c.ws_max_chunks : a.beta);
-        const uint32_t kch = rem && P % kXcds == 0 ? std::min<uint32_t>(kmax, (P / kXcds) / per_x) : 0;
+        // a split item's chunks run on workgroups congruent mod 8, which meet
+        // in one XCD's L2 only where workgroups are dealt to the XCDs
+        // round-robin (probed at context creation); elsewhere items run whole
+        const uint32_t kch = rem && P % kXcds == 0 && c.xcd_rr ? std::min<uint32_t>(a.beta, (P / kXcds) / per_x) : 0;
         if (kch >= 2 && rem <= kWsMaxSplit) {
             Arena &ar = arena_for(c, s);
             if (!ar.ws_counter) {
@@ -1076,7 +1077,6 @@ void launch_inner(const Ctx &c, InnerRows a, hipStream_t s) {
             a.kch = kch;
             a.partial = sc.alloc((size_t)rem * kch * 2 * W::ROWS * G::N2);
             a.counter = ar.ws_counter;
-            a.dev_err = c.err_dev;
             a.host_err = c.err_host_dev;
         }
     }
@@ -1156,8 +1156,8 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     r.cx_bstride = cx_stride ? cx_stride : (uint64_t)2 * QlP * c.N;
     r.key_table = key_table;
     // one key for all members: interleave them so they share its rows in L2
-    r.member_fast = batch > 1 && !key_table && !c.ws_member_major ? 1u : 0u;
-    if (batch == 1 && !c.ws_no_order) r.order = lv.ws_order;
+    r.member_fast = batch > 1 && !key_table ? 1u : 0u;
+    if (batch == 1) r.order = lv.ws_order;
     if (fold) {
         require(fold->base0 && fold->base1 && Ql >= 2 && (batch == 1 || fold->stride), "bad ModDown + rescale fold");
         r.fold_r = Ql - 1;

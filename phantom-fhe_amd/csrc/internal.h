@@ -130,28 +130,26 @@ struct Ctx {
     int ntt_wpc = 3;                 // resident workgroups per CU of the prefetching inverse rows pass
     int ntt_wpc_fwd = 4;             // the same for the passes without register prefetch
     uint64_t max_modulus = 0;        // the largest prime of the context
-    int bconv_mont = 1;              // Montgomery-accumulated integer conversions (PFA_BCONV_MONT=0: Shoup)
-    int tensor_rows = 1;             // HMult tensor with the INTT rows pass fused in (PFA_TENSOR_ROWS=0: apart)
-    int ntt_half_rows_inv = 1;       // the same for the prefetching inverse rows pass (PFA_NTT_HALF_ROWS_INV=0: full)
-    int ntt_half_rows = 1;           // forward rows pass on half-height tiles (PFA_NTT_HALF_ROWS=0: full)
     uint32_t ws_slots = 0;           // resident inner-product workgroups assumed (0: from the occupancy API)
-    uint32_t ws_max_chunks = 0;      // most digit chunks of a split inner-product item (0: beta)
-    bool ws_no_order = false;        // inner product in plain target order (PFA_WS_NO_ORDER)
-    bool ws_member_major = false;    // batched inner product in member-major item order (PFA_WS_MEMBER_MAJOR)
+    // true when the device deals a launch's workgroups to its 8 XCDs
+    // round-robin (probed once at context creation): the inner product splits
+    // left-over items into digit chunks only then, and the single-launch NTT
+    // is only enabled then
+    bool xcd_rr = false;
     // single-launch NTT (ntt_kernels.h, opt-in): needs a device that deals
     // workgroups to 8 XCDs round-robin; used for batches of at least
     // flow_min_jobs limbs at N = 2^16
     bool ntt_flow = false;
-    int flow_wpc = 2;                // workgroups per CU
-    uint32_t flow_window = 2;        // jobs ahead of the second-pass front
-    uint32_t flow_min_jobs = 8;
+    static constexpr int flow_wpc = 2;             // workgroups per CU
+    uint32_t flow_window = 2;                      // jobs ahead of the second-pass front
+    static constexpr uint32_t flow_min_jobs = 8;
     uint32_t flow_wait_ticks = 10000000;  // 100 ms at the 100 MHz s_memrealtime clock
-    // Errors kernels record while they run (bits or-ed into err_dev; any
-    // error also sets the mapped pinned word err_host): 1 a single-launch NTT's
-    // bounded wait expired, 2 a single-launch NTT ended with tiles not
-    // transformed, 4 the digit chunks of one inner-product item ran on
-    // different XCDs.  Reported by check_device_errors.
-    uint32_t *err_dev = nullptr;
+    // Errors kernels record while they run, as a bit stored into the mapped
+    // pinned host word err_host (1 a single-launch NTT's bounded wait expired,
+    // 2 a single-launch NTT ended with tiles not transformed, 4 the digit
+    // chunks of one inner-product item ran on different XCDs).  Reported by
+    // check_device_errors, which reads the host word only (no device access),
+    // at the entry of every C-ABI call that takes the context.
     uint32_t *err_host = nullptr;
     uint32_t *err_host_dev = nullptr;  // err_host's device address
     // ModDown (level independent): INTT scale [(P/p_j)^-1]_{p_j} (NTT pairs, [P]),
@@ -208,7 +206,9 @@ T *Ctx::upload(const std::vector<T> &v) {
 Ctx *ctx_of(const pfa_context *c);
 // Throws PFA_ERR_RUNTIME (and clears the record) if a kernel of this context
 // recorded an error on the device since the last check.  Kernels record it in
-// mapped host memory, so the check sees it once the kernel has run.
+// mapped host memory, so the check sees it once the kernel has run; it makes
+// no HIP call, so it is safe under stream capture.  ctx_of runs it, i.e. every
+// C-ABI call that takes a context checks before it launches anything.
 void check_device_errors(const Ctx &c);
 // The calling thread's workspace for stream s (its single-launch NTT control
 // blocks live there).

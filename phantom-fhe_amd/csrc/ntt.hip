@@ -1,6 +1,5 @@
 // NTT launchers and the raw-limb NTT entry points of the C ABI.
 #include <algorithm>
-#include <cstdio>
 #include <cstdlib>
 #include <vector>
 
@@ -65,7 +64,7 @@ void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     b2.src = b.dst;
     b2.sstride = b.dstride;
     constexpr int RH = half_rows<S1, S2>();
-    if (RH != G::ROWS && c.ntt_half_rows)
+    if (RH != G::ROWS)
         hipLaunchKernelGGL((ntt_fwd_rows<S1, S2, RH>), dim3(grid_for(c, ml * (G::N1 / RH), c.ntt_wpc_fwd * (G::ROWS / RH))),
                            dim3(RH * Sub<S2>::T), 0, s, b2, t);
     else
@@ -91,7 +90,7 @@ void inv(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     if (ml >= kInvStagedLimbs)
         hipLaunchKernelGGL((ntt_inv_rows_staged<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, 3)),
                            dim3(G::ROW_THREADS), 0, s, b, t);
-    else if (half_rows<S1, S2>() != G::ROWS && c.ntt_half_rows_inv)
+    else if (half_rows<S1, S2>() != G::ROWS)
         hipLaunchKernelGGL((ntt_inv_rows<S1, S2, half_rows<S1, S2>()>),
                            dim3(grid_for(c, ml * (G::N1 / half_rows<S1, S2>()), c.ntt_wpc * (G::ROWS / half_rows<S1, S2>()))),
                            dim3(half_rows<S1, S2>() * Sub<S2>::T), 0, s, b, t);
@@ -139,7 +138,6 @@ void flow(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     f.other_jobs = a.flow_dirty[1 - p];
     f.window = c.flow_window;
     f.wait_ticks = c.flow_wait_ticks;
-    f.dev_err = c.err_dev;
     f.host_err = c.err_host_dev;
     const uint32_t grid = (uint32_t)c.n_cu * (uint32_t)c.flow_wpc / kXcds * kXcds;
     if (FWD) {
@@ -181,7 +179,6 @@ void ntt_forward(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flo
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    check_device_errors(c);
     if (allow_flow && use_flow(c, b)) {
         flow<true>(c, b, t, s);
         return;
@@ -194,7 +191,6 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flo
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    check_device_errors(c);
     if (allow_flow && use_flow(c, b)) {
         flow<false>(c, b, t, s);
         return;
@@ -207,7 +203,6 @@ void ntt_inverse_cols(const Ctx &c, const NttLaunch &a, hipStream_t s) {
     check_launch(c, a);
     const NttBatch b = make_batch(c, a);
     const NttTables t = tables(c);
-    check_device_errors(c);
     PFA_NTT_DISPATCH(inv_cols);
     PFA_HIP(hipGetLastError());
 }
@@ -251,16 +246,9 @@ bool xcd_round_robin(const Ctx &c) {
     (void)hipFree(d);
     PFA_HIP(e);
     // round-robin from the XCD of workgroup 0, which depends on earlier dispatches
-    const bool debug = std::getenv("PFA_FLOW_DEBUG") != nullptr;
     const uint32_t r = h[0];
     for (uint32_t i = 0; i < G; i++)
-        if (h[i] != (i + r) % kXcds) {
-            if (debug)
-                std::fprintf(stderr, "pfa: workgroup %u ran on XCD %u, not %u: single-launch NTT disabled\n", i,
-                             h[i], (i + r) % kXcds);
-            return false;
-        }
-    if (debug) std::fprintf(stderr, "pfa: workgroups are dealt to %u XCDs round-robin (from XCD %u)\n", kXcds, r);
+        if (h[i] != (i + r) % kXcds) return false;
     return true;
 }
 

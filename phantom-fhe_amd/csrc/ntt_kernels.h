@@ -907,8 +907,7 @@ struct FlowCtl {
     uint32_t other_jobs;
     uint32_t window;       // 1 .. kFlowMaxWindow
     uint32_t wait_ticks;   // bound of one wait, s_memrealtime ticks (100 MHz)
-    uint32_t *dev_err;     // device error word (bits above), or-ed
-    uint32_t *host_err;    // mapped pinned host word, written on error only
+    uint32_t *host_err;    // mapped pinned host word: the error bits are stored there, on error only
 };
 
 template <int S1, int S2>
@@ -919,6 +918,20 @@ struct FlowGeo {
     static constexpr int LDS = G::COL_LDS > G::ROW_LDS ? G::COL_LDS : G::ROW_LDS;
     static constexpr int TWL = G::N1 > RowStage<S1, S2>::N ? G::N1 : RowStage<S1, S2>::N;
 };
+
+// The XCD-local hand-offs of this library (the single-launch NTT's second
+// pass below, the key-switch inner product's split items in fused_ks.hip) rely
+// on the cache behaviour of gfx942 / gfx950: a CU's L1 is write-through, each
+// XCD has one L2 that all its CUs share, and a vector store stays counted by
+// vmcnt until that L2 holds it.  So data a workgroup stored and waited for
+// (s_waitcnt vmcnt(0)) before a relaxed agent-scope atomic is in its XCD's L2
+// when another workgroup of the same XCD sees that atomic, and the reader gets
+// it after dropping its own CU's L1 (buffer_inv sc0).  That is not ordering the
+// HIP memory model guarantees; other targets would need release / acquire
+// fences, so they are refused here.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx942__) && !defined(__gfx950__)
+#error "the XCD-local hand-offs assume the gfx942 / gfx950 cache hierarchy"
+#endif
 
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t v;
@@ -936,8 +949,7 @@ __device__ __forceinline__ uint32_t flow_add(uint32_t *p, uint32_t v) {
 }
 
 __device__ __forceinline__ void flow_error(const FlowCtl &c, uint32_t bits) {
-    __hip_atomic_fetch_or(c.dev_err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(c.host_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(c.host_err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 constexpr uint32_t kFlowExit = 0xffffffffu, kFlowWait = 0xfffffffeu, kFlowPass2 = 0x80000000u;

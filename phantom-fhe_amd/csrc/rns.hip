@@ -333,12 +333,12 @@ void op_tensor(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *
 // op_tensor for a product whose d2 is key-switched next: at N <= 2^16 the
 // tensor kernel also runs the first pass of the key switch's INTT(d2) and the
 // returned buffer (count x Ql N, from sc) holds it for op_keyswitch /
-// op_keyswitch_rescale; otherwise (or with PFA_TENSOR_ROWS=0) plain op_tensor
+// op_keyswitch_rescale; otherwise plain op_tensor
 // and nullptr.
 const uint64_t *tensor_for_ks(const Ctx &c, Scratch &sc, uint32_t chain, const uint64_t *a, const uint64_t *b,
                               uint64_t *d0, uint64_t *d1, uint64_t *d2, hipStream_t s, uint32_t count = 1,
                               uint64_t in_stride = 0, uint64_t d_stride = 0, uint64_t d2_stride = 0) {
-    if (!c.tensor_rows || c.logN > 16) {
+    if (c.logN > 16) {
         op_tensor(c, chain, a, b, d0, d1, d2, s, count, in_stride, d_stride, d2_stride);
         return nullptr;
     }

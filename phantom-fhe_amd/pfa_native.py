@@ -227,7 +227,8 @@ class NativeContext:
     def synchronize(self, stream=None):
         """Waits for `stream` (default: torch's current stream on the context's
         device) and raises RuntimeError if a kernel of this context recorded an
-        error on the device (a single-launch NTT that did not finish)."""
+        error on the device (a single-launch NTT that did not finish, or a
+        key-switch inner product whose split item ran on two XCDs)."""
         if stream is None:
             import torch
 

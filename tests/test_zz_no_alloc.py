@@ -21,25 +21,27 @@ def test_rescale_noalloc_matches_rescale(dev):
     mods = O.create_coeff_modulus(N, [60] + [50] * 7 + [60] * 2)
     ctx = P.NativeContext(N, mods, 2)
     rng = np.random.default_rng(77)
+    # the allocation-free calls run first, on a stream of their own that no
+    # other call has used, so no workspace exists for them to reuse: a call
+    # that allocated would show in the device's free memory
+    fresh = torch.cuda.Stream(device=dev)
     # two calls in a row: 3 polys at chain 1 (8 limbs), then 2 polys at chain 4
     # (5 limbs) on the same context and stream
     for size, chain in [(3, 1), (2, 4)]:
         L = len(mods) - 2 - (chain - 1)
         x = to_dev(uniform_limbs(rng, (size, L, N), mods[:L]), dev)
-        want = empty((size, L - 1, N), dev)
-        ctx.rescale(chain, x, want)
-        torch.cuda.synchronize()
-        free0 = torch.cuda.mem_get_info()[0]
         got = empty((size, L - 1, N), dev)
         torch.cuda.synchronize()
         free1 = torch.cuda.mem_get_info()[0]
-        ctx.rescale_noalloc(chain, x, got)
-        ctx.synchronize()
+        ctx.rescale_noalloc(chain, x, got, stream=fresh.cuda_stream)
+        ctx.synchronize(fresh.cuda_stream)
         free2 = torch.cuda.mem_get_info()[0]
+        # the call itself takes no device memory (a workspace chunk is >= 256 MiB)
+        assert free1 - free2 < (16 << 20), (size, chain, free1, free2)
+        want = empty((size, L - 1, N), dev)
+        ctx.rescale(chain, x, want)
         g, w = to_host(got), to_host(want)
         assert np.array_equal(g, w), (size, chain, first_mismatch(g, w))
-        # the call itself takes no device memory (a workspace chunk is >= 256 MiB)
-        assert free1 - free2 < (16 << 20), (free0, free1, free2)
     # and against the oracle, so both are pinned
     orc = O.Oracle(N, mods, 2)
     xs = uniform_limbs(rng, (2, 8, N), mods[:8])
