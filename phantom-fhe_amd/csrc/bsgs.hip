@@ -389,11 +389,19 @@ void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src
         upload_async(c, key_dev, keys, B * sizeof(void *), s);
     }
     uint64_t *t = sc.alloc((size_t)B * 2 * LN);
-    hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2 * B), dim3(kThreads), 0, s, src, src_stride, t, add,
-                       c.mod, elt, elt_dev, Ql, c.N, c.logN);
-    PFA_HIP(hipGetLastError());
+    // up to N = 2^16 the permutation kernel also runs the first pass of the
+    // key switch's INTT over the permuted c1 (mid), as the HMult tensor kernel does
+    uint64_t *mid = nullptr;
+    if (c.logN <= 16) {
+        mid = sc.alloc((size_t)B * LN);
+        galois_rows(c, chain, src, src_stride, B, elt, elt_dev, add, t, mid, s);
+    } else {
+        hipLaunchKernelGGL(k_galois_ct, dim3(c.N / kThreads, Ql, 2 * B), dim3(kThreads), 0, s, src, src_stride, t,
+                           add, c.mod, elt, elt_dev, Ql, c.N, c.logN);
+        PFA_HIP(hipGetLastError());
+    }
     uint64_t *cx = sc.alloc((size_t)B * 2 * QlP * c.N);
-    fused_modup_inner(c, chain, t + LN, key, cx, s, B, 2 * LN, (uint64_t)2 * QlP * c.N, nullptr, key_dev);
+    fused_modup_inner(c, chain, t + LN, key, cx, s, B, 2 * LN, (uint64_t)2 * QlP * c.N, nullptr, key_dev, mid);
     fused_moddown(c, chain, cx, 2 * B, out, t, add ? add + LN : nullptr, s, 2 * LN);
 }
 

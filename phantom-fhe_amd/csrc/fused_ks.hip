@@ -1183,6 +1183,108 @@ void fused_tensor_rows(const Ctx &c, uint32_t chain, const uint64_t *a, const ui
     PFA_FUSED_DISPATCH(launch_tensor_rows, t);
 }
 
+// ------------------------------------------------------------ rotation input
+// Both polys of B ciphertexts through the Galois permutation of NTT slots
+// (apply_galois_ntt_permutation, src/galois.cu:11-18), with the first pass of
+// the key switch's INTT fused in for poly 1 (the c2 that apply_galois_with_ksk
+// key-switches, src/evaluate.cu:1607-1656):
+//   dst[i][k][l][n] = src[i][k][l][pi_i(n)]  (+ add0[l][n] for k = 0, B = 1)
+//   mid[i][l]       = inverse rows pass of dst[i][1][l]
+// A tile is R rows of one limb of one poly: its residues are gathered (the
+// permutation stays within the limb), stored, and for poly 1 also placed in
+// LDS, where the inverse rows pass takes them as k_tensor_rows does.
+struct GaloisRows {
+    const uint64_t *src;
+    uint64_t src_stride;
+    uint64_t *dst;          // [B][2][Ql][N]
+    const uint64_t *add0;   // [Ql][N] or null
+    uint64_t *mid;          // [B][Ql][N]
+    const uint32_t *elts;   // [B] device table, or null: every member uses elt
+    uint32_t elt, Ql, logN, B;
+};
+
+template <int S1, int S2, int R>
+__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(3, 8)))
+k_galois_rows(GaloisRows a, NttTables t) {
+    using G = Geo<S1, S2>;
+    using RS = RowStage<S1, S2, R>;
+    constexpr uint32_t TILES = G::N1 / R, NT = R * Sub<S2>::T, E = Sub<S2>::E;
+    static_assert(NT * E == R * G::N2, "a tile is NT threads x E residues");
+    __shared__ double lds[R * G::ROW_PITCH];
+    __shared__ ulonglong2 twl[RS::N];
+    const uint32_t k = blockIdx.y & 1u, i = blockIdx.y >> 1;
+    const TileRef r{i, blockIdx.x / TILES, blockIdx.x % TILES};
+    const uint64_t q = ld_const(t.mod + r.l);
+    const uint32_t e = a.elts ? uniform_u32(a.elts[i]) : a.elt;
+    const size_t row = ((size_t)k * a.Ql + r.l) * G::N;
+    const uint32_t tb = r.tile * R * G::N2;  // first element of the tile within the limb
+    const uint64_t *src = a.src + i * a.src_stride + row;
+    uint64_t *dst = a.dst + (size_t)i * 2 * a.Ql * G::N + row + tb;
+    RS stage;
+    if (k) stage.load(t, r.l, r.tile, false);  // requested before the residues
+    uint64_t v[E];
+#pragma unroll
+    for (uint32_t p = 0; p < E; p++) v[p] = src[galois_perm(e, tb + threadIdx.x + NT * p, a.logN)];
+    if (!k) {
+        if (a.add0) {
+            const uint64_t *ad = a.add0 + (size_t)r.l * G::N + tb;
+#pragma unroll
+            for (uint32_t p = 0; p < E; p++) v[p] = add_mod(v[p], ad[threadIdx.x + NT * p], q);
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < E; p++) st_stream(dst + threadIdx.x + NT * p, v[p]);
+        return;
+    }
+    // the staged twiddles were requested first: this waits for them only
+    stage.st.store(twl);
+    uint64_t *mid = a.mid + ((size_t)i * a.Ql + r.l) * G::N;
+    const TileTw w = RS::view(twl, t.itw + (size_t)r.l * G::N, threadIdx.x / Sub<S2>::T);
+    if (q < kF64PrimeBound) {
+        const ArithF64 ar(q);
+#pragma unroll
+        for (uint32_t p = 0; p < E; p++) {
+            const uint32_t j = threadIdx.x + NT * p;
+            st_stream(dst + j, v[p]);
+            lds[(j / G::N2) * G::ROW_PITCH + rpad(j % G::N2)] = ar.load(v[p]);
+        }
+        __syncthreads();
+        inv_rows_lds<ArithF64, S1, S2, R, true, R>(w, r, q, lds, mid);
+    } else {
+        const ArithInt ar(q);
+        uint64_t *li = reinterpret_cast<uint64_t *>(lds);
+#pragma unroll
+        for (uint32_t p = 0; p < E; p++) {
+            const uint32_t j = threadIdx.x + NT * p;
+            st_stream(dst + j, v[p]);
+            li[(j / G::N2) * G::ROW_PITCH + rpad(j % G::N2)] = ar.load(v[p]);
+        }
+        __syncthreads();
+        inv_rows_lds<ArithInt, S1, S2, R, true, R>(w, r, q, li, mid);
+    }
+}
+
+template <int S1, int S2>
+void launch_galois_rows(const Ctx &c, const GaloisRows &a, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    if constexpr (S2 > 8) {
+        fail(PFA_ERR_INVALID_ARGUMENT, "fused Galois rows pass: N above 2^16");
+    } else {
+        constexpr int R = S2 == 8 && G::ROWS == 16 ? 8 : G::ROWS;
+        hipLaunchKernelGGL((k_galois_rows<S1, S2, R>), dim3(a.Ql * (G::N1 / R), 2 * a.B), dim3(R * Sub<S2>::T), 0, s,
+                           a, tables_of(c));
+        PFA_HIP(hipGetLastError());
+    }
+}
+
+void galois_rows(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src_stride, uint32_t B, uint32_t elt,
+                 const uint32_t *elts, const uint64_t *add0, uint64_t *dst, uint64_t *mid, hipStream_t s) {
+    const uint32_t Ql = c.size_Ql(chain);
+    require(c.logN <= 16, "fused Galois rows pass: N above 2^16");
+    require(B >= 1 && B <= 32767, "bad rotation batch");
+    const GaloisRows g{src, src_stride, dst, add0, mid, elts, elt, Ql, c.logN, B};
+    PFA_FUSED_DISPATCH(launch_galois_rows, g);
+}
+
 // The rescale of base + ModDown(cx) without forming the ModDown output.  With
 // q_l the last prime, v_i the scaled INTT of P limb i and
 // t = INTT(base + cx [P^-1])_(l) - sum_i v_i [p_i^-1]_(q_l) mod q_l (the

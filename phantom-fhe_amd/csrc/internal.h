@@ -288,6 +288,13 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
 void fused_tensor_rows(const Ctx &c, uint32_t chain, const uint64_t *a, const uint64_t *b, uint64_t *d0,
                        uint64_t *d1, uint64_t *d2, uint64_t *mid, hipStream_t s, uint32_t count,
                        uint64_t in_stride, uint64_t d_stride, uint64_t d2_stride);
+// The rotation input of B ciphertexts (src[i] at src + i src_stride): dst
+// [B][2][Ql][N] = both polys through the Galois permutation of element elt (or
+// elts[i], a device table), plus add0 on poly 0 when given (B = 1), and mid
+// [B][Ql][N] = the inverse rows pass over dst's poly 1, the input
+// fused_modup_inner takes as c2_mid.  N = 2^10 .. 2^16.
+void galois_rows(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src_stride, uint32_t B, uint32_t elt,
+                 const uint32_t *elts, const uint64_t *add0, uint64_t *dst, uint64_t *mid, hipStream_t s);
 // cx [2][QlP][N] from fused_modup_inner with a fold over base -> out [2][Ql-1][N]
 // = rescale(base + ModDown(cx)), bit-identical to fused_moddown then fused_rescale.
 // With count > 1: cx [count][2][QlP][N], member i's bases at + i base_stride,

@@ -561,10 +561,17 @@ int pfa_apply_galois(const pfa_context *ctx, size_t chain_index, uint64_t *ct, u
         const size_t LN = (size_t)Ql * c.N;
         Scratch sc(c, s);
         uint64_t *t = sc.alloc(2 * LN);
-        op_galois(c, elt, ct, t, Ql, s);
-        op_galois(c, elt, ct + LN, t + LN, Ql, s);
         // c0' = sigma(c0) + KS0(sigma(c1)), c1' = KS1(sigma(c1))  (src/evaluate.cu:1607-1656)
-        op_keyswitch(c, (uint32_t)chain_index, t + LN, key, key_dnum, ct, Bases{{t, nullptr}}, s);
+        if (c.logN <= 16) {
+            // the permutation kernel also runs the first pass of the key switch's INTT
+            uint64_t *mid = sc.alloc(LN);
+            galois_rows(c, (uint32_t)chain_index, ct, 0, 1, elt, nullptr, nullptr, t, mid, s);
+            op_keyswitch(c, (uint32_t)chain_index, t + LN, key, key_dnum, ct, Bases{{t, nullptr}}, s, 1, 0, 0, mid);
+        } else {
+            op_galois(c, elt, ct, t, Ql, s);
+            op_galois(c, elt, ct + LN, t + LN, Ql, s);
+            op_keyswitch(c, (uint32_t)chain_index, t + LN, key, key_dnum, ct, Bases{{t, nullptr}}, s);
+        }
     });
 }
 
