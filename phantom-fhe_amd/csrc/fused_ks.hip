@@ -301,7 +301,12 @@ __device__ __forceinline__ void ws_decode(const InnerRows &a, uint32_t w0, uint3
 __device__ __forceinline__ const uint64_t *inner_src(const InnerRows &a, uint32_t b, uint32_t r, size_t rowoff,
                                                      uint32_t N, bool &own) {
     own = r < a.Ql && r >= b * a.alpha && r < b * a.alpha + a.alpha;
-    return own ? a.c2 + (size_t)r * N + rowoff : a.inter + ((size_t)b * a.QlP + r) * N + rowoff;
+    // chosen by arithmetic: a select between the two pointers made the compiler
+    // keep them in a scratch array, whose per-digit load (a vector memory
+    // access) waited behind the prefetched tile
+    const uintptr_t c2p = (uintptr_t)(a.c2 + (size_t)r * N + rowoff);
+    const uintptr_t inp = (uintptr_t)(a.inter + ((size_t)b * a.QlP + r) * N + rowoff);
+    return (const uint64_t *)(inp + (uintptr_t)own * (c2p - inp));
 }
 
 // One work item is a (target limb r, tile of ROWS rows) pair; its digits are
@@ -470,7 +475,11 @@ __device__ __forceinline__ void ws_out(const InnerRows &a, uint32_t k, uint32_t 
                                        uint64_t q, uint64_t v) {
     if (r == a.fold_r) {
         const ulonglong2 f = *a.fold_f;
-        v = add_mod(shoup(v, f.x, f.y, q), (k ? a.fold_base1 : a.fold_base0)[(size_t)r * N + off], q);
+        // base k as pointer arithmetic: a select between the two pointers made
+        // the compiler keep them in a scratch array indexed by k
+        const uintptr_t b0 = (uintptr_t)a.fold_base0, b1 = (uintptr_t)a.fold_base1;
+        const uint64_t *fb = (const uint64_t *)(b0 + (uintptr_t)k * (b1 - b0));
+        v = add_mod(shoup(v, f.x, f.y, q), fb[(size_t)r * N + off], q);
     }
     st_stream(a.cx + ((size_t)k * a.QlP + r) * N + off, v);
 }

@@ -782,11 +782,14 @@ ntt_inv_rows_staged(NttBatch b, NttTables t) {
     }
 }
 
-// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and, when scaled,
-// the limb's scale pair.
+// Columns pass: dst (intermediate) -> dst (canonical), N^-1 and, when scale is
+// not null, the limb's scale pair, read only after the rounds: held in
+// registers from the tile's start it made the pass spill (127 VGPRs and 12
+// bytes of scratch per lane at 4 waves per SIMD; config-2 inverse +2.2 us), and
+// read with scalar loads at the start the pass was slower still (+4.5 us).
 template <class A, int S1, int S2>
 __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E], const ulonglong2 *itw,
-                                              ulonglong2 ninv, bool scaled, ulonglong2 scale, const TileRef &r,
+                                              ulonglong2 ninv, const ulonglong2 *scale, const TileRef &r,
                                               uint64_t q, typename A::T *lds, uint64_t *olimb) {
     using G = Geo<S1, S2>;
     using SB = Sub<S1>;
@@ -804,9 +807,10 @@ __device__ __forceinline__ void inv_cols_tile(const uint64_t (&raw)[Sub<S1>::E],
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lds[(F + SB::T * e) * kColStride + c];
     inv_round_b<A, S1, true>(x, ar, itw, 1, ninv);
-    if (scaled) {
+    if (scale) {
+        const ulonglong2 sc = *scale;
 #pragma unroll
-        for (int e = 0; e < SB::E; e++) ar.mul(x[e], scale);
+        for (int e = 0; e < SB::E; e++) ar.mul(x[e], sc);
     }
 #pragma unroll
     for (int e = 0; e < SB::E; e++) st_stream(&data[(size_t)(F + SB::T * e) * G::N2 + c], ar.store(x[e]));
@@ -838,14 +842,13 @@ ntt_inv_cols(NttBatch b, NttTables t) {
         st.store(twl);
         __syncthreads();
         const uint64_t q = t.mod[prow];
-        const bool scaled = b.scale != nullptr;
-        const ulonglong2 sc = scaled ? b.scale[r.l] : ulonglong2{0, 0};
+        const ulonglong2 *sc = b.scale ? b.scale + r.l : nullptr;
         uint64_t *olimb = b.dst + r.m * b.dstride + (size_t)r.l * G::N;
         if (q < kF64PrimeBound)
-            inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q, lds, olimb);
+            inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], sc, r, q, lds, olimb);
         else
-            inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q,
-                                            reinterpret_cast<uint64_t *>(lds), olimb);
+            inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], sc, r, q, reinterpret_cast<uint64_t *>(lds),
+                                            olimb);
         __syncthreads();
     }
 }
@@ -1092,13 +1095,12 @@ struct FlowJob {
             for (int e = 0; e < S1B::E; e++) raw[e] = s[(size_t)(F * S1B::E + e) * G::N2 + c];
             st.store(twl);
             __syncthreads();
-            const bool scaled = b.scale != nullptr;
-            const ulonglong2 sc = scaled ? b.scale[l] : ulonglong2{0, 0};
+            const ulonglong2 *sc = b.scale ? b.scale + l : nullptr;
             if (q < kF64PrimeBound)
-                inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q, lds, limb);
+                inv_cols_tile<ArithF64, S1, S2>(raw, twl, t.ninv[prow], sc, r, q, lds, limb);
             else
-                inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], scaled, sc, r, q,
-                                                reinterpret_cast<uint64_t *>(lds), limb);
+                inv_cols_tile<ArithInt, S1, S2>(raw, twl, t.ninv[prow], sc, r, q, reinterpret_cast<uint64_t *>(lds),
+                                                limb);
         }
     }
 };
