@@ -925,14 +925,15 @@ struct TensorRows {
     const ulonglong2 *itw;  // set per workgroup: the tile's prime's inverse table
 };
 
-template <class A, int S1, int S2, int R>
+template <class A, int S1, int S2, int R, int MT>
 __device__ __forceinline__ void tensor_rows_tile(const TensorRows &a, RowStage<S1, S2, R> &stage,
                                                  ulonglong2 *twl, const TileRef &r, uint64_t q,
                                                  typename A::T *lds) {
     using G = Geo<S1, S2>;
     using RS = RowStage<S1, S2, R>;
-    constexpr uint32_t NT = R * Sub<S2>::T;
-    constexpr int P = Sub<S2>::E / 2, H = P / 2;
+    // the tensor phase runs on all MT R T threads, the rows pass on the first R T
+    constexpr uint32_t NR = R * Sub<S2>::T, NT = MT * NR;
+    constexpr int P = Sub<S2>::E / 2 / MT, H = P / 2;
     static_assert(2 * NT * P == R * G::N2 && 2 * H == P, "a tile is NT threads x 2P residues");
     const A ar(q);
     ulonglong2 rt{0, 0};
@@ -985,11 +986,12 @@ __device__ __forceinline__ void tensor_rows_tile(const TensorRows &a, RowStage<S
     }
     __syncthreads();
     const TileTw w = RS::view(twl, a.itw, threadIdx.x / Sub<S2>::T);
-    inv_rows_lds<A, S1, S2, R, true, R>(w, r, q, lds, a.mid + r.m * a.mid_stride + (size_t)r.l * G::N);
+    inv_rows_lds<A, S1, S2, R, true, R>(w, r, q, lds, a.mid + r.m * a.mid_stride + (size_t)r.l * G::N,
+                                        threadIdx.x < NR);
 }
 
-template <int S1, int S2, int R>
-__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(4, 8)))
+template <int S1, int S2, int R, int MT>
+__global__ void __launch_bounds__(MT * R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(4, 8)))
 k_tensor_rows(TensorRows a, NttTables t) {
     using G = Geo<S1, S2>;
     using RS = RowStage<S1, S2, R>;
@@ -1003,9 +1005,9 @@ k_tensor_rows(TensorRows a, NttTables t) {
     RS stage;
     stage.load(t, r.l, r.tile, false);
     if (q < kF64PrimeBound)
-        tensor_rows_tile<ArithF64, S1, S2, R>(a, stage, twl, r, q, lds);
+        tensor_rows_tile<ArithF64, S1, S2, R, MT>(a, stage, twl, r, q, lds);
     else
-        tensor_rows_tile<ArithInt, S1, S2, R>(a, stage, twl, r, q, reinterpret_cast<uint64_t *>(lds));
+        tensor_rows_tile<ArithInt, S1, S2, R, MT>(a, stage, twl, r, q, reinterpret_cast<uint64_t *>(lds));
 }
 
 // ------------------------------------------------------------ launchers
@@ -1033,6 +1035,16 @@ void launch_bconv(const Ctx &c, const BconvCols &a0, hipStream_t s) {
 
 // Rows per tile: 8 for rows of 256 (N = 2^15, 2^16: 8 workgroups of 128
 // threads fill a CU), the inverse rows pass's own height otherwise.
+// The tensor phase of k_tensor_rows runs on twice the rows pass's threads
+// (8 residues each instead of 16; the second half waits out the rows pass):
+// its 1.5-2.2 waves per SIMD were too few to hide the loads (110 VGPRs,
+// config-3 HMult 0.2753/0.2763/0.2759 -> 0.2733/0.2731/0.2734 ms, L = 35
+// 0.7943/0.7940/0.7927 -> 0.7904/0.7896/0.7913 ms, interleaved on one box).
+// The same split made the batch-1 rotation's Galois kernel slower (apply_galois
+// 221.5/225.0/227.7 -> 225.3/231.2/233.0 us), so k_galois_rows keeps one.
+constexpr int kTensorRowsMT = 2;
+constexpr int kGaloisRowsMT = 1;
+
 template <int S1, int S2>
 void launch_tensor_rows(const Ctx &c, const TensorRows &a, hipStream_t s) {
     using G = Geo<S1, S2>;
@@ -1040,8 +1052,9 @@ void launch_tensor_rows(const Ctx &c, const TensorRows &a, hipStream_t s) {
         fail(PFA_ERR_INVALID_ARGUMENT, "fused tensor rows pass: N above 2^16");
     } else {
         constexpr int R = S2 == 8 && G::ROWS == 16 ? 8 : G::ROWS;
-        hipLaunchKernelGGL((k_tensor_rows<S1, S2, R>), dim3(a.Ql * (G::N1 / R), a.count), dim3(R * Sub<S2>::T), 0, s,
-                           a, tables_of(c));
+        constexpr int MT = kTensorRowsMT;
+        hipLaunchKernelGGL((k_tensor_rows<S1, S2, R, MT>), dim3(a.Ql * (G::N1 / R), a.count),
+                           dim3(MT * R * Sub<S2>::T), 0, s, a, tables_of(c));
         PFA_HIP(hipGetLastError());
     }
 }
@@ -1212,12 +1225,13 @@ struct GaloisRows {
     uint32_t elt, Ql, logN, B;
 };
 
-template <int S1, int S2, int R>
-__global__ void __launch_bounds__(R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(3, 8)))
+template <int S1, int S2, int R, int MT>
+__global__ void __launch_bounds__(MT * R * Sub<S2>::T) __attribute__((amdgpu_waves_per_eu(3, 8)))
 k_galois_rows(GaloisRows a, NttTables t) {
     using G = Geo<S1, S2>;
     using RS = RowStage<S1, S2, R>;
-    constexpr uint32_t TILES = G::N1 / R, NT = R * Sub<S2>::T, E = Sub<S2>::E;
+    // the gathers run on all MT R T threads, the rows pass on the first R T
+    constexpr uint32_t TILES = G::N1 / R, NR = R * Sub<S2>::T, NT = MT * NR, E = Sub<S2>::E / MT;
     static_assert(NT * E == R * G::N2, "a tile is NT threads x E residues");
     __shared__ double lds[R * G::ROW_PITCH];
     __shared__ ulonglong2 twl[RS::N];
@@ -1257,7 +1271,7 @@ k_galois_rows(GaloisRows a, NttTables t) {
             lds[(j / G::N2) * G::ROW_PITCH + rpad(j % G::N2)] = ar.load(v[p]);
         }
         __syncthreads();
-        inv_rows_lds<ArithF64, S1, S2, R, true, R>(w, r, q, lds, mid);
+        inv_rows_lds<ArithF64, S1, S2, R, true, R>(w, r, q, lds, mid, threadIdx.x < NR);
     } else {
         const ArithInt ar(q);
         uint64_t *li = reinterpret_cast<uint64_t *>(lds);
@@ -1268,7 +1282,7 @@ k_galois_rows(GaloisRows a, NttTables t) {
             li[(j / G::N2) * G::ROW_PITCH + rpad(j % G::N2)] = ar.load(v[p]);
         }
         __syncthreads();
-        inv_rows_lds<ArithInt, S1, S2, R, true, R>(w, r, q, li, mid);
+        inv_rows_lds<ArithInt, S1, S2, R, true, R>(w, r, q, li, mid, threadIdx.x < NR);
     }
 }
 
@@ -1279,8 +1293,9 @@ void launch_galois_rows(const Ctx &c, const GaloisRows &a, hipStream_t s) {
         fail(PFA_ERR_INVALID_ARGUMENT, "fused Galois rows pass: N above 2^16");
     } else {
         constexpr int R = S2 == 8 && G::ROWS == 16 ? 8 : G::ROWS;
-        hipLaunchKernelGGL((k_galois_rows<S1, S2, R>), dim3(a.Ql * (G::N1 / R), 2 * a.B), dim3(R * Sub<S2>::T), 0, s,
-                           a, tables_of(c));
+        constexpr int MT = kGaloisRowsMT;
+        hipLaunchKernelGGL((k_galois_rows<S1, S2, R, MT>), dim3(a.Ql * (G::N1 / R), 2 * a.B),
+                           dim3(MT * R * Sub<S2>::T), 0, s, a, tables_of(c));
         PFA_HIP(hipGetLastError());
     }
 }

@@ -652,9 +652,11 @@ ntt_fwd_rows(NttBatch b, NttTables t) {
 // Rows pass first: src (canonical) -> dst (intermediate).
 // The pass over a tile whose residues are in LDS already (element k of tile row
 // rr at lds[rr ROW_PITCH + rpad(k)], as A::load gives it), after a barrier.
+// With active false (whole waves beyond the tile's R T threads of a larger
+// workgroup) a thread only takes part in the barriers.
 template <class A, int S1, int S2, int RBS, bool NT = true, int R = Geo<S1, S2>::ROWS>
 __device__ __forceinline__ void inv_rows_lds(const TileTw &w, const TileRef &r, uint64_t q, typename A::T *lds,
-                                             uint64_t *olimb) {
+                                             uint64_t *olimb, bool active = true) {
     using G = Geo<S1, S2>;
     using SB = Sub<S2>;
     using T = typename A::T;
@@ -664,16 +666,21 @@ __device__ __forceinline__ void inv_rows_lds(const TileTw &w, const TileRef &r, 
     uint64_t *drow = olimb + (size_t)k1 * G::N2;
     T *lr = lds + rr * G::ROW_PITCH;
     T x[SB::E];
+    if (active) {
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
-    if constexpr (A::kF64)
-        inv_round_a_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow, F);
-    else
-        inv_round_a<A, S2>(x, ar, w.full, G::N1 + k1, F);
+        for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F * SB::E + e)];
+        if constexpr (A::kF64)
+            inv_round_a_derived<S2, RBS>(x, ar, w.rb, w.small, w.rrow, F);
+        else
+            inv_round_a<A, S2>(x, ar, w.full, G::N1 + k1, F);
+    }
     __syncthreads();
+    if (active) {
 #pragma unroll
-    for (int e = 0; e < SB::E; e++) lr[rpad(F * SB::E + e)] = x[e];
+        for (int e = 0; e < SB::E; e++) lr[rpad(F * SB::E + e)] = x[e];
+    }
     __syncthreads();
+    if (!active) return;
 #pragma unroll
     for (int e = 0; e < SB::E; e++) x[e] = lr[rpad(F + SB::T * e)];
     if constexpr (A::kF64)
