@@ -379,7 +379,67 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             order.insert(order.end(), tail.begin(), tail.end());
             lv.ws_order = c.upload(order);
         }
+        {
+            // k_bconv_cols of a batch-1 ModUp: items (digit b's column tile,
+            // target position j) in grouped order; the digit's own limbs are
+            // skipped, and an integer-policy target (a prime of 50 bits or
+            // more: Montgomery sums and Shoup butterflies) costs about three
+            // FP64 ones
+            const uint32_t col_tiles = (1u << (c.logN - c.logN / 2)) / 16u;
+            const uint32_t NG = lv.beta * col_tiles, total = grouped_total(NG, QlP);
+            const uint32_t R = std::min(total, (uint32_t)c.n_cu * 4u);
+            std::vector<uint8_t> cost(total, 0);
+            for (uint32_t w = 0; w < total; ++w) {
+                uint32_t g, j;
+                if (!grouped_item(w, NG, QlP, g, j)) continue;
+                const uint32_t b = g / col_tiles, n_in = std::min(alpha, Ql - b * alpha);
+                if (j >= b * alpha && j < b * alpha + n_in) continue;
+                cost[w] = moduli[c.qlp_row(Ql, j)] < kF64PrimeBound ? 1 : 3;
+            }
+            const std::vector<uint32_t> sched = lpt_schedule(cost, R);
+            if (!sched.empty()) {
+                lv.modup_sched = c.upload(sched);
+                lv.modup_sched_grid = R;
+                lv.modup_sched_total = total;
+            }
+        }
     }
+}
+
+std::vector<uint32_t> lpt_schedule(const std::vector<uint8_t> &cost, uint32_t R) {
+    const uint32_t total = (uint32_t)cost.size();
+    if (R == 0 || R % 8 || total <= R) return {};
+    std::vector<uint32_t> perm(total, ~0u), used(R, 0), load(R, 0);
+    auto npos = [&](uint32_t b) { return (total - b + R - 1) / R; };
+    for (uint32_t x = 0; x < 8; ++x) {
+        std::vector<uint32_t> items;
+        for (uint32_t w = x; w < total; w += 8) items.push_back(w);
+        std::stable_sort(items.begin(), items.end(), [&](uint32_t a, uint32_t b) { return cost[a] > cost[b]; });
+        // min-heap on (assigned cost, positions, workgroup): ties go to the
+        // workgroup with fewer positions, which has fewer items left to take
+        using E = std::pair<std::pair<uint32_t, uint32_t>, uint32_t>;
+        std::vector<E> heap;
+        for (uint32_t b = x; b < R; b += 8)
+            if (npos(b)) heap.push_back({{0u, npos(b)}, b});
+        auto later = [](const E &a, const E &b) { return a > b; };
+        std::make_heap(heap.begin(), heap.end(), later);
+        for (uint32_t w : items) {
+            if (heap.empty()) return {};
+            std::pop_heap(heap.begin(), heap.end(), later);
+            const uint32_t b = heap.back().second;
+            heap.pop_back();
+            perm[b + used[b] * R] = w;
+            ++used[b];
+            load[b] += cost[w];
+            if (used[b] < npos(b)) {
+                heap.push_back({{load[b], npos(b)}, b});
+                std::push_heap(heap.begin(), heap.end(), later);
+            }
+        }
+    }
+    for (uint32_t p : perm)
+        if (p == ~0u) return {};
+    return perm;
 }
 
 Arena &arena_for(const Ctx &c, hipStream_t s) {

@@ -93,6 +93,11 @@ struct BconvCols {
     // one Montgomery reduction (the context's constants -q^-1 mod 2^64); set by
     // the launcher when every input sum stays below 2^64, else null (Shoup)
     const ulonglong2 *mont = nullptr;
+    // position -> item table (a permutation of the launch's positions) built
+    // for sched_grid workgroups over sched_total positions; the launcher drops
+    // it when its launch differs.  null: position p runs item p
+    const uint32_t *sched = nullptr;
+    uint32_t sched_grid = 0, sched_total = 0;
 };
 
 __device__ __forceinline__ uint32_t bconv_in_row(const BconvCols &a, uint32_t row0, uint32_t i) {
@@ -205,7 +210,8 @@ __global__ void __launch_bounds__((Geo<S1, S2>::COL_THREADS)) k_bconv_cols(Bconv
     __shared__ ulonglong2 twl[G::N1];  // the target prime's columns-pass twiddles
     const uint32_t NG = a.batch * a.groups * G::COL_TILES;
     const uint32_t total = grouped_total(NG, a.J);
-    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+    for (uint32_t p = blockIdx.x; p < total; p += gridDim.x) {
+        const uint32_t w = a.sched ? ld_const(a.sched + p) : p;
         uint32_t gt, j;
         if (!grouped_item(w, NG, a.J, gt, j)) continue;
         const uint32_t mg = gt / G::COL_TILES, tile = gt % G::COL_TILES;
@@ -1028,8 +1034,9 @@ void launch_bconv(const Ctx &c, const BconvCols &a0, hipStream_t s) {
     // below the context's largest prime
     if (c.max_modulus <= ~0ull / std::max(a.n_in, a.n_in_last)) a.mont = c.mont;
     const uint32_t total = grouped_total(a.batch * a.groups * G::COL_TILES, a.J);
-    hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(fgrid(c, total, 4)), dim3(G::COL_THREADS), 0, s, a,
-                       tables_of(c));
+    const uint32_t grid = fgrid(c, total, 4);
+    if (a.sched && (grid != a.sched_grid || total != a.sched_total)) a.sched = nullptr;
+    hipLaunchKernelGGL((k_bconv_cols<S1, S2>), dim3(grid), dim3(G::COL_THREADS), 0, s, a, tables_of(c));
     PFA_HIP(hipGetLastError());
 }
 
@@ -1170,6 +1177,11 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.batch = batch;
     b.in_bstride = LN;
     b.out_bstride = IN;
+    if (batch == 1) {
+        b.sched = lv.modup_sched;
+        b.sched_grid = lv.modup_sched_grid;
+        b.sched_total = lv.modup_sched_total;
+    }
     PFA_FUSED_DISPATCH(launch_bconv, b);
     InnerRows r{inter, c2, key, cx, c.mont, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
     r.batch = batch;

@@ -86,7 +86,34 @@ struct Level {
     // key-switch inner product: the QlP targets with the FP64-policy primes
     // first (in order), then the integer-policy ones
     uint32_t *ws_order = nullptr;
+    // ModUp base conversion of one key switch (batch 1): position -> item
+    // table of k_bconv_cols for a grid of modup_sched_grid workgroups over
+    // modup_sched_total positions (null: positions are the items)
+    uint32_t *modup_sched = nullptr;
+    uint32_t modup_sched_grid = 0, modup_sched_total = 0;
 };
+
+// Work item w of a grouped launch: G groups of J items that read the same input
+// tile.  A group's items all carry the same w mod 8, so in a grid whose size
+// is a multiple of 8 they run on workgroups of one XCD (workgroups are dealt to
+// the XCDs round-robin) and share its L2 copy of the input tile.
+__host__ __device__ inline bool grouped_item(uint32_t w, uint32_t G, uint32_t J, uint32_t &g, uint32_t &j) {
+    const uint32_t x = w & 7u, k = w >> 3;
+    j = k % J;
+    g = (k / J) * 8u + x;
+    return g < G;
+}
+
+__host__ __device__ inline uint32_t grouped_total(uint32_t G, uint32_t J) { return ((G + 7u) / 8u) * 8u * J; }
+
+// Static schedule of a persistent launch whose workgroup b runs positions b,
+// b + R, b + 2R, ... < cost.size(): returns the position -> item permutation
+// that gives the items, heaviest first, to the workgroup with the least
+// assigned cost that still has a free position (longest-processing-time
+// order), keeping every item on a workgroup congruent to it mod 8 (the same
+// XCD when workgroups are dealt round-robin).  Empty when R is not a
+// multiple of 8 or every workgroup has at most one position.
+std::vector<uint32_t> lpt_schedule(const std::vector<uint8_t> &cost, uint32_t R);
 
 // Device workspace of one (host thread, stream): chunks grown on demand and
 // kept until the context is destroyed, handed out by a bump pointer.  Work on

@@ -256,6 +256,9 @@ __device__ __forceinline__ uint64_t wave_uniform(uint64_t v) {
 __device__ __forceinline__ uint64_t ld_const(const uint64_t *p) {
     return *(const __attribute__((address_space(4))) uint64_t *)p;
 }
+__device__ __forceinline__ uint32_t ld_const(const uint32_t *p) {
+    return *(const __attribute__((address_space(4))) uint32_t *)p;
+}
 __device__ __forceinline__ ulonglong2 ld_const(const ulonglong2 *p) {
     const uint64_t *w = reinterpret_cast<const uint64_t *>(p);
     return ulonglong2{ld_const(w), ld_const(w + 1)};

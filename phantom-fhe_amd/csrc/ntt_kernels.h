@@ -356,19 +356,6 @@ __device__ __forceinline__ uint32_t next_tile(const NttBatch &b, uint32_t tiles,
     return id;
 }
 
-// Work item w of a grouped launch: G groups of J items that read the same input
-// tile.  A group's items all carry the same w mod 8, so in a grid whose size
-// is a multiple of 8 they run on workgroups of one XCD (workgroups are dealt to
-// the XCDs round-robin) and share its L2 copy of the input tile.
-__device__ __forceinline__ bool grouped_item(uint32_t w, uint32_t G, uint32_t J, uint32_t &g, uint32_t &j) {
-    const uint32_t x = w & 7u, k = w >> 3;
-    j = k % J;
-    g = (k / J) * 8u + x;
-    return g < G;
-}
-
-__host__ __device__ inline uint32_t grouped_total(uint32_t G, uint32_t J) { return ((G + 7u) / 8u) * 8u * J; }
-
 // ================================================================ twiddles
 // Where a tile's twiddle factors come from.  Columns passes index col[0 .. N1-1]
 // (entries 1 .. N1-1 of the prime's table).  Rows passes index, in the integer
