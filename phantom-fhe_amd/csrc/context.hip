@@ -379,31 +379,43 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
             order.insert(order.end(), tail.begin(), tail.end());
             lv.ws_order = c.upload(order);
         }
-        {
-            // k_bconv_cols of a batch-1 ModUp: items (digit b's column tile,
-            // target position j) in grouped order; the digit's own limbs are
-            // skipped, and an integer-policy target (a prime of 50 bits or
-            // more: Montgomery sums and Shoup butterflies) costs about three
-            // FP64 ones
-            const uint32_t col_tiles = (1u << (c.logN - c.logN / 2)) / 16u;
-            const uint32_t NG = lv.beta * col_tiles, total = grouped_total(NG, QlP);
-            const uint32_t R = std::min(total, (uint32_t)c.n_cu * 4u);
-            std::vector<uint8_t> cost(total, 0);
-            for (uint32_t w = 0; w < total; ++w) {
-                uint32_t g, j;
-                if (!grouped_item(w, NG, QlP, g, j)) continue;
-                const uint32_t b = g / col_tiles, n_in = std::min(alpha, Ql - b * alpha);
-                if (j >= b * alpha && j < b * alpha + n_in) continue;
-                cost[w] = moduli[c.qlp_row(Ql, j)] < kF64PrimeBound ? 1 : 3;
-            }
-            const std::vector<uint32_t> sched = lpt_schedule(cost, R);
-            if (!sched.empty()) {
-                lv.modup_sched = c.upload(sched);
-                lv.modup_sched_grid = R;
-                lv.modup_sched_total = total;
-            }
-        }
     }
+}
+
+Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch) {
+    if (batch == 0 || batch > 64) return {};
+    std::lock_guard<std::mutex> lock(c.sched_mu);
+    const auto key = std::make_pair(chain, batch);
+    const auto it = c.scheds.find(key);
+    if (it != c.scheds.end()) return it->second;
+    // items (member, digit b's column tile, target position j) in the
+    // grouped order of k_bconv_cols; the digit's own limbs are skipped, and an
+    // integer-policy target (a prime of 50 bits or more: Montgomery sums and
+    // Shoup butterflies) costs about three FP64 ones
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    const uint32_t col_tiles = (1u << (c.logN - c.logN / 2)) / 16u;
+    const uint32_t NG = batch * lv.beta * col_tiles, total = grouped_total(NG, QlP);
+    const uint32_t R = std::min(total, (uint32_t)c.n_cu * 4u);
+    std::vector<uint8_t> cost(total, 0);
+    for (uint32_t w = 0; w < total; ++w) {
+        uint32_t g, j;
+        if (!grouped_item(w, NG, QlP, g, j)) continue;
+        const uint32_t b = (g / col_tiles) % lv.beta, n_in = std::min(alpha, Ql - b * alpha);
+        if (j >= b * alpha && j < b * alpha + n_in) continue;
+        cost[w] = c.moduli[c.qlp_row(Ql, j)] < kF64PrimeBound ? 1 : 3;
+    }
+    Sched sc;
+    const std::vector<uint32_t> perm = lpt_schedule(cost, R);
+    if (!perm.empty()) {
+        void *p = nullptr;
+        PFA_HIP(hipMalloc(&p, perm.size() * sizeof(uint32_t)));
+        c.sched_allocs.push_back(p);
+        PFA_HIP(hipMemcpy(p, perm.data(), perm.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+        sc = Sched{(const uint32_t *)p, R, total};
+    }
+    c.scheds[key] = sc;
+    return sc;
 }
 
 std::vector<uint32_t> lpt_schedule(const std::vector<uint8_t> &cost, uint32_t R) {
@@ -507,6 +519,7 @@ static void destroy(Ctx *c) {
         delete kv.second;
     }
     for (void *p : c->allocations) (void)hipFree(p);
+    for (void *p : c->sched_allocs) (void)hipFree(p);
     (void)hipSetDevice(prev);
     delete c;
 }

@@ -1177,11 +1177,10 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.batch = batch;
     b.in_bstride = LN;
     b.out_bstride = IN;
-    if (batch == 1) {
-        b.sched = lv.modup_sched;
-        b.sched_grid = lv.modup_sched_grid;
-        b.sched_total = lv.modup_sched_total;
-    }
+    const Sched sch = modup_schedule(c, chain, batch);
+    b.sched = sch.table;
+    b.sched_grid = sch.grid;
+    b.sched_total = sch.total;
     PFA_FUSED_DISPATCH(launch_bconv, b);
     InnerRows r{inter, c2, key, cx, c.mont, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
     r.batch = batch;

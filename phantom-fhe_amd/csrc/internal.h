@@ -86,11 +86,13 @@ struct Level {
     // key-switch inner product: the QlP targets with the FP64-policy primes
     // first (in order), then the integer-policy ones
     uint32_t *ws_order = nullptr;
-    // ModUp base conversion of one key switch (batch 1): position -> item
-    // table of k_bconv_cols for a grid of modup_sched_grid workgroups over
-    // modup_sched_total positions (null: positions are the items)
-    uint32_t *modup_sched = nullptr;
-    uint32_t modup_sched_grid = 0, modup_sched_total = 0;
+};
+
+// Position -> item table of one k_bconv_cols launch shape: a permutation of
+// `total` positions for a grid of `grid` workgroups (see lpt_schedule)
+struct Sched {
+    const uint32_t *table = nullptr;
+    uint32_t grid = 0, total = 0;
 };
 
 // Work item w of a grouped launch: G groups of J items that read the same input
@@ -209,6 +211,11 @@ struct Ctx {
     hipEvent_t stage_ev[kStageSlots] = {};
     mutable std::mutex stage_mu;
     mutable size_t stage_next = 0;
+    // ModUp base-conversion schedules by (chain index, batch), built on first
+    // use (modup_schedule); their device tables are freed with the context
+    mutable std::mutex sched_mu;
+    mutable std::map<std::pair<uint32_t, uint32_t>, Sched> scheds;
+    mutable std::vector<void *> sched_allocs;
 
     uint32_t size_Ql(uint32_t chain) const { return Q - (chain - 1); }
     const Level &level(uint32_t chain) const {
@@ -229,6 +236,13 @@ T *Ctx::upload(const std::vector<T> &v) {
     if (!v.empty()) PFA_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
     return (T *)p;
 }
+
+// The schedule of the ModUp base conversion of `batch` key switches at chain
+// index `chain` (k_bconv_cols over batch x beta digits x column tiles x QlP
+// targets), built and uploaded on first use: a synchronous upload, so the
+// first key switch of a shape must not run under stream capture (the first
+// call of a shape also grows the workspace).  Batches above 64 get none.
+Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch);
 
 Ctx *ctx_of(const pfa_context *c);
 // Throws PFA_ERR_RUNTIME (and clears the record) if a kernel of this context
