@@ -29,7 +29,9 @@
  *   - Temporaries come from a device workspace kept per (host thread, stream)
  *     and grown on first use, where the reference makes stream-ordered
  *     allocations (cuda_auto_ptr, include/cuda_wrapper.cuh:185-189); calls in
- *     steady state allocate nothing.
+ *     steady state allocate nothing.  The first key switch of a (level,
+ *     batch) shape also builds and uploads its base-conversion work schedule
+ *     (kept with the context), so a shape's first call must not be captured.
  */
 #ifndef PHANTOM_AMD_H
 #define PHANTOM_AMD_H
