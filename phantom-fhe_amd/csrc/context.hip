@@ -382,29 +382,14 @@ static void build(Ctx &c, uint64_t N, const uint64_t *moduli, size_t QP, size_t 
     }
 }
 
-Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch) {
-    if (batch == 0 || batch > 64) return {};
+// The cached schedule for `key`, built from the item costs `make` returns
+// for a grid of R workgroups on first use.
+template <class F>
+static Sched cached_schedule(const Ctx &c, const std::array<uint32_t, 4> &key, uint32_t R, F make) {
     std::lock_guard<std::mutex> lock(c.sched_mu);
-    const auto key = std::make_pair(chain, batch);
     const auto it = c.scheds.find(key);
     if (it != c.scheds.end()) return it->second;
-    // items (member, digit b's column tile, target position j) in the
-    // grouped order of k_bconv_cols; the digit's own limbs are skipped, and an
-    // integer-policy target (a prime of 50 bits or more: Montgomery sums and
-    // Shoup butterflies) costs about three FP64 ones
-    const Level &lv = c.level(chain);
-    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
-    const uint32_t col_tiles = (1u << (c.logN - c.logN / 2)) / 16u;
-    const uint32_t NG = batch * lv.beta * col_tiles, total = grouped_total(NG, QlP);
-    const uint32_t R = std::min(total, (uint32_t)c.n_cu * 4u);
-    std::vector<uint8_t> cost(total, 0);
-    for (uint32_t w = 0; w < total; ++w) {
-        uint32_t g, j;
-        if (!grouped_item(w, NG, QlP, g, j)) continue;
-        const uint32_t b = (g / col_tiles) % lv.beta, n_in = std::min(alpha, Ql - b * alpha);
-        if (j >= b * alpha && j < b * alpha + n_in) continue;
-        cost[w] = c.moduli[c.qlp_row(Ql, j)] < kF64PrimeBound ? 1 : 3;
-    }
+    const std::vector<uint8_t> cost = make();
     Sched sc;
     const std::vector<uint32_t> perm = lpt_schedule(cost, R);
     if (!perm.empty()) {
@@ -412,10 +397,47 @@ Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch) {
         PFA_HIP(hipMalloc(&p, perm.size() * sizeof(uint32_t)));
         c.sched_allocs.push_back(p);
         PFA_HIP(hipMemcpy(p, perm.data(), perm.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
-        sc = Sched{(const uint32_t *)p, R, total};
+        sc = Sched{(const uint32_t *)p, R, (uint32_t)cost.size()};
     }
     c.scheds[key] = sc;
     return sc;
+}
+
+// An integer-policy target (a prime of 50 bits or more: Montgomery sums and
+// Shoup butterflies) costs about three FP64 ones.
+static uint8_t target_cost(const Ctx &c, uint32_t row) { return c.moduli[row] < kF64PrimeBound ? 1 : 3; }
+
+Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch) {
+    if (batch == 0 || batch > 64) return {};
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    const uint32_t col_tiles = (1u << (c.logN - c.logN / 2)) / 16u;
+    const uint32_t NG = batch * lv.beta * col_tiles, total = grouped_total(NG, QlP);
+    const uint32_t R = std::min(total, (uint32_t)c.n_cu * 4u);
+    // items (member, digit b's column tile, target position j) in the
+    // grouped order of k_bconv_cols; the digit's own limbs are skipped
+    return cached_schedule(c, {0u, chain, batch, 0u}, R, [&] {
+        std::vector<uint8_t> cost(total, 0);
+        for (uint32_t w = 0; w < total; ++w) {
+            uint32_t g, j;
+            if (!grouped_item(w, NG, QlP, g, j)) continue;
+            const uint32_t b = (g / col_tiles) % lv.beta, n_in = std::min(alpha, Ql - b * alpha);
+            if (j >= b * alpha && j < b * alpha + n_in) continue;
+            cost[w] = target_cost(c, c.qlp_row(Ql, j));
+        }
+        return cost;
+    });
+}
+
+Sched epi_schedule(const Ctx &c, uint32_t J, uint32_t M, uint32_t tiles, uint32_t grid) {
+    const uint64_t total = (uint64_t)M * J * tiles;
+    if (total <= grid || total > (1u << 20) || J > c.Q) return {};
+    // item w: row tile w mod tiles of poly (w / tiles) mod M, target (w / tiles) / M
+    return cached_schedule(c, {1u, J, M, tiles}, grid, [&] {
+        std::vector<uint8_t> cost(total);
+        for (uint32_t w = 0; w < total; ++w) cost[w] = target_cost(c, (w / tiles) / M);
+        return cost;
+    });
 }
 
 std::vector<uint32_t> lpt_schedule(const std::vector<uint8_t> &cost, uint32_t R) {

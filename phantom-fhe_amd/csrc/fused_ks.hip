@@ -774,6 +774,13 @@ struct EpiRows {
     // fused ModDown + rescale: when set ([J] pairs in each limb's NTT policy),
     // out = (c f1 + base - NTT(D)) f instead
     const ulonglong2 *f1 = nullptr;
+    // the launcher may look up (and on first use build) a work schedule; the
+    // allocation-free rescale turns that off
+    bool allow_sched = true;
+    // position -> item table for sched_grid workgroups over sched_total
+    // positions (set by the launcher), or null: position p runs item p
+    const uint32_t *sched = nullptr;
+    uint32_t sched_grid = 0, sched_total = 0;
 };
 
 template <class A, int S1, int S2>
@@ -867,7 +874,8 @@ k_epi_rows(EpiRows a, NttTables t) {
     __shared__ ulonglong2 twl[S2 * FG::ROWS + (1 << (S2 - 1))];
     const uint32_t rr = threadIdx.x / Sub<S2>::T;
     const uint32_t total = a.M * a.J * FG::TILES;
-    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+    for (uint32_t p = blockIdx.x; p < total; p += gridDim.x) {
+        const uint32_t w = a.sched ? ld_const(a.sched + p) : p;
         const uint32_t tile = w % FG::TILES, mj = w / FG::TILES;
         const uint32_t m = mj % a.M, j = mj / a.M;
         const uint64_t q = t.mod[j];
@@ -1114,10 +1122,19 @@ void launch_inner(const Ctx &c, InnerRows a, hipStream_t s) {
 }
 
 template <int S1, int S2>
-void launch_epi(const Ctx &c, const EpiRows &a, hipStream_t s) {
+void launch_epi(const Ctx &c, const EpiRows &a0, hipStream_t s) {
     using FG = FGeo<S1, S2>;
-    hipLaunchKernelGGL((k_epi_rows<S1, S2>), dim3(fgrid(c, a.M * a.J * FG::TILES, 8)), dim3(FG::THREADS), 0, s, a,
-                       tables_of(c));
+    EpiRows a = a0;
+    const uint32_t total = a.M * a.J * FG::TILES, grid = fgrid(c, total, 8);
+    if (a.allow_sched) {
+        const Sched sch = epi_schedule(c, a.J, a.M, FG::TILES, grid);
+        if (sch.table && sch.grid == grid && sch.total == total) {
+            a.sched = sch.table;
+            a.sched_grid = sch.grid;
+            a.sched_total = sch.total;
+        }
+    }
+    hipLaunchKernelGGL((k_epi_rows<S1, S2>), dim3(grid), dim3(FG::THREADS), 0, s, a, tables_of(c));
     PFA_HIP(hipGetLastError());
 }
 
@@ -1442,6 +1459,7 @@ void fused_rescale_with(const Ctx &c, uint32_t chain, const uint64_t *in, uint32
     b.bc_istride = 0;
     PFA_FUSED_DISPATCH(launch_bconv, b);
     EpiRows e{inter, in, nullptr, nullptr, out, lv.rescale_inv_p, (uint64_t)L * c.N, size, L - 1};
+    e.allow_sched = allow_flow;
     PFA_FUSED_DISPATCH(launch_epi, e);
 }
 

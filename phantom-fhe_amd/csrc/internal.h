@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <array>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -211,10 +212,11 @@ struct Ctx {
     hipEvent_t stage_ev[kStageSlots] = {};
     mutable std::mutex stage_mu;
     mutable size_t stage_next = 0;
-    // ModUp base-conversion schedules by (chain index, batch), built on first
-    // use (modup_schedule); their device tables are freed with the context
+    // work schedules of the base-conversion and epilogue launches by (kind,
+    // shape), built on first use (modup_schedule, epi_schedule); their device
+    // tables are freed with the context
     mutable std::mutex sched_mu;
-    mutable std::map<std::pair<uint32_t, uint32_t>, Sched> scheds;
+    mutable std::map<std::array<uint32_t, 4>, Sched> scheds;
     mutable std::vector<void *> sched_allocs;
 
     uint32_t size_Ql(uint32_t chain) const { return Q - (chain - 1); }
@@ -243,6 +245,11 @@ T *Ctx::upload(const std::vector<T> &v) {
 // first key switch of a shape must not run under stream capture (the first
 // call of a shape also grows the workspace).  Batches above 64 get none.
 Sched modup_schedule(const Ctx &c, uint32_t chain, uint32_t batch);
+// The schedule of a k_epi_rows launch over M polys x J target limbs (the
+// level's first J primes) x `tiles` row tiles on `grid` workgroups, built
+// and uploaded on first use like modup_schedule; none when every workgroup
+// has at most one item.
+Sched epi_schedule(const Ctx &c, uint32_t J, uint32_t M, uint32_t tiles, uint32_t grid);
 
 Ctx *ctx_of(const pfa_context *c);
 // Throws PFA_ERR_RUNTIME (and clears the record) if a kernel of this context
@@ -352,7 +359,8 @@ void fused_rescale(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t si
 // The same with the caller's buffers for the last limb's coefficients (last,
 // size N) and the base conversion's intermediate (inter, size (Ql - 1) N; may
 // be out itself: the epilogue rewrites each tile of it in place); allocates
-// nothing when allow_flow is false.
+// nothing when allow_flow is false (no single-launch NTT control blocks, no
+// epilogue work schedule).
 void fused_rescale_with(const Ctx &c, uint32_t chain, const uint64_t *in, uint32_t size, uint64_t *out,
                         uint64_t *last, uint64_t *inter, hipStream_t s, bool allow_flow);
 // Allocation-free entry points (noalloc.hip): takes the address of this
