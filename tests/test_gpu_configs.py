@@ -6,6 +6,9 @@ only by bench.py.
   alpha = 1, dnum = 35): multiply_and_relin, rescale and the fused call are
   bit-exact against the oracle's multiply_and_relin_inplace
   (src/evaluate.cu:1061-1104) followed by rescale_to_next (src/rns.cu:1128-1184).
+* Batched HMult (config 3) and batched rotation (config 4 shape) at full size:
+  every member equals the single call, which covers the work schedules of the
+  batched base-conversion and epilogue launches.
 * Config 4, the BSGS matrix-vector product at N = 2^16 (4096 x 4096 matrix
   uniform in [-1/64, 1/64], baby 64 / giant 64, L = 20, scale 2^40): decode
   within 1e-5 of numpy's W x.  The reference's own check of this product is a
@@ -49,6 +52,63 @@ def test_hmult_L35_alpha1_full_size(dev):
     st.ctx.multiply_relin_rescale(1, da, db, dk, fused)
     got = to_host(fused)
     assert np.array_equal(got, want_r), first_mismatch(got, want_r)
+
+
+@pytest.mark.parametrize("count", [2, 5])
+def test_hmult_config3_batch_equals_single_full_size(dev, count):
+    """Batched HMult at config 3's full size (N = 2^16, |Q| = 24, alpha = 4):
+    every member of pfa_multiply_and_relin_batch and
+    pfa_multiply_relin_rescale_batch equals the single call on its pair, bit for
+    bit.  At this size the batched base conversion and ModDown epilogue have more
+    work items than workgroups and run through their work schedules (position
+    -> item tables), which the small-N batch tests of test_gpu_keyswitch.py never
+    reach; the single calls are pinned against the oracle at this size there
+    (test_multiply_and_relin_config3, test_multiply_relin_rescale_config3)."""
+    st = Setup(16, 24, 4, seed=40 + count)
+    a = np.stack([st.ct(1) for _ in range(count)])
+    b = np.stack([st.ct(1) for _ in range(count)])
+    key = st.key()
+    da, db, dk = to_dev(a, dev), to_dev(b, dev), to_dev(key, dev)
+    single = empty((count, 2, 24, st.N), dev)
+    single_r = empty((count, 2, 23, st.N), dev)
+    for i in range(count):
+        st.ctx.multiply_and_relin(1, da[i], db[i], dk, single[i])
+        st.ctx.multiply_relin_rescale(1, da[i], db[i], dk, single_r[i])
+    out = empty((count, 2, 24, st.N), dev)
+    st.ctx.multiply_and_relin_batch(1, count, da, db, dk, out)
+    res = empty((count, 2, 23, st.N), dev)
+    st.ctx.multiply_relin_rescale_batch(1, count, da, db, dk, res)
+    want, got = to_host(single), to_host(out)
+    for i in range(count):
+        assert np.array_equal(got[i], want[i]), (i, first_mismatch(got[i], want[i]))
+    want, got = to_host(single_r), to_host(res)
+    for i in range(count):
+        assert np.array_equal(got[i], want[i]), (i, first_mismatch(got[i], want[i]))
+    st.ctx.synchronize()
+
+
+def test_rotate_batch_config4_equals_single_full_size(dev):
+    """pfa_rotate_batch at config 4's shape (N = 2^16, chain {60, 40 x 19, 60 x 4},
+    alpha = 4; 3 members, each with its own step and key) equals
+    pfa_apply_galois on each member, bit for bit: the batched ModUp conversion
+    runs through its work schedule here (single rotations at this shape are
+    pinned against the oracle's apply_galois at N = 2^12 and 2^13 in
+    test_gpu_keyswitch.py)."""
+    import pfa_native as P
+
+    st = Setup(16, 20, 4, seed=44, bits=[60] + [40] * 19 + [60] * 4)
+    cts = np.stack([st.ct(1) for _ in range(3)])
+    keys = [to_dev(st.key(), dev) for _ in range(3)]
+    elts = [P.galois_elt_from_step(s, st.N) for s in (64, 1, -3)]
+    out = empty(cts.shape, dev)
+    st.ctx.rotate_batch(1, to_dev(cts, dev), elts, keys, out)
+    got = to_host(out)
+    for i in range(3):
+        one = to_dev(cts[i], dev)
+        st.ctx.apply_galois(1, one, elts[i], keys[i])
+        want = to_host(one)
+        assert np.array_equal(got[i], want), (i, first_mismatch(got[i], want))
+    st.ctx.synchronize()
 
 
 def test_bsgs_config4_full_size(dev):
