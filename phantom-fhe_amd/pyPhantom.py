@@ -2510,3 +2510,295 @@ def bootstrap(context: context, encoder: ckks_encoder, ct: ciphertext, bk: boots
     out = apply_s2c_inplace(ctx, y, bk)
     out.set_scale(scale * out.scale() / q0)
     return out
+
+
+# ---------------------------------------------------------------- CKKS engine
+class ckks_engine_config:
+    """CKKSEngineConfig (include/ckks_engine.h:29-95, python/src/binding.cu:339-355):
+    the knobs of the bootstrappable facade, with the reference's defaults."""
+
+    def __init__(self):
+        self.log_n = 16
+        self.user_scale = 2.0 ** 40
+        self.num_scale_levels = 14
+        self.sparse_hw = 128
+        self.num_special_primes = 6
+        self.include_user_rotations = True
+        self.user_rotation_steps = []
+        self.user_rotation_target_chain_indices = []
+        self.split_scale_down = False
+        self.build_two_scale_arrays = False
+        self.use_bootstrap_to_17_levels = False
+
+
+def _long_double(v: int):
+    """The integer 0 <= v < 2^64 as a numpy long double, exactly (the x87
+    extended format of x86-64 has a 64-bit significand), as the reference's
+    static_cast<long double>(uint64_t) makes it."""
+    return np.longdouble(v >> 32) * np.longdouble(1 << 32) + np.longdouble(v & 0xFFFFFFFF)
+
+
+# EvalMod levels of the engine's pipeline (evalmod_k28_r3: 6 sine + 3 double angle)
+_ENGINE_EVALMOD_LEVELS = 9
+
+
+class ckks_engine:
+    """CKKSEngine (src/ckks_engine.cu, include/ckks_engine.h) with the methods
+    its Python binding exposes (python/src/binding.cu:357-382): a CKKS context
+    on a bootstrappable chain, its secret, relinearization, bootstrap and user
+    rotation keys, where the caller sees a user_level counter only.  User level
+    0 is the freshest level of the user-scale segment, each rescale adds 1,
+    max_user_level() = num_scale_levels - 1 is the deepest one (two primes
+    left), and bootstrap_inplace brings a ciphertext at any user level back to
+    user level 0 (1 with split_scale_down).
+
+    Chain (src/ckks_engine.cu:76-127), bottom to top, then the special primes:
+      default:  58 | 40 x num_scale_levels | 58 x 3 | 58 x 9 | 29 x 3 | 58 x special
+      use_bootstrap_to_17_levels: 40 x num_scale_levels | 29 | 54 x 12 | 42 | 60 x special
+    (the second chain only: encode / encrypt / decrypt; bootstrap_inplace
+    refuses it, as the reference does).  Residues follow the library's
+    bootstrap and key switching; the keys come from this build's seedable
+    sampler (`seed`), so they equal the reference's only given the same key
+    material."""
+
+    def __init__(self, config: ckks_engine_config | None = None, seed=None):
+        import copy
+
+        cfg = copy.deepcopy(config) if config is not None else ckks_engine_config()
+        self._cfg = cfg
+        if int(cfg.log_n) != 16:
+            raise ValueError("CKKSEngine: this port pins log_n=16")
+        nsl, nsp = int(cfg.num_scale_levels), int(cfg.num_special_primes)
+        if nsl < 2:
+            raise ValueError("CKKSEngine: num_scale_levels must be >= 2")
+        if nsp < 1:
+            raise ValueError("CKKSEngine: num_special_primes must be >= 1")
+        size_Q = nsl + 14 if cfg.use_bootstrap_to_17_levels else 1 + nsl + 3 + 9 + 3
+        if size_Q % nsp:
+            raise ValueError("CKKSEngine: size_Q must be divisible by num_special_primes "
+                             "(required by the hybrid KSK decomposition).")
+        N = 1 << int(cfg.log_n)
+        if cfg.use_bootstrap_to_17_levels:
+            bits = [40] * nsl + [29] + [54] * 12 + [42] + [60] * nsp
+        else:
+            bits = ckks_engine_coeff_bits(nsl, nsp)
+        # Galois elements: the CoeffToSlot / SlotToCoeff steps, the user steps
+        # (the explicit list, else +-1 and +-2), then conjugation
+        stages = [5, 5, 5]
+        c2s, s2c = build_c2s_diagonals(cfg.log_n, stages), build_s2c_diagonals(cfg.log_n, stages)
+        boot_steps = set(c2s_required_rotation_steps(c2s, N // 2)) | set(c2s_required_rotation_steps(s2c, N // 2))
+        if cfg.user_rotation_steps:
+            user_steps = [int(s) for s in cfg.user_rotation_steps]
+        elif cfg.include_user_rotations:
+            user_steps = [1, -1, 2, -2]
+        else:
+            user_steps = []
+        conj = 2 * N - 1
+        elts = get_elts_from_steps(sorted(boot_steps | set(user_steps)), N) + [conj]
+        p = params(scheme_type.ckks)
+        p.set_poly_modulus_degree(N)
+        p.set_special_modulus_size(nsp)
+        p.set_coeff_modulus(create_coeff_modulus(N, bits))
+        p.set_galois_elts(elts)
+        self._ctx = context(p)
+        rng = _rng(seed)
+        self._sk = secret_key(self._ctx, seed=rng)
+        self._enc = ckks_encoder(self._ctx)
+        self._bk = None
+        self._user_glk = galois_key(self._ctx.galois_elts)
+        first = self._ctx.get_first_index()
+        self._bottom = self._ctx.total_parm_size() - 1
+        self._ckks_scale, self._ckks_rescaled_scale = [], []
+        if cfg.use_bootstrap_to_17_levels:
+            # CoeffToSlot 1 + EvalRound 9 + SlotToCoeff 3 primes above the
+            # user segment, whose first rescale drops the 29-bit prime
+            self._freshest = first + 13
+            if self._freshest + nsl != self._bottom:
+                raise RuntimeError("CKKSEngine: BootstrapTo17Levels chain mismatch: "
+                                   "freshest + num_scale_levels != bottom.")
+            if cfg.build_two_scale_arrays:
+                self._build_scale_arrays()
+            return
+        self._bk = create_bootstrap_key(self._ctx, self._enc, self._sk, sparse_hamming_weight=int(cfg.sparse_hw),
+                                        eval_mod_levels=_ENGINE_EVALMOD_LEVELS, user_scale=float(cfg.user_scale),
+                                        split_scale_down=bool(cfg.split_scale_down), stages_per_layer=stages,
+                                        seed=rng)
+        nl = len(stages)
+        self._freshest = first + nl + _ENGINE_EVALMOD_LEVELS + nl
+        if self._freshest + nsl != self._bottom:
+            raise RuntimeError("CKKSEngine: chain layout mismatch: freshest + num_scale_levels != bottom. "
+                               "Check chain construction.")
+        glk = self._bk.glk
+        if not user_steps:
+            # the bootstrap key's user bundle: conjugation only
+            self._user_glk.keys[conj] = glk.keys[conj]
+        else:
+            targets = [int(t) for t in cfg.user_rotation_target_chain_indices]
+            if targets:
+                if not cfg.user_rotation_steps:
+                    raise ValueError("CKKSEngine: user_rotation_target_chain_indices set but "
+                                     "user_rotation_steps is empty")
+                if len(targets) != len(cfg.user_rotation_steps):
+                    raise ValueError("CKKSEngine: user_rotation_target_chain_indices size "
+                                     "must match user_rotation_steps size")
+            index = {e: i for i, e in enumerate(self._ctx.galois_elts)}
+
+            def find_idx(elt):
+                if elt not in index:
+                    raise RuntimeError("CKKSEngine: configured galois elt not in registered set")
+                return index[elt]
+
+            # conjugation with the partitions of the one level the bootstrap
+            # applies it at (here before CoeffToSlot's last rescale, chain
+            # first + nl - 1; the reference's pipeline rescales first and uses
+            # first + nl); a user step that CoeffToSlot / SlotToCoeff also use
+            # shares that key instead of getting one of its own
+            # (src/ckks_engine.cu:227-379)
+            idxs, levels, shared = [find_idx(conj)], [first + nl - 1], []
+            for i, step in enumerate(user_steps):
+                elt = get_elt_from_step(step, N)
+                j = find_idx(elt)
+                if step in boot_steps:
+                    shared.append(elt)
+                    continue
+                idxs.append(j)
+                levels.append(targets[i] if targets else self._freshest)
+            self._user_glk = self._sk.create_galois_keys_per_level(self._ctx, idxs, levels, seed=rng)
+            for elt in shared:
+                self._user_glk.keys[elt] = glk.keys[elt]
+            # the bootstrap's conjugation reads the user bundle's key
+            glk.keys[conj] = self._user_glk.keys[conj]
+        if cfg.build_two_scale_arrays:
+            self._build_scale_arrays()
+
+    def _build_scale_arrays(self):
+        """build_scale_arrays (src/ckks_engine.cu:435-460) in long double:
+        ckks_scale[i] = the squared scale at chain index i, starting from
+        user_scale^2; ckks_rescaled_scale[i] = ckks_scale[i] / (that level's last
+        prime), and ckks_scale[i + 1] = ckks_rescaled_scale[i]^2."""
+        ctx = self._ctx
+        cur = np.longdouble(float(self._cfg.user_scale)) ** 2
+        sc, rs = [], []
+        for idx in range(ctx.total_parm_size()):
+            sc.append(cur)
+            last = ctx.moduli[-1] if idx == 0 else ctx.moduli[ctx.size_Ql(idx) - 1]
+            r = cur / _long_double(last)
+            rs.append(r)
+            cur = r * r
+        self._ckks_scale, self._ckks_rescaled_scale = sc, rs
+
+    # ---- user-facing properties
+    def slot_count(self) -> int:
+        return self._ctx.N // 2
+
+    def user_scale(self) -> float:
+        return float(self._cfg.user_scale)
+
+    def max_user_level(self) -> int:
+        return int(self._cfg.num_scale_levels) - 1
+
+    def user_level(self, ct: ciphertext) -> int:
+        ci = ct.chain_index()
+        if ci < self._freshest or ci > self._bottom - 1:
+            raise ValueError("CKKSEngine::user_level: ciphertext chain_index is outside the user-scale segment")
+        return ci - self._freshest
+
+    def user_level_chain_index(self, user_level: int) -> int:
+        if user_level < 0 or user_level >= int(self._cfg.num_scale_levels):
+            raise ValueError("CKKSEngine::user_level_chain_index: user_level out of range")
+        return self._freshest + int(user_level)
+
+    # ---- encoding / encryption
+    def encode(self, values, user_level: int = 0) -> plaintext:
+        """CKKSEngine::encode (src/ckks_engine.cu:487-499): complex slot values
+        at user_scale, at the user level's chain index."""
+        if user_level < 0 or user_level >= int(self._cfg.num_scale_levels):
+            raise ValueError("CKKSEngine::encode: user_level out of range")
+        return self._enc.encode_complex_vector(self._ctx, values, float(self._cfg.user_scale),
+                                               self._freshest + int(user_level))
+
+    def encrypt(self, pt: plaintext, seed=None) -> ciphertext:
+        return self._sk.encrypt_symmetric(self._ctx, pt, seed=seed)
+
+    def decrypt_decode(self, ct: ciphertext) -> list:
+        return self._enc.decode_complex_vector(self._ctx, self._sk.decrypt(self._ctx, ct))
+
+    # ---- arithmetic and level management (the C++ class's, src/ckks_engine.cu:515-551)
+    @staticmethod
+    def _set(dst: ciphertext, r: ciphertext) -> None:
+        dst.data, dst._chain_index, dst._scale = r.data, r._chain_index, r._scale
+
+    def add_inplace(self, dst: ciphertext, src: ciphertext) -> None:
+        self._set(dst, add(self._ctx, dst, src))
+
+    def sub_inplace(self, dst: ciphertext, src: ciphertext) -> None:
+        self._set(dst, sub(self._ctx, dst, src))
+
+    def mul_and_relin_inplace(self, dst: ciphertext, src: ciphertext) -> None:
+        self._set(dst, multiply_and_relin(self._ctx, dst, src, self.relin_key()))
+
+    def mul_plain_inplace(self, dst: ciphertext, pt: plaintext) -> None:
+        self._set(dst, multiply_plain(self._ctx, dst, pt))
+
+    def rescale_inplace(self, ct: ciphertext) -> None:
+        """rescale_to_next, refused from the deepest user level (the next
+        level, one prime, is the bootstrap's own)."""
+        if ct.chain_index() >= self._bottom - 1:
+            raise RuntimeError("CKKSEngine::rescale_inplace: ciphertext is already at max user_level "
+                               "(pre_boot_index); call bootstrap_inplace next.")
+        self._set(ct, rescale_to_next(self._ctx, ct))
+
+    def rotate_inplace(self, ct: ciphertext, step: int) -> None:
+        self._set(ct, rotate(self._ctx, ct, step, self._user_glk))
+
+    # ---- bootstrap
+    def bootstrap_inplace(self, ct: ciphertext) -> None:
+        """CKKSEngine::bootstrap_inplace (src/ckks_engine.cu:553-601): a
+        ciphertext at any user level is switched down to the deepest one,
+        its scale set to user_scale, bootstrapped, and lands at user level 0
+        (1 with split_scale_down) at scale user_scale."""
+        if self._cfg.use_bootstrap_to_17_levels:
+            raise RuntimeError("CKKSEngine::bootstrap_inplace: use_bootstrap_to_17_levels chain does not have "
+                               "a bootstrap algorithm yet.")
+        self.user_level(ct)
+        pre_boot = self._bottom - 1
+        if ct.chain_index() != pre_boot:
+            mod_switch_to_inplace(self._ctx, ct, pre_boot)
+        ct.set_scale(float(self._cfg.user_scale))
+        out = bootstrap(self._ctx, self._enc, ct, self._bk, float(self._cfg.user_scale),
+                        bool(self._cfg.split_scale_down))
+        expected = self._freshest + (1 if self._cfg.split_scale_down else 0)
+        if out.chain_index() != expected:
+            raise RuntimeError("CKKSEngine::bootstrap_inplace: post-bootstrap chain_index != expected")
+        ct.data, ct._chain_index = out.data, out.chain_index()
+        ct.set_scale(float(self._cfg.user_scale))
+
+    # ---- read-only views
+    def context(self) -> context:
+        return self._ctx
+
+    def encoder(self) -> ckks_encoder:
+        return self._enc
+
+    def secret_key(self) -> secret_key:
+        return self._sk
+
+    def relin_key(self) -> relin_key:
+        return self._bk.rlk if self._bk is not None else relin_key()
+
+    def galois_key(self) -> galois_key:
+        return self._user_glk
+
+    def bootstrap_key(self) -> bootstrap_key:
+        return self._bk
+
+    # ---- per-level scale arrays (build_two_scale_arrays)
+    def scale_array_size(self) -> int:
+        return len(self._ckks_rescaled_scale)
+
+    def ckks_scale_at(self, chain_index: int) -> float:
+        return float(self._ckks_scale[chain_index]) if chain_index < len(self._ckks_scale) else 0.0
+
+    def ckks_rescaled_scale_at(self, chain_index: int) -> float:
+        return (float(self._ckks_rescaled_scale[chain_index])
+                if chain_index < len(self._ckks_rescaled_scale) else 0.0)
