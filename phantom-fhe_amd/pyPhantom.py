@@ -2802,3 +2802,118 @@ class ckks_engine:
     def ckks_rescaled_scale_at(self, chain_index: int) -> float:
         return (float(self._ckks_rescaled_scale[chain_index])
                 if chain_index < len(self._ckks_rescaled_scale) else 0.0)
+
+
+# ---------------------------------------------------------------- slot sums, polynomials
+def inner_sum(context: context, galois_key: galois_key, ct: ciphertext, block_size: int) -> ciphertext:
+    """inner_sum (src/linear.cu:9-25): each block_size-wide block's sum in its
+    first slot (the other slots hold partial sums), by log2(block_size)
+    rotate-and-add steps with strides 1, 2, 4, ..."""
+    block_size = int(block_size)
+    if block_size == 0 or block_size & (block_size - 1):
+        raise ValueError("inner_sum: block_size must be a power of 2")
+    acc, stride = ct, 1
+    while stride < block_size:
+        acc = add(context, acc, rotate(context, acc, stride, galois_key))
+        stride <<= 1
+    return acc
+
+
+def replicate(context: context, galois_key: galois_key, ct: ciphertext, period: int, num_slots: int) -> ciphertext:
+    """replicate (src/linear.cu:27-50): slots [0, period) copied into every
+    period of num_slots (slot k period + i = slot i, given the other slots
+    start at zero), by rotations by -period, -2 period, ... and additions."""
+    period, num_slots = int(period), int(num_slots)
+    if period == 0 or period & (period - 1):
+        raise ValueError("replicate: period must be a power of 2")
+    if num_slots == 0 or num_slots & (num_slots - 1):
+        raise ValueError("replicate: num_slots must be a power of 2")
+    if period > num_slots:
+        raise ValueError("replicate: period exceeds num_slots")
+    acc, stride = ct, period
+    while stride < num_slots:
+        acc = add(context, acc, rotate(context, acc, -stride, galois_key))
+        stride <<= 1
+    return acc
+
+
+def _ps_mul_scalar(ctx: context, ct: ciphertext, c: float, nominal: float) -> ciphertext:
+    """ct * c by a constant plaintext at the scale of the level's last prime,
+    a rescale, and the scale set back to `nominal` (src/ps.cu:26-39)."""
+    q = float(ctx.moduli[ctx.size_Ql(ct.chain_index()) - 1])
+    out = rescale_to_next(ctx, multiply_plain(ctx, ct, _const_plain(ctx, c, q, ct.chain_index())))
+    out.set_scale(nominal)
+    return out
+
+
+def _ps_add_scalar(ctx: context, ct: ciphertext, c: float) -> ciphertext:
+    """ct + c in ceil(|c| / 100) equal pieces, each encoded at the ciphertext's
+    scale (src/ps.cu:52-66)."""
+    if c == 0.0:
+        return ct
+    pieces = max(1, int(np.ceil(abs(c) / 100.0)))
+    piece = c / pieces
+    for _ in range(pieces):
+        ct = add_plain(ctx, ct, _const_plain(ctx, piece, ct.scale(), ct.chain_index()))
+    return ct
+
+
+def _ps_chunk(ctx, coeffs, babies, k: int, m: int, target: int, nominal: float) -> ciphertext:
+    """c_k(x) = a_(k m) + sum_(j = 1 .. m-1) a_(k m + j) x^j at chain index
+    `target` (src/ps.cu:72-124): each nonzero linear term is its baby switched
+    to target - 1 and multiplied by the scalar (which brings it to target)."""
+    d, base = len(coeffs) - 1, k * m
+    terms = [(j, coeffs[base + j]) for j in range(1, m) if base + j <= d and coeffs[base + j] != 0.0]
+    const = coeffs[base] if base <= d else 0.0
+    prev = target - 1 if target > 0 else 0
+    acc = None
+    for j, a in terms or [(1, 0.0)]:  # no linear term: a zero at target via x * 0
+        t = mod_switch_to(ctx, babies[j - 1], prev)
+        t = _ps_mul_scalar(ctx, t, a, nominal)
+        acc = t if acc is None else add(ctx, acc, t)
+    return _ps_add_scalar(ctx, acc, const)
+
+
+def eval_polynomial(context: context, encoder: ckks_encoder, relin_key: relin_key, ct: ciphertext,
+                    coeffs) -> ciphertext:
+    """eval_polynomial (src/ps.cu:129-200, include/ps.h): p(x) = a_0 + a_1 x +
+    ... + a_d x^d by Paterson-Stockmeyer with m = ceil(sqrt(d + 1)) baby powers
+    and l = ceil((d + 1) / m) giant chunks in Horner order; every product is
+    rescaled and its scale set back to the input's.  The result is at chain
+    index ct.chain_index() + m + l - 2 (include/ps.h states m + l - 1; its
+    code, followed here step for step, consumes one level less).  Constants
+    are encoded exactly (coefficient 0 = round(c scale))."""
+    ctx = context
+    coeffs = [float(c) for c in coeffs]
+    if len(coeffs) < 2:
+        raise ValueError("eval_polynomial: degree must be >= 1")
+    d = len(coeffs) - 1
+    m = int(np.ceil(np.sqrt(d + 1.0)))
+    l = (d + 1 + m - 1) // m
+    nominal, c0 = ct.scale(), ct.chain_index()
+    # baby powers x^1 .. x^(m-1)
+    babies, x_run = [ct], ct
+    for i in range(2, m):
+        nxt = rescale_to_next(ctx, multiply_and_relin(ctx, babies[i - 2], x_run, relin_key))
+        nxt.set_scale(nominal)
+        babies.append(nxt)
+        if i < m - 1:  # x_run one level down, to meet babies[i - 1]
+            x_run = _ps_mul_scalar(ctx, x_run, 1.0, nominal)
+    baby_lvl = c0 + m - 2 if m >= 2 else c0
+    babies = [mod_switch_to(ctx, b, baby_lvl) for b in babies]
+    x_run = mod_switch_to(ctx, x_run, baby_lvl)
+    # giant base x^m
+    x_m = None
+    if l >= 2:
+        x_m = rescale_to_next(ctx, multiply_and_relin(ctx, babies[-1], x_run, relin_key))
+        x_m.set_scale(nominal)
+    # Horner over the giant chunks
+    result = _ps_chunk(ctx, coeffs, babies, l - 1, m, baby_lvl + 1, nominal)
+    for kk in range(l - 2, -1, -1):
+        if x_m is None:
+            raise RuntimeError("eval_polynomial: x_m absent with l>=2")
+        x_m = mod_switch_to(ctx, x_m, result.chain_index())
+        result = rescale_to_next(ctx, multiply_and_relin(ctx, result, x_m, relin_key))
+        result.set_scale(nominal)
+        result = add(ctx, result, _ps_chunk(ctx, coeffs, babies, kk, m, result.chain_index(), nominal))
+    return result
