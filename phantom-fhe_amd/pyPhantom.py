@@ -72,7 +72,77 @@ class mul_tech_type(enum.IntEnum):
     hps_overq_leveled = 4
 
 
-create_coeff_modulus = _N.create_coeff_modulus
+class sec_level_type(enum.IntEnum):
+    """include/host/modulus.h security levels (binding.cu:46-50)."""
+    none = 0
+    tc128 = 128
+    tc192 = 192
+    tc256 = 256
+
+
+class modulus(int):
+    """arith::Modulus (include/host/modulus.h:14-80, binding.cu:53-54): a prime or
+    zero of at most 61 bits.  An int subclass, so a list of them goes anywhere a
+    list of moduli goes; `.value` is the reference's value()."""
+
+    def __new__(cls, value: int = 0):
+        v = int(value)
+        # src/host/modulus.cu:15-24: 0 is allowed, 1 and values past 61 bits are not
+        if v < 0 or v >> 61 or v == 1:
+            raise ValueError("value can be at most 61-bit and cannot be 1")
+        return super().__new__(cls, v)
+
+    @property
+    def value(self) -> int:
+        return int(self)
+
+    def bit_count(self) -> int:
+        return int(self).bit_length()
+
+    def is_zero(self) -> bool:
+        return int(self) == 0
+
+    def __repr__(self):
+        return f"modulus({int(self)})"
+
+
+def create_coeff_modulus(poly_modulus_degree: int, bit_sizes) -> list[modulus]:
+    """CoeffModulus::Create (binding.cu:56): distinct NTT-friendly primes
+    (p = 1 mod 2N) of the given bit sizes, in the reference's order."""
+    return [modulus(p) for p in _N.create_coeff_modulus(poly_modulus_degree, list(bit_sizes))]
+
+
+def create_plain_modulus(poly_modulus_degree: int, bit_size: int) -> modulus:
+    """PlainModulus::Batching (binding.cu:58): one batching-friendly prime of the
+    given size.  Only BFV/BGV parameters take it; `params.set_plain_modulus` of
+    this CKKS core rejects it."""
+    return create_coeff_modulus(poly_modulus_degree, [bit_size])[0]
+
+
+class cuda_stream:
+    """util::cuda_stream_wrapper (binding.cu:69-70): a new device stream at the
+    default priority.  Used as a context manager, every call inside it runs on
+    this stream, because this module launches on the calling thread's current
+    stream."""
+
+    def __init__(self):
+        t = _torch()
+        if not t.cuda.is_available():
+            raise RuntimeError("cuda_stream: no GPU device is visible")
+        self.stream = t.cuda.Stream()
+        self._ctx = None
+
+    def synchronize(self):
+        self.stream.synchronize()
+
+    def __enter__(self):
+        self._ctx = _torch().cuda.stream(self.stream)
+        self._ctx.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        ctx, self._ctx = self._ctx, None
+        return ctx.__exit__(*exc)
 
 
 def set_cuda_device(device_id: int) -> None:

@@ -287,6 +287,32 @@ def test_device_helpers(dev):
     assert ctx.device == 0
 
 
+def test_cuda_stream_runs_calls_on_its_stream(dev):
+    """cuda_stream (binding.cu:69-70): calls made inside `with cuda_stream()` run
+    on that stream and give the residues the default stream gives; results
+    made on it are read correctly from the default stream afterwards."""
+    import torch
+
+    ph, ctx = make_ctx(13, [60, 40, 40, 60], 1)
+    ph.set_seed(3)
+    sk = ph.secret_key(ctx)
+    rlk = sk.gen_relinkey(ctx)
+    enc = ph.ckks_encoder(ctx)
+    rng = np.random.default_rng(8)
+    a = rng.uniform(-1, 1, enc.slot_count())
+    ca = sk.encrypt_symmetric(ctx, enc.encode_double_vector(ctx, a, 2.0 ** 40))
+    want = to_host(ph.multiply_and_relin_rescale(ctx, ca, ca, rlk).data)
+    s = ph.cuda_stream()
+    assert s.stream != torch.cuda.current_stream()
+    with s:
+        assert torch.cuda.current_stream() == s.stream
+        got = ph.multiply_and_relin_rescale(ctx, ca, ca, rlk)
+    assert torch.cuda.current_stream() != s.stream
+    assert np.array_equal(to_host(got.data), want)
+    out = np.array(enc.decode_double_vector(ctx, sk.decrypt(ctx, got)))
+    assert np.max(np.abs(out - a * a)) < TOL
+
+
 def test_api_errors(dev):
     ph, ctx = make_ctx(12, [60, 40, 40, 60], 1)
     sk = ph.secret_key(ctx)
