@@ -6,6 +6,12 @@ only by bench.py.
   alpha = 1, dnum = 35): multiply_and_relin, rescale and the fused call are
   bit-exact against the oracle's multiply_and_relin_inplace
   (src/evaluate.cu:1061-1104) followed by rescale_to_next (src/rns.cu:1128-1184).
+* The key switches of bootstrapping and of the BSGS product at full size
+  (N = 2^16, both bootstrappable chains, |Q| = 30 with 6 special primes,
+  dnum = 5, top and inner levels; config 4's chain): a rotation and the fused
+  HMult + relinearize + rescale bit-exact against the oracle, so the residue
+  arithmetic of configs 4 and 5 is pinned at their own shapes, not only at
+  N = 2^12.
 * Batched HMult (config 3) and batched rotation (config 4 shape) at full size:
   every member equals the single call, which covers the work schedules of the
   batched base-conversion and epilogue launches.
@@ -54,6 +60,46 @@ def test_hmult_L35_alpha1_full_size(dev):
     assert np.array_equal(got, want_r), first_mismatch(got, want_r)
 
 
+def _full_size_chains():
+    """name -> (prime bits, special primes) of the chains configs 4 and 5 run."""
+    import pyPhantom as ph
+
+    return {"cheb63": (ph.bootstrap_coeff_bits(), 6), "engine": (ph.ckks_engine_coeff_bits(), 6),
+            "config4": ([60] + [40] * 19 + [60] * 4, 4)}
+
+
+@pytest.mark.parametrize("chain_name,chain", [("cheb63", 1), ("cheb63", 15), ("engine", 1), ("engine", 13),
+                                              ("config4", 1)])
+def test_keyswitch_bootstrap_chains_full_size(dev, chain_name, chain):
+    """The key switches bootstrapping and the BSGS product run, at their full
+    size: N = 2^16 over the two bootstrappable chains (|Q| = 30, 6 special
+    primes, dnum = 5; 60-, 58- and 50-bit primes in the integer policy next to
+    40- and 29-bit ones in the FP64 policy), at the top level (CoeffToSlot's)
+    and at a level inside EvalMod / SlotToCoeff, and over config 4's chain
+    (|Q| = 20, alpha = 4, dnum = 5).  A rotation (src/evaluate.cu:1607-1656) and
+    the fused HMult + relinearize + rescale are bit-exact against the oracle."""
+    import pfa_native as P
+
+    bits, alpha = _full_size_chains()[chain_name]
+    st = Setup(16, len(bits) - alpha, alpha, seed=50 + chain, bits=bits)
+    assert st.orc.dnum == 5
+    Ql = st.orc.size_Ql(chain)
+    key = st.key()
+    dk = to_dev(key, dev)
+    ct = st.ct(chain)
+    elt = P.galois_elt_from_step(-37, st.N)
+    d = to_dev(ct, dev)
+    st.ctx.apply_galois(chain, d, elt, dk)
+    got, want = to_host(d), st.orc.apply_galois(chain, ct, elt, key, threads=16)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    a, b = st.ct(chain), st.ct(chain)
+    out = empty((2, Ql - 1, st.N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), dk, out)
+    want = st.orc.rescale(chain, st.orc.multiply_and_relin(chain, a, b, key, threads=16), threads=16)
+    got = to_host(out)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
 @pytest.mark.parametrize("count", [2, 5])
 def test_hmult_config3_batch_equals_single_full_size(dev, count):
     """Batched HMult at config 3's full size (N = 2^16, |Q| = 24, alpha = 4):
@@ -91,9 +137,9 @@ def test_rotate_batch_config4_equals_single_full_size(dev):
     """pfa_rotate_batch at config 4's shape (N = 2^16, chain {60, 40 x 19, 60 x 4},
     alpha = 4; 3 members, each with its own step and key) equals
     pfa_apply_galois on each member, bit for bit: the batched ModUp conversion
-    runs through its work schedule here (single rotations at this shape are
-    pinned against the oracle's apply_galois at N = 2^12 and 2^13 in
-    test_gpu_keyswitch.py)."""
+    runs through its work schedule here (a single rotation at this shape is
+    pinned against the oracle's apply_galois by
+    test_keyswitch_bootstrap_chains_full_size)."""
     import pfa_native as P
 
     st = Setup(16, 20, 4, seed=44, bits=[60] + [40] * 19 + [60] * 4)
