@@ -693,19 +693,21 @@ __device__ __forceinline__ void ws_combine(const InnerRows &a0, const NttTables 
     }
 }
 
-// Items 0 .. full-1 are processed whole, by workgroup w0 mod grid.  When the
-// item count is not a multiple of the resident workgroups, the rem items left
-// over would run as a second round on a mostly idle chip; they are split into
-// kch digit chunks instead, which fill one short round.  Counting workgroups
-// from the end of the grid, g = grid - 1 - blockIdx, workgroup g takes chunk
-// (u mod kch) of item full + (u / kch) 8 + (g mod 8), u = g / 8, so the
-// chunks of the last split items (with one member: the integer-policy
-// targets, the longest) go to the workgroups dispatched first.  Only the
-// pairing of whole items and chunks on a workgroup depends on the direction;
-// counting from the end measured faster than from the start (interleaved, two
-// boxes: L = 35 HMult -4.3% and -4.5%; config 3, batch-1 rotation, BSGS and
-// bootstrap within 0.8%; the same residues).  The grid is a multiple of 8, so the
-// chunks of an item run on workgroups congruent mod 8, i.e. on one XCD (a
+// Items 0 .. full-1 are processed whole, item full - 1 - i by workgroup
+// i mod grid.  When the item count is not a multiple of the resident
+// workgroups, the rem items left over would run as a second round on a mostly
+// idle chip; they are split into kch digit chunks instead, which fill one
+// short round.  Counting workgroups from the end of the grid,
+// g = grid - 1 - blockIdx, workgroup g takes chunk (u mod kch) of item
+// full + (u / kch) 8 + (g mod 8), u = g / 8.  Both directions hand the last
+// items to the workgroups dispatched first: with one member those are the
+// integer-policy targets, the longest items.  Interleaved on one box against
+// the forward directions: config 3 HMult 263.5 -> 255.7 us, L = 35
+// 781.3 -> 747.5 us, batch-1 rotation 189.2 -> 184.2 us (the reversed chunks
+// alone: L = 35 -4.3 to -4.5% on two boxes; the reversed whole items alone:
+// config 3 -3%, rotation -3%; in separate processes BSGS 27.0 -> 26.4-26.7 ms,
+// bootstrap 28.5 -> 28.2-28.3 ms), the same residues.  The grid is a multiple of
+// 8, so the chunks of an item run on workgroups congruent mod 8, i.e. on one XCD (a
 // launch's workgroups are dealt to the 8 XCDs round-robin), and their partial
 // sums meet in that XCD's L2; nothing waits for anything.  Each chunk marks
 // its XCD in the item's counter, and the last to arrive records an error if
@@ -731,7 +733,8 @@ k_inner_ws(InnerRows a0, NttTables t) {
     ulonglong2 *tws = reinterpret_cast<ulonglong2 *>(lds + (W::USE_TAB ? W::ROWS * Geo<S1, S2>::ROW_PITCH : W::LDS));
     const uint32_t total = a0.batch * a0.QlP * W::TILES;
     const uint32_t full = a0.full < total ? a0.full : total;
-    for (uint32_t w0 = blockIdx.x; w0 < full; w0 += gridDim.x) {
+    for (uint32_t i = blockIdx.x; i < full; i += gridDim.x) {
+        const uint32_t w0 = full - 1 - i;  // the last items (the longest) first
         ws_item<S1, S2>(a0, t, w0, 0, a0.beta, nullptr, lds, tws);
         __syncthreads();
     }
