@@ -171,8 +171,8 @@ __device__ __forceinline__ void load_step(const MacArgs &a, uint32_t g0, uint32_
 // rows, not the bytes, limit it); from the tiled layout an item's plaintext
 // spans are one contiguous 2 MiB region.
 // FP64 policy: each product is within 0.875 q (|x y / q| < q < 2^50), so four
-// of them on top of a reduced sum stay below 4 q < 2^53; integer policy: each
-// product reduced (Barrett) and summed modulo q.
+// of them on top of a reduced sum stay below 4 q < 2^53; integer policy:
+// 128-bit sums of full products, reduced every 8 babies (Barrett).
 template <int SRC, bool F64>
 __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t tile, uint32_t g0, uint32_t K,
                                          uint64_t q, const ulonglong2 *ratio) {
@@ -237,14 +237,18 @@ __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t 
             }
         }
     } else {
+        // 128-bit sums of the full products (4 multiplies each), folded by one
+        // Barrett reduction every 8 babies: with q < 2^62 a product is below
+        // 2^124, so a folded value (< q) plus 8 products stays below 2^128.
+        // The same residues as reducing every product.
         ulonglong2 r = ratio[j];
         r.x = wave_uniform(r.x);
         r.y = wave_uniform(r.y);
-        uint64_t acc0[kGB][kPer], acc1[kGB][kPer];
+        U128 acc0[kGB][kPer], acc1[kGB][kPer];
 #pragma unroll
         for (uint32_t k = 0; k < kGB; k++)
 #pragma unroll
-            for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = 0;
+            for (int e = 0; e < kPer; e++) acc0[k][e] = acc1[k][e] = U128{0, 0};
         for (uint32_t b = 0; b < a.M; b++) {
             const uint64_t *c = a.baby(b);
             const Pair c0 = ld_pair(c + off0), c1 = ld_pair(c + off1);
@@ -254,17 +258,25 @@ __device__ __forceinline__ void mac_item(const MacArgs &a, uint32_t j, uint32_t 
             for (uint32_t k = 0; k < kGB; k++)
 #pragma unroll
                 for (int e = 0; e < kPer; e++) {
-                    const uint64_t x = xv[k][e];
-                    acc0[k][e] = add_mod(acc0[k][e], barrett128(U128{x * c0[e], mulhi64(x, c0[e])}, q, r.x, r.y), q);
-                    acc1[k][e] = add_mod(acc1[k][e], barrett128(U128{x * c1[e], mulhi64(x, c1[e])}, q, r.x, r.y), q);
+                    mac(acc0[k][e], xv[k][e], c0[e]);
+                    mac(acc1[k][e], xv[k][e], c1[e]);
                 }
+            if ((b & 7u) == 7u) {
+#pragma unroll
+                for (uint32_t k = 0; k < kGB; k++)
+#pragma unroll
+                    for (int e = 0; e < kPer; e++) {
+                        acc0[k][e] = U128{barrett128(acc0[k][e], q, r.x, r.y), 0};
+                        acc1[k][e] = U128{barrett128(acc1[k][e], q, r.x, r.y), 0};
+                    }
+            }
         }
 #pragma unroll
         for (uint32_t k = 0; k < kGB; k++) {
             if (k < K) {
                 uint64_t *o = a.out[g0 + k];
-                st_pair_stream(o + off0, Pair{acc0[k][0], acc0[k][1]});
-                st_pair_stream(o + off1, Pair{acc1[k][0], acc1[k][1]});
+                st_pair_stream(o + off0, Pair{barrett128(acc0[k][0], q, r.x, r.y), barrett128(acc0[k][1], q, r.x, r.y)});
+                st_pair_stream(o + off1, Pair{barrett128(acc1[k][0], q, r.x, r.y), barrett128(acc1[k][1], q, r.x, r.y)});
             }
         }
     }
