@@ -2796,7 +2796,7 @@ class ckks_engine:
     # ---- arithmetic and level management (the C++ class's, src/ckks_engine.cu:515-551)
     @staticmethod
     def _set(dst: ciphertext, r: ciphertext) -> None:
-        dst.data, dst._chain_index, dst._scale = r.data, r._chain_index, r._scale
+        dst.__dict__.update(r.__dict__)  # data, level, scale and the rest of the state
 
     def add_inplace(self, dst: ciphertext, src: ciphertext) -> None:
         self._set(dst, add(self._ctx, dst, src))
@@ -2840,7 +2840,7 @@ class ckks_engine:
         expected = self._freshest + (1 if self._cfg.split_scale_down else 0)
         if out.chain_index() != expected:
             raise RuntimeError("CKKSEngine::bootstrap_inplace: post-bootstrap chain_index != expected")
-        ct.data, ct._chain_index = out.data, out.chain_index()
+        self._set(ct, out)
         ct.set_scale(float(self._cfg.user_scale))
 
     # ---- read-only views
