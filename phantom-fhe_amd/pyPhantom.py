@@ -1326,6 +1326,9 @@ class ComplexFoldMode(enum.Enum):
     ColsConj = 1
 
 
+complex_fold_mode = ComplexFoldMode  # the binding's name for the enum (binding.cu:570-572)
+
+
 class complex_bsgs_diagonals:
     """ComplexBsgsDiagonals (include/bsgs.h:77-79): the same structure as
     bsgs_diagonals, with complex-folded diagonals."""

@@ -43,6 +43,27 @@ def test_create_plain_modulus_and_ckks_rejection():
         ph.params(ph.scheme_type.ckks).set_plain_modulus(t)
 
 
+def test_binding_names_present():
+    """Every class, enum and function name the reference's module binds for
+    the CKKS path is importable here (binding.cu:31-590; the LLM blocks and
+    BFV's batch_encoder are outside this core)."""
+    names = ["scheme_type", "mul_tech_type", "sec_level_type", "modulus", "create_coeff_modulus",
+             "create_plain_modulus", "params", "cuda_stream", "context", "secret_key", "public_key", "relin_key",
+             "galois_key", "get_elt_from_step", "get_elts_from_steps", "ckks_encoder", "plaintext", "ciphertext",
+             "negate", "add", "add_plain", "add_many", "sub", "sub_plain", "multiply", "multiply_and_relin",
+             "multiply_plain", "relinearize", "rescale_to_next", "mod_switch_to_next", "mod_switch_to",
+             "mod_switch_to_inplace", "apply_galois", "rotate", "apply_galois_with_key", "rotate_with_key",
+             "hoisting", "hoist_rotations", "small_bootstrap_key", "bootstrap_key", "bootstrap_required_galois_elts",
+             "create_bootstrap_key", "bootstrap", "ckks_engine_config", "ckks_engine", "set_cuda_device",
+             "get_cuda_device_count", "single_chain_plaintext", "encode_single_chain_plaintext", "scp_from_bytes",
+             "expand_single_chain_to_full", "inner_sum", "replicate", "bsgs_diagonals", "pre_encode_bsgs_diagonals",
+             "bsgs_required_steps", "bsgs_matmul_preencoded", "compute_bsgs_babies", "bsgs_apply_giants_with_babies",
+             "complex_fold_mode", "pre_encode_bsgs_diagonals_complex", "eval_polynomial", "complex_bsgs_diagonals",
+             "bsgs_apply_giants_with_babies_complex"]
+    assert [n for n in names if not hasattr(ph, n)] == []
+    assert [m.name for m in ph.complex_fold_mode] == ["Rows", "ColsConj"]
+
+
 def test_cuda_stream_needs_a_device():
     import torch
 
