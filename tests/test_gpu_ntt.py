@@ -5,7 +5,8 @@ values, for both arithmetic policies (primes < 2^50 run in FP64, larger ones in
 
 Mirrors the reference's test/ntt_test.cu (forward then inverse round trip on
 N = 2^8..2^17, batch 1 and 10) and adds the known-answer comparison that test
-lacks."""
+lacks, plus a seeded sweep of random degrees, batch sizes, limb runs and
+prime-size mixes."""
 import numpy as np
 import pytest
 
@@ -219,3 +220,37 @@ def test_ntt_deterministic_across_calls(dev):
         ctx.ntt_forward(d, 2, 6, 0)
         outs.append(to_host(d))
     assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+def _ntt_shapes(n, seed):
+    """(logn, M, L, start, bits): degree 2^10 .. 2^17, 1-4 polys, a run of L
+    limbs starting at a random table row of a chain of random prime sizes."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        logn = int(rng.integers(10, 18))
+        total = int(rng.integers(2, 13))
+        bits = [int(b) for b in rng.choice([30, 36, 40, 45, 49, 50, 55, 58, 60], size=total)]
+        start = int(rng.integers(0, total))
+        L = int(rng.integers(1, total - start + 1))
+        M = int(rng.integers(1, 5)) if logn < 17 else 1
+        out.append((logn, M, L, start, bits))
+    return out
+
+
+@pytest.mark.parametrize("logn,M,L,start,bits", _ntt_shapes(10, 77))
+def test_ntt_random_shapes(dev, logn, M, L, start, bits):
+    """Seeded random degrees, batch sizes, limb runs and prime-size mixes:
+    forward against the oracle, inverse back to the input, bit for bit."""
+    N = 1 << logn
+    mods, ctx, orc = make(N, bits)
+    rng = np.random.default_rng(logn * 100 + L)
+    x = uniform_limbs(rng, (M, L, N), mods[start:start + L])
+    d = to_dev(x, dev)
+    ctx.ntt_forward(d, M, L, start)
+    got = to_host(d)
+    want = orc.ntt_fwd(x, start=start, threads=8)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    ctx.ntt_inverse(d, M, L, start)
+    back = to_host(d)
+    assert np.array_equal(back, x), first_mismatch(back, x)
