@@ -109,8 +109,9 @@ int pfa_ntt_inverse(const pfa_context *ctx, uint64_t *inout, size_t M, size_t L,
  * round-robin), 0 if it runs as two launches. */
 int pfa_ntt_single_launch(const pfa_context *ctx, size_t M, size_t L, int *out);
 
-/* No reference counterpart (a measurement aid): copies n uint64 words (n even)
- * from src to dst with nontemporal 16-byte loads and stores, on `workgroups`
+/* No reference counterpart (a measurement aid): copies n uint64 words (n even,
+ * dst and src 16-byte aligned) from src to dst with nontemporal 16-byte loads
+ * and stores, on `workgroups`
  * workgroups of 256 threads (0: one per 16 KiB), the achievable one-read
  * one-write bandwidth against which the NTT is measured. */
 int pfa_stream_copy(uint64_t *dst, const uint64_t *src, size_t n, size_t workgroups, void *stream);

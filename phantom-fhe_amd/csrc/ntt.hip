@@ -272,6 +272,8 @@ int pfa_stream_copy(uint64_t *dst, const uint64_t *src, size_t n, size_t workgro
     return guarded([&] {
         require(dst && src, "null data pointer");
         require(n % 2 == 0, "copy length must be a multiple of 2 words");
+        require((reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0,
+                "copy buffers must be 16-byte aligned");
         const uint64_t n2 = n / 2;
         if (n2 == 0) return;
         const uint64_t need = (n2 + 256 * 4 - 1) / (256 * 4);

@@ -287,6 +287,38 @@ def test_device_helpers(dev):
     assert ctx.device == 0
 
 
+@pytest.mark.parametrize("n,workgroups", [(2, 0), (2050, 0), (2050, 1), (2 * 35 * 65536, 0), (2 * 35 * 65536, 7)])
+def test_stream_copy_exact(dev, n, workgroups):
+    """pfa_stream_copy, the bench's copy ceiling: an exact copy of n words
+    whatever the grid (a partial last group, a grid smaller than the data)."""
+    import torch
+
+    import pfa_native as P
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(n + workgroups)
+    src = torch.randint(-2 ** 62, 2 ** 62, (n,), dtype=torch.int64, device=dev, generator=g).view(torch.uint64)
+    dst = torch.zeros_like(src)
+    P.stream_copy(dst, src, workgroups)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.view(torch.int64), src.view(torch.int64))
+
+
+def test_stream_copy_errors(dev):
+    import torch
+
+    import pfa_native as P
+
+    a = torch.zeros(8, dtype=torch.int64, device=dev).view(torch.uint64)
+    b = torch.zeros(8, dtype=torch.int64, device=dev).view(torch.uint64)
+    with pytest.raises(ValueError):
+        P.stream_copy(a, b[:7])  # sizes differ
+    with pytest.raises(ValueError):
+        P.stream_copy(a[:7], b[:7])  # odd length
+    with pytest.raises(ValueError):
+        P.stream_copy(a[1:7], b[1:7])  # 8-byte aligned only
+
+
 def test_cuda_stream_runs_calls_on_its_stream(dev):
     """cuda_stream (binding.cu:69-70): calls made inside `with cuda_stream()` run
     on that stream and give the residues the default stream gives; results
