@@ -20,6 +20,8 @@ only by bench.py.
   within 1e-5 of numpy's W x.  The reference's own check of this product is a
   decode tolerance (python/llm_project/blocks/bsgs_test.py:77); its residues are
   pinned bit-exactly at N = 2^12 in test_gpu_bsgs.py.
+* Config 5's transforms at full size: the first CoeffToSlot layer and the last
+  SlotToCoeff layer bit-exact against the oracle running the same operations.
 * Config 5, bootstrapping at N = 2^16 (2^15 slots uniform in [-1, 1], |Q| = 30
   with 6 special primes, dnum = 5, sparse secret h = 192): at least 15 bits of
   refreshed precision (the reference's acceptance bound is 1e-3, about 10 bits,
@@ -210,6 +212,40 @@ def boot16(dev):
 
     del bk
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("which", ["c2s_first", "s2c_last"])
+def test_bootstrap_transform_layer_full_size(boot16, which):
+    """One CoeffToSlot layer (the first, at the top of the chain) and one
+    SlotToCoeff layer (the last) at config 5's size, as bootstrap runs them
+    (hoisted babies, pfa_bsgs_mac, the batched giants, the sum, the rescale),
+    bit-exact against the oracle running the same operations one by one: the
+    residue pin of the transforms at N = 2^16 (all six layers are pinned at
+    N = 2^12 in test_gpu_bootstrap.py)."""
+    import py_oracle as O
+    from test_gpu_bootstrap import _oracle_layer
+
+    ph, ctx, sk, enc, bk = boot16
+    if which == "c2s_first":
+        lt, pts, i, chain = bk.c2s, bk.c2s_pts, 0, 1
+    else:
+        lt, pts, i = bk.s2c, bk.s2c_pts, len(bk.s2c_pts) - 1
+        chain = bk.s2c_start + i
+    plan = pts[i]
+    rng = np.random.default_rng(60 + i)
+    z = rng.uniform(-1, 1, enc.slot_count()) + 1j * rng.uniform(-1, 1, enc.slot_count())
+    ct = sk.encrypt_symmetric(ctx, enc.encode_complex_vector(ctx, z, 2.0 ** 40, chain), seed=61)
+    got = ph._apply_layer(ctx, ct, lt, pts, i, bk.glk)
+    assert got.chain_index() == chain + 1
+    orc = O.Oracle(ctx.N, ctx.moduli, ctx.size_P)
+    # only the layer's own keys come to the host (one is up to 180 MB here)
+    n1, unit = lt.baby_giant(i)[0], lt.units[i]
+    used = {ph.get_elt_from_step(b * unit, ctx.N) for b in plan.babies if b}
+    used |= {ph.get_elt_from_step(ph._signed_step(g * n1 * unit, lt.n), ctx.N) for g in plan.giants if g}
+    keys = {e: to_host(bk.glk.keys[e]) for e in used}
+    want = _oracle_layer(orc, ph, ctx.N, chain, to_host(ct.data), lt, plan, i, keys)
+    got = to_host(got.data)
+    assert np.array_equal(got, want), first_mismatch(got, want)
 
 
 def test_bootstrap_config5_full_size(boot16):
