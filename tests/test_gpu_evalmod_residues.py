@@ -1,7 +1,8 @@
 """EvalMod residues on the GPU equal the oracle running the same operation
 sequence: the reference's K = 28 family (evalmod_k28_r3: src/evalmod.cu:196-335
 Chebyshev basis and weighted sums, :464-605 the K = 28 factoring and double
-angles) and this build's degree-63 Chebyshev EvalMod (cheb63), at N = 2^12.
+angles) and this build's degree-63 Chebyshev EvalMod (cheb63), at N = 2^12 and
+at the bootstrap's N = 2^16.
 
 Both sides run pyPhantom's EvalMod code unchanged over an engine of ciphertext
 operations: the native library's (pyPhantom._GpuEngine) and the CPU oracle's
@@ -27,10 +28,10 @@ CASES = {
 }
 
 
-def _setup(variant, dev, seed):
+def _setup(variant, dev, seed, logN=12):
     import pyPhantom as ph
 
-    N = 1 << 12
+    N = 1 << logN
     bits, special, scale = CASES[variant]
     mods = ph.create_coeff_modulus(N, bits)
     p = ph.params(ph.scheme_type.ckks)
@@ -50,9 +51,10 @@ def _setup(variant, dev, seed):
     return ph, ctx, orc, mods, Q, ct, ct_np, rk, key_np, scale
 
 
+@pytest.mark.parametrize("logN", [12, 16])
 @pytest.mark.parametrize("variant", sorted(CASES))
-def test_evalmod_residues_match_oracle(dev, variant):
-    ph, ctx, orc, mods, Q, ct, ct_np, rk, key_np, scale = _setup(variant, dev, 0xE7A1 + len(variant))
+def test_evalmod_residues_match_oracle(dev, variant, logN):
+    ph, ctx, orc, mods, Q, ct, ct_np, rk, key_np, scale = _setup(variant, dev, 0xE7A1 + len(variant) + logN, logN)
     gpu = ph._GpuEngine(ctx, rk)
     cpu = OracleEngine(orc, mods, Q, key_np)
     x = OCt(ct_np, 1, scale)
