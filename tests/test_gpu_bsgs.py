@@ -133,6 +133,37 @@ def test_bsgs_tiled_packed_limbs(dev, M, G):
         assert torch.equal(got[g], want[g]), g
 
 
+def test_bsgs_tiled_packed_mac_config4_full_size(dev):
+    """The accumulation config 4 runs (tiled set, its 19 limbs of 40 bits
+    packed to 5 bytes, the 60-bit limb in the integer policy) at N = 2^16 on
+    config 4's chain, against the oracle's products summed mod q: 16 babies
+    and 3 giants of the real 64 x 64."""
+    import pfa_native as P
+
+    N = 1 << 16
+    mods = O.create_coeff_modulus(N, [60] + [40] * 19 + [60] * 4)
+    ctx = P.NativeContext(N, mods, 4)
+    orc = O.Oracle(N, mods, 4)
+    chain, M, G = 1, 16, 3
+    Ql = orc.size_Ql(chain)
+    qs = mods[:Ql]
+    D = M * G
+    rng = np.random.default_rng(404)
+    pts = uniform_limbs(rng, (D, Ql, N), qs)
+    babies = [uniform_limbs(rng, (2, Ql, N), qs) for _ in range(M)]
+    tiled = empty(((ctx.bsgs_tiled_size(chain, D) + 7) // 8,), dev)
+    ctx.bsgs_tile_plaintexts(chain, to_dev(pts, dev), D, tiled, 0, D)
+    got = [empty((2, Ql, N), dev) for _ in range(G)]
+    ctx.bsgs_mac_tiled(chain, tiled, [to_dev(b, dev) for b in babies], got)
+    for g in range(G):
+        want = np.zeros((2, Ql, N), dtype=np.uint64)
+        for b in range(M):
+            for k in range(2):
+                want[k] = add_mod(want[k], orc.mul_poly(pts[g * M + b], babies[b][k]), qs)
+        h = to_host(got[g])
+        assert np.array_equal(h, want), (g, first_mismatch(h, want))
+
+
 def test_bsgs_mac_rejects_bad_arguments(dev):
     import pfa_native as P
 
