@@ -20,19 +20,22 @@ from gpu_util import empty, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 
-def test_mod_raise_matches_oracle(dev):
+@pytest.mark.parametrize("logN,bits,special", [(12, [60, 40, 40, 50, 60, 60], 2), (16, None, 6)])
+def test_mod_raise_matches_oracle(dev, logN, bits, special):
+    """At N = 2^12 and on config 5's chain at N = 2^16 (30 primes + 6 special)."""
     import pfa_native as P
+    import pyPhantom as ph
 
-    N = 1 << 12
-    mods = O.create_coeff_modulus(N, [60, 40, 40, 50, 60, 60])
-    ctx = P.NativeContext(N, mods, 2)
-    orc = O.Oracle(N, mods, 2)
+    N = 1 << logN
+    mods = O.create_coeff_modulus(N, bits or ph.bootstrap_coeff_bits())
+    ctx = P.NativeContext(N, mods, special)
+    orc = O.Oracle(N, mods, special)
     q0 = mods[0]
     rng = np.random.default_rng(21)
     coef = rng.integers(0, q0, (2, 1, N), dtype=np.uint64)
     coef[0, 0, :4] = [0, q0 >> 1, (q0 >> 1) - 1, q0 - 1]
     ct = orc.ntt_fwd(coef)
-    Q = len(mods) - 2
+    Q = len(mods) - special
     out = empty((2, Q, N), dev)
     ctx.mod_raise(to_dev(ct, dev), out)
     got, want = to_host(out), orc.mod_raise(ct, Q)
