@@ -473,7 +473,9 @@ void orc_modup(const orc_ctx *c, size_t chain_index, const uint64_t *c2, uint64_
 
 /* key_switch_inner_prod_c2_and_evk (src/eval_key_switch.cu:175-230):
  * cx[k][r] = sum_{b < beta} t_mod_up[b][r] * key[b][k][row(r)]  mod q_row(r),
- * accumulated exactly and reduced once. */
+ * accumulated in 128 bits and folded to its residue every 32 digits (with
+ * primes below 2^61 a product is below 2^122, so 65 products of 61-bit
+ * residues would pass 2^128), i.e. the exact sum mod q. */
 void orc_ks_inner_prod(const orc_ctx *c, size_t chain_index, const uint64_t *t_mod_up, const uint64_t *key,
                        size_t key_dnum, uint64_t *cx) {
     (void)key_dnum;
@@ -488,6 +490,10 @@ void orc_ks_inner_prod(const orc_ctx *c, size_t chain_index, const uint64_t *t_m
                 uint64_t x = t_mod_up[(b * QlP + r) * N + k];
                 acc0 += (u128)x * key[((b * 2 + 0) * QP + row) * N + k];
                 acc1 += (u128)x * key[((b * 2 + 1) * QP + row) * N + k];
+                if ((b & 31) == 31) {
+                    acc0 %= q;
+                    acc1 %= q;
+                }
             }
             cx[r * N + k] = (uint64_t)(acc0 % q);
             cx[(QlP + r) * N + k] = (uint64_t)(acc1 % q);

@@ -154,7 +154,10 @@ k_modup_bconv(const uint64_t *t, const uint64_t *c2, uint64_t *out, const uint64
 
 // key_switch_inner_prod_c2_and_evk (src/eval_key_switch.cu:175-230):
 //   cx[k][r] = sum_{b < beta} t[b][r] * key[b][k][row(r)]  mod q_row(r)
-// accumulated in 128 bits and reduced once.  With elt != 0 the slabs are read
+// accumulated in 128 bits, folded to its residue every 32 digits (a residue
+// plus 32 products below 2^122 stays below 2^128; the reference folds at a
+// threshold derived from the prime sizes) and reduced at the end: the same
+// residues as reducing once.  With elt != 0 the slabs are read
 // through the Galois permutation (hoisted rotations, src/evaluate.cu:2039-2049).
 // With acc set the result is added to cx (hoisting accumulates the inner
 // products of all rotations before one ModDown, src/evaluate.cu:1836-1879).
@@ -165,15 +168,19 @@ k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t 
     const uint32_t r = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t row = r < Ql ? r : Q + (r - Ql);
     const uint32_t sn = elt ? galois_perm(elt, n, logN) : n;
+    const uint64_t q = mod[row];
+    const ulonglong2 rt = ratio[row];
     U128 a0{0, 0}, a1{0, 0};
     for (uint32_t b = 0; b < beta; b++) {
         const uint64_t x = t[((size_t)b * QlP + r) * N + sn];
         const uint64_t *kb = key + (size_t)b * 2 * QP * N + (size_t)row * N + n;
         mac(a0, x, ld_stream(&kb[0]));
         mac(a1, x, ld_stream(&kb[(size_t)QP * N]));
+        if ((b & 31u) == 31u) {
+            a0 = U128{barrett128(a0, q, rt.x, rt.y), 0};
+            a1 = U128{barrett128(a1, q, rt.x, rt.y), 0};
+        }
     }
-    const uint64_t q = mod[row];
-    const ulonglong2 rt = ratio[row];
     uint64_t v0 = barrett128(a0, q, rt.x, rt.y), v1 = barrett128(a1, q, rt.x, rt.y);
     uint64_t *o0 = cx + (size_t)r * N + n, *o1 = cx + ((size_t)QlP + r) * N + n;
     if (acc) {

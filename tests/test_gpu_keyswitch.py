@@ -95,6 +95,39 @@ def test_inner_product(dev, logN, nq, alpha, chain):
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
+def test_inner_product_many_digits(dev):
+    """70 one-prime digits below primes near 2^61 at N = 2^10, with maximal
+    residues at half the positions: 65 such products pass 2^128, so the staged
+    inner product must fold its 128-bit sums on the way (the reference folds at
+    a threshold from the prime sizes, src/eval_key_switch.cu:175-230); the fused
+    multiply_and_relin (src/evaluate.cu:1061-1104) at the same depth too."""
+    import pfa_native as P
+    from gpu_util import primes_near_2_61
+
+    N, nq, alpha, chain = 1 << 10, 70, 1, 1
+    mods = primes_near_2_61(N, nq + alpha)
+    ctx, orc = P.NativeContext(N, mods, alpha), O.Oracle(N, mods, alpha)
+    Ql, beta, QP = orc.size_Ql(chain), orc.beta(chain), len(mods)
+    assert beta == 70 and beta * (min(mods) - 1) ** 2 >= 1 << 128
+    rng = np.random.default_rng(70)
+    qlp = np.array(mods[:Ql] + mods[nq:], dtype=np.uint64)
+    t = uniform_limbs(rng, (beta, Ql + alpha, N), list(qlp))
+    t[..., : N // 2] = (qlp - 1)[None, :, None]
+    key = uniform_limbs(rng, (orc.dnum, 2, QP, N), mods)
+    key[..., : N // 2] = (np.array(mods, dtype=np.uint64) - 1)[None, None, :, None]
+    dkey = to_dev(key, dev)
+    cx = empty((2, Ql + alpha, N), dev)
+    ctx.ks_inner_prod(chain, to_dev(t, dev), dkey, cx)
+    got, want = to_host(cx), orc.ks_inner_prod(chain, t, key)
+    assert np.array_equal(got, want), ("inner product", first_mismatch(got, want))
+    a = uniform_limbs(rng, (2, Ql, N), mods[:Ql])
+    b = uniform_limbs(rng, (2, Ql, N), mods[:Ql])
+    out = empty((2, Ql, N), dev)
+    ctx.multiply_and_relin(chain, to_dev(a, dev), to_dev(b, dev), dkey, out)
+    got, want = to_host(out), orc.multiply_and_relin(chain, a, b, key, threads=8)
+    assert np.array_equal(got, want), ("multiply_and_relin", first_mismatch(got, want))
+
+
 @pytest.mark.parametrize("logN,nq,alpha,chain", KEYLESS_SHAPES)
 def test_moddown(dev, logN, nq, alpha, chain):
     st = Setup(logN, nq, alpha, seed=3)

@@ -277,6 +277,37 @@ def test_inner_product_direct():
             assert [int(x) for x in cx[k, r]] == exp
 
 
+def test_inner_product_many_digits_bigint():
+    """70 digits of residues below primes near 2^61: 65 products of such
+    residues pass 2^128, so the 128-bit sums must be folded on the way
+    (src/eval_key_switch.cu:175-230 folds at a threshold from the prime
+    sizes).  Residues q - 1 at half the positions make every product maximal;
+    checked against Python integers."""
+    from gpu_util import primes_near_2_61
+
+    N, nq, alpha, chain = 16, 70, 1, 1
+    mods = primes_near_2_61(N, nq + alpha)
+    o = O.Oracle(N, mods, alpha)
+    Ql, beta, QP = o.size_Ql(chain), o.beta(chain), len(mods)
+    assert beta == 70 and beta * (mods[-1] - 1) ** 2 >= 1 << 128
+    rng = np.random.default_rng(7)
+    rows = list(range(Ql)) + list(range(nq, QP))
+    t = np.zeros((beta, Ql + alpha, N), dtype=np.uint64)
+    key = np.zeros((o.dnum, 2, QP, N), dtype=np.uint64)
+    for r, row in enumerate(rows):
+        t[:, r] = rng.integers(0, mods[row], (beta, N), dtype=np.uint64)
+        t[:, r, : N // 2] = mods[row] - 1
+    for row in range(QP):
+        key[:, :, row] = rng.integers(0, mods[row], (o.dnum, 2, N), dtype=np.uint64)
+        key[:, :, row, : N // 2] = mods[row] - 1
+    cx = o.ks_inner_prod(chain, t, key)
+    for k in range(2):
+        for r, row in enumerate(rows):
+            q = mods[row]
+            exp = [sum(int(t[b, r, n]) * int(key[b, k, row, n]) for b in range(beta)) % q for n in range(N)]
+            assert [int(x) for x in cx[k, r]] == exp
+
+
 @pytest.mark.parametrize("alpha", [1, 2, 3])
 def test_moddown_exact_on_multiples_of_P(alpha):
     """ModDown(P*c extended with zero P-limbs) == c exactly."""
