@@ -8,7 +8,9 @@ Per shape: the fused multiply + relinearize + rescale (src/evaluate.cu:
 (src/evaluate.cu:1607-1656) alone and as a batch of two with different steps
 and keys, and hoisted rotations (src/evaluate.cu:1929-2082).  The fixed shapes
 of test_gpu_keyswitch.py pin the regular cases; this sweep covers prime-size
-orders and digit splits no hand-picked list does.
+orders and digit splits no hand-picked list does.  Two further tests take the
+limits: digits of 5 to 16 special primes, and 20 hoisted rotations / a batch
+of 70 rotations (past the per-launch groups and work-schedule sizes).
 """
 import numpy as np
 import pytest
@@ -101,3 +103,67 @@ def test_random_shapes_cover_both_policies():
     assert any(s[3] > 1 for s in SHAPES)
     assert all(any(b < 50 for b in s[4]) or any(b >= 50 for b in s[4]) for s in SHAPES)
     assert sum(1 for s in SHAPES if any(b < 50 for b in s[4]) and any(b >= 50 for b in s[4])) >= 8
+
+
+@pytest.mark.parametrize("nq,alpha", [(16, 8), (16, 16), (18, 6)])
+def test_wide_digits_bit_exact(dev, nq, alpha):
+    """Digits of 5 to 16 special primes (the library's limit is 16): the fused
+    HMult + relinearize + rescale, a rotation and hoisted rotations against the
+    oracle, with 60-bit and 50-bit primes mixed in the chain and the digits."""
+    import pfa_native as P
+
+    bits = [60] + [50, 55, 36, 60] * 8
+    st = Setup(12, nq, alpha, seed=nq * alpha, bits=bits[:nq] + ([60, 49] * 8)[:alpha])
+    orc, N = st.orc, st.N
+    chain = 1
+    Ql = orc.size_Ql(chain)
+    assert orc.beta(chain) <= orc.dnum
+    key = st.key()
+    dkey = to_dev(key, dev)
+    a, b = st.ct(chain), st.ct(chain)
+    want = orc.rescale(chain, orc.multiply_and_relin(chain, a, b, key, threads=8), threads=8)
+    out = empty((2, Ql - 1, N), dev)
+    st.ctx.multiply_relin_rescale(chain, to_dev(a, dev), to_dev(b, dev), dkey, out)
+    got = to_host(out)
+    assert np.array_equal(got, want), ("hmult", first_mismatch(got, want))
+    elt = P.galois_elt_from_step(-9, N)
+    ct = st.ct(chain)
+    d = to_dev(ct, dev)
+    st.ctx.apply_galois(chain, d, elt, dkey)
+    got, want = to_host(d), orc.apply_galois(chain, ct, elt, key, threads=8)
+    assert np.array_equal(got, want), ("rotate", first_mismatch(got, want))
+    elts = [P.galois_elt_from_step(s, N) for s in (1, 5)]
+    hoisted = empty((2, 2, Ql, N), dev)
+    st.ctx.hoist_rotations(chain, d, elts, [dkey, dkey], hoisted)
+    want = orc.hoist_rotations(chain, to_host(d), elts, [key, key], threads=8)
+    got = to_host(hoisted)
+    assert np.array_equal(got, want), ("hoist", first_mismatch(got, want))
+
+
+def test_many_rotations_bit_exact(dev):
+    """20 hoisted rotations (two groups of the launcher's 16 per ModDown) and a
+    rotation batch of 70 members (past the 64-member work schedules), each
+    member against the oracle's apply_galois / hoist_rotations."""
+    import pfa_native as P
+
+    st = Setup(12, 4, 2, seed=20, bits=[60, 50, 50, 50, 60, 60])
+    orc, N, chain = st.orc, st.N, 1
+    Ql = orc.size_Ql(chain)
+    keys = [st.key() for _ in range(4)]
+    dkeys = [to_dev(k, dev) for k in keys]
+    steps = list(range(1, 21))
+    elts = [P.galois_elt_from_step(s, N) for s in steps]
+    ct = st.ct(chain)
+    out = empty((20, 2, Ql, N), dev)
+    st.ctx.hoist_rotations(chain, to_dev(ct, dev), elts, [dkeys[i % 4] for i in range(20)], out)
+    want = orc.hoist_rotations(chain, ct, elts, [keys[i % 4] for i in range(20)], threads=8)
+    got = to_host(out)
+    assert np.array_equal(got, want), ("hoist 20", first_mismatch(got, want))
+    cts = np.stack([st.ct(chain) for _ in range(70)])
+    belts = [elts[i % 20] for i in range(70)]
+    out = empty(cts.shape, dev)
+    st.ctx.rotate_batch(chain, to_dev(cts, dev), belts, [dkeys[i % 4] for i in range(70)], out)
+    got = to_host(out)
+    for i in range(70):
+        want = orc.apply_galois(chain, cts[i], belts[i], keys[i % 4], threads=8)
+        assert np.array_equal(got[i], want), ("rotate batch", i, first_mismatch(got[i], want))
