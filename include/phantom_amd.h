@@ -258,22 +258,28 @@ int pfa_poly_from_signed(const pfa_context *ctx, const int64_t *in, uint64_t *ou
 /* PhantomCKKSEncoder::encode (src/ckks.cu:71-137; special FFT src/fft.cu):
  * n_values <= N/2 complex slot values (device, interleaved re/im doubles;
  * missing slots are zero) times `scale`, rounded, into a plaintext of L limbs
- * (primes 0..L-1) in NTT form.  INVALID_ARGUMENT if a coefficient reaches
- * 2^62 ("encoded values are too large").  Synchronizes the stream. */
+ * (primes 0..L-1) in NTT form; a rounded coefficient of any size is reduced
+ * into each prime exactly.  INVALID_ARGUMENT, as the reference, if
+ * floor(log2(scale)) + 1 or ceil(log2(max |coefficient|)) + 1 reaches the
+ * bit length of q_0 ... q_(L-1) ("scale out of bounds", "encoded values are
+ * too large").  Synchronizes the stream. */
 int pfa_ckks_encode(const pfa_context *ctx, const double *values, size_t n_values, double scale, uint64_t *out,
                     size_t L, void *stream);
 
 /* PhantomCKKSEncoder::decode (src/ckks.cu:139-190): plaintext of L limbs in
  * NTT form -> N/2 complex slot values (device, interleaved re/im) divided by
- * `scale`.  Coefficients are composed from the first two limbs. */
+ * `scale`.  Coefficients are composed from all L limbs and centred, exact for
+ * any |m| < Q / 2 (compose_array, src/rns_base.cu:173-253).  INVALID_ARGUMENT
+ * if floor(log2(scale)) reaches the bit length of q_0 ... q_(L-1). */
 int pfa_ckks_decode(const pfa_context *ctx, const uint64_t *in, size_t L, double scale, double *values,
                     void *stream);
 
 /* encode_single_chain_plaintext (src/single_chain_plaintext.cu:93-150): the
- * same slot encoding as pfa_ckks_encode, returned as the N rounded signed
- * coefficients (device int64) instead of residues -- the reference's
- * level-independent plaintext.  Expand with pfa_expand_signed and
- * pfa_ntt_forward at the level of use.  Synchronizes the stream. */
+ * same slot encoding as pfa_ckks_encode (at chain index 1, with its bounds),
+ * returned as the N rounded coefficients reduced mod q_0 and centred (device
+ * int64) instead of residues -- the reference's level-independent plaintext.
+ * Expand with pfa_expand_signed and pfa_ntt_forward at the level of use.
+ * Synchronizes the stream. */
 int pfa_ckks_encode_coeffs(const pfa_context *ctx, const double *values, size_t n_values, double scale,
                            int64_t *coeffs, void *stream);
 

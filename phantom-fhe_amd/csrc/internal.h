@@ -199,6 +199,7 @@ struct Ctx {
     // key construction: [P]_{q_i} Shoup pairs over all QP rows (0 on P rows)
     ulonglong2 *pmodq = nullptr;
     uint32_t *slot_perm = nullptr;   // [N/2] CKKS slot j -> DFT index (5^j mod 2N - 1) / 4
+    ulonglong2 *crt_inv = nullptr;   // [Q][Q] q_i^-1 mod q_j (i < j) as Shoup pairs: the decoder's Garner composition
     std::vector<Level> levels;  // index = chain index (0 unused)
     std::vector<void *> allocations;
     mutable std::mutex arena_mu;

@@ -117,6 +117,78 @@ def test_encode_decode_roundtrip(dev, logN, chain):
     assert np.max(np.abs(dc[:100] - cv)) < 1e-9 and np.max(np.abs(dc[100:])) < 1e-9
 
 
+def _crt_centred(res, mods):
+    """Residues [L][N] -> the centred integers they represent (Python ints)."""
+    Q = 1
+    for q in mods:
+        Q *= q
+    out = []
+    for k in range(res.shape[1]):
+        x = 0
+        for l, q in enumerate(mods):
+            Ql = Q // q
+            x += int(res[l, k]) * Ql * pow(Ql, -1, q)
+        x %= Q
+        out.append(x - Q if x > (Q - 1) // 2 else x)
+    return out
+
+
+def test_encoder_large_coefficients_exact(dev):
+    """Scale 2^125 over four primes (210 bits): coefficients near 2^119 are
+    reduced into every prime exactly (the reference's multi-word decomposition,
+    src/rns_base.cu:75-170), so the residues CRT-compose to integers whose
+    embedding is the input; decoding composes all four limbs (compose_array,
+    src/rns_base.cu:173-253), beyond q0 q1 / 2 ~ 2^109 where two limbs stop
+    being enough.  The single-chain coefficients at the same scale are those
+    integers reduced mod q0 and centred (src/single_chain_plaintext.cu:93-150)."""
+    import torch
+
+    ph, ctx = make_ctx(12, [60, 50, 50, 50, 60], 1)
+    n, L, scale = ctx.N, ctx.size_Ql(1), 2.0 ** 125
+    rng = np.random.default_rng(125)
+    vals = rng.uniform(-1, 1, n // 2) + 1j * rng.uniform(-1, 1, n // 2)
+    pt = empty((L, n), dev)
+    dv = torch.from_numpy(vals).to(dev)
+    ctx.native.ckks_encode(dv, scale, pt, L)
+    mods = list(ctx.moduli[:L])
+    X = _crt_centred(O.Oracle(n, ctx.moduli, 1).ntt_inv(to_host(pt)), mods)
+    assert max(abs(x) for x in X) > 1 << 112  # beyond two 50/60-bit limbs
+    back = embed_direct(np.array([float(x) / scale for x in X]), n)
+    assert np.max(np.abs(back - vals)) < 1e-9
+    out = torch.empty(n // 2, dtype=torch.complex128, device=dev)
+    ctx.native.ckks_decode(pt, L, scale, out)
+    assert np.max(np.abs(out.cpu().numpy() - vals)) < 1e-9
+    sc = torch.empty(n, dtype=torch.int64, device=dev)
+    ctx.native.ckks_encode_coeffs(dv, scale, sc)
+    q0 = mods[0]
+    want = [(x % q0) - q0 if x % q0 > q0 // 2 else x % q0 for x in X]
+    assert [int(v) for v in sc.cpu().numpy()] == want
+
+
+def test_encoder_bounds(dev):
+    """The reference's bounds (src/ckks.cu:87-89, :122-126, :148-151): a
+    scale whose bit count reaches the level's modulus, and coefficients whose
+    bit count does, are refused; just below they are accepted."""
+    import torch
+
+    ph, ctx = make_ctx(12, [60, 50, 50, 50, 60], 1)
+    n = ctx.N
+    Q = 1
+    for q in ctx.moduli[:4]:
+        Q *= q
+    tb = Q.bit_length()  # the level's total_coeff_modulus_bit_count
+    v = torch.from_numpy(np.full(4, 0.5 + 0.25j)).to(dev)
+    pt = empty((4, n), dev)
+    ctx.native.ckks_encode(v, 2.0 ** (tb - 2), pt, 4)
+    with pytest.raises(ValueError):
+        ctx.native.ckks_encode(v, 2.0 ** (tb - 1), pt, 4)  # scale out of bounds
+    with pytest.raises(ValueError):
+        ctx.native.ckks_encode(torch.from_numpy(np.full(4, 1e30 + 0j)).to(dev), 2.0 ** (tb - 60), pt, 4)
+    out = torch.empty(n // 2, dtype=torch.complex128, device=dev)
+    with pytest.raises(ValueError):
+        ctx.native.ckks_decode(pt, 4, 2.0 ** tb, out)
+
+
 def test_encoder_errors(dev):
     ph, ctx = make_ctx(12, [60, 40, 60], 1)
     enc = ph.ckks_encoder(ctx)
@@ -125,7 +197,7 @@ def test_encoder_errors(dev):
     with pytest.raises(ValueError):
         enc.encode_double_vector(ctx, np.zeros(enc.slot_count() + 1), 2.0 ** 40)
     with pytest.raises(ValueError):
-        enc.encode_double_vector(ctx, [1e30], 2.0 ** 40)  # coefficients beyond 2^62
+        enc.encode_double_vector(ctx, [1e30], 2.0 ** 40)  # coefficients of more bits than q0 q1
 
 
 # ----------------------------------------------------------------- end to end
