@@ -129,7 +129,9 @@ static uint32_t bitrev(uint32_t x, int bits) {
 // candidates are 2^b - 2N + 1, 2^b - 4N + 1, ... (q = 1 mod 2N, q > 2^(b-1));
 // the k requests of size b receive the k largest such primes, smallest first.
 static void create_coeff_modulus(uint64_t N, const int *bits, size_t count, uint64_t *out) {
-    require(N >= 2 && (N & (N - 1)) == 0, "poly_modulus_degree must be a power of two");
+    // the reference's limits (src/host/modulus.cu:80-94, include/host/defines.h:11-24)
+    require(N >= 2 && N <= 131072 && (N & (N - 1)) == 0, "poly_modulus_degree is invalid");
+    require(count <= 64, "bit_sizes is invalid: at most 64 moduli");
     for (size_t i = 0; i < count; ++i) require(bits[i] >= 2 && bits[i] <= 60, "bit size must be in [2, 60]");
     std::vector<int> sizes(bits, bits + count);
     std::sort(sizes.begin(), sizes.end());

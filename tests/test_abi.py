@@ -58,6 +58,11 @@ def test_create_coeff_modulus_errors():
         P.create_coeff_modulus(8192, [61])  # above the 60-bit limit
     with pytest.raises(ValueError):
         P.create_coeff_modulus(1000, [50])  # degree not a power of two
+    with pytest.raises(ValueError):
+        P.create_coeff_modulus(1 << 18, [50])  # degree above 2^17
+    with pytest.raises(ValueError):
+        P.create_coeff_modulus(1 << 12, [40] * 65)  # more than 64 moduli
+    assert len(P.create_coeff_modulus(1 << 12, [40] * 64)) == 64
     with pytest.raises(RuntimeError):
         P.create_coeff_modulus(1 << 16, [18])  # no 18-bit prime = 1 mod 2^17
     assert "prime" in P.lib().pfa_last_error().decode()
