@@ -157,22 +157,17 @@ k_modup_bconv(const uint64_t *t, const uint64_t *c2, uint64_t *out, const uint64
 // accumulated in 128 bits, folded to its residue every 32 digits (a residue
 // plus 32 products below 2^122 stays below 2^128; the reference folds at a
 // threshold derived from the prime sizes) and reduced at the end: the same
-// residues as reducing once.  With elt != 0 the slabs are read
-// through the Galois permutation (hoisted rotations, src/evaluate.cu:2039-2049).
-// With acc set the result is added to cx (hoisting accumulates the inner
-// products of all rotations before one ModDown, src/evaluate.cu:1836-1879).
+// residues as reducing once.
 __global__ void __launch_bounds__(kThreads)
 k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t *mod, const ulonglong2 *ratio,
-           uint32_t Ql, uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N, uint32_t elt,
-           uint32_t logN, uint32_t acc) {
+           uint32_t Ql, uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N) {
     const uint32_t r = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t row = r < Ql ? r : Q + (r - Ql);
-    const uint32_t sn = elt ? galois_perm(elt, n, logN) : n;
     const uint64_t q = mod[row];
     const ulonglong2 rt = ratio[row];
     U128 a0{0, 0}, a1{0, 0};
     for (uint32_t b = 0; b < beta; b++) {
-        const uint64_t x = t[((size_t)b * QlP + r) * N + sn];
+        const uint64_t x = t[((size_t)b * QlP + r) * N + n];
         const uint64_t *kb = key + (size_t)b * 2 * QP * N + (size_t)row * N + n;
         mac(a0, x, ld_stream(&kb[0]));
         mac(a1, x, ld_stream(&kb[(size_t)QP * N]));
@@ -183,10 +178,6 @@ k_ks_inner(const uint64_t *t, const uint64_t *key, uint64_t *cx, const uint64_t 
     }
     uint64_t v0 = barrett128(a0, q, rt.x, rt.y), v1 = barrett128(a1, q, rt.x, rt.y);
     uint64_t *o0 = cx + (size_t)r * N + n, *o1 = cx + ((size_t)QlP + r) * N + n;
-    if (acc) {
-        v0 = add_mod(v0, *o0, q);
-        v1 = add_mod(v1, *o1, q);
-    }
     *o0 = v0;
     *o1 = v1;
 }
@@ -200,6 +191,79 @@ __global__ void __launch_bounds__(kThreads)
 k_galois(const uint64_t *src, uint64_t *dst, uint32_t elt, uint32_t N, uint32_t logN) {
     const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
     dst[(size_t)l * N + n] = src[(size_t)l * N + galois_perm(elt, n, logN)];
+}
+
+// The inner products of up to m hoisted rotations in one launch (the loop of
+// src/evaluate.cu:2036-2050, one rotation per member e):
+//   cx_e[k][r] = sum_b t[b][r][sigma_e(n)] key_e[b][k][row(r)][n]  mod q_row(r)
+// with the sums of k_ks_inner (folded every 32 digits).  With sum set the
+// members' products go into one output, cx_0 (hoisting accumulates the inner
+// products of all rotations before one ModDown, src/evaluate.cu:1836-1879):
+// the same residues as adding the members' reduced sums.
+// Every member reads limb t[b][r] through its own permutation, so the work is
+// dealt so that those reads meet in one L2: an item is (target r, half h of
+// its positions, block of 256 positions), and the blocks of one (r, h) run on
+// workgroups congruent mod 8, i.e. on one XCD (a launch's workgroups are dealt
+// to the XCDs round-robin), each XCD taking its pairs (r, h) in turn.
+// elts and keys are device tables of m entries.
+__global__ void __launch_bounds__(kThreads)
+k_ks_inner_hoist(const uint64_t *t, const uint32_t *elts, const uint64_t *const *keys, uint32_t m, uint32_t sum,
+                 uint64_t *cx, uint64_t cx_stride, const uint64_t *mod, const ulonglong2 *ratio, uint32_t Ql,
+                 uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N, uint32_t logN) {
+    const uint32_t bph = N / kThreads / 2;  // blocks per half of a limb
+    const uint32_t jj = blockIdx.x / 8;
+    const uint32_t p = (jj / bph) * 8 + blockIdx.x % 8;
+    if (p >= 2 * QlP) return;
+    const uint32_t r = p >> 1;
+    const uint32_t n = ((p & 1) * bph + jj % bph) * kThreads + threadIdx.x;
+    const uint32_t row = r < Ql ? r : Q + (r - Ql);
+    const uint64_t q = mod[row];
+    const ulonglong2 rt = ratio[row];
+    const uint64_t *tr = t + (size_t)r * N;
+    U128 a0{0, 0}, a1{0, 0};
+    uint32_t terms = 0;
+    for (uint32_t e = 0; e < m; e++) {
+        const uint32_t sn = galois_perm(ld_const(elts + e), n, logN);
+        const uint64_t *kr = reinterpret_cast<const uint64_t *>(ld_const(reinterpret_cast<const uint64_t *>(keys + e))) +
+                             (size_t)row * N + n;
+        for (uint32_t b = 0; b < beta; b++) {
+            const uint64_t x = tr[(size_t)b * QlP * N + sn];
+            const uint64_t *kb = kr + (size_t)b * 2 * QP * N;
+            mac(a0, x, ld_stream(&kb[0]));
+            mac(a1, x, ld_stream(&kb[(size_t)QP * N]));
+            if (++terms == 32) {
+                a0 = U128{barrett128(a0, q, rt.x, rt.y), 0};
+                a1 = U128{barrett128(a1, q, rt.x, rt.y), 0};
+                terms = 0;
+            }
+        }
+        if (!sum || e + 1 == m) {
+            uint64_t *o = cx + (sum ? 0 : (size_t)e * cx_stride) + (size_t)r * N + n;
+            o[0] = barrett128(a0, q, rt.x, rt.y);
+            o[(size_t)QlP * N] = barrett128(a1, q, rt.x, rt.y);
+            a0 = a1 = U128{0, 0};
+            terms = 0;
+        }
+    }
+}
+
+// sigma_e(src) for m members (dst_e = dst + e dst_stride), or with sum set
+// their sum into dst: the Galois permutation of each hoisted rotation's c0
+// (src/galois.cu:11-18), in one launch.
+__global__ void __launch_bounds__(kThreads)
+k_galois_hoist(const uint64_t *src, uint64_t *dst, uint64_t dst_stride, const uint32_t *elts, uint32_t m,
+               uint32_t sum, const uint64_t *mod, uint32_t N, uint32_t logN) {
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    const uint64_t *sl = src + (size_t)l * N;
+    if (sum) {
+        const uint64_t q = mod[l];
+        uint64_t acc = 0;
+        for (uint32_t e = 0; e < m; e++) acc = add_mod(acc, sl[galois_perm(ld_const(elts + e), n, logN)], q);
+        dst[(size_t)l * N + n] = acc;
+        return;
+    }
+    const uint32_t e = blockIdx.z;
+    dst[(size_t)e * dst_stride + (size_t)l * N + n] = sl[galois_perm(ld_const(elts + e), n, logN)];
 }
 
 // generate_one_kswitch_key (src/secretkey.cu:354-398) with
@@ -265,14 +329,34 @@ void op_modup(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, h
 }
 
 void op_inner(const Ctx &c, uint32_t chain, const uint64_t *t, const uint64_t *key, size_t dnum, uint64_t *cx,
-              uint32_t elt, hipStream_t s, bool acc = false) {
+              hipStream_t s) {
     check_chain(c, chain);
     const Level &lv = c.level(chain);
     require(key != nullptr, "null key");
     require(lv.beta <= dnum, "key has fewer digits than the ciphertext level needs");
     const uint32_t QlP = lv.Ql + c.P;
     hipLaunchKernelGGL(k_ks_inner, grid(c, QlP), dim3(kThreads), 0, s, t, key, cx, c.mod, c.ratio, lv.Ql, QlP, c.Q,
-                       c.QP, lv.beta, c.N, elt, c.logN, acc ? 1u : 0u);
+                       c.QP, lv.beta, c.N);
+    PFA_HIP(hipGetLastError());
+}
+
+// The c0 permutations and key inner products of m hoisted rotations of ct
+// (ModUp output mu, [beta][QlP][N]): sigma_e(c0) into c0out + e c0_stride and
+// member e's inner product into cx + e cx_stride, or with sum set the sum of
+// the permuted c0 into c0out and of the inner products into cx.  elts and keys
+// are device tables of m entries.
+void hoist_inner(const Ctx &c, uint32_t chain, const uint64_t *ct, const uint64_t *mu, const uint32_t *elts,
+                 const uint64_t *const *keys, size_t key_dnum, uint32_t m, bool sum, uint64_t *c0out,
+                 uint64_t c0_stride, uint64_t *cx, uint64_t cx_stride, hipStream_t s) {
+    const Level &lv = c.level(chain);
+    require(lv.beta <= key_dnum, "key has fewer digits than the ciphertext level needs");
+    const uint32_t Ql = lv.Ql, QlP = Ql + c.P;
+    hipLaunchKernelGGL(k_galois_hoist, dim3(c.N / kThreads, Ql, sum ? 1 : m), dim3(kThreads), 0, s, ct, c0out,
+                       c0_stride, elts, m, sum ? 1u : 0u, c.mod, c.N, c.logN);
+    PFA_HIP(hipGetLastError());
+    const uint32_t pairs8 = (2 * QlP + 7) / 8 * 8, bph = c.N / kThreads / 2;
+    hipLaunchKernelGGL(k_ks_inner_hoist, dim3(pairs8 * bph), dim3(kThreads), 0, s, mu, elts, keys, m,
+                       sum ? 1u : 0u, cx, cx_stride, c.mod, c.ratio, Ql, QlP, c.Q, c.QP, lv.beta, c.N, c.logN);
     PFA_HIP(hipGetLastError());
 }
 
@@ -386,7 +470,7 @@ int pfa_ks_inner_prod(const pfa_context *ctx, size_t chain_index, const uint64_t
                       size_t key_dnum, uint64_t *cx, void *stream) {
     return guarded([&] {
         require(t_mod_up && cx, "null argument");
-        op_inner(*ctx_of(ctx), (uint32_t)chain_index, t_mod_up, key, key_dnum, cx, 0, as_stream(stream));
+        op_inner(*ctx_of(ctx), (uint32_t)chain_index, t_mod_up, key, key_dnum, cx, as_stream(stream));
     });
 }
 
@@ -598,22 +682,25 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
         Scratch sc(c, s);
         uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
         op_modup(c, chain, ct + LN, mu, s);
-        // each rotation's inner product into its own slot, then one ModDown
-        // over the 2 n polys of up to kHoistGroup rotations (its small INTT and
-        // base-conversion launches are latency-bound, so one launch for the
-        // group costs about what one rotation's did): poly 2e adds sigma_e(c0),
-        // already in out
+        // up to kHoistGroup rotations at a time: their c0 permutations (into
+        // poly 0 of each output) and inner products (each into its own slot)
+        // in one launch each, then one ModDown over the group's 2 m polys
+        // (its small INTT and base-conversion launches are latency-bound, so
+        // one launch for the group costs about what one rotation's did), poly
+        // 2e adding sigma_e(c0)
         constexpr size_t kHoistGroup = 16;
         const size_t CX = (size_t)2 * QlP * c.N;
-        uint64_t *cx = sc.alloc(std::min(n, kHoistGroup) * CX);
+        const size_t G = std::min(n, kHoistGroup);
+        uint64_t *cx = sc.alloc(G * CX);
+        uint32_t *elt_dev = sc.alloc<uint32_t>(G);
+        const uint64_t **key_dev = sc.alloc<const uint64_t *>(G);
         for (size_t e0 = 0; e0 < n; e0 += kHoistGroup) {
-            const size_t m = std::min(kHoistGroup, n - e0);
-            for (size_t e = 0; e < m; ++e) {
-                op_galois(c, elts[e0 + e], ct, out + (e0 + e) * 2 * LN, Ql, s);
-                op_inner(c, chain, mu, keys[e0 + e], key_dnum, cx + e * CX, elts[e0 + e], s);
-            }
+            const uint32_t m = (uint32_t)std::min(kHoistGroup, n - e0);
+            upload_async(c, elt_dev, elts + e0, m * sizeof(uint32_t), s);
+            upload_async(c, key_dev, keys + e0, m * sizeof(void *), s);
             uint64_t *o = out + e0 * 2 * LN;
-            fused_moddown(c, chain, cx, (uint32_t)(2 * m), o, o, nullptr, s, 2 * LN);
+            hoist_inner(c, chain, ct, mu, elt_dev, key_dev, key_dnum, m, false, o, 2 * LN, cx, CX, s);
+            fused_moddown(c, chain, cx, 2 * m, o, o, nullptr, s, 2 * LN);
         }
     });
 }
@@ -634,16 +721,12 @@ int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct,
         uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
         op_modup(c, chain, ct + LN, mu, s);
         uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
-        uint64_t *c0 = sc.alloc(2 * LN);  // accumulated sigma(c0), and one sigma(c0) term
-        for (size_t e = 0; e < n; ++e) {
-            op_galois(c, elts[e], ct, e == 0 ? c0 : c0 + LN, Ql, s);
-            if (e > 0) {
-                hipLaunchKernelGGL(k_poly_binop, grid(c, Ql), dim3(kThreads), 0, s, (int)kAdd, c0, c0 + LN, c0,
-                                   c.mod, c.ratio, 0u, c.N);
-                PFA_HIP(hipGetLastError());
-            }
-            op_inner(c, chain, mu, keys[e], key_dnum, cx, elts[e], s, e > 0);
-        }
+        uint64_t *c0 = sc.alloc(LN);  // sum of sigma_e(c0)
+        uint32_t *elt_dev = sc.alloc<uint32_t>(n);
+        const uint64_t **key_dev = sc.alloc<const uint64_t *>(n);
+        upload_async(c, elt_dev, elts, n * sizeof(uint32_t), s);
+        upload_async(c, key_dev, keys, n * sizeof(void *), s);
+        hoist_inner(c, chain, ct, mu, elt_dev, key_dev, key_dnum, (uint32_t)n, true, c0, 0, cx, 0, s);
         // c0' = sum sigma(c0) + ModDown(acc0), c1' = ModDown(acc1)
         op_moddown(c, chain, cx, 2, out, Bases{{c0, nullptr}}, s);
     });
