@@ -1166,15 +1166,17 @@ void launch_epi(const Ctx &c, const EpiRows &a0, hipStream_t s) {
 
 // c2 [Ql][N] (NTT form) -> cx [2][QlP][N]: ModUp and the key-switch inner
 // product against key [dnum][2][QP][N].
-void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
-                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold,
-                       const uint64_t *const *key_table, const uint64_t *c2_mid) {
+// The ModUp of batch members c2 (+ i c2_stride) up to the forward NTT's
+// columns pass: the scaled INTT, then the base conversion fused with the
+// columns pass into inter [batch][beta][QlP][N] (each digit's own limbs not
+// written).  With c2_mid the INTT runs its columns pass only, on c2_mid.
+static void modup_cols(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t c2_stride, const uint64_t *c2_mid,
+                       uint64_t *inter, uint32_t batch, hipStream_t s) {
     const Level &lv = c.level(chain);
     const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
     const uint64_t LN = (uint64_t)Ql * c.N, IN = (uint64_t)lv.beta * QlP * c.N;
     Scratch sc(c, s);
     uint64_t *tin = sc.alloc((size_t)batch * LN);
-    uint64_t *inter = sc.alloc((size_t)batch * IN);
     if (c2_mid) {
         NttLaunch inv{c2_mid, tin, LN, LN, batch, Ql};
         inv.scale = lv.modup_scale;
@@ -1210,6 +1212,32 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
     b.sched_grid = sch.grid;
     b.sched_total = sch.total;
     PFA_FUSED_DISPATCH(launch_bconv, b);
+}
+
+void fused_modup_ntt(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, hipStream_t s) {
+    const Level &lv = c.level(chain);
+    const uint32_t QlP = lv.Ql + c.P;
+    modup_cols(c, chain, c2, 0, nullptr, out, 1, s);
+    NttLaunch fw{out, out, (uint64_t)QlP * c.N, (uint64_t)QlP * c.N, lv.beta, QlP};
+    fw.start = 0;
+    fw.split = lv.Ql;
+    fw.split_base = c.Q;
+    fw.ex_lo = 0;
+    fw.ex_step = c.P;
+    fw.ex_len = c.P;
+    fw.ex_cap = lv.Ql;
+    ntt_forward_rows(c, fw, s);
+}
+
+void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const uint64_t *key, uint64_t *cx,
+                       hipStream_t s, uint32_t batch, uint64_t c2_stride, uint64_t cx_stride, const KsFold *fold,
+                       const uint64_t *const *key_table, const uint64_t *c2_mid) {
+    const Level &lv = c.level(chain);
+    const uint32_t Ql = lv.Ql, alpha = c.P, QlP = Ql + alpha;
+    const uint64_t IN = (uint64_t)lv.beta * QlP * c.N;
+    Scratch sc(c, s);
+    uint64_t *inter = sc.alloc((size_t)batch * IN);
+    modup_cols(c, chain, c2, c2_stride, c2_mid, inter, batch, s);
     InnerRows r{inter, c2, key, cx, c.mont, Ql, QlP, alpha, lv.beta, c.Q, c.QP};
     r.batch = batch;
     r.inter_bstride = IN;

@@ -306,6 +306,8 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flo
 // The inverse's columns pass alone: a.src holds the output of its rows pass
 // (fused_tensor_rows), a.dst receives the canonical coefficients.
 void ntt_inverse_cols(const Ctx &c, const NttLaunch &a, hipStream_t s);
+// the forward NTT's rows pass alone, over a columns pass's output in a.src
+void ntt_forward_rows(const Ctx &c, const NttLaunch &a, hipStream_t s);
 // True when the device deals a launch's workgroups to 8 XCDs round-robin
 // (workgroup w on XCD (w + r) mod 8 for some r), which the single-launch NTT is
 // built for; runs a probe kernel.
@@ -329,6 +331,10 @@ void fused_modup_inner(const Ctx &c, uint32_t chain, const uint64_t *c2, const u
                        hipStream_t s, uint32_t batch = 1, uint64_t c2_stride = 0, uint64_t cx_stride = 0,
                        const KsFold *fold = nullptr, const uint64_t *const *key_table = nullptr,
                        const uint64_t *c2_mid = nullptr);
+// ModUp of c2 (Ql limbs, NTT form) into out [beta][QlP][N] in NTT form, by the
+// fused base conversion + columns pass and then the rows pass; each digit's
+// own limbs are not written (they are c2's).
+void fused_modup_ntt(const Ctx &c, uint32_t chain, const uint64_t *c2, uint64_t *out, hipStream_t s);
 // The tensor product of count ciphertext pairs (as op_tensor: member i reads
 // a, b at + i in_stride, writes d0, d1 at + i d_stride, d2 at + i d2_stride)
 // with the first pass of the key switch's INTT(d2) fused in: mid [count][Ql][N]

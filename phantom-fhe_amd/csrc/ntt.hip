@@ -54,6 +54,20 @@ constexpr int half_rows() {
     return S2 == 8 && G::ROWS == 16 ? 8 : G::ROWS;
 }
 
+// the forward rows pass alone: b.src holds a columns pass's output
+template <int S1, int S2>
+void fwd_rows(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
+    using G = Geo<S1, S2>;
+    const uint32_t ml = b.M * b.L;
+    constexpr int RH = half_rows<S1, S2>();
+    if (RH != G::ROWS)
+        hipLaunchKernelGGL((ntt_fwd_rows<S1, S2, RH>), dim3(grid_for(c, ml * (G::N1 / RH), c.ntt_wpc_fwd * (G::ROWS / RH))),
+                           dim3(RH * Sub<S2>::T), 0, s, b, t);
+    else
+        hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc_fwd)), dim3(G::ROW_THREADS), 0, s, b,
+                           t);
+}
+
 template <int S1, int S2>
 void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     using G = Geo<S1, S2>;
@@ -63,13 +77,7 @@ void fwd(const Ctx &c, const NttBatch &b, const NttTables &t, hipStream_t s) {
     NttBatch b2 = b;
     b2.src = b.dst;
     b2.sstride = b.dstride;
-    constexpr int RH = half_rows<S1, S2>();
-    if (RH != G::ROWS)
-        hipLaunchKernelGGL((ntt_fwd_rows<S1, S2, RH>), dim3(grid_for(c, ml * (G::N1 / RH), c.ntt_wpc_fwd * (G::ROWS / RH))),
-                           dim3(RH * Sub<S2>::T), 0, s, b2, t);
-    else
-        hipLaunchKernelGGL((ntt_fwd_rows<S1, S2>), dim3(grid_for(c, ml * G::ROW_TILES, c.ntt_wpc_fwd)), dim3(G::ROW_THREADS), 0, s, b2,
-                           t);
+    fwd_rows<S1, S2>(c, b2, t, s);
 }
 
 // batches of at least this many limbs take the inverse rows pass with staged twiddles
@@ -196,6 +204,14 @@ void ntt_inverse(const Ctx &c, const NttLaunch &a, hipStream_t s, bool allow_flo
         return;
     }
     PFA_NTT_DISPATCH(inv);
+    PFA_HIP(hipGetLastError());
+}
+
+void ntt_forward_rows(const Ctx &c, const NttLaunch &a, hipStream_t s) {
+    check_launch(c, a);
+    const NttBatch b = make_batch(c, a);
+    const NttTables t = tables(c);
+    PFA_NTT_DISPATCH(fwd_rows);
     PFA_HIP(hipGetLastError());
 }
 

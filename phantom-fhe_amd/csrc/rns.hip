@@ -205,11 +205,14 @@ k_galois(const uint64_t *src, uint64_t *dst, uint32_t elt, uint32_t N, uint32_t 
 // its positions, block of 256 positions), and the blocks of one (r, h) run on
 // workgroups congruent mod 8, i.e. on one XCD (a launch's workgroups are dealt
 // to the XCDs round-robin), each XCD taking its pairs (r, h) in turn.
-// elts and keys are device tables of m entries.
+// elts and keys are device tables of m entries.  Digit b's own limbs
+// (r in [b alpha, b alpha + alpha), r < Ql) are read from own, the rotated
+// ciphertext's c1 in NTT form, and t holds the other (digit, limb) pairs.
 __global__ void __launch_bounds__(kThreads)
-k_ks_inner_hoist(const uint64_t *t, const uint32_t *elts, const uint64_t *const *keys, uint32_t m, uint32_t sum,
-                 uint64_t *cx, uint64_t cx_stride, const uint64_t *mod, const ulonglong2 *ratio, uint32_t Ql,
-                 uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t beta, uint32_t N, uint32_t logN) {
+k_ks_inner_hoist(const uint64_t *t, const uint64_t *own, const uint32_t *elts, const uint64_t *const *keys,
+                 uint32_t m, uint32_t sum, uint64_t *cx, uint64_t cx_stride, const uint64_t *mod,
+                 const ulonglong2 *ratio, uint32_t Ql, uint32_t QlP, uint32_t Q, uint32_t QP, uint32_t alpha,
+                 uint32_t beta, uint32_t N, uint32_t logN) {
     const uint32_t bph = N / kThreads / 2;  // blocks per half of a limb
     const uint32_t jj = blockIdx.x / 8;
     const uint32_t p = (jj / bph) * 8 + blockIdx.x % 8;
@@ -227,7 +230,8 @@ k_ks_inner_hoist(const uint64_t *t, const uint32_t *elts, const uint64_t *const 
         const uint64_t *kr = reinterpret_cast<const uint64_t *>(ld_const(reinterpret_cast<const uint64_t *>(keys + e))) +
                              (size_t)row * N + n;
         for (uint32_t b = 0; b < beta; b++) {
-            const uint64_t x = tr[(size_t)b * QlP * N + sn];
+            const uint64_t *src = r < Ql && r / alpha == b ? own + (size_t)r * N : tr + (size_t)b * QlP * N;
+            const uint64_t x = src[sn];
             const uint64_t *kb = kr + (size_t)b * 2 * QP * N;
             mac(a0, x, ld_stream(&kb[0]));
             mac(a1, x, ld_stream(&kb[(size_t)QP * N]));
@@ -341,7 +345,8 @@ void op_inner(const Ctx &c, uint32_t chain, const uint64_t *t, const uint64_t *k
 }
 
 // The c0 permutations and key inner products of m hoisted rotations of ct
-// (ModUp output mu, [beta][QlP][N]): sigma_e(c0) into c0out + e c0_stride and
+// (ModUp output mu, [beta][QlP][N], each digit's own limbs taken from ct's
+// c1): sigma_e(c0) into c0out + e c0_stride and
 // member e's inner product into cx + e cx_stride, or with sum set the sum of
 // the permuted c0 into c0out and of the inner products into cx.  elts and keys
 // are device tables of m entries.
@@ -355,8 +360,9 @@ void hoist_inner(const Ctx &c, uint32_t chain, const uint64_t *ct, const uint64_
                        c0_stride, elts, m, sum ? 1u : 0u, c.mod, c.N, c.logN);
     PFA_HIP(hipGetLastError());
     const uint32_t pairs8 = (2 * QlP + 7) / 8 * 8, bph = c.N / kThreads / 2;
-    hipLaunchKernelGGL(k_ks_inner_hoist, dim3(pairs8 * bph), dim3(kThreads), 0, s, mu, elts, keys, m,
-                       sum ? 1u : 0u, cx, cx_stride, c.mod, c.ratio, Ql, QlP, c.Q, c.QP, lv.beta, c.N, c.logN);
+    hipLaunchKernelGGL(k_ks_inner_hoist, dim3(pairs8 * bph), dim3(kThreads), 0, s, mu, ct + (size_t)Ql * c.N, elts,
+                       keys, m, sum ? 1u : 0u, cx, cx_stride, c.mod, c.ratio, Ql, QlP, c.Q, c.QP, c.P, lv.beta, c.N,
+                       c.logN);
     PFA_HIP(hipGetLastError());
 }
 
@@ -681,7 +687,7 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
         for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
         Scratch sc(c, s);
         uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
-        op_modup(c, chain, ct + LN, mu, s);
+        fused_modup_ntt(c, chain, ct + LN, mu, s);
         // up to kHoistGroup rotations at a time: their c0 permutations (into
         // poly 0 of each output) and inner products (each into its own slot)
         // in one launch each, then one ModDown over the group's 2 m polys
@@ -719,7 +725,7 @@ int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct,
         for (size_t e = 0; e < n; ++e) require((elts[e] & 1) && elts[e] < 2 * c.N, "bad Galois element");
         Scratch sc(c, s);
         uint64_t *mu = sc.alloc((size_t)lv.beta * QlP * c.N);
-        op_modup(c, chain, ct + LN, mu, s);
+        fused_modup_ntt(c, chain, ct + LN, mu, s);
         uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
         uint64_t *c0 = sc.alloc(LN);  // sum of sigma_e(c0)
         uint32_t *elt_dev = sc.alloc<uint32_t>(n);
