@@ -839,12 +839,18 @@ def _check_scale(a, b):
         raise ValueError("scale mismatch")
 
 
+def _signed_sum(ctx: context, like: ciphertext, terms) -> ciphertext:
+    """sum_t k_t x_t over every poly of ciphertexts shaped like `like`, as one
+    pfa_ct_lincomb launch (weights +-1: canonical sums, the same residues as
+    the polynomial-wise add / sub / negate of src/evaluate.cu)."""
+    L = ctx.size_Ql(like.chain_index())
+    out = ctx._empty(*like.data.shape)
+    ctx.native.ct_lincomb(L, [x.data for x, _ in terms], [k for _, k in terms], out)
+    return like._like(out)
+
+
 def negate(ctx: context, ct: ciphertext) -> ciphertext:
-    L = ctx.size_Ql(ct.chain_index())
-    out = ctx._empty(*ct.data.shape)
-    for i in range(ct.size()):
-        ctx.native.poly_negate(ct.data[i], out[i], L)
-    return ct._like(out)
+    return _signed_sum(ctx, ct, [(ct, -1)])
 
 
 def add(ctx: context, a: ciphertext, b: ciphertext) -> ciphertext:
@@ -852,33 +858,31 @@ def add(ctx: context, a: ciphertext, b: ciphertext) -> ciphertext:
     _check_scale(a, b)
     if a.size() != b.size():
         raise ValueError("ciphertext sizes differ")
-    L = ctx.size_Ql(a.chain_index())
-    out = ctx._empty(*a.data.shape)
-    for i in range(a.size()):
-        ctx.native.poly_add(a.data[i], b.data[i], out[i], L)
-    return a._like(out)
+    return _signed_sum(ctx, a, [(a, 1), (b, 1)])
 
 
 def add_many(ctx: context, cts, _unused=None) -> ciphertext:
+    """add_many (src/evaluate.cu): up to 8 ciphertexts per launch."""
     if not cts:
         raise ValueError("empty list")
-    acc = cts[0]
     for c in cts[1:]:
-        acc = add(ctx, acc, c)
+        _check_same(cts[0], c)
+        _check_scale(cts[0], c)
+        if c.size() != cts[0].size():
+            raise ValueError("ciphertext sizes differ")
+    acc, rest = cts[0], list(cts[1:])
+    while rest:
+        chunk, rest = rest[:7], rest[7:]
+        acc = _signed_sum(ctx, acc, [(acc, 1)] + [(c, 1) for c in chunk])
     return acc
 
 
 def sub(ctx: context, a: ciphertext, b: ciphertext, negate: bool = False) -> ciphertext:
     _check_same(a, b)
     _check_scale(a, b)
-    L = ctx.size_Ql(a.chain_index())
-    out = ctx._empty(*a.data.shape)
-    for i in range(a.size()):
-        if negate:
-            ctx.native.poly_sub(b.data[i], a.data[i], out[i], L)
-        else:
-            ctx.native.poly_sub(a.data[i], b.data[i], out[i], L)
-    return a._like(out)
+    if a.size() != b.size():
+        raise ValueError("ciphertext sizes differ")
+    return _signed_sum(ctx, a, [(a, -1), (b, 1)] if negate else [(a, 1), (b, -1)])
 
 
 def add_plain(ctx: context, ct: ciphertext, pt: plaintext) -> ciphertext:
