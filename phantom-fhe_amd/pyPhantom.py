@@ -1050,7 +1050,16 @@ def mod_switch_to_next(ctx: context, obj):
         pt = plaintext()
         pt.data, pt._chain_index, pt._scale = obj.data[:L - 1].contiguous(), chain + 1, obj.scale()
         return pt
-    return obj._like(obj.data[:, :L - 1].contiguous(), chain=chain + 1)
+    return obj._like(_drop_limbs(ctx, obj.data, L - 1), chain=chain + 1)
+
+
+def _drop_limbs(ctx: context, data, L: int):
+    """The first L limbs of every poly of [size][L'][N] data, as one launch:
+    a one-term weighted sum with weight 1 reads each poly's first L limbs at
+    the input's own poly stride (canonical residues, copied unchanged)."""
+    out = ctx._empty(data.shape[0], L, data.shape[2])
+    ctx.native.ct_lincomb(L, [data], [1], out)
+    return out
 
 
 def mod_switch_to(ctx: context, obj, chain_index: int):
@@ -1067,7 +1076,7 @@ def mod_switch_to(ctx: context, obj, chain_index: int):
         pt = plaintext()
         pt.data, pt._chain_index, pt._scale = obj.data[:L].contiguous(), chain_index, obj.scale()
         return pt
-    return obj._like(obj.data[:, :L].contiguous(), chain=chain_index)
+    return obj._like(_drop_limbs(ctx, obj.data, L), chain=chain_index)
 
 
 def mod_switch_to_inplace(ctx: context, obj, chain_index: int) -> None:
