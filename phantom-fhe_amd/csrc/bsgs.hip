@@ -395,10 +395,10 @@ void rotate_into(const Ctx &c, uint32_t chain, const uint64_t *src, uint64_t src
     uint32_t *elt_dev = nullptr;
     const uint64_t **key_dev = nullptr;
     if (elts) {
-        elt_dev = sc.alloc<uint32_t>(B);
-        upload_async(c, elt_dev, elts, B * sizeof(uint32_t), s);
-        key_dev = sc.alloc<const uint64_t *>(B);
-        upload_async(c, key_dev, keys, B * sizeof(void *), s);
+        void *dev[2];
+        upload_parts(c, sc, s, {{elts, B * sizeof(uint32_t)}, {keys, B * sizeof(void *)}}, dev);
+        elt_dev = (uint32_t *)dev[0];
+        key_dev = (const uint64_t **)dev[1];
     }
     uint64_t *t = sc.alloc((size_t)B * 2 * LN);
     // up to N = 2^16 the permutation kernel also runs the first pass of the
@@ -449,29 +449,21 @@ MacArgs mac_args(const Ctx &c, size_t chain_index, const uint64_t *const *pts, c
     uint64_t st = 0;
     a.tiled = reinterpret_cast<const uint8_t *>(tiled);
     if (tiled) a.lay = tiled_layout(c, a.Ql, (uint64_t)M * G);
-    if (!tiled) {
-        if (progression((const void *const *)pts, M * G, st)) {
-            a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
-        } else {
-            const uint64_t **t = sc.alloc<const uint64_t *>(M * G);
-            upload_async(c, t, pts, M * G * sizeof(void *), s);
-            a.pt = PtrList<const uint64_t>{t, nullptr, 0};
-        }
-    }
-    if (progression((const void *const *)out, G, st)) {
-        a.out = PtrList<uint64_t>{nullptr, out[0], st};
-    } else {
-        uint64_t **t = sc.alloc<uint64_t *>(G);
-        upload_async(c, t, out, G * sizeof(void *), s);
-        a.out = PtrList<uint64_t>{t, nullptr, 0};
-    }
-    if (progression((const void *const *)babies, M, st)) {
-        a.babies = PtrList<const uint64_t>{nullptr, babies[0], st};
-    } else {
-        const uint64_t **t = sc.alloc<const uint64_t *>(M);
-        upload_async(c, t, babies, M * sizeof(void *), s);
-        a.babies = PtrList<const uint64_t>{t, nullptr, 0};
-    }
+    // lists that are not arithmetic progressions go as tables, uploaded together
+    const bool pt_tab = !tiled && !progression((const void *const *)pts, M * G, st);
+    if (!tiled && !pt_tab) a.pt = PtrList<const uint64_t>{nullptr, pts[0], st};
+    const bool out_tab = !progression((const void *const *)out, G, st);
+    if (!out_tab) a.out = PtrList<uint64_t>{nullptr, out[0], st};
+    const bool bab_tab = !progression((const void *const *)babies, M, st);
+    if (!bab_tab) a.babies = PtrList<const uint64_t>{nullptr, babies[0], st};
+    void *dev[3];
+    upload_parts(c, sc, s,
+                 {{pts, pt_tab ? M * G * sizeof(void *) : 0}, {out, out_tab ? G * sizeof(void *) : 0},
+                  {babies, bab_tab ? M * sizeof(void *) : 0}},
+                 dev);
+    if (pt_tab) a.pt = PtrList<const uint64_t>{(const uint64_t *const *)dev[0], nullptr, 0};
+    if (out_tab) a.out = PtrList<uint64_t>{(uint64_t *const *)dev[1], nullptr, 0};
+    if (bab_tab) a.babies = PtrList<const uint64_t>{(const uint64_t *const *)dev[2], nullptr, 0};
     return a;
 }
 

@@ -526,6 +526,21 @@ void upload_async(const Ctx &c, void *dst, const void *src, size_t n, hipStream_
     PFA_HIP(hipEventRecord(c.stage_ev[i], s));
 }
 
+void upload_parts(const Ctx &c, Scratch &sc, hipStream_t s, std::initializer_list<HostPart> parts, void **dev) {
+    size_t total = 0;
+    for (const HostPart &p : parts) total += (p.bytes + 15) & ~(size_t)15;
+    if (total == 0) return;
+    std::vector<char> packed(total);
+    char *block = sc.alloc<char>(total);
+    size_t off = 0, i = 0;
+    for (const HostPart &p : parts) {
+        if (p.bytes) std::memcpy(packed.data() + off, p.src, p.bytes);
+        dev[i++] = block + off;
+        off += (p.bytes + 15) & ~(size_t)15;
+    }
+    upload_async(c, block, packed.data(), total, s);
+}
+
 static void destroy(Ctx *c) {
     if (!c) return;
     int prev = 0;

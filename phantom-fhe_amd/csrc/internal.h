@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <array>
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -270,6 +271,14 @@ void encoder_init(Ctx &c);
 // without waiting for the stream (pinned staging; larger copies than a slot
 // fall back to a plain asynchronous copy).
 void upload_async(const Ctx &c, void *dst, const void *src, size_t n, hipStream_t s);
+// Host tables packed into one block of sc (each part at a 16-byte aligned
+// offset) and uploaded with one copy on s; dev[i] receives part i's address.
+struct HostPart {
+    const void *src;
+    size_t bytes;
+};
+class Scratch;
+void upload_parts(const Ctx &c, Scratch &sc, hipStream_t s, std::initializer_list<HostPart> parts, void **dev);
 
 class Scratch {
   public:

@@ -698,12 +698,12 @@ int pfa_hoist_rotations(const pfa_context *ctx, size_t chain_index, const uint64
         const size_t CX = (size_t)2 * QlP * c.N;
         const size_t G = std::min(n, kHoistGroup);
         uint64_t *cx = sc.alloc(G * CX);
-        uint32_t *elt_dev = sc.alloc<uint32_t>(G);
-        const uint64_t **key_dev = sc.alloc<const uint64_t *>(G);
         for (size_t e0 = 0; e0 < n; e0 += kHoistGroup) {
             const uint32_t m = (uint32_t)std::min(kHoistGroup, n - e0);
-            upload_async(c, elt_dev, elts + e0, m * sizeof(uint32_t), s);
-            upload_async(c, key_dev, keys + e0, m * sizeof(void *), s);
+            void *dev[2];
+            upload_parts(c, sc, s, {{elts + e0, m * sizeof(uint32_t)}, {keys + e0, m * sizeof(void *)}}, dev);
+            const uint32_t *elt_dev = (const uint32_t *)dev[0];
+            const uint64_t *const *key_dev = (const uint64_t *const *)dev[1];
             uint64_t *o = out + e0 * 2 * LN;
             hoist_inner(c, chain, ct, mu, elt_dev, key_dev, key_dnum, m, false, o, 2 * LN, cx, CX, s);
             fused_moddown(c, chain, cx, 2 * m, o, o, nullptr, s, 2 * LN);
@@ -728,11 +728,10 @@ int pfa_hoisting(const pfa_context *ctx, size_t chain_index, const uint64_t *ct,
         fused_modup_ntt(c, chain, ct + LN, mu, s);
         uint64_t *cx = sc.alloc((size_t)2 * QlP * c.N);
         uint64_t *c0 = sc.alloc(LN);  // sum of sigma_e(c0)
-        uint32_t *elt_dev = sc.alloc<uint32_t>(n);
-        const uint64_t **key_dev = sc.alloc<const uint64_t *>(n);
-        upload_async(c, elt_dev, elts, n * sizeof(uint32_t), s);
-        upload_async(c, key_dev, keys, n * sizeof(void *), s);
-        hoist_inner(c, chain, ct, mu, elt_dev, key_dev, key_dnum, (uint32_t)n, true, c0, 0, cx, 0, s);
+        void *dev[2];
+        upload_parts(c, sc, s, {{elts, n * sizeof(uint32_t)}, {keys, n * sizeof(void *)}}, dev);
+        hoist_inner(c, chain, ct, mu, (const uint32_t *)dev[0], (const uint64_t *const *)dev[1], key_dnum,
+                    (uint32_t)n, true, c0, 0, cx, 0, s);
         // c0' = sum sigma(c0) + ModDown(acc0), c1' = ModDown(acc1)
         op_moddown(c, chain, cx, 2, out, Bases{{c0, nullptr}}, s);
     });
