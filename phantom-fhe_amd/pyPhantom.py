@@ -1768,12 +1768,16 @@ class bootstrap_key:
 
 
 class _LayerPlan:
-    """One transform layer, ready for pfa_bsgs_mac: the baby offsets b (in
-    units), the giant indices g, and the diagonal plaintexts as a [G][M] grid
-    (a shared zero plaintext where (g, b) has no diagonal)."""
+    """One transform layer, ready for the BSGS accumulation: the baby offsets b
+    (in units), the giant indices g, the diagonal plaintexts as a [G][M] grid
+    (a shared zero plaintext where (g, b) has no diagonal), and the same grid
+    in the accumulation's tiled layout (pfa_bsgs_tile_plaintexts: each work
+    item's plaintexts contiguous, limbs below 2^40 in 5 bytes a residue),
+    which the accumulation reads."""
 
-    def __init__(self, babies, giants, grid, scale, zero):
+    def __init__(self, babies, giants, grid, scale, zero, tiled=None):
         self.babies, self.giants, self.grid, self.scale, self.zero = babies, giants, grid, scale, zero
+        self.tiled = tiled
 
 
 def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, scale_div: int = 1,
@@ -1800,7 +1804,11 @@ def _encode_layer(ctx, enc, lt: _LTLayers, i: int, chain: int, factor: complex, 
                 if zero is None:
                     zero = ctx._empty(L, ctx.N).zero_()
                 grid.append(zero)
-    return _LayerPlan(babies, giants, grid, scale, zero)
+    D = len(grid)
+    tiled = ctx._empty((ctx.native.bsgs_tiled_size(chain, D) + 7) // 8)
+    for d, pt in enumerate(grid):
+        ctx.native.bsgs_tile_plaintexts(chain, pt, 1, tiled, d, D)
+    return _LayerPlan(babies, giants, grid, scale, zero, tiled)
 
 
 BOOT_EVALMODS = ("k28_r3", "cheb63")
@@ -1903,7 +1911,7 @@ def _apply_layer(ctx, ct: ciphertext, lt: _LTLayers, pts, i: int, glk, rescale: 
             rotated[b] = r
     L = ctx.size_Ql(ct.chain_index())
     parts = ctx._empty(len(plan.giants), 2, L, ctx.N)
-    ctx.native.bsgs_mac(ct.chain_index(), plan.grid, [rotated[b].data for b in plan.babies],
+    ctx.native.bsgs_mac_tiled(ct.chain_index(), plan.tiled, [rotated[b].data for b in plan.babies],
                         [parts[k] for k in range(len(plan.giants))])
     # the giants' rotations are independent: one batched rotation (each part
     # its own element and key) when every key is present, then one weighted
