@@ -245,6 +245,12 @@ int pfa_poly_sub(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, u
                  void *stream);
 int pfa_poly_mul(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t L, size_t start,
                  void *stream);
+
+/* multiply_plain_ntt (src/evaluate.cu:1224-1250): out[k] = ct[k] * pt over
+ * limbs 0..L-1 for every poly k < size of ct [size][L][N] (NTT form), in one
+ * launch (the reference launches one multiply per poly).  out may equal ct. */
+int pfa_ct_multiply_plain(const pfa_context *ctx, const uint64_t *ct, size_t size, const uint64_t *pt, uint64_t *out,
+                          size_t L, void *stream);
 int pfa_poly_negate(const pfa_context *ctx, const uint64_t *a, uint64_t *out, size_t L, size_t start, void *stream);
 
 /* Reduces signed 64-bit coefficients (one poly, N values) into L limbs using

@@ -27,8 +27,14 @@ enum BinOp { kAdd, kSub, kMul, kNeg };
 
 __global__ void __launch_bounds__(kThreads)
 k_poly_binop(int op, const uint64_t *a, const uint64_t *b, uint64_t *out, const uint64_t *mod,
-             const ulonglong2 *ratio, uint32_t start, uint32_t N) {
-    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+             const ulonglong2 *ratio, uint32_t start, uint32_t N, uint64_t a_stride, uint64_t b_stride,
+             uint64_t out_stride) {
+    // poly blockIdx.z of a batch: a, b, out advanced by their strides (b_stride
+    // 0: one b for every poly)
+    const uint32_t l = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x, k = blockIdx.z;
+    a += k * a_stride;
+    b += k * b_stride;
+    out += k * out_stride;
     const uint64_t q = mod[start + l];
     const size_t i = (size_t)l * N + n;
     const uint64_t x = a[i];
@@ -757,7 +763,7 @@ static int binop(const pfa_context *ctx, int op, const uint64_t *a, const uint64
         require(a && out && (op == kNeg || b), "null argument");
         require(L >= 1 && start + L <= c.QP, "limb range exceeds the context's primes");
         hipLaunchKernelGGL(k_poly_binop, grid(c, (uint32_t)L), dim3(kThreads), 0, as_stream(stream), op, a,
-                           op == kNeg ? a : b, out, c.mod, c.ratio, (uint32_t)start, c.N);
+                           op == kNeg ? a : b, out, c.mod, c.ratio, (uint32_t)start, c.N, 0ull, 0ull, 0ull);
         PFA_HIP(hipGetLastError());
     });
 }
@@ -774,6 +780,20 @@ int pfa_poly_mul(const pfa_context *ctx, const uint64_t *a, const uint64_t *b, u
                  void *stream) {
     return binop(ctx, kMul, a, b, out, L, start, stream);
 }
+int pfa_ct_multiply_plain(const pfa_context *ctx, const uint64_t *ct, size_t size, const uint64_t *pt, uint64_t *out,
+                          size_t L, void *stream) {
+    return guarded([&] {
+        const Ctx &c = *ctx_of(ctx);
+        require(ct && pt && out, "null argument");
+        require(L >= 1 && L <= c.Q, "limb count out of range");
+        require(size >= 1 && size <= 65535, "bad ciphertext size");
+        const uint64_t LN = (uint64_t)L * c.N;
+        hipLaunchKernelGGL(k_poly_binop, grid(c, (uint32_t)L, (uint32_t)size), dim3(kThreads), 0, as_stream(stream),
+                           (int)kMul, ct, pt, out, c.mod, c.ratio, 0u, c.N, LN, 0ull, LN);
+        PFA_HIP(hipGetLastError());
+    });
+}
+
 int pfa_poly_negate(const pfa_context *ctx, const uint64_t *a, uint64_t *out, size_t L, size_t start, void *stream) {
     return binop(ctx, kNeg, a, nullptr, out, L, start, stream);
 }

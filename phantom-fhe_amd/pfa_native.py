@@ -59,6 +59,7 @@ SIGNATURES = {
     "pfa_poly_sub": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_mul": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_poly_negate": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "pfa_ct_multiply_plain": (_i32, [_vp, _vp, _sz, _vp, _vp, _sz, _vp]),
     "pfa_poly_from_signed": (_i32, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "pfa_ckks_encode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _sz, _vp]),
     "pfa_ckks_decode": (_i32, [_vp, _vp, _sz, C.c_double, _vp, _vp]),
@@ -316,6 +317,12 @@ class NativeContext:
 
     def poly_mul(self, a, b, out, L, start=0, stream=None):
         call("pfa_poly_mul", self._h, ptr(a), ptr(b), ptr(out), L, start, stream or stream_of(a))
+
+    def ct_multiply_plain(self, ct, pt, out, L, stream=None):
+        """out[k] = ct[k] * pt over limbs 0..L-1 for every poly of ct [size][L][N]."""
+        if ct.shape[0] != out.shape[0] or not ct.is_contiguous() or not out.is_contiguous():
+            raise ValueError("ct and out must be contiguous [size][L][N] tensors of one size")
+        call("pfa_ct_multiply_plain", self._h, ptr(ct), ct.shape[0], ptr(pt), ptr(out), L, stream or stream_of(ct))
 
     def poly_negate(self, a, out, L, start=0, stream=None):
         call("pfa_poly_negate", self._h, ptr(a), ptr(out), L, start, stream or stream_of(a))

@@ -910,8 +910,7 @@ def multiply_plain(ctx: context, ct: ciphertext, pt: plaintext) -> ciphertext:
         raise ValueError("encrypted and plain parameter mismatch")
     L = ctx.size_Ql(ct.chain_index())
     out = ctx._empty(*ct.data.shape)
-    for i in range(ct.size()):
-        ctx.native.poly_mul(ct.data[i], pt.data, out[i], L)
+    ctx.native.ct_multiply_plain(ct.data, pt.data, out, L)
     return ct._like(out, scale=ct.scale() * pt.scale())
 
 
@@ -2444,8 +2443,7 @@ def _times_i(ctx, ct: ciphertext, sign: int = 1) -> ciphertext:
 
     mono = ctx._cached_const(("times_i", sign, L), make)
     out = ctx._empty(*ct.data.shape)
-    for k in range(ct.size()):
-        ctx.native.poly_mul(ct.data[k], mono, out[k], L)
+    ctx.native.ct_multiply_plain(ct.data, mono, out, L)
     return ct._like(out)
 
 

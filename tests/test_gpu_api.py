@@ -600,3 +600,26 @@ def torch_int64():
     import torch
 
     return torch.int64
+
+
+def test_ct_multiply_plain_matches_per_poly(dev):
+    """pfa_ct_multiply_plain (multiply_plain_ntt, src/evaluate.cu:1224-1250) over
+    4 polys in one launch equals poly_mul per poly, in place too; 50- and
+    60-bit primes (both arithmetic policies)."""
+    import pfa_native as P
+
+    N = 1 << 12
+    mods = O.create_coeff_modulus(N, [60, 50, 55, 60])
+    ctx = P.NativeContext(N, mods, 1)
+    rng = np.random.default_rng(4)
+    L = 3
+    ct = uniform_limbs(rng, (4, L, N), mods[:L])
+    pt = uniform_limbs(rng, (L, N), mods[:L])
+    dct, dpt = to_dev(ct, dev), to_dev(pt, dev)
+    out = empty((4, L, N), dev)
+    ctx.ct_multiply_plain(dct, dpt, out, L)
+    want = np.stack([np.stack([(ct[k, l].astype(object) * pt[l].astype(object)) % mods[l] for l in range(L)])
+                     for k in range(4)]).astype(np.uint64)
+    assert np.array_equal(to_host(out), want)
+    ctx.ct_multiply_plain(dct, dpt, dct, L)
+    assert np.array_equal(to_host(dct), want)
