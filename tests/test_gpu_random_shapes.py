@@ -141,9 +141,9 @@ def test_wide_digits_bit_exact(dev, nq, alpha):
 
 
 def test_many_rotations_bit_exact(dev):
-    """20 hoisted rotations (two groups of the launcher's 16 per ModDown) and a
-    rotation batch of 70 members (past the 64-member work schedules), each
-    member against the oracle's apply_galois / hoist_rotations."""
+    """20 hoisted rotations (two groups of the launcher's 16 per ModDown), their
+    sum (hoisting), and a rotation batch of 70 members (past the 64-member work
+    schedules), against the oracle's hoist_rotations / hoisting / apply_galois."""
     import pfa_native as P
 
     st = Setup(12, 4, 2, seed=20, bits=[60, 50, 50, 50, 60, 60])
@@ -159,6 +159,12 @@ def test_many_rotations_bit_exact(dev):
     want = orc.hoist_rotations(chain, ct, elts, [keys[i % 4] for i in range(20)], threads=8)
     got = to_host(out)
     assert np.array_equal(got, want), ("hoist 20", first_mismatch(got, want))
+    # the sum of the 20 rotations (hoisting: one launch for all members)
+    summed = empty((2, Ql, N), dev)
+    st.ctx.hoisting(chain, to_dev(ct, dev), elts, [dkeys[i % 4] for i in range(20)], summed)
+    want = orc.hoisting(chain, ct, elts, [keys[i % 4] for i in range(20)], threads=8)
+    got = to_host(summed)
+    assert np.array_equal(got, want), ("hoisting 20", first_mismatch(got, want))
     cts = np.stack([st.ct(chain) for _ in range(70)])
     belts = [elts[i % 20] for i in range(70)]
     out = empty(cts.shape, dev)
