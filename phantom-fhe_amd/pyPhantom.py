@@ -1084,10 +1084,13 @@ def mod_switch_to_inplace(ctx: context, obj, chain_index: int) -> None:
 
 
 def _apply_galois_key(ctx: context, ct: ciphertext, elt: int, key) -> ciphertext:
+    """apply_galois_with_ksk (src/evaluate.cu:1607-1656) into a new ciphertext:
+    a rotation batch of one, which reads ct and writes the output (the same
+    residues as the in-place pfa_apply_galois, without copying ct first)."""
     if ct.size() != 2:
         raise ValueError("ciphertext size must be 2")
-    out = ct.data.clone()
-    ctx.native.apply_galois(ct.chain_index(), out, elt, key)
+    out = ctx._empty(*ct.data.shape)
+    ctx.native.rotate_batch(ct.chain_index(), ct.data.contiguous(), [elt], [key], out)
     return ct._like(out)
 
 
