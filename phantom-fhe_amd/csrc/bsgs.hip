@@ -548,8 +548,11 @@ int pfa_rotate_batch(const pfa_context *ctx, size_t chain_index, size_t count, c
             require((elts[i] & 1) && elts[i] < 2 * c.N, "bad Galois element");
             check_key(c, chain, keys[i], key_dnum);
         }
-        rotate_into(c, chain, in, ct_elems, (uint32_t)count, 0, nullptr, nullptr, out, as_stream(stream), elts,
-                    keys);
+        if (count == 1)  // one element and key: no device tables to upload
+            rotate_into(c, chain, in, ct_elems, 1, elts[0], keys[0], nullptr, out, as_stream(stream));
+        else
+            rotate_into(c, chain, in, ct_elems, (uint32_t)count, 0, nullptr, nullptr, out, as_stream(stream), elts,
+                        keys);
     });
 }
 
