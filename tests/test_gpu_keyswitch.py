@@ -354,7 +354,7 @@ def test_apply_galois(dev, logN, nq, alpha, chain):
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 6, 2, 1), (12, 5, 1, 2), (16, 6, 3, 1)])
+@pytest.mark.parametrize("logN,nq,alpha,chain", [(12, 6, 2, 1), (12, 5, 1, 2), (16, 6, 3, 1), (17, 3, 1, 1)])
 def test_hoist_rotations(dev, logN, nq, alpha, chain):
     import pfa_native as P
 
