@@ -19,8 +19,8 @@ pytestmark = pytest.mark.gpu
 def test_streams_concurrent_keyswitch(dev, logN, nq, alpha):
     """Config 3's shape (whose inner product splits its left-over items into
     digit chunks) and a small one: three threads, each on its own stream, each
-    enqueueing 6 fused HMult + relinearize + rescale calls and 6 rotations,
-    concurrently."""
+    enqueueing 6 fused HMult + relinearize + rescale calls, 6 rotations and 6
+    pairs of hoisted rotations, concurrently."""
     import torch
 
     import pfa_native as P
@@ -33,7 +33,7 @@ def test_streams_concurrent_keyswitch(dev, logN, nq, alpha):
     a = [to_dev(st.ct(chain), dev) for _ in range(T)]
     b = [to_dev(st.ct(chain), dev) for _ in range(T)]
     elts = [P.galois_elt_from_step(s, N) for s in (1, -7, 33)]
-    want_m, want_r = [], []
+    want_m, want_r, want_h = [], [], []
     for i in range(T):
         o = empty((2, Ql - 1, N), dev)
         st.ctx.multiply_relin_rescale(chain, a[i], b[i], key, o)
@@ -41,6 +41,9 @@ def test_streams_concurrent_keyswitch(dev, logN, nq, alpha):
         d = a[i].clone()
         st.ctx.apply_galois(chain, d, elts[i], key)
         want_r.append(to_host(d))
+        h = empty((2, 2, Ql, N), dev)
+        st.ctx.hoist_rotations(chain, b[i], elts[:2], [key, key], h)
+        want_h.append(to_host(h))
     torch.cuda.synchronize()
     results, errors = [None] * T, []
 
@@ -54,9 +57,11 @@ def test_streams_concurrent_keyswitch(dev, logN, nq, alpha):
                     st.ctx.multiply_relin_rescale(chain, a[i], b[i], key, o)
                     d = a[i].clone()
                     st.ctx.apply_galois(chain, d, elts[i], key)
-                    outs.append((o, d))
+                    h = empty((2, 2, Ql, N), dev)
+                    st.ctx.hoist_rotations(chain, b[i], elts[:2], [key, key], h)
+                    outs.append((o, d, h))
             st.ctx.synchronize(s.cuda_stream)
-            results[i] = [(o.cpu().numpy(), d.cpu().numpy()) for o, d in outs]
+            results[i] = [(o.cpu().numpy(), d.cpu().numpy(), h.cpu().numpy()) for o, d, h in outs]
         except Exception as e:  # reported below
             errors.append((i, repr(e)))
 
@@ -67,6 +72,7 @@ def test_streams_concurrent_keyswitch(dev, logN, nq, alpha):
         t.join()
     assert errors == []
     for i in range(T):
-        for rep, (m, r) in enumerate(results[i]):
+        for rep, (m, r, h) in enumerate(results[i]):
             assert np.array_equal(m, want_m[i]), ("hmult", i, rep, first_mismatch(m, want_m[i]))
             assert np.array_equal(r, want_r[i]), ("rotate", i, rep, first_mismatch(r, want_r[i]))
+            assert np.array_equal(h, want_h[i]), ("hoist", i, rep, first_mismatch(h, want_h[i]))
