@@ -2194,13 +2194,17 @@ def _ct_lincomb(ctx, L: int, ins, consts, out, bias, members: int = 1) -> None:
 
 def _bundle(ctx, cts) -> ciphertext:
     """Size-2 ciphertexts at one level and scale -> one bundle (their data stacked)."""
-    t = _torch()
     c0 = cts[0]
     for c in cts:
         if c.size() != 2 or c._members != 1 or c.chain_index() != c0.chain_index():
             raise ValueError("bundle members must be size-2 ciphertexts at one level")
         _check_scale(c, c0)
-    b = c0._like(t.cat([c.data for c in cts]).contiguous())
+    # copied with the library's streaming copy: a torch kernel between the
+    # library's launches on torch's default stream costs far more than the copy
+    data = ctx._empty(2 * len(cts), *c0.data.shape[1:])
+    for i, c in enumerate(cts):
+        _N.stream_copy(data[2 * i:2 * i + 2], c.data.contiguous())
+    b = c0._like(data)
     b._members = len(cts)
     return b
 
