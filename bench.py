@@ -72,8 +72,10 @@ def spin_up(torch, step, ms=40.0, chunk=20, cap=20000):
 def time_ntt(torch, ctx, batches, steps, warmup, inverse=False):
     """Returns (wall seconds for `steps` transforms, average ms per transform from
     HIP events recorded on the launch stream around the whole timed region)."""
+    import pfa_native as P
+
     stream = torch.cuda.current_stream()
-    h = stream.cuda_stream
+    h = P.stream_handle(stream)
     fn = ctx.ntt_inverse if inverse else ctx.ntt_forward
     spin_up(torch, lambda i: fn(batches[i % len(batches)], POLYS, LIMBS, 0, h))
     for i in range(warmup):
@@ -96,7 +98,7 @@ def time_copy(torch, P, batches, steps, warmup):
     destinations: the achievable one-read-one-write rate the NTT's 73.4 MB per
     transform is measured against.  Returns microseconds per copy (HIP events)."""
     stream = torch.cuda.current_stream()
-    h = stream.cuda_stream
+    h = P.stream_handle(stream)
     dsts = [torch.empty_like(b) for b in batches]
     n = len(batches)
     spin_up(torch, lambda i: P.stream_copy(dsts[(i + 3) % n], batches[i % n], 0, h))
@@ -122,7 +124,7 @@ def ntt_limb_sweep(torch, P, dev, gen, steps):
     mods = P.create_coeff_modulus(N, [50] * 48 + [60])
     ctx = P.NativeContext(N, mods, 1)
     stream = torch.cuda.current_stream()
-    h = stream.cuda_stream
+    h = P.stream_handle(stream)
     rows = []
     for L in (28, 30, 32, 33, 34, 35, 36, 40, 48):
         bs = [uniform(torch, (POLYS, L, N), mods, dev, gen) for _ in range(10)]
@@ -158,7 +160,7 @@ def time_hmult(torch, P, dev, gen, nq, alpha, steps, warmup):
         key[d] = uniform(torch, (2, nq + alpha, N), mods, dev, gen)
     out = torch.empty((2, nq, N), dtype=torch.uint64, device=dev)
     res = torch.empty((2, nq - 1, N), dtype=torch.uint64, device=dev)
-    s = torch.cuda.current_stream().cuda_stream
+    s = P.stream_handle(torch.cuda.current_stream())
 
     def separate(_):
         ctx.multiply_and_relin(1, a, b, key, out, s)

@@ -139,11 +139,26 @@ def ptr(t) -> int:
     return t.data_ptr()
 
 
+# torch's default stream reports handle 0 and is HIP's legacy default stream;
+# the C ABI reads a NULL stream as hipStreamPerThread (the reference's
+# cudaStreamPerThread), a different stream that the legacy one synchronizes
+# with implicitly.  A torch kernel followed by the library's work on those two
+# streams then cost ~70 us of GPU time per switch (and a bootstrap with one
+# such switch ~2 ms), so the default stream is passed as hipStreamLegacy.
+HIP_STREAM_LEGACY = 1
+
+
+def stream_handle(stream) -> int:
+    """The hipStream_t to pass for a torch stream (its handle, or
+    hipStreamLegacy for torch's default stream)."""
+    return stream.cuda_stream or HIP_STREAM_LEGACY
+
+
 def stream_of(t=None):
     import torch
 
     dev = t.device if t is not None else torch.device("cuda", torch.cuda.current_device())
-    return torch.cuda.current_stream(dev).cuda_stream
+    return stream_handle(torch.cuda.current_stream(dev))
 
 
 def stream_copy(dst, src, workgroups: int = 0, stream=None):
@@ -233,7 +248,7 @@ class NativeContext:
         if stream is None:
             import torch
 
-            stream = torch.cuda.current_stream(self.device).cuda_stream
+            stream = stream_handle(torch.cuda.current_stream(self.device))
         call("pfa_synchronize", self._h, stream)
 
     def modup(self, chain_index, c2, out, stream=None):
