@@ -71,3 +71,17 @@ def test_cuda_stream_needs_a_device():
         pytest.skip("a device is visible; the GPU tests cover cuda_stream")
     with pytest.raises(RuntimeError):
         ph.cuda_stream()
+
+
+def test_stream_handle_maps_torch_default_stream():
+    """torch's default stream (handle 0) goes to the library as hipStreamLegacy
+    (1), not as NULL, which the C ABI reads as hipStreamPerThread; any other
+    stream's handle passes through."""
+    import pfa_native as P
+
+    class S:
+        def __init__(self, h):
+            self.cuda_stream = h
+
+    assert P.stream_handle(S(0)) == P.HIP_STREAM_LEGACY == 1
+    assert P.stream_handle(S(0x5A5A0)) == 0x5A5A0
